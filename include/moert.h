@@ -1,0 +1,207 @@
+/*
+ * moert.h — C ABI of the MI355X (gfx950) Granite-MoE decode engine.
+ *
+ * The library (libmoert.so, built with hipcc for gfx950) replaces the GPU side of the reference crate
+ * `rust/moe-rt` (brenoperucchi/lastro-rust). Every entry point names the reference item it stands in for.
+ * Paths are relative to the reference repository root.
+ *
+ * Conventions
+ *  - Every function returns an int status: 0 (MOERT_OK) or a negative MOERT_E_* code. moert_last_error()
+ *    returns a thread-local message for the last failure on the calling thread
+ *    (mirrors CudaError::{Driver, Kernel, Config}, rust/moe-rt/src/cuda_backend.rs:61-67).
+ *  - After a device error the handle is poisoned: the stream is synchronised before any buffer is released,
+ *    and later calls on the handle return MOERT_E_POISONED (rust/moe-rt/src/gpu_model.rs:249-267,
+ *    rust/moe-rt/src/gpu.rs:451-466).
+ *  - All pointers in signatures are host pointers unless a name ends in `_dev`. Sizes are element counts.
+ *  - Matrices are row-major [rows, cols]. Quantised matrices use the GGML block layouts:
+ *      Q8_0: 34-byte blocks {fp16 d; int8 q[32]}, w = q * d
+ *      Q4_0: 18-byte blocks {fp16 d; uint8 nib[16]}, w[j] = ((nib[j] & 15) - 8) * d,
+ *            w[j + 16] = ((nib[j] >> 4) - 8) * d
+ *    Blocks run along a row; cols must be a multiple of 32.
+ *  - One handle must not be used from two threads at once (the reference keeps backend state behind a
+ *    Mutex, rust/moe-rt/src/cuda_backend.rs:243).
+ */
+#ifndef MOERT_H
+#define MOERT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  MOERT_OK = 0,
+  MOERT_E_DEVICE = -1,   /* a HIP call failed (CudaError::Driver) */
+  MOERT_E_CONFIG = -2,   /* shape or argument refused before any launch (CudaError::Config) */
+  MOERT_E_POISONED = -3, /* the handle saw an earlier device error */
+  MOERT_E_FULL = -4,     /* KV cache full (rust/moe-rt/src/gpu_model.rs:252-254) */
+  MOERT_E_RANGE = -5     /* token or index out of range (rust/moe-rt/src/gpu_model.rs:255-257) */
+};
+
+typedef enum { MOERT_F32 = 0, MOERT_Q8_0 = 1, MOERT_Q4_0 = 2 } moert_dtype;
+
+/* Model constants; mirrors `Config` (rust/moe-rt/src/model.rs:14-31). */
+typedef struct {
+  int hidden, inter, layers, heads, kv_heads, head_dim, vocab, experts, top_k;
+  float rope_theta, eps, embedding_multiplier, residual_multiplier, attention_multiplier, logits_scaling;
+} moert_config;
+
+/* A host matrix in one of the dtypes above. */
+typedef struct {
+  const void* data;
+  int dtype; /* moert_dtype */
+} moert_tensor;
+
+/* One decoder layer; mirrors `HostDecoder` + `HostLayer` (rust/moe-rt/src/model.rs:76-85,
+ * rust/moe-rt/src/block.rs:9-19). */
+typedef struct {
+  const float* ln_attn;      /* [H] */
+  const float* ln_moe;       /* [H] */
+  moert_tensor q, k, v, o;   /* [heads*d, H], [kv*d, H], [kv*d, H], [H, heads*d] */
+  moert_tensor router;       /* [E, H] */
+  const float* router_bias;  /* [E] added to the router logits, or NULL (the Granite router has none;
+                                the skewed-routing workloads use one) */
+  moert_tensor gate_up;      /* [E, 2I, H]: rows [0, I) gate, [I, 2I) up */
+  moert_tensor down;         /* [E, H, I] */
+} moert_layer_weights;
+
+/* Whole model; mirrors `HostModel` (rust/moe-rt/src/model.rs:87-93). The embedding is tied to the head. */
+typedef struct {
+  moert_tensor embed;                /* [V, H] */
+  const float* norm;                 /* [H] */
+  const moert_layer_weights* layers; /* [layers] */
+} moert_model_weights;
+
+typedef struct moert_model moert_model;
+typedef struct moert_block moert_block;
+typedef struct moert_pool moert_pool;
+
+const char* moert_last_error(void);
+
+/* Device count and name of device 0 (0 devices is not an error). */
+int moert_device_info(int* count, char* name, int name_len);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Whole-model decode. Replaces GpuModel::{upload, step, reset} (rust/moe-rt/src/gpu_model.rs:191-267) and the
+ * model-mode inherent methods of CudaBackend (new_model, begin_token, read_logits, reset_sequence,
+ * rust/moe-rt/src/cuda_backend.rs:466-633).
+ * ------------------------------------------------------------------------------------------------------- */
+
+/* Uploads every weight to HBM (all experts resident) and allocates an fp16 KV cache of max_len positions.
+ * attn_splits is the number of split-KV blocks per KV head (ATTN_NS, rust/moe-rt/src/gpu_model.rs:22).
+ * Replaces GpuModel::upload (rust/moe-rt/src/gpu_model.rs:191-194). */
+int moert_model_create(const moert_config* cfg, const moert_model_weights* w, int max_len, int attn_splits,
+                       moert_model** out);
+int moert_model_destroy(moert_model* m);
+
+/* One token at the current position: logits of the next position (vocab floats, divided by logits_scaling),
+ * the router decision of every layer (layers*top_k ids and weights, top-k order) and the greedy argmax.
+ * Any output pointer may be NULL. Replaces GpuModel::step (rust/moe-rt/src/gpu_model.rs:251-267). */
+int moert_decode_step(moert_model* m, int token, float* logits, int* route_ids, float* route_weights,
+                      int* argmax);
+
+/* Greedy generation with no host synchronisation between tokens: feeds the n_prompt tokens one position at a
+ * time, then n_new tokens chosen by argmax (last index on ties). out_tokens receives the n_new generated ids;
+ * gaps (optional, n_new floats) receives top1 - top2 of the logits each generated token was chosen from.
+ * Replaces the prompt + generation loop of rust/moe-rt/src/bin/m1b-gulosa.rs:85-105. */
+int moert_generate(moert_model* m, const int* prompt, int n_prompt, int n_new, int* out_tokens, float* gaps);
+
+/* Back to position 0 (old KV stays, masked by the length). Replaces GpuModel::reset
+ * (rust/moe-rt/src/gpu_model.rs:245-247) and CudaBackend::reset_sequence (cuda_backend.rs:555-558). */
+int moert_reset_sequence(moert_model* m);
+
+/* Writes positions [0, n) of layer `layer`'s KV cache from fp16 host arrays laid out [kv_heads, n, head_dim]
+ * and leaves the position unchanged. moert_set_position then selects where decoding resumes. */
+int moert_kv_prefill_fp16(moert_model* m, int layer, const uint16_t* k, const uint16_t* v, int n);
+int moert_set_position(moert_model* m, int pos);
+int moert_get_position(moert_model* m, int* pos);
+
+/* Reads positions [0, n) of layer `layer` back (fp16, layout as above). Replaces CudaBackend::read_kv
+ * (rust/moe-rt/src/cuda_backend.rs:597-604). */
+int moert_read_kv_fp16(moert_model* m, int layer, uint16_t* k, uint16_t* v, int n);
+
+/* Hidden state after the last step (hidden floats, before the final norm). */
+int moert_read_hidden(moert_model* m, float* h);
+
+/* Times `iters` graph replays of the decode step (after `warmup`) with HIP events on the model's stream.
+ * ms_per_step receives the mean. The position advances by warmup + iters. */
+int moert_time_steps(moert_model* m, int warmup, int iters, double* ms_per_step);
+
+/* Per-kernel timing: replays the step `iters` times as individual launches with a HIP event pair around every
+ * launch of kernel class `kind` (see moert_kernel_kind) and returns the mean duration of one launch in
+ * microseconds and the number of launches timed. Position advances by iters. */
+typedef enum {
+  MOERT_K_EMBED = 0, MOERT_K_QKV = 1, MOERT_K_ATTN = 2, MOERT_K_OPROJ = 3, MOERT_K_ROUTER = 4,
+  MOERT_K_EXPERT_UP = 5, MOERT_K_EXPERT_DOWN = 6, MOERT_K_HEAD = 7, MOERT_K_COUNT = 8
+} moert_kernel_kind;
+int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch, int* launches);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * One MoE block with every expert resident. Replaces GpuLayer::{upload, add_into_routed, run}
+ * (rust/moe-rt/src/gpu.rs:430-541) and HostLayer::forward_cpu (rust/moe-rt/src/block.rs:56-62).
+ * ------------------------------------------------------------------------------------------------------- */
+int moert_block_create(int hidden, int inter, int experts, int top_k, const moert_tensor* router,
+                       const float* router_bias, const moert_tensor* gate_up, const moert_tensor* down,
+                       moert_block** out);
+int moert_block_destroy(moert_block* b);
+/* y = sum_j w_j * expert_{id_j}(x) over the top_k experts, ids/weights in top-k order. x is the already
+ * normalised block input (hidden floats). */
+int moert_block_forward(moert_block* b, const float* x, float* y, int* ids, float* weights);
+/* Mean microseconds of one block forward over `iters` launches (inputs resident in HBM). */
+int moert_block_time(moert_block* b, int iters, double* us);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Unit-parity entry points: one kernel on host buffers (copied in and out). For tests of each subsystem.
+ * ------------------------------------------------------------------------------------------------------- */
+
+/* Top-k of logits (ties to the lower index, total order on floats) and softmax over the k.
+ * Replaces route_topk (rust/moe-rt/src/route.rs:18-75) / Routing::from_logits (rust/moe-rt/src/block.rs:81-89). */
+int moert_router_topk(const float* logits, int n_experts, int k, int* ids, float* weights);
+
+/* Greedy sampler: index of the largest value, last index on ties (rust/moe-rt/src/bin/m1b-gulosa.rs:22-24). */
+int moert_argmax(const float* v, int n, int* idx);
+
+/* y = W x for a host matrix of any dtype (rust/moe-rt/src/gpu.rs:21-38, Cpu::gemv cpu.rs:108-113). */
+int moert_gemv(const moert_tensor* w, int rows, int cols, const float* x, float* y);
+
+/* Device dequantisation of a quantised matrix to f32 (for the bit-exact dequant check). */
+int moert_dequant(const moert_tensor* w, int rows, int cols, float* out);
+
+/* out = w * x / sqrt(mean(x^2) + eps) (rust/moe-rt/src/model.rs:141-145; gpu.rs:108-128). */
+int moert_rmsnorm(const float* x, const float* w, int n, float eps, float* out);
+
+/* rotate_half RoPE of `heads` heads of head_dim in place, at position pos (model.rs:148-158, gpu.rs:133-144). */
+int moert_rope(float* x, int heads, int head_dim, float theta, int pos);
+
+/* Decode attention of `heads` query heads against an fp16 cache [kv_heads, max_len, head_dim] holding `len`
+ * valid positions, in `splits` split-KV blocks per KV head
+ * (attn_split + attn_combine, rust/moe-rt/src/gpu.rs:205-292; CpuSession attention model.rs:200-222). */
+int moert_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, int heads, int kv_heads,
+                      int head_dim, int max_len, int len, float scale, int splits, float* out);
+
+/* Canonical exponential used by every kernel (softmax, SiLU, top-k weights), evaluated on the device. */
+int moert_exp_device(const float* x, float* y, int n);
+
+/* ---------------------------------------------------------------------------------------------------------
+ * Host utilities (no device needed).
+ * ------------------------------------------------------------------------------------------------------- */
+
+/* f32 -> GGML Q8_0 / Q4_0 blocks (n multiple of 32). */
+int moert_quantize(const float* x, size_t n, int dtype, void* out);
+/* Bytes of n elements of a dtype. */
+size_t moert_dtype_bytes(int dtype, size_t n);
+
+/* Seeded synthetic data: N(0, 1) * scale + offset as f32, a counter-based generator so that any sub-range can
+ * be produced independently (stream = tensor id). */
+int moert_synth_normal(uint64_t seed, uint64_t stream, size_t n, float scale, float offset, float* out);
+/* Same values quantised straight to Q8_0 / Q4_0 blocks (n multiple of 32), multithreaded. */
+int moert_synth_quantized(uint64_t seed, uint64_t stream, size_t n, float scale, int dtype, void* out);
+/* Same values rounded to fp16. */
+int moert_synth_fp16(uint64_t seed, uint64_t stream, size_t n, float scale, uint16_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

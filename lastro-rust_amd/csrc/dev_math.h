@@ -1,0 +1,156 @@
+// Device arithmetic shared by every kernel of the decode engine (gfx950, wave64).
+//
+// Evaluation order is fixed so that results are reproducible bit for bit:
+//   - dot products: a row is cut into chunks of 16 bytes of payload (Q8_0: 16 elements, Q4_0: 32, f32: 4);
+//     chunk j is accumulated by lane j % 64 (chunks in increasing j, elements in increasing index,
+//     acc = fma(w, x, acc) from +0); the 64 lane sums are combined by an xor butterfly, which leaves every lane
+//     holding the balanced pairwise tree of the 64 sums;
+//   - exp is dexp below (Cody-Waite reduction, degree-7 Taylor polynomial), never the hardware exp2;
+//   - division and sqrt are IEEE correctly rounded (hipcc's default), nothing else is fused (-ffp-contract=off).
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moert {
+
+constexpr int kWave = 64;
+
+// exp(x): x = n*ln2 + r with ln2 split into a 15-bit head and a tail (Cody & Waite), e^r by the degree-7 Taylor
+// polynomial in Horner form (|r| <= ln2/2, truncation < 1e-8 relative), result 2p * 2^(n-1) with both factors
+// exact. x < -86.5 gives 0 (no subnormal results), x > 89 gives +inf.
+__device__ __forceinline__ float dexp(float x) {
+  if (x != x) return x;
+  if (x > 89.0f) return __int_as_float(0x7f800000);
+  if (x < -86.5f) return 0.0f;
+  float n = __builtin_rintf(x * 1.44269504088896341f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  r = __builtin_fmaf(-n, 1.42860682030941723212e-6f, r);
+  float p = 1.98412698412698413e-4f;
+  p = __builtin_fmaf(p, r, 1.38888888888888889e-3f);
+  p = __builtin_fmaf(p, r, 8.33333333333333333e-3f);
+  p = __builtin_fmaf(p, r, 4.16666666666666667e-2f);
+  p = __builtin_fmaf(p, r, 1.66666666666666667e-1f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  return (p * 2.0f) * __int_as_float((ni - 1 + 127) << 23);
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + dexp(-g))) * u; }
+
+// Butterfly sum over the lanes [0, W) of each W-lane group; every lane ends with the pairwise-tree sum.
+template <int W = kWave>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int s = 1; s < W; s <<= 1) v = v + __shfl_xor(v, s);
+  return v;
+}
+
+template <int W = kWave>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int s = 1; s < W; s <<= 1) {
+    float o = __shfl_xor(v, s);
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+// Total order on floats as integers (Rust's f32::total_cmp).
+__device__ __forceinline__ int total_key(float f) {
+  int s = __float_as_int(f);
+  return s >= 0 ? s : (s ^ 0x7fffffff);
+}
+
+__device__ __forceinline__ float h2f(uint16_t h) { return __half2float(__ushort_as_half(h)); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __half_as_ushort(__float2half_rn(f)); }
+
+// Quantised matrix in HBM, struct-of-arrays: the payload plane (int8 values for Q8_0, GGML nibble pairs for
+// Q4_0, f32 for F32) row-major, then one fp16 scale per 32-element block.
+struct DMat {
+  const uint8_t* q;
+  const uint16_t* d;
+  int dtype;
+  int rows, cols;
+};
+
+enum { DT_F32 = 0, DT_Q8_0 = 1, DT_Q4_0 = 2 };
+
+template <int DT> struct Fmt;
+template <> struct Fmt<DT_Q8_0> {
+  static constexpr int kElems = 16;  // elements per 16-byte chunk
+  __device__ static size_t row_bytes(int cols) { return (size_t)cols; }
+};
+template <> struct Fmt<DT_Q4_0> {
+  static constexpr int kElems = 32;
+  __device__ static size_t row_bytes(int cols) { return (size_t)cols / 2; }
+};
+template <> struct Fmt<DT_F32> {
+  static constexpr int kElems = 4;
+  __device__ static size_t row_bytes(int cols) { return (size_t)cols * 4; }
+};
+
+// One 16-byte chunk j of a row, loaded raw, with its scale.
+struct RawChunk {
+  uint4 v;
+  float d;
+};
+
+template <int DT>
+__device__ __forceinline__ RawChunk load_chunk(const DMat& m, size_t row, int j) {
+  RawChunk c;
+  const uint8_t* base = m.q + row * Fmt<DT>::row_bytes(m.cols);
+  c.v = *reinterpret_cast<const uint4*>(base + (size_t)j * 16);
+  if (DT == DT_Q8_0)
+    c.d = h2f(m.d[row * (size_t)(m.cols / 32) + (j >> 1)]);
+  else if (DT == DT_Q4_0)
+    c.d = h2f(m.d[row * (size_t)(m.cols / 32) + j]);
+  else
+    c.d = 1.0f;
+  return c;
+}
+
+// acc = fma chain over the chunk's elements in index order; x holds the chunk's Fmt<DT>::kElems activations.
+template <int DT>
+__device__ __forceinline__ float fma_chunk(const RawChunk& c, const float* x, float acc) {
+  const uint32_t w[4] = {c.v.x, c.v.y, c.v.z, c.v.w};
+  if (DT == DT_Q8_0) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      float q = (float)(int8_t)(w[i >> 2] >> (8 * (i & 3)));
+      acc = __builtin_fmaf(q * c.d, x[i], acc);
+    }
+  } else if (DT == DT_Q4_0) {
+    // GGML Q4_0: byte b holds element b (low nibble) and element b + 16 (high nibble).
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      float q = (float)((int)((w[i >> 2] >> (8 * (i & 3))) & 15u) - 8);
+      acc = __builtin_fmaf(q * c.d, x[i], acc);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      float q = (float)((int)((w[i >> 2] >> (8 * (i & 3) + 4)) & 15u) - 8);
+      acc = __builtin_fmaf(q * c.d, x[16 + i], acc);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc = __builtin_fmaf(__uint_as_float(w[i]), x[i], acc);
+  }
+  return acc;
+}
+
+// Dequantised element i of a chunk (for the dequant kernel).
+template <int DT>
+__device__ __forceinline__ float chunk_elem(const RawChunk& c, int i) {
+  const uint32_t w[4] = {c.v.x, c.v.y, c.v.z, c.v.w};
+  if (DT == DT_Q8_0) return (float)(int8_t)(w[i >> 2] >> (8 * (i & 3))) * c.d;
+  if (DT == DT_Q4_0) {
+    int b = i & 15, sh = 8 * (b & 3) + (i >= 16 ? 4 : 0);
+    return (float)((int)((w[b >> 2] >> sh) & 15u) - 8) * c.d;
+  }
+  return __uint_as_float(w[i]);
+}
+
+}  // namespace moert

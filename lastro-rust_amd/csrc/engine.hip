@@ -1,0 +1,909 @@
+// Host side of the decode engine: C++ classes that mirror the reference's GpuModel / GpuLayer
+// (rust/moe-rt/src/gpu_model.rs, gpu.rs) and the extern "C" ABI declared in include/moert.h.
+//
+// Memory: every weight is resident in HBM as struct-of-arrays (payload plane + fp16 scale plane); q/k/v of a
+// layer are stacked into one [q; k; v] matrix; experts of a layer are one [E*2I, H] gate_up and one [E*H, I] down
+// matrix. The KV cache is fp16 [kv_heads, max_len, head_dim] per layer. One decode step is a fixed sequence of
+// kernels captured once into a hipGraph: the token and the position live in device memory (seq, state), so the
+// same graph serves every position and greedy generation needs no host synchronisation between tokens.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/moert.h"
+#include "host_utils.h"
+#include "kernels.h"
+
+using namespace moert;
+
+namespace {
+
+thread_local std::string g_err;
+
+void set_err(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+}
+
+#define CHECK_HIP(expr)                                                           \
+  do {                                                                            \
+    hipError_t e_ = (expr);                                                       \
+    if (e_ != hipSuccess) {                                                       \
+      set_err("%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_), __FILE__, __LINE__); \
+      return MOERT_E_DEVICE;                                                      \
+    }                                                                             \
+  } while (0)
+
+#define CHECK_CFG(cond, ...)   \
+  do {                         \
+    if (!(cond)) {             \
+      set_err(__VA_ARGS__);    \
+      return MOERT_E_CONFIG;   \
+    }                          \
+  } while (0)
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+// Device allocations owned by one handle, freed only after its stream is idle
+// (Release after both streams synced, rust/moe-rt/src/motor/mem.rs:1-13).
+struct Arena {
+  std::vector<void*> ptrs;
+  int alloc(void** p, size_t bytes) {
+    *p = nullptr;
+    if (bytes == 0) bytes = 256;
+    CHECK_HIP(hipMalloc(p, bytes));
+    ptrs.push_back(*p);
+    return MOERT_OK;
+  }
+  void release() {
+    for (void* p : ptrs) (void)hipFree(p);
+    ptrs.clear();
+  }
+};
+
+bool valid_dtype(int dt) { return dt == MOERT_F32 || dt == MOERT_Q8_0 || dt == MOERT_Q4_0; }
+
+// Repacks `parts` (each [rows_i, cols] of one dtype, GGML blocks) into one SoA device matrix.
+struct Part {
+  const void* data;
+  int rows;
+};
+int upload_matrix(Arena& a, hipStream_t s, const std::vector<Part>& parts, int dtype, int cols, DMat* out) {
+  CHECK_CFG(valid_dtype(dtype), "unknown dtype %d", dtype);
+  CHECK_CFG(cols % 32 == 0, "row length %d is not a multiple of 32", cols);
+  size_t rows = 0;
+  for (const Part& p : parts) {
+    CHECK_CFG(p.data != nullptr, "missing weight tensor");
+    rows += (size_t)p.rows;
+  }
+  size_t plane = dtype == MOERT_Q8_0 ? rows * cols : dtype == MOERT_Q4_0 ? rows * cols / 2 : rows * cols * 4;
+  size_t scales = dtype == MOERT_F32 ? 0 : rows * (cols / 32) * 2;
+  void* dev;
+  int rc = a.alloc(&dev, align256(plane) + scales);
+  if (rc) return rc;
+  std::vector<uint8_t> q(plane);
+  std::vector<uint16_t> d(scales / 2);
+  size_t r0 = 0;
+  for (const Part& p : parts) {
+    const uint8_t* src = (const uint8_t*)p.data;
+    size_t nb = (size_t)p.rows * (cols / 32);
+    if (dtype == MOERT_F32) {
+      std::memcpy(q.data() + r0 * cols * 4, src, (size_t)p.rows * cols * 4);
+    } else if (dtype == MOERT_Q8_0) {
+      uint8_t* qd = q.data() + r0 * cols;
+      uint16_t* dd = d.data() + r0 * (cols / 32);
+      for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = src + b * 34;
+        dd[b] = (uint16_t)(blk[0] | (blk[1] << 8));
+        std::memcpy(qd + b * 32, blk + 2, 32);
+      }
+    } else {
+      uint8_t* qd = q.data() + r0 * cols / 2;
+      uint16_t* dd = d.data() + r0 * (cols / 32);
+      for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = src + b * 18;
+        dd[b] = (uint16_t)(blk[0] | (blk[1] << 8));
+        std::memcpy(qd + b * 16, blk + 2, 16);
+      }
+    }
+    r0 += (size_t)p.rows;
+  }
+  CHECK_HIP(hipMemcpyAsync(dev, q.data(), plane, hipMemcpyHostToDevice, s));
+  if (scales) CHECK_HIP(hipMemcpyAsync((uint8_t*)dev + align256(plane), d.data(), scales, hipMemcpyHostToDevice, s));
+  CHECK_HIP(hipStreamSynchronize(s));
+  out->q = (const uint8_t*)dev;
+  out->d = scales ? (const uint16_t*)((uint8_t*)dev + align256(plane)) : nullptr;
+  out->dtype = dtype;
+  out->rows = (int)rows;
+  out->cols = cols;
+  return MOERT_OK;
+}
+
+int upload_f32(Arena& a, hipStream_t s, const float* src, size_t n, float** out) {
+  void* p;
+  int rc = a.alloc(&p, n * 4);
+  if (rc) return rc;
+  if (src) CHECK_HIP(hipMemcpyAsync(p, src, n * 4, hipMemcpyHostToDevice, s));
+  else CHECK_HIP(hipMemsetAsync(p, 0, n * 4, s));
+  *out = (float*)p;
+  return MOERT_OK;
+}
+
+template <class T>
+int zeros(Arena& a, hipStream_t s, size_t n, T** out) {
+  void* p;
+  int rc = a.alloc(&p, n * sizeof(T));
+  if (rc) return rc;
+  CHECK_HIP(hipMemsetAsync(p, 0, n * sizeof(T), s));
+  *out = (T*)p;
+  return MOERT_OK;
+}
+
+bool k_supported(int k) { return k == 128 || k == 256 || k == 512 || k == 1024 || k == 1536; }
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------------------------------
+// GpuModel (rust/moe-rt/src/gpu_model.rs:180-445).
+struct moert_model {
+  moert_config cfg{};
+  Dims dims{};
+  int max_len = 0, splits = 0, host_pos = 0;
+  bool poisoned = false;
+  hipStream_t stream = nullptr;
+  Arena arena;
+  std::vector<LayerDev> layers;
+  DMat embed{};
+  float* norm = nullptr;
+  StepBufs b{};
+  int n_head_blocks = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+
+  // Launches one decode step. With `timed` >= 0, records an event pair around every launch of that kernel class.
+  int enqueue(int timed, std::vector<hipEvent_t>* ev) {
+    auto t0 = [&](int kind) {
+      if (kind == timed) (void)hipEventRecord((*ev)[ev_i], stream);
+    };
+    auto t1 = [&](int kind) {
+      if (kind == timed) {
+        (void)hipEventRecord((*ev)[ev_i + 1], stream);
+        ev_i += 2;
+      }
+    };
+    ev_i = 0;
+    t0(MOERT_K_EMBED);
+    CHECK_HIP(launch_embed(stream, embed, dims, b));
+    t1(MOERT_K_EMBED);
+    for (size_t l = 0; l < layers.size(); l++) {
+      const LayerDev& L = layers[l];
+      t0(MOERT_K_QKV);
+      CHECK_HIP(launch_qkv(stream, L, dims, b));
+      t1(MOERT_K_QKV);
+      t0(MOERT_K_ATTN);
+      CHECK_HIP(launch_attn(stream, L, dims, b));
+      t1(MOERT_K_ATTN);
+      t0(MOERT_K_OPROJ);
+      CHECK_HIP(launch_oproj(stream, L, dims, b));
+      t1(MOERT_K_OPROJ);
+      t0(MOERT_K_ROUTER);
+      CHECK_HIP(launch_router(stream, L, dims, b, (int)l, true));
+      t1(MOERT_K_ROUTER);
+      t0(MOERT_K_EXPERT_UP);
+      CHECK_HIP(launch_expert_up(stream, L, dims, b, (int)l));
+      t1(MOERT_K_EXPERT_UP);
+      t0(MOERT_K_EXPERT_DOWN);
+      CHECK_HIP(launch_expert_down(stream, L, dims, b, (int)l, true));
+      t1(MOERT_K_EXPERT_DOWN);
+    }
+    t0(MOERT_K_HEAD);
+    CHECK_HIP(launch_head(stream, embed, norm, dims, b));
+    t1(MOERT_K_HEAD);
+    return MOERT_OK;
+  }
+  int ev_i = 0;
+
+  int fail(int rc) {
+    if (rc == MOERT_E_DEVICE) {
+      poisoned = true;
+      (void)hipStreamSynchronize(stream);
+    }
+    return rc;
+  }
+
+  int build_graph() {
+    CHECK_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+    int rc = enqueue(-1, nullptr);
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(stream, &g);
+    if (rc) return rc;
+    CHECK_HIP(e);
+    graph = g;
+    CHECK_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+    return MOERT_OK;
+  }
+
+  int write_state(int pos, int fixed) {
+    int st[ST_WORDS] = {pos, fixed, 0, 0};
+    CHECK_HIP(hipMemcpyAsync(b.state, st, sizeof st, hipMemcpyHostToDevice, stream));
+    CHECK_HIP(hipStreamSynchronize(stream));
+    host_pos = pos;
+    return MOERT_OK;
+  }
+
+  ~moert_model() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    arena.release();
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+};
+
+static int model_create(const moert_config* c, const moert_model_weights* w, int max_len, int splits,
+                        moert_model** out) {
+  CHECK_CFG(c && w && out, "null argument");
+  *out = nullptr;
+  CHECK_CFG(c->head_dim == 64, "head_dim %d: the attention kernels are built for 64", c->head_dim);
+  CHECK_CFG(c->heads > 0 && c->kv_heads > 0 && c->heads % c->kv_heads == 0 && c->heads / c->kv_heads <= 4,
+            "heads %d / kv_heads %d: need a group of at most 4 query heads per KV head", c->heads, c->kv_heads);
+  CHECK_CFG(c->experts >= 1 && c->experts <= 64 && c->top_k >= 1 && c->top_k <= 8 && c->top_k <= c->experts,
+            "experts %d, top_k %d: need top_k <= 8 and experts <= 64", c->experts, c->top_k);
+  CHECK_CFG(k_supported(c->hidden) && k_supported(c->heads * 64) && (c->inter == 128 || c->inter == 256 || c->inter == 512),
+            "hidden %d / heads*64 %d / inter %d outside the compiled row lengths", c->hidden, c->heads * 64, c->inter);
+  CHECK_CFG(max_len >= 64 && max_len % 64 == 0, "max_len %d must be a positive multiple of 64", max_len);
+  CHECK_CFG(splits >= 1 && splits <= 1024, "attn_splits %d", splits);
+  CHECK_CFG(c->layers >= 1 && c->vocab >= 1 && w->layers && w->norm, "empty model");
+  const int H = c->hidden, d = 64, qd = c->heads * d, kvd = c->kv_heads * d, I = c->inter, E = c->experts;
+  for (int l = 0; l < c->layers; l++) {
+    const moert_layer_weights& L = w->layers[l];
+    CHECK_CFG(L.q.dtype == L.k.dtype && L.q.dtype == L.v.dtype, "layer %d: q, k, v must share a dtype", l);
+    CHECK_CFG(L.ln_attn && L.ln_moe, "layer %d: missing norm weights", l);
+  }
+  moert_model* m = new moert_model;
+  m->cfg = *c;
+  m->max_len = max_len;
+  m->splits = splits;
+  m->dims = Dims{H, I, c->heads, c->kv_heads, d, c->vocab, E, c->top_k, max_len, splits,
+                 c->eps, c->embedding_multiplier, c->residual_multiplier, c->attention_multiplier, c->logits_scaling};
+  auto bail = [&](int rc) {
+    delete m;
+    return rc;
+  };
+  if (hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking) != hipSuccess) {
+    set_err("hipStreamCreate failed");
+    return bail(MOERT_E_DEVICE);
+  }
+  hipStream_t s = m->stream;
+  Arena& a = m->arena;
+  int rc;
+  m->layers.resize(c->layers);
+  for (int l = 0; l < c->layers; l++) {
+    const moert_layer_weights& W = w->layers[l];
+    LayerDev& L = m->layers[l];
+    float* tmp;
+    if ((rc = upload_f32(a, s, W.ln_attn, H, &tmp))) return bail(rc);
+    L.ln_attn = tmp;
+    if ((rc = upload_f32(a, s, W.ln_moe, H, &tmp))) return bail(rc);
+    L.ln_moe = tmp;
+    if ((rc = upload_matrix(a, s, {{W.q.data, qd}, {W.k.data, kvd}, {W.v.data, kvd}}, W.q.dtype, H, &L.qkv))) return bail(rc);
+    if ((rc = upload_matrix(a, s, {{W.o.data, H}}, W.o.dtype, qd, &L.o))) return bail(rc);
+    if ((rc = upload_matrix(a, s, {{W.router.data, E}}, W.router.dtype, H, &L.router))) return bail(rc);
+    L.router_bias = nullptr;
+    if (W.router_bias) {
+      if ((rc = upload_f32(a, s, W.router_bias, E, &tmp))) return bail(rc);
+      L.router_bias = tmp;
+    }
+    if ((rc = upload_matrix(a, s, {{W.gate_up.data, E * 2 * I}}, W.gate_up.dtype, H, &L.gate_up))) return bail(rc);
+    if ((rc = upload_matrix(a, s, {{W.down.data, E * H}}, W.down.dtype, I, &L.down))) return bail(rc);
+    if ((rc = zeros(a, s, (size_t)c->kv_heads * max_len * d, &L.k_cache))) return bail(rc);
+    if ((rc = zeros(a, s, (size_t)c->kv_heads * max_len * d, &L.v_cache))) return bail(rc);
+  }
+  if ((rc = upload_matrix(a, s, {{w->embed.data, c->vocab}}, w->embed.dtype, H, &m->embed))) return bail(rc);
+  if ((rc = upload_f32(a, s, w->norm, H, &m->norm))) return bail(rc);
+  // RoPE table computed on the host as in rust/moe-rt/src/model.rs:63-73 (f32 powf, cosf, sinf).
+  std::vector<float> rope((size_t)max_len * d);
+  for (int p = 0; p < max_len; p++)
+    for (int j = 0; j < d / 2; j++) {
+      float f = 1.0f / powf(c->rope_theta, (float)(2 * j) / (float)d);
+      float ang = (float)p * f;
+      rope[(size_t)p * d + j] = cosf(ang);
+      rope[(size_t)p * d + d / 2 + j] = sinf(ang);
+    }
+  StepBufs& b = m->b;
+  float* rp;
+  if ((rc = upload_f32(a, s, rope.data(), rope.size(), &rp))) return bail(rc);
+  b.rope = rp;
+  m->n_head_blocks = head_blocks(m->embed);
+  if ((rc = zeros(a, s, H, &b.h)) || (rc = zeros(a, s, qd, &b.q)) || (rc = zeros(a, s, qd, &b.att)) ||
+      (rc = zeros(a, s, (size_t)c->heads * splits * 66, &b.part)) || (rc = zeros(a, s, c->kv_heads, &b.attn_cnt)) ||
+      (rc = zeros(a, s, H, &b.xn)) || (rc = zeros(a, s, (size_t)c->top_k * I, &b.act)) ||
+      (rc = zeros(a, s, (size_t)c->layers * c->top_k, &b.route_ids)) ||
+      (rc = zeros(a, s, (size_t)c->layers * c->top_k, &b.route_w)) || (rc = zeros(a, s, c->vocab, &b.logits)) ||
+      (rc = zeros(a, s, (size_t)m->n_head_blocks, &b.best)) || (rc = zeros(a, s, 1, &b.head_cnt)) ||
+      (rc = zeros(a, s, max_len, &b.seq)) || (rc = zeros(a, s, max_len, &b.argmax_hist)) ||
+      (rc = zeros(a, s, ST_WORDS, &b.state)))
+    return bail(rc);
+  if (hipStreamSynchronize(s) != hipSuccess) {
+    set_err("upload failed");
+    return bail(MOERT_E_DEVICE);
+  }
+  if ((rc = m->build_graph())) return bail(rc);
+  *out = m;
+  return MOERT_OK;
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// One MoE block with every expert resident (GpuLayer, rust/moe-rt/src/gpu.rs:368-541).
+struct moert_block {
+  Dims dims{};
+  hipStream_t stream = nullptr;
+  Arena arena;
+  LayerDev L{};
+  StepBufs b{};
+  float* x = nullptr;
+  ~moert_block() {
+    if (stream) (void)hipStreamSynchronize(stream);
+    arena.release();
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+  int enqueue() {
+    CHECK_HIP(launch_router(stream, L, dims, b, 0, false));
+    CHECK_HIP(launch_expert_up(stream, L, dims, b, 0));
+    CHECK_HIP(launch_expert_down(stream, L, dims, b, 0, false));
+    return MOERT_OK;
+  }
+};
+
+// ------------------------------------------------------------------------------------------------------------
+// Per-call device context for the unit-parity entry points.
+namespace {
+struct Scoped {
+  std::vector<void*> ptrs;
+  hipStream_t s = nullptr;
+  ~Scoped() {
+    if (s) (void)hipStreamSynchronize(s);
+    for (void* p : ptrs) (void)hipFree(p);
+    if (s) (void)hipStreamDestroy(s);
+  }
+  int init() {
+    CHECK_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    return MOERT_OK;
+  }
+  template <class T>
+  int dev(T** p, size_t n, const void* src = nullptr) {
+    void* q;
+    CHECK_HIP(hipMalloc(&q, n * sizeof(T) ? n * sizeof(T) : 4));
+    ptrs.push_back(q);
+    if (src)
+      CHECK_HIP(hipMemcpyAsync(q, src, n * sizeof(T), hipMemcpyHostToDevice, s));
+    else
+      CHECK_HIP(hipMemsetAsync(q, 0, n * sizeof(T) ? n * sizeof(T) : 4, s));
+    *p = (T*)q;
+    return MOERT_OK;
+  }
+  int get(void* dst, const void* src, size_t bytes) {
+    CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s));
+    CHECK_HIP(hipStreamSynchronize(s));
+    return MOERT_OK;
+  }
+};
+
+int unit_matrix(Scoped& sc, const moert_tensor* w, int rows, int cols, DMat* out) {
+  Arena a;
+  int rc = upload_matrix(a, sc.s, {{w->data, rows}}, w->dtype, cols, out);
+  for (void* p : a.ptrs) sc.ptrs.push_back(p);
+  return rc;
+}
+}  // namespace
+
+#define TRY(expr)              \
+  do {                         \
+    int rc_ = (expr);          \
+    if (rc_) return rc_;       \
+  } while (0)
+
+extern "C" {
+
+const char* moert_last_error(void) { return g_err.c_str(); }
+
+int moert_device_info(int* count, char* name, int name_len) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+  if (count) *count = n;
+  if (name && name_len > 0) {
+    name[0] = 0;
+    hipDeviceProp_t p;
+    if (n > 0 && hipGetDeviceProperties(&p, 0) == hipSuccess) snprintf(name, name_len, "%s (%s)", p.name, p.gcnArchName);
+  }
+  return MOERT_OK;
+}
+
+int moert_model_create(const moert_config* cfg, const moert_model_weights* w, int max_len, int attn_splits,
+                       moert_model** out) {
+  return model_create(cfg, w, max_len, attn_splits, out);
+}
+
+int moert_model_destroy(moert_model* m) {
+  delete m;
+  return MOERT_OK;
+}
+
+#define MODEL_OK(m)                                                      \
+  do {                                                                   \
+    if (!(m)) {                                                          \
+      set_err("null model");                                             \
+      return MOERT_E_CONFIG;                                             \
+    }                                                                    \
+    if ((m)->poisoned) {                                                 \
+      set_err("model unusable after an earlier device error");          \
+      return MOERT_E_POISONED;                                           \
+    }                                                                    \
+  } while (0)
+
+#define MTRY(m, expr)                 \
+  do {                                \
+    int rc_ = (expr);                 \
+    if (rc_) return (m)->fail(rc_);   \
+  } while (0)
+
+static int model_copy_in(moert_model* m, void* dst, const void* src, size_t bytes) {
+  CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, m->stream));
+  return MOERT_OK;
+}
+static int model_copy_out(moert_model* m, void* dst, const void* src, size_t bytes) {
+  CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, m->stream));
+  return MOERT_OK;
+}
+static int model_launch(moert_model* m) {
+  CHECK_HIP(hipGraphLaunch(m->exec, m->stream));
+  return MOERT_OK;
+}
+static int model_sync(moert_model* m) {
+  CHECK_HIP(hipStreamSynchronize(m->stream));
+  return MOERT_OK;
+}
+
+int moert_decode_step(moert_model* m, int token, float* logits, int* route_ids, float* route_weights, int* argmax) {
+  MODEL_OK(m);
+  if (m->host_pos >= m->max_len) {
+    set_err("KV cache full (%d positions)", m->max_len);
+    return MOERT_E_FULL;
+  }
+  if (token < 0 || token >= m->cfg.vocab) {
+    set_err("token %d outside the vocabulary (%d)", token, m->cfg.vocab);
+    return MOERT_E_RANGE;
+  }
+  int pos = m->host_pos;
+  int st[2] = {pos, pos + 1};
+  MTRY(m, model_copy_in(m, m->b.seq + pos, &token, 4));
+  MTRY(m, model_copy_in(m, m->b.state, st, sizeof st));
+  MTRY(m, model_launch(m));
+  const moert_config& c = m->cfg;
+  if (logits) MTRY(m, model_copy_out(m, logits, m->b.logits, (size_t)c.vocab * 4));
+  if (route_ids) MTRY(m, model_copy_out(m, route_ids, m->b.route_ids, (size_t)c.layers * c.top_k * 4));
+  if (route_weights) MTRY(m, model_copy_out(m, route_weights, m->b.route_w, (size_t)c.layers * c.top_k * 4));
+  int am = 0;
+  MTRY(m, model_copy_out(m, &am, m->b.argmax_hist + pos, 4));
+  MTRY(m, model_sync(m));
+  if (argmax) *argmax = am;
+  m->host_pos = pos + 1;
+  return MOERT_OK;
+}
+
+int moert_generate(moert_model* m, const int* prompt, int n_prompt, int n_new, int* out_tokens, float* gaps) {
+  MODEL_OK(m);
+  if (!prompt || n_prompt < 1 || n_new < 1 || !out_tokens) {
+    set_err("generate needs a prompt of at least one token and n_new >= 1");
+    return MOERT_E_CONFIG;
+  }
+  int pos0 = m->host_pos, steps = n_prompt + n_new - 1;
+  if (pos0 + steps > m->max_len) {
+    set_err("KV cache full: %d + %d steps > %d positions", pos0, steps, m->max_len);
+    return MOERT_E_FULL;
+  }
+  for (int i = 0; i < n_prompt; i++)
+    if (prompt[i] < 0 || prompt[i] >= m->cfg.vocab) {
+      set_err("prompt token %d outside the vocabulary", prompt[i]);
+      return MOERT_E_RANGE;
+    }
+  int st[2] = {pos0, pos0 + n_prompt};
+  MTRY(m, model_copy_in(m, m->b.seq + pos0, prompt, (size_t)n_prompt * 4));
+  MTRY(m, model_copy_in(m, m->b.state, st, sizeof st));
+  std::vector<float> lg(gaps ? m->cfg.vocab : 0);
+  for (int i = 0; i < steps; i++) {
+    MTRY(m, model_launch(m));
+    if (gaps && i >= n_prompt - 1) {
+      MTRY(m, model_copy_out(m, lg.data(), m->b.logits, lg.size() * 4));
+      MTRY(m, model_sync(m));
+      float t1 = -INFINITY, t2 = -INFINITY;
+      for (float v : lg) {
+        if (v > t1) {
+          t2 = t1;
+          t1 = v;
+        } else if (v > t2) {
+          t2 = v;
+        }
+      }
+      gaps[i - (n_prompt - 1)] = t1 - t2;
+    }
+  }
+  // token i was chosen at position pos0 + n_prompt - 1 + i (the last one is never fed back)
+  MTRY(m, model_copy_out(m, out_tokens, m->b.argmax_hist + pos0 + n_prompt - 1, (size_t)n_new * 4));
+  MTRY(m, model_sync(m));
+  m->host_pos = pos0 + steps;
+  return MOERT_OK;
+}
+
+int moert_reset_sequence(moert_model* m) {
+  MODEL_OK(m);
+  MTRY(m, m->write_state(0, 0));
+  return MOERT_OK;
+}
+
+int moert_set_position(moert_model* m, int pos) {
+  MODEL_OK(m);
+  if (pos < 0 || pos >= m->max_len) {
+    set_err("position %d outside [0, %d)", pos, m->max_len);
+    return MOERT_E_RANGE;
+  }
+  MTRY(m, m->write_state(pos, 0));
+  return MOERT_OK;
+}
+
+int moert_get_position(moert_model* m, int* pos) {
+  MODEL_OK(m);
+  if (pos) *pos = m->host_pos;
+  return MOERT_OK;
+}
+
+int moert_kv_prefill_fp16(moert_model* m, int layer, const uint16_t* k, const uint16_t* v, int n) {
+  MODEL_OK(m);
+  const moert_config& c = m->cfg;
+  if (layer < 0 || layer >= c.layers || n < 0 || n > m->max_len || !k || !v) {
+    set_err("kv prefill: layer %d, n %d", layer, n);
+    return MOERT_E_RANGE;
+  }
+  const LayerDev& L = m->layers[layer];
+  for (int g = 0; g < c.kv_heads; g++) {
+    size_t src = (size_t)g * n * 64, dst = (size_t)g * m->max_len * 64;
+    MTRY(m, model_copy_in(m, L.k_cache + dst, k + src, (size_t)n * 64 * 2));
+    MTRY(m, model_copy_in(m, L.v_cache + dst, v + src, (size_t)n * 64 * 2));
+  }
+  MTRY(m, model_sync(m));
+  return MOERT_OK;
+}
+
+int moert_read_kv_fp16(moert_model* m, int layer, uint16_t* k, uint16_t* v, int n) {
+  MODEL_OK(m);
+  const moert_config& c = m->cfg;
+  if (layer < 0 || layer >= c.layers || n < 0 || n > m->max_len || !k || !v) {
+    set_err("read kv: layer %d, n %d", layer, n);
+    return MOERT_E_RANGE;
+  }
+  const LayerDev& L = m->layers[layer];
+  for (int g = 0; g < c.kv_heads; g++) {
+    size_t dst = (size_t)g * n * 64, src = (size_t)g * m->max_len * 64;
+    MTRY(m, model_copy_out(m, k + dst, L.k_cache + src, (size_t)n * 64 * 2));
+    MTRY(m, model_copy_out(m, v + dst, L.v_cache + src, (size_t)n * 64 * 2));
+  }
+  MTRY(m, model_sync(m));
+  return MOERT_OK;
+}
+
+int moert_read_hidden(moert_model* m, float* h) {
+  MODEL_OK(m);
+  MTRY(m, model_copy_out(m, h, m->b.h, (size_t)m->cfg.hidden * 4));
+  MTRY(m, model_sync(m));
+  return MOERT_OK;
+}
+
+static int time_steps_impl(moert_model* m, int warmup, int iters, double* ms) {
+  hipEvent_t e0, e1;
+  CHECK_HIP(hipEventCreate(&e0));
+  CHECK_HIP(hipEventCreate(&e1));
+  for (int i = 0; i < warmup; i++) CHECK_HIP(hipGraphLaunch(m->exec, m->stream));
+  CHECK_HIP(hipEventRecord(e0, m->stream));
+  for (int i = 0; i < iters; i++) CHECK_HIP(hipGraphLaunch(m->exec, m->stream));
+  CHECK_HIP(hipEventRecord(e1, m->stream));
+  CHECK_HIP(hipEventSynchronize(e1));
+  float t = 0.0f;
+  CHECK_HIP(hipEventElapsedTime(&t, e0, e1));
+  *ms = iters > 0 ? t / iters : 0.0;
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  m->host_pos += warmup + iters;
+  return MOERT_OK;
+}
+
+int moert_time_steps(moert_model* m, int warmup, int iters, double* ms_per_step) {
+  MODEL_OK(m);
+  if (warmup < 0 || iters < 0 || m->host_pos + warmup + iters > m->max_len) {
+    set_err("time_steps: %d + %d + %d positions exceed max_len %d", m->host_pos, warmup, iters, m->max_len);
+    return MOERT_E_FULL;
+  }
+  int st[2] = {m->host_pos, 0};
+  MTRY(m, model_copy_in(m, m->b.state, st, sizeof st));
+  MTRY(m, time_steps_impl(m, warmup, iters, ms_per_step));
+  return MOERT_OK;
+}
+
+static int time_kernel_impl(moert_model* m, int kind, int iters, double* us, int* launches) {
+  int per_step = (kind == MOERT_K_EMBED || kind == MOERT_K_HEAD) ? 1 : m->cfg.layers;
+  std::vector<hipEvent_t> ev(2 * per_step);
+  for (auto& e : ev) CHECK_HIP(hipEventCreate(&e));
+  double total = 0.0;
+  int n = 0;
+  for (int it = 0; it < iters; it++) {
+    TRY(m->enqueue(kind, &ev));
+    CHECK_HIP(hipStreamSynchronize(m->stream));
+    for (int i = 0; i < per_step; i++) {
+      float t = 0.0f;
+      CHECK_HIP(hipEventElapsedTime(&t, ev[2 * i], ev[2 * i + 1]));
+      total += t;
+      n++;
+    }
+  }
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  *us = n ? total * 1000.0 / n : 0.0;
+  if (launches) *launches = n;
+  m->host_pos += iters;
+  return MOERT_OK;
+}
+
+int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch, int* launches) {
+  MODEL_OK(m);
+  if (kind < 0 || kind >= MOERT_K_COUNT || iters < 1 || !us_per_launch) {
+    set_err("time_kernel: kind %d, iters %d", kind, iters);
+    return MOERT_E_CONFIG;
+  }
+  if (m->host_pos + iters > m->max_len) {
+    set_err("time_kernel: %d + %d positions exceed max_len %d", m->host_pos, iters, m->max_len);
+    return MOERT_E_FULL;
+  }
+  int st[2] = {m->host_pos, 0};
+  MTRY(m, model_copy_in(m, m->b.state, st, sizeof st));
+  MTRY(m, time_kernel_impl(m, kind, iters, us_per_launch, launches));
+  return MOERT_OK;
+}
+
+// ---- MoE block ----------------------------------------------------------------------------------------------
+int moert_block_create(int hidden, int inter, int experts, int top_k, const moert_tensor* router,
+                       const float* router_bias, const moert_tensor* gate_up, const moert_tensor* down,
+                       moert_block** out) {
+  CHECK_CFG(out && router && gate_up && down, "null argument");
+  *out = nullptr;
+  CHECK_CFG(k_supported(hidden) && (inter == 128 || inter == 256 || inter == 512), "hidden %d / inter %d", hidden, inter);
+  CHECK_CFG(experts >= 1 && experts <= 64 && top_k >= 1 && top_k <= 8 && top_k <= experts, "experts %d, top_k %d",
+            experts, top_k);
+  moert_block* b = new moert_block;
+  auto bail = [&](int rc) {
+    delete b;
+    return rc;
+  };
+  if (hipStreamCreateWithFlags(&b->stream, hipStreamNonBlocking) != hipSuccess) {
+    set_err("hipStreamCreate failed");
+    return bail(MOERT_E_DEVICE);
+  }
+  b->dims = Dims{hidden, inter, 1, 1, 64, hidden, experts, top_k, 64, 1, 0.0f, 1.0f, 1.0f, 1.0f, 1.0f};
+  hipStream_t s = b->stream;
+  Arena& a = b->arena;
+  int rc;
+  if ((rc = upload_matrix(a, s, {{router->data, experts}}, router->dtype, hidden, &b->L.router))) return bail(rc);
+  if ((rc = upload_matrix(a, s, {{gate_up->data, experts * 2 * inter}}, gate_up->dtype, hidden, &b->L.gate_up))) return bail(rc);
+  if ((rc = upload_matrix(a, s, {{down->data, experts * hidden}}, down->dtype, inter, &b->L.down))) return bail(rc);
+  float* tmp;
+  b->L.router_bias = nullptr;
+  if (router_bias) {
+    if ((rc = upload_f32(a, s, router_bias, experts, &tmp))) return bail(rc);
+    b->L.router_bias = tmp;
+  }
+  if ((rc = zeros(a, s, hidden, &b->x)) || (rc = zeros(a, s, hidden, &b->b.xn)) ||
+      (rc = zeros(a, s, (size_t)top_k * inter, &b->b.act)) || (rc = zeros(a, s, top_k, &b->b.route_ids)) ||
+      (rc = zeros(a, s, top_k, &b->b.route_w)) || (rc = zeros(a, s, hidden, &b->b.logits)))
+    return bail(rc);
+  b->b.h = b->x;
+  if (hipStreamSynchronize(s) != hipSuccess) {
+    set_err("block upload failed");
+    return bail(MOERT_E_DEVICE);
+  }
+  *out = b;
+  return MOERT_OK;
+}
+
+int moert_block_destroy(moert_block* b) {
+  delete b;
+  return MOERT_OK;
+}
+
+int moert_block_forward(moert_block* b, const float* x, float* y, int* ids, float* weights) {
+  CHECK_CFG(b && x, "null argument");
+  const Dims& d = b->dims;
+  CHECK_HIP(hipMemcpyAsync(b->x, x, (size_t)d.hidden * 4, hipMemcpyHostToDevice, b->stream));
+  TRY(b->enqueue());
+  if (y) CHECK_HIP(hipMemcpyAsync(y, b->b.logits, (size_t)d.hidden * 4, hipMemcpyDeviceToHost, b->stream));
+  if (ids) CHECK_HIP(hipMemcpyAsync(ids, b->b.route_ids, (size_t)d.top_k * 4, hipMemcpyDeviceToHost, b->stream));
+  if (weights) CHECK_HIP(hipMemcpyAsync(weights, b->b.route_w, (size_t)d.top_k * 4, hipMemcpyDeviceToHost, b->stream));
+  CHECK_HIP(hipStreamSynchronize(b->stream));
+  return MOERT_OK;
+}
+
+int moert_block_time(moert_block* b, int iters, double* us) {
+  CHECK_CFG(b && us && iters > 0, "bad argument");
+  hipEvent_t e0, e1;
+  CHECK_HIP(hipEventCreate(&e0));
+  CHECK_HIP(hipEventCreate(&e1));
+  TRY(b->enqueue());
+  CHECK_HIP(hipEventRecord(e0, b->stream));
+  for (int i = 0; i < iters; i++) TRY(b->enqueue());
+  CHECK_HIP(hipEventRecord(e1, b->stream));
+  CHECK_HIP(hipEventSynchronize(e1));
+  float t = 0;
+  CHECK_HIP(hipEventElapsedTime(&t, e0, e1));
+  *us = (double)t * 1000.0 / iters;
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  return MOERT_OK;
+}
+
+// ---- unit-parity entry points ---------------------------------------------------------------------------------
+int moert_router_topk(const float* logits, int n, int k, int* ids, float* weights) {
+  CHECK_CFG(logits && ids && weights && n >= 1 && n <= 64 && k >= 1 && k <= n, "router_topk: n %d, k %d", n, k);
+  Scoped sc;
+  TRY(sc.init());
+  float *dl, *dw;
+  int* di;
+  TRY(sc.dev(&dl, n, logits));
+  TRY(sc.dev(&di, k));
+  TRY(sc.dev(&dw, k));
+  CHECK_HIP(launch_topk(sc.s, dl, nullptr, n, k, di, dw));
+  TRY(sc.get(ids, di, (size_t)k * 4));
+  TRY(sc.get(weights, dw, (size_t)k * 4));
+  return MOERT_OK;
+}
+
+int moert_argmax(const float* v, int n, int* idx) {
+  CHECK_CFG(v && idx && n >= 1, "argmax: n %d", n);
+  Scoped sc;
+  TRY(sc.init());
+  float* dv;
+  int2* best;
+  int *cnt, *out;
+  TRY(sc.dev(&dv, n, v));
+  TRY(sc.dev(&best, 1024));
+  TRY(sc.dev(&cnt, 1));
+  TRY(sc.dev(&out, 1));
+  CHECK_HIP(launch_argmax(sc.s, dv, n, best, cnt, out));
+  TRY(sc.get(idx, out, 4));
+  return MOERT_OK;
+}
+
+int moert_gemv(const moert_tensor* w, int rows, int cols, const float* x, float* y) {
+  CHECK_CFG(w && x && y && rows >= 1 && k_supported(cols), "gemv: rows %d, cols %d", rows, cols);
+  Scoped sc;
+  TRY(sc.init());
+  DMat m;
+  TRY(unit_matrix(sc, w, rows, cols, &m));
+  float *dx, *dy;
+  TRY(sc.dev(&dx, cols, x));
+  TRY(sc.dev(&dy, rows));
+  CHECK_HIP(launch_gemv(sc.s, m, dx, dy));
+  TRY(sc.get(y, dy, (size_t)rows * 4));
+  return MOERT_OK;
+}
+
+int moert_dequant(const moert_tensor* w, int rows, int cols, float* out) {
+  CHECK_CFG(w && out && rows >= 1 && cols >= 32 && cols % 32 == 0, "dequant: rows %d, cols %d", rows, cols);
+  Scoped sc;
+  TRY(sc.init());
+  DMat m;
+  TRY(unit_matrix(sc, w, rows, cols, &m));
+  float* d;
+  TRY(sc.dev(&d, (size_t)rows * cols));
+  CHECK_HIP(launch_dequant(sc.s, m, d));
+  TRY(sc.get(out, d, (size_t)rows * cols * 4));
+  return MOERT_OK;
+}
+
+int moert_rmsnorm(const float* x, const float* w, int n, float eps, float* out) {
+  CHECK_CFG(x && w && out && n >= 16 && n % 16 == 0, "rmsnorm: n %d must be a multiple of 16", n);
+  Scoped sc;
+  TRY(sc.init());
+  float *dx, *dw, *dout;
+  TRY(sc.dev(&dx, n, x));
+  TRY(sc.dev(&dw, n, w));
+  TRY(sc.dev(&dout, n));
+  CHECK_HIP(launch_rmsnorm(sc.s, dx, dw, n, eps, dout));
+  TRY(sc.get(out, dout, (size_t)n * 4));
+  return MOERT_OK;
+}
+
+int moert_rope(float* x, int heads, int head_dim, float theta, int pos) {
+  CHECK_CFG(x && heads >= 1 && head_dim >= 2 && head_dim % 2 == 0, "rope: heads %d, head_dim %d", heads, head_dim);
+  std::vector<float> cs(head_dim);
+  for (int j = 0; j < head_dim / 2; j++) {
+    float f = 1.0f / powf(theta, (float)(2 * j) / (float)head_dim);
+    float a = (float)pos * f;
+    cs[j] = cosf(a);
+    cs[head_dim / 2 + j] = sinf(a);
+  }
+  Scoped sc;
+  TRY(sc.init());
+  float *dx, *dc;
+  TRY(sc.dev(&dx, (size_t)heads * head_dim, x));
+  TRY(sc.dev(&dc, head_dim, cs.data()));
+  CHECK_HIP(launch_rope(sc.s, dx, heads, head_dim, dc));
+  TRY(sc.get(x, dx, (size_t)heads * head_dim * 4));
+  return MOERT_OK;
+}
+
+int moert_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, int heads, int kv_heads,
+                      int head_dim, int max_len, int len, float scale, int splits, float* out) {
+  CHECK_CFG(q && k_cache && v_cache && out, "null argument");
+  CHECK_CFG(head_dim == 64 && heads % kv_heads == 0 && heads / kv_heads <= 4 && max_len % 64 == 0 && len >= 1 &&
+                len <= max_len && splits >= 1,
+            "attn: heads %d, kv %d, d %d, max_len %d, len %d, splits %d", heads, kv_heads, head_dim, max_len, len,
+            splits);
+  Scoped sc;
+  TRY(sc.init());
+  float *dq, *part, *dout;
+  uint16_t *dk, *dv;
+  int *cnt, *dlen;
+  size_t kvn = (size_t)kv_heads * max_len * 64;
+  TRY(sc.dev(&dq, (size_t)heads * 64, q));
+  TRY(sc.dev(&dk, kvn, k_cache));
+  TRY(sc.dev(&dv, kvn, v_cache));
+  TRY(sc.dev(&part, (size_t)heads * splits * 66));
+  TRY(sc.dev(&cnt, kv_heads));
+  TRY(sc.dev(&dlen, 1, &len));
+  TRY(sc.dev(&dout, (size_t)heads * 64));
+  CHECK_HIP(launch_attn_unit(sc.s, dq, dk, dv, heads, kv_heads, max_len, dlen, scale, splits, part, cnt, dout));
+  TRY(sc.get(out, dout, (size_t)heads * 64 * 4));
+  return MOERT_OK;
+}
+
+int moert_exp_device(const float* x, float* y, int n) {
+  CHECK_CFG(x && y && n >= 1, "exp: n %d", n);
+  Scoped sc;
+  TRY(sc.init());
+  float *dx, *dy;
+  TRY(sc.dev(&dx, n, x));
+  TRY(sc.dev(&dy, n));
+  CHECK_HIP(launch_exp(sc.s, dx, dy, n));
+  TRY(sc.get(y, dy, (size_t)n * 4));
+  return MOERT_OK;
+}
+
+// ---- host utilities --------------------------------------------------------------------------------------------
+int moert_quantize(const float* x, size_t n, int dtype, void* out) {
+  CHECK_CFG(x && out && valid_dtype(dtype) && n % 32 == 0, "quantize: n %zu, dtype %d", n, dtype);
+  return quantize(x, n, dtype, out);
+}
+
+size_t moert_dtype_bytes(int dtype, size_t n) { return dtype_bytes(dtype, n); }
+
+int moert_synth_normal(uint64_t seed, uint64_t stream, size_t n, float scale, float offset, float* out) {
+  CHECK_CFG(out, "null output");
+  return synth_normal(seed, stream, n, scale, offset, out);
+}
+
+int moert_synth_quantized(uint64_t seed, uint64_t stream, size_t n, float scale, int dtype, void* out) {
+  CHECK_CFG(out && valid_dtype(dtype) && n % 32 == 0, "synth_quantized: n %zu, dtype %d", n, dtype);
+  return synth_quantized(seed, stream, n, scale, dtype, out);
+}
+
+int moert_synth_fp16(uint64_t seed, uint64_t stream, size_t n, float scale, uint16_t* out) {
+  CHECK_CFG(out, "null output");
+  return synth_fp16(seed, stream, n, scale, out);
+}
+
+}  // extern "C"

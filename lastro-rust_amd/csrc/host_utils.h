@@ -1,0 +1,19 @@
+// Host utilities of libmoert (no device code).
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#include <atomic>
+#include <functional>
+
+namespace moert {
+
+uint16_t host_f2h(float f);
+float host_h2f(uint16_t h);
+size_t dtype_bytes(int dtype, size_t n);
+int quantize(const float* x, size_t n, int dtype, void* out);
+int synth_normal(uint64_t seed, uint64_t stream, size_t n, float scale, float offset, float* out);
+int synth_quantized(uint64_t seed, uint64_t stream, size_t n, float scale, int dtype, void* out);
+int synth_fp16(uint64_t seed, uint64_t stream, size_t n, float scale, uint16_t* out);
+
+}  // namespace moert

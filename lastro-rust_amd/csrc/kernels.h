@@ -1,0 +1,78 @@
+// Launchers of the decode-step kernels (kernels.hip). All take device pointers and enqueue on `s`.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dev_math.h"
+
+namespace moert {
+
+// Device sequence state, one int each: position of the token being decoded, first position whose token the
+// greedy argmax may write (positions before it are forced prompt tokens), last argmax.
+enum { ST_POS = 0, ST_FIXED = 1, ST_ARGMAX = 2, ST_WORDS = 4 };
+
+struct LayerDev {
+  const float* ln_attn;
+  const float* ln_moe;
+  DMat qkv;           // [heads*d + 2*kv*d, H]: q rows, then k rows, then v rows
+  DMat o;             // [H, heads*d]
+  DMat router;        // [E, H]
+  const float* router_bias;  // [E] or null
+  DMat gate_up;       // [E*2I, H]
+  DMat down;          // [E*H, I]
+  uint16_t* k_cache;  // [kv, max_len, d] fp16
+  uint16_t* v_cache;
+};
+
+struct Dims {
+  int hidden, inter, heads, kv_heads, head_dim, vocab, experts, top_k, max_len, splits;
+  float eps, emb_mult, res_mult, attn_mult, logits_scaling;
+};
+
+// Scratch buffers of one decode step (device).
+struct StepBufs {
+  float* h;          // [H] residual stream
+  float* q;          // [heads*d]
+  float* att;        // [heads*d]
+  float* part;       // [heads, splits, 2 + d] split-KV partials
+  int* attn_cnt;     // [kv_heads] arrival counters (left at 0)
+  float* xn;         // [H] normalised MoE input
+  float* act;        // [k, I] SwiGLU activations
+  int* route_ids;    // [layers, k]
+  float* route_w;    // [layers, k]
+  float* logits;     // [V]
+  int2* best;        // [head blocks] per-block argmax
+  int* head_cnt;     // [1]
+  int* seq;          // [max_len] token of each position
+  int* argmax_hist;  // [max_len] argmax produced at each position
+  int* state;        // [ST_WORDS]
+  const float* rope; // [max_len, d]: cos of the d/2 frequencies, then sin
+};
+
+hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const StepBufs& b);
+hipError_t launch_qkv(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
+hipError_t launch_attn(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
+hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
+// normalize: rmsnorm h with ln_moe first (decode step); otherwise h is the block input as is.
+hipError_t launch_router(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
+                         bool normalize);
+hipError_t launch_expert_up(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer);
+// accumulate: h += res * y (decode step); otherwise y is written to b.logits (standalone MoE block output).
+hipError_t launch_expert_down(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
+                              bool accumulate);
+hipError_t launch_head(hipStream_t s, const DMat& head, const float* norm, const Dims& d, const StepBufs& b);
+int head_blocks(const DMat& head);
+
+// Unit kernels.
+hipError_t launch_gemv(hipStream_t s, const DMat& w, const float* x, float* y);
+hipError_t launch_dequant(hipStream_t s, const DMat& w, float* out);
+hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* w, int n, float eps, float* out);
+hipError_t launch_rope(hipStream_t s, float* x, int heads, int head_dim, const float* cs);
+hipError_t launch_topk(hipStream_t s, const float* logits, const float* bias, int n, int k, int* ids, float* w);
+hipError_t launch_argmax(hipStream_t s, const float* v, int n, int2* best, int* cnt, int* out);
+hipError_t launch_exp(hipStream_t s, const float* x, float* y, int n);
+hipError_t launch_attn_unit(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vc, int heads,
+                            int kv_heads, int max_len, const int* len_dev, float scale, int splits, float* part,
+                            int* cnt, float* out);
+
+}  // namespace moert

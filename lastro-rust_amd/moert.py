@@ -1,0 +1,486 @@
+"""Python binding of libmoert (include/moert.h), the gfx950 Granite-MoE decode engine.
+
+Mirrors the host API of the reference crate rust/moe-rt (brenoperucchi/lastro-rust):
+  Config            <- model.rs:14-61 (Config / from_json)
+  SynthModel        <- model.rs:87-132 (HostModel) built from seeded synthetic weights instead of a checkpoint
+  GpuModel          <- gpu_model.rs:180-445 (upload, step, reset) + cuda_backend.rs model mode (read_kv, reset)
+  GpuBlock          <- gpu.rs:368-541 (GpuLayer) / block.rs:56-62 (forward_cpu)
+  router_topk       <- route.rs:18-75 / block.rs:81-89
+  argmax            <- bin/m1b-gulosa.rs:22-24
+The library is required: every entry point raises if libmoert.so is missing or a call fails.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import numpy as np
+
+F32, Q8_0, Q4_0 = 0, 1, 2
+DTYPE_NAMES = {F32: "f32", Q8_0: "q8_0", Q4_0: "q4_0"}
+
+K_EMBED, K_QKV, K_ATTN, K_OPROJ, K_ROUTER, K_EXPERT_UP, K_EXPERT_DOWN, K_HEAD = range(8)
+KERNEL_NAMES = ["embed", "qkv", "attn", "oproj", "router", "expert_up", "expert_down", "head"]
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmoert.so")
+
+E_NAMES = {-1: "DEVICE", -2: "CONFIG", -3: "POISONED", -4: "FULL", -5: "RANGE"}
+
+
+class MoertError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"moert error {code} ({E_NAMES.get(code, '?')}): {msg}")
+        self.code = code
+
+
+class moert_config(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in
+                ("hidden", "inter", "layers", "heads", "kv_heads", "head_dim", "vocab", "experts", "top_k")] + \
+               [(n, ctypes.c_float) for n in
+                ("rope_theta", "eps", "embedding_multiplier", "residual_multiplier", "attention_multiplier",
+                 "logits_scaling")]
+
+
+class moert_tensor(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("dtype", ctypes.c_int)]
+
+
+class moert_layer_weights(ctypes.Structure):
+    _fields_ = [("ln_attn", ctypes.c_void_p), ("ln_moe", ctypes.c_void_p), ("q", moert_tensor),
+                ("k", moert_tensor), ("v", moert_tensor), ("o", moert_tensor), ("router", moert_tensor),
+                ("router_bias", ctypes.c_void_p), ("gate_up", moert_tensor), ("down", moert_tensor)]
+
+
+class moert_model_weights(ctypes.Structure):
+    _fields_ = [("embed", moert_tensor), ("norm", ctypes.c_void_p),
+                ("layers", ctypes.POINTER(moert_layer_weights))]
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libmoert.so (built by `make -C lastro-rust_amd`); raises if it is missing."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(f"{LIB_PATH} is missing: build it with `make -C {_HERE}`")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, ip, fp, i, f, sz = ctypes.c_void_p, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_float), \
+            ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+        u64 = ctypes.c_uint64
+        sig = {
+            "moert_last_error": (ctypes.c_char_p, []),
+            "moert_device_info": (i, [ip, ctypes.c_char_p, i]),
+            "moert_model_create": (i, [ctypes.POINTER(moert_config), ctypes.POINTER(moert_model_weights), i, i,
+                                       ctypes.POINTER(vp)]),
+            "moert_model_destroy": (i, [vp]),
+            "moert_decode_step": (i, [vp, i, vp, vp, vp, ip]),
+            "moert_generate": (i, [vp, vp, i, i, vp, vp]),
+            "moert_reset_sequence": (i, [vp]),
+            "moert_kv_prefill_fp16": (i, [vp, i, vp, vp, i]),
+            "moert_set_position": (i, [vp, i]),
+            "moert_get_position": (i, [vp, ip]),
+            "moert_read_kv_fp16": (i, [vp, i, vp, vp, i]),
+            "moert_read_hidden": (i, [vp, vp]),
+            "moert_time_steps": (i, [vp, i, i, ctypes.POINTER(ctypes.c_double)]),
+            "moert_time_kernel": (i, [vp, i, i, ctypes.POINTER(ctypes.c_double), ip]),
+            "moert_block_create": (i, [i, i, i, i, ctypes.POINTER(moert_tensor), vp, ctypes.POINTER(moert_tensor),
+                                       ctypes.POINTER(moert_tensor), ctypes.POINTER(vp)]),
+            "moert_block_destroy": (i, [vp]),
+            "moert_block_forward": (i, [vp, vp, vp, vp, vp]),
+            "moert_block_time": (i, [vp, i, ctypes.POINTER(ctypes.c_double)]),
+            "moert_router_topk": (i, [vp, i, i, vp, vp]),
+            "moert_argmax": (i, [vp, i, ip]),
+            "moert_gemv": (i, [ctypes.POINTER(moert_tensor), i, i, vp, vp]),
+            "moert_dequant": (i, [ctypes.POINTER(moert_tensor), i, i, vp]),
+            "moert_rmsnorm": (i, [vp, vp, i, f, vp]),
+            "moert_rope": (i, [vp, i, i, f, i]),
+            "moert_attn_decode": (i, [vp, vp, vp, i, i, i, i, i, f, i, vp]),
+            "moert_exp_device": (i, [vp, vp, i]),
+            "moert_quantize": (i, [vp, sz, i, vp]),
+            "moert_dtype_bytes": (sz, [i, sz]),
+            "moert_synth_normal": (i, [u64, u64, sz, f, f, vp]),
+            "moert_synth_quantized": (i, [u64, u64, sz, f, i, vp]),
+            "moert_synth_fp16": (i, [u64, u64, sz, f, vp]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moert_model_destroy",
+            "moert_decode_step", "moert_generate", "moert_reset_sequence", "moert_kv_prefill_fp16",
+            "moert_set_position", "moert_get_position", "moert_read_kv_fp16", "moert_read_hidden",
+            "moert_time_steps", "moert_time_kernel", "moert_block_create", "moert_block_destroy",
+            "moert_block_forward", "moert_block_time", "moert_router_topk", "moert_argmax", "moert_gemv",
+            "moert_dequant", "moert_rmsnorm", "moert_rope", "moert_attn_decode", "moert_exp_device",
+            "moert_quantize", "moert_dtype_bytes", "moert_synth_normal", "moert_synth_quantized",
+            "moert_synth_fp16"]
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise MoertError(rc, lib().moert_last_error().decode(errors="replace"))
+
+
+def ptr(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def device_info():
+    n = ctypes.c_int(0)
+    name = ctypes.create_string_buffer(256)
+    check(lib().moert_device_info(ctypes.byref(n), name, 256))
+    return n.value, name.value.decode()
+
+
+def dtype_bytes(dtype: int, n: int) -> int:
+    return int(lib().moert_dtype_bytes(dtype, n))
+
+
+def quantize(x: np.ndarray, dtype: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if dtype == F32:
+        return x.copy()
+    out = np.empty(dtype_bytes(dtype, x.size), np.uint8)
+    check(lib().moert_quantize(ptr(x), x.size, dtype, ptr(out)))
+    return out
+
+
+def synth_normal(seed: int, stream: int, n: int, scale: float = 1.0, offset: float = 0.0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    check(lib().moert_synth_normal(seed, stream, n, scale, offset, ptr(out)))
+    return out
+
+
+def synth_quantized(seed: int, stream: int, n: int, scale: float, dtype: int) -> np.ndarray:
+    if dtype == F32:
+        return synth_normal(seed, stream, n, scale)
+    out = np.empty(dtype_bytes(dtype, n), np.uint8)
+    check(lib().moert_synth_quantized(seed, stream, n, scale, dtype, ptr(out)))
+    return out
+
+
+def synth_fp16(seed: int, stream: int, n: int, scale: float = 1.0) -> np.ndarray:
+    out = np.empty(n, np.uint16)
+    check(lib().moert_synth_fp16(seed, stream, n, scale, ptr(out)))
+    return out
+
+
+# ----------------------------------------------------------------------------------------------------------------
+@dataclass
+class Config:
+    """Model constants (rust/moe-rt/src/model.rs:14-31)."""
+    hidden: int
+    inter: int
+    layers: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    vocab: int
+    experts: int
+    top_k: int
+    rope_theta: float = 10000.0
+    eps: float = 1e-6
+    embedding_multiplier: float = 12.0
+    residual_multiplier: float = 0.22
+    attention_multiplier: float = 0.015625
+    logits_scaling: float = 6.0
+
+    @staticmethod
+    def from_json(v: dict) -> "Config":
+        """Config::from_json (model.rs:34-61): refuses non-granitemoe models and unsupported variants."""
+        if v.get("model_type") != "granitemoe":
+            raise ValueError(f"model_type {v.get('model_type')!r} (expected granitemoe)")
+        if v.get("rope_scaling") is not None or v.get("attention_bias") is True or \
+                v.get("tie_word_embeddings") is False:
+            raise ValueError("unsupported variant (rope_scaling, attention_bias or untied embeddings)")
+        h, heads = int(v["hidden_size"]), int(v["num_attention_heads"])
+        return Config(hidden=h, inter=int(v["intermediate_size"]), layers=int(v["num_hidden_layers"]), heads=heads,
+                      kv_heads=int(v["num_key_value_heads"]), head_dim=int(v.get("head_dim") or h // heads),
+                      vocab=int(v["vocab_size"]), experts=int(v["num_local_experts"]),
+                      top_k=int(v["num_experts_per_tok"]), rope_theta=float(v["rope_theta"]),
+                      eps=float(v["rms_norm_eps"]), embedding_multiplier=float(v["embedding_multiplier"]),
+                      residual_multiplier=float(v["residual_multiplier"]),
+                      attention_multiplier=float(v["attention_multiplier"]),
+                      logits_scaling=float(v["logits_scaling"]))
+
+    def c(self) -> moert_config:
+        return moert_config(*[getattr(self, n) for n, _ in moert_config._fields_])
+
+    def inv_freq(self) -> np.ndarray:
+        d = np.float32(self.head_dim)
+        return np.array([np.float32(1.0) / np.power(np.float32(self.rope_theta), np.float32(2 * j) / d)
+                         for j in range(self.head_dim // 2)], np.float32)
+
+
+# Workload shapes named by the reference's model family (configs of the decode benchmark).
+GRANITE_1B = dict(hidden=1024, inter=512, layers=24, heads=16, kv_heads=8, head_dim=64, vocab=49155, experts=32,
+                  top_k=8)
+GRANITE_3B = dict(hidden=1536, inter=512, layers=32, heads=24, kv_heads=8, head_dim=64, vocab=49155, experts=40,
+                  top_k=8)
+TINY = dict(hidden=256, inter=128, layers=2, heads=4, kv_heads=2, head_dim=64, vocab=33, experts=4, top_k=2)
+
+
+@dataclass
+class SynthModel:
+    """Random-init Granite-MoE weights (HostModel, model.rs:87-132): matrices N(0, std) quantised to `wdtype`,
+    norm weights 1 + N(0, std), embedding/head in `embed_dtype`. `zipf_s` adds the router bias
+    b_e = -s * ln(rank_e) over a seeded permutation of the experts (skewed expert loads)."""
+    cfg: Config
+    seed: int = 1234
+    wdtype: int = Q8_0
+    embed_dtype: int = Q8_0
+    std: float = 0.02
+    zipf_s: Optional[float] = None
+    arrays: dict = field(default_factory=dict)
+
+    def __post_init__(self):
+        c, s, a = self.cfg, self.seed, self.arrays
+        H, d, I, E = c.hidden, c.head_dim, c.inter, c.experts
+        qd, kvd = c.heads * d, c.kv_heads * d
+        a["embed"] = synth_quantized(s, 1, c.vocab * H, self.std, self.embed_dtype)
+        a["norm"] = synth_normal(s, 2, H, self.std, 1.0)
+        for l in range(c.layers):
+            b = 100 + 16 * l
+            a[f"{l}.ln_attn"] = synth_normal(s, b, H, self.std, 1.0)
+            a[f"{l}.ln_moe"] = synth_normal(s, b + 1, H, self.std, 1.0)
+            a[f"{l}.q"] = synth_quantized(s, b + 2, qd * H, self.std, self.wdtype)
+            a[f"{l}.k"] = synth_quantized(s, b + 3, kvd * H, self.std, self.wdtype)
+            a[f"{l}.v"] = synth_quantized(s, b + 4, kvd * H, self.std, self.wdtype)
+            a[f"{l}.o"] = synth_quantized(s, b + 5, H * qd, self.std, self.wdtype)
+            a[f"{l}.router"] = synth_quantized(s, b + 6, E * H, self.std, self.wdtype)
+            a[f"{l}.gate_up"] = synth_quantized(s, b + 7, E * 2 * I * H, self.std, self.wdtype)
+            a[f"{l}.down"] = synth_quantized(s, b + 8, E * H * I, self.std, self.wdtype)
+            if self.zipf_s is not None:
+                rng = np.random.default_rng(s * 1000 + l)
+                rank = np.empty(E, np.int64)
+                rank[rng.permutation(E)] = np.arange(1, E + 1)
+                a[f"{l}.router_bias"] = (-self.zipf_s * np.log(rank)).astype(np.float32)
+        self._struct = None
+
+    def weights(self) -> moert_model_weights:
+        """The moert_model_weights struct pointing into the numpy arrays (kept alive by this object)."""
+        if self._struct is None:
+            c, a = self.cfg, self.arrays
+            wd = self.wdtype
+            self._layers = (moert_layer_weights * c.layers)()
+            for l in range(c.layers):
+                L = self._layers[l]
+                L.ln_attn = a[f"{l}.ln_attn"].ctypes.data
+                L.ln_moe = a[f"{l}.ln_moe"].ctypes.data
+                for n in ("q", "k", "v", "o", "router", "gate_up", "down"):
+                    setattr(L, n, moert_tensor(a[f"{l}.{n}"].ctypes.data, wd))
+                bias = a.get(f"{l}.router_bias")
+                L.router_bias = None if bias is None else bias.ctypes.data
+            self._struct = moert_model_weights(moert_tensor(a["embed"].ctypes.data, self.embed_dtype),
+                                               a["norm"].ctypes.data, self._layers)
+        return self._struct
+
+    def weight_bytes(self) -> int:
+        return sum(v.nbytes for v in self.arrays.values())
+
+
+class GpuModel:
+    """All weights resident in HBM (GpuModel::upload, gpu_model.rs:191-194) and an fp16 KV cache of max_len."""
+
+    def __init__(self, model: SynthModel, max_len: int, attn_splits: int = 64):
+        self.model, self.cfg, self.max_len = model, model.cfg, max_len
+        h = ctypes.c_void_p()
+        check(lib().moert_model_create(ctypes.byref(model.cfg.c()), ctypes.byref(model.weights()), max_len,
+                                       attn_splits, ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().moert_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def step(self, token: int, want_logits: bool = True):
+        """One token: (logits, route ids [layers, k], route weights [layers, k], argmax) (GpuModel::step)."""
+        c = self.cfg
+        lg = np.empty(c.vocab, np.float32) if want_logits else None
+        ids = np.empty((c.layers, c.top_k), np.int32)
+        w = np.empty((c.layers, c.top_k), np.float32)
+        am = ctypes.c_int(0)
+        check(lib().moert_decode_step(self.h, int(token), ptr(lg), ptr(ids), ptr(w), ctypes.byref(am)))
+        return lg, ids, w, am.value
+
+    def generate(self, prompt, n_new: int, gaps: bool = False):
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(n_new, np.int32)
+        g = np.empty(n_new, np.float32) if gaps else None
+        check(lib().moert_generate(self.h, ptr(p), p.size, n_new, ptr(out), ptr(g)))
+        return (out, g) if gaps else out
+
+    def reset(self):
+        check(lib().moert_reset_sequence(self.h))
+
+    def set_position(self, pos: int):
+        check(lib().moert_set_position(self.h, pos))
+
+    def position(self) -> int:
+        p = ctypes.c_int(0)
+        check(lib().moert_get_position(self.h, ctypes.byref(p)))
+        return p.value
+
+    def kv_prefill(self, layer: int, k: np.ndarray, v: np.ndarray):
+        """k, v: fp16 bits [kv_heads, n, head_dim]."""
+        k = np.ascontiguousarray(k, np.uint16)
+        v = np.ascontiguousarray(v, np.uint16)
+        check(lib().moert_kv_prefill_fp16(self.h, layer, ptr(k), ptr(v), k.shape[1]))
+
+    def read_kv(self, layer: int, n: int):
+        c = self.cfg
+        k = np.empty((c.kv_heads, n, c.head_dim), np.uint16)
+        v = np.empty_like(k)
+        check(lib().moert_read_kv_fp16(self.h, layer, ptr(k), ptr(v), n))
+        return k, v
+
+    def hidden(self) -> np.ndarray:
+        out = np.empty(self.cfg.hidden, np.float32)
+        check(lib().moert_read_hidden(self.h, ptr(out)))
+        return out
+
+    def time_steps(self, warmup: int, iters: int) -> float:
+        ms = ctypes.c_double(0)
+        check(lib().moert_time_steps(self.h, warmup, iters, ctypes.byref(ms)))
+        return ms.value
+
+    def time_kernel(self, kind: int, iters: int):
+        us, n = ctypes.c_double(0), ctypes.c_int(0)
+        check(lib().moert_time_kernel(self.h, kind, iters, ctypes.byref(us), ctypes.byref(n)))
+        return us.value, n.value
+
+
+def kv_prefill_data(cfg: Config, seed: int, layer: int, n: int):
+    """fp16 N(0, 1) K and V of n positions for one layer, [kv_heads, n, head_dim] (the long-context workload)."""
+    cnt = cfg.kv_heads * n * cfg.head_dim
+    k = synth_fp16(seed, 50000 + 2 * layer, cnt).reshape(cfg.kv_heads, n, cfg.head_dim)
+    v = synth_fp16(seed, 50001 + 2 * layer, cnt).reshape(cfg.kv_heads, n, cfg.head_dim)
+    return k, v
+
+
+class GpuBlock:
+    """One MoE block, all experts resident (GpuLayer, gpu.rs:368-541)."""
+
+    def __init__(self, hidden, inter, experts, top_k, router, gate_up, down, dtype=Q8_0, router_bias=None):
+        self._keep = (router, gate_up, down, router_bias)
+        self.hidden, self.top_k = hidden, top_k
+        h = ctypes.c_void_p()
+        check(lib().moert_block_create(hidden, inter, experts, top_k, ctypes.byref(moert_tensor(router.ctypes.data, dtype)),
+                                       ptr(router_bias), ctypes.byref(moert_tensor(gate_up.ctypes.data, dtype)),
+                                       ctypes.byref(moert_tensor(down.ctypes.data, dtype)), ctypes.byref(h)))
+        self.h = h
+
+    def forward(self, x: np.ndarray):
+        x = np.ascontiguousarray(x, np.float32)
+        y = np.empty(self.hidden, np.float32)
+        ids = np.empty(self.top_k, np.int32)
+        w = np.empty(self.top_k, np.float32)
+        check(lib().moert_block_forward(self.h, ptr(x), ptr(y), ptr(ids), ptr(w)))
+        return y, ids, w
+
+    def time(self, iters: int) -> float:
+        us = ctypes.c_double(0)
+        check(lib().moert_block_time(self.h, iters, ctypes.byref(us)))
+        return us.value
+
+    def close(self):
+        if self.h:
+            lib().moert_block_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---- unit-parity entry points ------------------------------------------------------------------------------------
+def router_topk(logits: np.ndarray, k: int):
+    l = np.ascontiguousarray(logits, np.float32)
+    ids = np.empty(k, np.int32)
+    w = np.empty(k, np.float32)
+    check(lib().moert_router_topk(ptr(l), l.size, k, ptr(ids), ptr(w)))
+    return ids, w
+
+
+def argmax(v: np.ndarray) -> int:
+    v = np.ascontiguousarray(v, np.float32)
+    i = ctypes.c_int(0)
+    check(lib().moert_argmax(ptr(v), v.size, ctypes.byref(i)))
+    return i.value
+
+
+def gemv(w: np.ndarray, dtype: int, rows: int, cols: int, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(rows, np.float32)
+    check(lib().moert_gemv(ctypes.byref(moert_tensor(w.ctypes.data, dtype)), rows, cols, ptr(x), ptr(y)))
+    return y
+
+
+def dequant(w: np.ndarray, dtype: int, rows: int, cols: int) -> np.ndarray:
+    out = np.empty(rows * cols, np.float32)
+    check(lib().moert_dequant(ctypes.byref(moert_tensor(w.ctypes.data, dtype)), rows, cols, ptr(out)))
+    return out
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty_like(x)
+    check(lib().moert_rmsnorm(ptr(x), ptr(w), x.size, eps, ptr(out)))
+    return out
+
+
+def rope(x: np.ndarray, head_dim: int, theta: float, pos: int) -> np.ndarray:
+    y = np.ascontiguousarray(x, np.float32).copy()
+    check(lib().moert_rope(ptr(y), y.size // head_dim, head_dim, theta, pos))
+    return y
+
+
+def attn_decode(q, k_cache, v_cache, heads, kv_heads, max_len, length, scale, splits):
+    q = np.ascontiguousarray(q, np.float32)
+    k_cache = np.ascontiguousarray(k_cache, np.uint16)
+    v_cache = np.ascontiguousarray(v_cache, np.uint16)
+    out = np.empty(heads * 64, np.float32)
+    check(lib().moert_attn_decode(ptr(q), ptr(k_cache), ptr(v_cache), heads, kv_heads, 64, max_len, length, scale,
+                                  splits, ptr(out)))
+    return out
+
+
+def exp_device(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    check(lib().moert_exp_device(ptr(x), ptr(y), x.size))
+    return y
+
+
+def step_bytes(cfg: Config, wdtype: int, embed_dtype: int, context: int) -> int:
+    """Algorithmic HBM bytes of one decode step at `context` cached positions (weights once, KV once)."""
+    H, d, I = cfg.hidden, cfg.head_dim, cfg.inter
+    qd, kvd = cfg.heads * d, cfg.kv_heads * d
+    attn = dtype_bytes(wdtype, (qd + 2 * kvd) * H) + dtype_bytes(wdtype, H * qd)
+    router = dtype_bytes(wdtype, cfg.experts * H)
+    experts = cfg.top_k * (dtype_bytes(wdtype, 2 * I * H) + dtype_bytes(wdtype, H * I))
+    norms = 2 * H * 4
+    per_layer = attn + router + experts + norms
+    kv = cfg.layers * 2 * kvd * 2 * context
+    head = dtype_bytes(embed_dtype, cfg.vocab * H)
+    return cfg.layers * per_layer + kv + head

@@ -1,0 +1,76 @@
+/*
+ * Oracle: CPU restatement of the reference decode path (brenoperucchi/lastro-rust, rust/moe-rt), used ONLY as
+ * test infrastructure — by tests/, by __graft_entry__.smoke() as the checker, and by bench.py's cpu_baseline
+ * leg. Nothing in the product (lastro-rust_amd/) links or calls it.
+ *
+ * It follows rust/moe-rt/src/model.rs:181-243 (CpuSession::step), block.rs:56-89 (forward_cpu, Routing),
+ * cpu.rs:65-150 (swiglu, Cpu::gemv, Cpu::experts), cpu.rs:239-296 (experts_step), pool.rs:96-199 (Pool) and
+ * gpu.rs:205-292 (split-KV decode attention), with these build formats in place of the reference's BF16:
+ *   - weights are GGML Q8_0 / Q4_0 blocks or f32, dequantised exactly (q * d fits the f32 mantissa);
+ *   - the KV cache is fp16, laid out [kv_heads, max_len, head_dim] per layer.
+ *
+ * Floating-point evaluation order ("canonical order"), shared with the HIP kernels so that results can be
+ * compared bit for bit:
+ *   dot(w_row, x): the row is cut into chunks of 16 bytes of payload (Q8_0: 16 elements, Q4_0: 32, f32: 4);
+ *     chunk j belongs to lane j % 64; each lane accumulates its chunks in increasing j, elements in increasing
+ *     index, acc = fmaf(w, x, acc) from +0; the 64 lane sums are added as a balanced pairwise tree
+ *     (strides 1, 2, 4, ..., 32).
+ *   exp: orc_exp below (Cody-Waite reduction + degree-7 Taylor polynomial), not libm.
+ *   division and sqrt are IEEE correctly rounded; no other operation is fused.
+ */
+#ifndef MOERT_ORACLE_H
+#define MOERT_ORACLE_H
+#include "../include/moert.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct orc_session orc_session;
+
+float orc_exp(float x);
+void orc_exp_n(const float* x, float* y, size_t n);
+void orc_h2f_n(const uint16_t* h, float* f, size_t n);
+void orc_f2h_n(const float* f, uint16_t* h, size_t n);
+
+/* Exact dequantisation of a GGML blob (or f32 copy). */
+void orc_dequant(const void* w, int dtype, size_t n, float* out);
+/* Canonical dot of row `row` of a [rows, cols] matrix with x. */
+float orc_dot(const void* w, int dtype, int cols, size_t row, const float* x);
+void orc_gemv(const void* w, int dtype, int rows, int cols, const float* x, float* y, int threads);
+
+void orc_rmsnorm(const float* x, const float* w, int n, float eps, float* out);
+void orc_rope_cos_sin(float theta, int head_dim, int pos, float* cs);
+void orc_rope(float* x, int n, int head_dim, const float* cs);
+/* Routing::from_logits with an optional bias added first. */
+void orc_route(const float* logits, const float* bias, int n, int k, int* ids, float* weights);
+void orc_swiglu(const float* h, int inter, float* a);
+int orc_argmax(const float* v, int n);
+
+/* HostLayer::forward_cpu on a normalised x. */
+void orc_moe_block(int hidden, int inter, int experts, int k, const moert_tensor* router, const float* bias,
+                   const moert_tensor* gate_up, const moert_tensor* down, const float* x, float* y, int* ids,
+                   float* weights, int threads);
+
+/* Split-KV decode attention, canonical order (see oracle.cpp). */
+void orc_attention(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, int heads, int kv_heads,
+                   int head_dim, int max_len, int len, float scale, int splits, float* out);
+
+/* Cpu::experts_step: m positions, per-position top-k routing; y written for every position. */
+void orc_experts_step(int hidden, int inter, int m, int k, const moert_tensor* gate_up, const moert_tensor* down,
+                      const float* x, const int* ids, const float* weights, float* y, int threads);
+
+/* CpuSession. */
+int orc_session_create(const moert_config* cfg, const moert_model_weights* w, int max_len, int attn_splits,
+                       int threads, orc_session** out);
+void orc_session_destroy(orc_session* s);
+int orc_session_step(orc_session* s, int token, float* logits, int* route_ids, float* route_weights, float* hidden);
+void orc_session_set_pos(orc_session* s, int pos);
+int orc_session_pos(orc_session* s);
+int orc_session_kv_prefill(orc_session* s, int layer, const uint16_t* k, const uint16_t* v, int n);
+int orc_session_read_kv(orc_session* s, int layer, uint16_t* k, uint16_t* v, int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,253 @@
+"""ctypes wrapper of the oracle (oracle/liboracle.so) — test infrastructure only.
+
+Imported by tests/, by __graft_entry__.smoke() as the checker, and by bench.py's cpu_baseline leg; never by the
+product package. The C++ restatement it wraps follows rust/moe-rt/src/{model.rs,block.rs,cpu.rs,pool.rs} and the
+split-KV attention of gpu.rs:205-292 (see oracle.h for the evaluation order).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        vp, i, f, sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
+        sig = {
+            "orc_exp": (f, [f]),
+            "orc_exp_n": (None, [vp, vp, sz]),
+            "orc_h2f_n": (None, [vp, vp, sz]),
+            "orc_f2h_n": (None, [vp, vp, sz]),
+            "orc_dequant": (None, [vp, i, sz, vp]),
+            "orc_dot": (f, [vp, i, i, sz, vp]),
+            "orc_gemv": (None, [vp, i, i, i, vp, vp, i]),
+            "orc_rmsnorm": (None, [vp, vp, i, f, vp]),
+            "orc_rope_cos_sin": (None, [f, i, i, vp]),
+            "orc_rope": (None, [vp, i, i, vp]),
+            "orc_route": (None, [vp, vp, i, i, vp, vp]),
+            "orc_swiglu": (None, [vp, i, vp]),
+            "orc_argmax": (i, [vp, i]),
+            "orc_moe_block": (None, [i, i, i, i, vp, vp, vp, vp, vp, vp, vp, vp, i]),
+            "orc_attention": (None, [vp, vp, vp, i, i, i, i, i, f, i, vp]),
+            "orc_experts_step": (None, [i, i, i, i, vp, vp, vp, vp, vp, vp, i]),
+            "orc_session_create": (i, [vp, vp, i, i, i, ctypes.POINTER(vp)]),
+            "orc_session_destroy": (None, [vp]),
+            "orc_session_step": (i, [vp, i, vp, vp, vp, vp]),
+            "orc_session_set_pos": (None, [vp, i]),
+            "orc_session_pos": (i, [vp]),
+            "orc_session_kv_prefill": (i, [vp, i, vp, vp, i]),
+            "orc_session_read_kv": (i, [vp, i, vp, vp, i]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, np.float32)
+
+
+def exp(x):
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().orc_exp_n(_p(x), _p(y), x.size)
+    return y
+
+
+def h2f(h):
+    h = np.ascontiguousarray(h, np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().orc_h2f_n(_p(h), _p(out), h.size)
+    return out
+
+
+def f2h(x):
+    x = _f32(x)
+    out = np.empty(x.shape, np.uint16)
+    lib().orc_f2h_n(_p(x), _p(out), x.size)
+    return out
+
+
+def dequant(w, dtype, n):
+    out = np.empty(n, np.float32)
+    lib().orc_dequant(_p(w), dtype, n, _p(out))
+    return out
+
+
+def dot(w, dtype, cols, row, x):
+    return float(lib().orc_dot(_p(w), dtype, cols, row, _p(_f32(x))))
+
+
+def gemv(w, dtype, rows, cols, x, threads=4):
+    y = np.empty(rows, np.float32)
+    lib().orc_gemv(_p(w), dtype, rows, cols, _p(_f32(x)), _p(y), threads)
+    return y
+
+
+def rmsnorm(x, w, eps):
+    x, w = _f32(x), _f32(w)
+    out = np.empty_like(x)
+    lib().orc_rmsnorm(_p(x), _p(w), x.size, eps, _p(out))
+    return out
+
+
+def rope_cos_sin(theta, head_dim, pos):
+    cs = np.empty(head_dim, np.float32)
+    lib().orc_rope_cos_sin(theta, head_dim, pos, _p(cs))
+    return cs
+
+
+def rope(x, head_dim, cs):
+    y = _f32(x).copy()
+    lib().orc_rope(_p(y), y.size, head_dim, _p(_f32(cs)))
+    return y
+
+
+def route(logits, k, bias=None):
+    l = _f32(logits)
+    ids = np.empty(k, np.int32)
+    w = np.empty(k, np.float32)
+    lib().orc_route(_p(l), _p(None if bias is None else _f32(bias)), l.size, k, _p(ids), _p(w))
+    return ids, w
+
+
+def swiglu(h):
+    h = _f32(h)
+    a = np.empty(h.size // 2, np.float32)
+    lib().orc_swiglu(_p(h), h.size // 2, _p(a))
+    return a
+
+
+def argmax(v):
+    v = _f32(v)
+    return int(lib().orc_argmax(_p(v), v.size))
+
+
+def _moert():
+    import importlib
+    import sys
+    pkg = os.path.join(os.path.dirname(_HERE), "lastro-rust_amd")
+    if pkg not in sys.path:
+        sys.path.insert(0, pkg)
+    return importlib.import_module("moert")
+
+
+def moe_block(hidden, inter, experts, k, router, gate_up, down, dtype, x, bias=None, threads=4):
+    mt = _moert()
+    r, gu, dn = (mt.moert_tensor(a.ctypes.data, dtype) for a in (router, gate_up, down))
+    x = _f32(x)
+    y = np.empty(hidden, np.float32)
+    ids = np.empty(k, np.int32)
+    w = np.empty(k, np.float32)
+    lib().orc_moe_block(hidden, inter, experts, k, ctypes.byref(r), _p(None if bias is None else _f32(bias)),
+                        ctypes.byref(gu), ctypes.byref(dn), _p(x), _p(y), _p(ids), _p(w), threads)
+    return y, ids, w
+
+
+def attention(q, k_cache, v_cache, heads, kv_heads, max_len, length, scale, splits):
+    q = _f32(q)
+    kc = np.ascontiguousarray(k_cache, np.uint16)
+    vc = np.ascontiguousarray(v_cache, np.uint16)
+    out = np.empty(heads * 64, np.float32)
+    lib().orc_attention(_p(q), _p(kc), _p(vc), heads, kv_heads, 64, max_len, length, scale, splits, _p(out))
+    return out
+
+
+def experts_step(hidden, inter, m, k, gate_up, down, dtype, x, ids, weights, threads=4):
+    mt = _moert()
+    gu, dn = mt.moert_tensor(gate_up.ctypes.data, dtype), mt.moert_tensor(down.ctypes.data, dtype)
+    x = _f32(x)
+    ids = np.ascontiguousarray(ids, np.int32)
+    weights = _f32(weights)
+    y = np.empty(m * hidden, np.float32)
+    lib().orc_experts_step(hidden, inter, m, k, ctypes.byref(gu), ctypes.byref(dn), _p(x), _p(ids), _p(weights),
+                           _p(y), threads)
+    return y.reshape(m, hidden)
+
+
+class CpuSession:
+    """CpuSession (rust/moe-rt/src/model.rs:160-243) over a moert.SynthModel, fp16 KV cache of max_len."""
+
+    def __init__(self, model, max_len, attn_splits=64, threads=None):
+        self.model, self.cfg = model, model.cfg
+        threads = threads or min(16, os.cpu_count() or 1)
+        self.threads = threads
+        h = ctypes.c_void_p()
+        rc = lib().orc_session_create(ctypes.byref(model.cfg.c()), ctypes.byref(model.weights()), max_len,
+                                      attn_splits, threads, ctypes.byref(h))
+        if rc != 0:
+            raise RuntimeError(f"orc_session_create failed: {rc}")
+        self.h = h
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_session_destroy(self.h)
+            self.h = None
+
+    def step(self, token, want_logits=True):
+        c = self.cfg
+        lg = np.empty(c.vocab, np.float32) if want_logits else None
+        ids = np.empty((c.layers, c.top_k), np.int32)
+        w = np.empty((c.layers, c.top_k), np.float32)
+        hid = np.empty(c.hidden, np.float32)
+        rc = lib().orc_session_step(self.h, int(token), _p(lg), _p(ids), _p(w), _p(hid))
+        if rc != 0:
+            raise RuntimeError(f"orc_session_step failed: {rc}")
+        return lg, ids, w, hid
+
+    def set_position(self, pos):
+        lib().orc_session_set_pos(self.h, pos)
+
+    def position(self):
+        return int(lib().orc_session_pos(self.h))
+
+    def kv_prefill(self, layer, k, v):
+        k = np.ascontiguousarray(k, np.uint16)
+        v = np.ascontiguousarray(v, np.uint16)
+        rc = lib().orc_session_kv_prefill(self.h, layer, _p(k), _p(v), k.shape[1])
+        if rc != 0:
+            raise RuntimeError(f"kv_prefill failed: {rc}")
+
+    def read_kv(self, layer, n):
+        c = self.cfg
+        k = np.empty((c.kv_heads, n, c.head_dim), np.uint16)
+        v = np.empty_like(k)
+        lib().orc_session_read_kv(self.h, layer, _p(k), _p(v), n)
+        return k, v
+
+    def generate(self, prompt, n_new):
+        """Greedy: prompt token by token, then n_new argmax tokens (m1b-gulosa.rs:85-105); also the top1-top2 gaps."""
+        lg = None
+        for t in prompt:
+            lg, _, _, self.last_hidden = self.step(int(t))
+        out, gaps = [], []
+        for i in range(n_new):
+            nxt = argmax(lg)
+            s = np.sort(lg)
+            gaps.append(float(s[-1] - s[-2]))
+            out.append(nxt)
+            if i + 1 < n_new:
+                lg, _, _, self.last_hidden = self.step(nxt)
+        return np.array(out, np.int32), np.array(gaps, np.float32)

@@ -1,0 +1,34 @@
+import os
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "lastro-rust_amd")
+ORACLE = os.path.join(ROOT, "oracle")
+for p in (PKG, ORACLE, os.path.join(ROOT, "tests", "golden")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950); runs on the GPU box")
+    # Build what is missing (the round's build step normally leaves both libraries in place).
+    if not os.path.exists(os.path.join(ORACLE, "liboracle.so")):
+        subprocess.run(["make", "-s", "-C", ORACLE], check=True)
+    if not os.path.exists(os.path.join(PKG, "libmoert.so")):
+        subprocess.run(["make", "-s", "-j4", "-C", PKG], check=True)
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    """The device; GPU tests are skipped without one unless MOERT_REQUIRE_GPU=1 (then they fail)."""
+    import moert
+    n, name = moert.device_info()
+    if n == 0:
+        if os.environ.get("MOERT_REQUIRE_GPU") == "1":
+            pytest.fail("MOERT_REQUIRE_GPU=1 and no GPU visible")
+        pytest.skip("no GPU visible")
+    print(f"\n[gpu] {name}", flush=True)
+    return name
