@@ -13,11 +13,16 @@ constexpr int kWavesPerBlock = kBlock / kWave;
 // Row geometry of a [rows, K] matrix of dtype DT: NCH chunks of CE elements per row. When NCH < 64 a row only
 // needs LPR = next power of two >= NCH lanes, so a wave covers RPW = 64 / LPR rows per pass (the canonical
 // 64-lane tree then only adds zeros beyond LPR). Lane `sub` of a row owns chunks sub, sub + LPR, ... (NJ of them).
+// Lanes per row: the smallest power of two >= NCH, at most 64 (chunk j must sit in lane j % 64).
+__host__ __device__ constexpr int lanes_per_row(int nch) {
+  return nch > 32 ? 64 : nch > 16 ? 32 : nch > 8 ? 16 : nch > 4 ? 8 : nch > 2 ? 4 : nch > 1 ? 2 : 1;
+}
+
 template <int DT, int K>
 struct Geo {
   static constexpr int CE = Fmt<DT>::kElems;
   static constexpr int NCH = K / CE;
-  static constexpr int LPR = NCH >= 64 ? 64 : NCH >= 32 ? 32 : NCH >= 16 ? 16 : NCH >= 8 ? 8 : NCH >= 4 ? 4 : NCH >= 2 ? 2 : 1;
+  static constexpr int LPR = lanes_per_row(NCH);
   static constexpr int RPW = kWave / LPR;
   static constexpr int NJ = (NCH + LPR - 1) / LPR;
   static_assert(K % CE == 0 && K % 32 == 0, "row length must be a multiple of 32");
@@ -887,11 +892,9 @@ hipError_t launch_expert_down(hipStream_t s, const LayerDev& L, const Dims& d, c
 }
 
 int head_blocks(const DMat& head) {
-  int rpw = 1;
+  int rpw;
   int ce = head.dtype == DT_Q8_0 ? 16 : head.dtype == DT_Q4_0 ? 32 : 4;
-  int nch = head.cols / ce;
-  int lpr = nch >= 64 ? 64 : nch >= 32 ? 32 : nch >= 16 ? 16 : nch >= 8 ? 8 : nch >= 4 ? 4 : nch >= 2 ? 2 : 1;
-  rpw = kWave / lpr;
+  rpw = kWave / lanes_per_row(head.cols / ce);
   return cdiv(head.rows, kWavesPerBlock * kHeadP * rpw);
 }
 
