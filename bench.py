@@ -38,8 +38,7 @@ def kernel_bytes(kind, cfg, ctx, wd, ed):
         moert.K_QKV: b(wd, (qd + 2 * kvd) * H),
         moert.K_ATTN: 2 * kvd * 2 * ctx,
         moert.K_OPROJ: b(wd, H * qd),
-        moert.K_ROUTER: b(wd, cfg.experts * H),
-        moert.K_EXPERT_UP: cfg.top_k * b(wd, 2 * I * H),
+        moert.K_ROUTE_UP: b(wd, cfg.experts * H) + cfg.top_k * b(wd, 2 * I * H),
         moert.K_EXPERT_DOWN: cfg.top_k * b(wd, H * I),
         moert.K_HEAD: b(ed, cfg.vocab * H),
     }[kind]
@@ -95,7 +94,7 @@ def main():
     log(f"{args.steps} steps in {wall * 1e3:.1f} ms wall ({ms_event:.3f} ms/step by events): {tok_s:.1f} tok/s")
 
     kernels = {}
-    for kind in range(8):
+    for kind in range(len(moert.KERNEL_NAMES)):
         g.set_position(pos0)
         us, launches = g.time_kernel(kind, args.kernel_iters)
         per_step = launches // args.kernel_iters
@@ -107,7 +106,7 @@ def main():
     dk = kernels[dom]
     log("kernels: " + ", ".join(f"{k} {v['us']:.2f}us x{v['launches_per_step']} {v['gbs']:.0f}GB/s"
                                 for k, v in kernels.items()))
-    moe = {k: kernels[k] for k in ("expert_up", "expert_down")}
+    moe = {k: kernels[k] for k in ("route_up", "expert_down")}
     g.close()
 
     cpu = None

@@ -90,7 +90,8 @@ int moert_device_info(int* count, char* name, int name_len);
  * ------------------------------------------------------------------------------------------------------- */
 
 /* Uploads every weight to HBM (all experts resident) and allocates an fp16 KV cache of max_len positions.
- * attn_splits is the number of split-KV blocks per KV head (ATTN_NS, rust/moe-rt/src/gpu_model.rs:22).
+ * attn_splits (1..64) caps the split-KV blocks per KV head (ATTN_NS, rust/moe-rt/src/gpu_model.rs:22): each split
+ * covers ceil(ceil(max_len/64) / attn_splits) tiles of 64 positions.
  * Replaces GpuModel::upload (rust/moe-rt/src/gpu_model.rs:191-194). */
 int moert_model_create(const moert_config* cfg, const moert_model_weights* w, int max_len, int attn_splits,
                        moert_model** out);
@@ -133,8 +134,14 @@ int moert_time_steps(moert_model* m, int warmup, int iters, double* ms_per_step)
  * launch of kernel class `kind` (see moert_kernel_kind) and returns the mean duration of one launch in
  * microseconds and the number of launches timed. Position advances by iters. */
 typedef enum {
-  MOERT_K_EMBED = 0, MOERT_K_QKV = 1, MOERT_K_ATTN = 2, MOERT_K_OPROJ = 3, MOERT_K_ROUTER = 4,
-  MOERT_K_EXPERT_UP = 5, MOERT_K_EXPERT_DOWN = 6, MOERT_K_HEAD = 7, MOERT_K_COUNT = 8
+  MOERT_K_EMBED = 0,       /* embedding row */
+  MOERT_K_QKV = 1,         /* rmsnorm + q/k/v + RoPE + KV write */
+  MOERT_K_ATTN = 2,        /* split-KV attention + combine */
+  MOERT_K_OPROJ = 3,       /* output projection + residual */
+  MOERT_K_ROUTE_UP = 4,    /* rmsnorm + router + top-k + gate/up + SwiGLU of the routed experts */
+  MOERT_K_EXPERT_DOWN = 5, /* down of the routed experts + weighted combine + residual */
+  MOERT_K_HEAD = 6,        /* final rmsnorm + LM head + greedy argmax */
+  MOERT_K_COUNT = 7
 } moert_kernel_kind;
 int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch, int* launches);
 
@@ -176,10 +183,10 @@ int moert_rmsnorm(const float* x, const float* w, int n, float eps, float* out);
 int moert_rope(float* x, int heads, int head_dim, float theta, int pos);
 
 /* Decode attention of `heads` query heads against an fp16 cache [kv_heads, max_len, head_dim] holding `len`
- * valid positions, in `splits` split-KV blocks per KV head
+ * valid positions; split-KV blocks of tiles_per_split 64-position tiles (at most 64 splits per cache)
  * (attn_split + attn_combine, rust/moe-rt/src/gpu.rs:205-292; CpuSession attention model.rs:200-222). */
 int moert_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, int heads, int kv_heads,
-                      int head_dim, int max_len, int len, float scale, int splits, float* out);
+                      int head_dim, int max_len, int len, float scale, int tiles_per_split, float* out);
 
 /* Canonical exponential used by every kernel (softmax, SiLU, top-k weights), evaluated on the device. */
 int moert_exp_device(const float* x, float* y, int n);

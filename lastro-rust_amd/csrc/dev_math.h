@@ -40,22 +40,67 @@ __device__ __forceinline__ float dexp(float x) {
 
 __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + dexp(-g))) * u; }
 
-// Butterfly sum over the lanes [0, W) of each W-lane group; every lane ends with the pairwise-tree sum.
+// Cross-lane partner of stage S of a butterfly: a lane in the other half of its aligned 2S-lane group. DPP for
+// S <= 8 (quad_perm, row_half_mirror, row_mirror), permlane16/32_swap for S = 16, 32. After stage S every lane of
+// an aligned 2S-group holds the same value, so v + partner(v) equals the xor butterfly bit for bit: every lane
+// ends with the balanced pairwise tree of the group.
+template <int S>
+__device__ __forceinline__ uint32_t partner_u32(uint32_t v) {
+  if (S == 1) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, true);  // quad_perm 1,0,3,2
+  if (S == 2) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, true);  // quad_perm 2,3,0,1
+  if (S == 4) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xF, 0xF, true);  // row_half_mirror
+  if (S == 8) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, true);  // row_mirror
+  if (S == 16) {
+    auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (threadIdx.x & 16) ? r[0] : r[1];
+  }
+  auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (threadIdx.x & 32) ? r[0] : r[1];
+}
+
+template <int S>
+__device__ __forceinline__ float partner(float v) {
+  return __uint_as_float(partner_u32<S>(__float_as_uint(v)));
+}
+template <int S>
+__device__ __forceinline__ int partner(int v) {
+  return (int)partner_u32<S>((uint32_t)v);
+}
+
+// Butterfly sum over the lanes [0, W) of each aligned W-lane group (all 64 lanes must be active).
 template <int W = kWave>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int s = 1; s < W; s <<= 1) v = v + __shfl_xor(v, s);
+  if (W > 1) v = v + partner<1>(v);
+  if (W > 2) v = v + partner<2>(v);
+  if (W > 4) v = v + partner<4>(v);
+  if (W > 8) v = v + partner<8>(v);
+  if (W > 16) v = v + partner<16>(v);
+  if (W > 32) v = v + partner<32>(v);
   return v;
+}
+
+template <int S>
+__device__ __forceinline__ float max_stage(float v) {
+  float o = partner<S>(v);
+  return o > v ? o : v;
 }
 
 template <int W = kWave>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int s = 1; s < W; s <<= 1) {
-    float o = __shfl_xor(v, s);
-    v = o > v ? o : v;
-  }
+  if (W > 1) v = max_stage<1>(v);
+  if (W > 2) v = max_stage<2>(v);
+  if (W > 4) v = max_stage<4>(v);
+  if (W > 8) v = max_stage<8>(v);
+  if (W > 16) v = max_stage<16>(v);
+  if (W > 32) v = max_stage<32>(v);
   return v;
+}
+
+// LDS writes of this wave become visible to its other lanes (no workgroup barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
 // Total order on floats as integers (Rust's f32::total_cmp).

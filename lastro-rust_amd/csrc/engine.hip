@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdlib>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -195,12 +196,9 @@ struct moert_model {
       t0(MOERT_K_OPROJ);
       CHECK_HIP(launch_oproj(stream, L, dims, b));
       t1(MOERT_K_OPROJ);
-      t0(MOERT_K_ROUTER);
-      CHECK_HIP(launch_router(stream, L, dims, b, (int)l, true));
-      t1(MOERT_K_ROUTER);
-      t0(MOERT_K_EXPERT_UP);
-      CHECK_HIP(launch_expert_up(stream, L, dims, b, (int)l));
-      t1(MOERT_K_EXPERT_UP);
+      t0(MOERT_K_ROUTE_UP);
+      CHECK_HIP(launch_route_up(stream, L, dims, b, (int)l, true));
+      t1(MOERT_K_ROUTE_UP);
       t0(MOERT_K_EXPERT_DOWN);
       CHECK_HIP(launch_expert_down(stream, L, dims, b, (int)l, true));
       t1(MOERT_K_EXPERT_DOWN);
@@ -261,19 +259,22 @@ static int model_create(const moert_config* c, const moert_model_weights* w, int
   CHECK_CFG(k_supported(c->hidden) && k_supported(c->heads * 64) && (c->inter == 128 || c->inter == 256 || c->inter == 512),
             "hidden %d / heads*64 %d / inter %d outside the compiled row lengths", c->hidden, c->heads * 64, c->inter);
   CHECK_CFG(max_len >= 64 && max_len % 64 == 0, "max_len %d must be a positive multiple of 64", max_len);
-  CHECK_CFG(splits >= 1 && splits <= 1024, "attn_splits %d", splits);
+  CHECK_CFG(splits >= 1 && splits <= 64, "attn_splits %d outside [1, 64]", splits);
   CHECK_CFG(c->layers >= 1 && c->vocab >= 1 && w->layers && w->norm, "empty model");
   const int H = c->hidden, d = 64, qd = c->heads * d, kvd = c->kv_heads * d, I = c->inter, E = c->experts;
   for (int l = 0; l < c->layers; l++) {
     const moert_layer_weights& L = w->layers[l];
     CHECK_CFG(L.q.dtype == L.k.dtype && L.q.dtype == L.v.dtype, "layer %d: q, k, v must share a dtype", l);
+    CHECK_CFG(L.router.dtype == L.gate_up.dtype, "layer %d: router and gate_up must share a dtype", l);
     CHECK_CFG(L.ln_attn && L.ln_moe, "layer %d: missing norm weights", l);
   }
   moert_model* m = new moert_model;
   m->cfg = *c;
   m->max_len = max_len;
   m->splits = splits;
-  m->dims = Dims{H, I, c->heads, c->kv_heads, d, c->vocab, E, c->top_k, max_len, splits,
+  // tiles of 64 positions per attention split: the cache is cut into at most `splits` splits
+  const int tps = ((max_len / 64) + splits - 1) / splits;
+  m->dims = Dims{H, I, c->heads, c->kv_heads, d, c->vocab, E, c->top_k, max_len, tps,
                  c->eps, c->embedding_multiplier, c->residual_multiplier, c->attention_multiplier, c->logits_scaling};
   auto bail = [&](int rc) {
     delete m;
@@ -325,11 +326,11 @@ static int model_create(const moert_config* c, const moert_model_weights* w, int
   b.rope = rp;
   m->n_head_blocks = head_blocks(m->embed);
   if ((rc = zeros(a, s, H, &b.h)) || (rc = zeros(a, s, qd, &b.q)) || (rc = zeros(a, s, qd, &b.att)) ||
-      (rc = zeros(a, s, (size_t)c->heads * splits * 66, &b.part)) || (rc = zeros(a, s, c->kv_heads, &b.attn_cnt)) ||
-      (rc = zeros(a, s, H, &b.xn)) || (rc = zeros(a, s, (size_t)c->top_k * I, &b.act)) ||
+      (rc = zeros(a, s, (size_t)c->heads * attn_splits_for(max_len, tps) * 66, &b.part)) ||
+      (rc = zeros(a, s, (size_t)c->top_k * I, &b.act)) ||
       (rc = zeros(a, s, (size_t)c->layers * c->top_k, &b.route_ids)) ||
       (rc = zeros(a, s, (size_t)c->layers * c->top_k, &b.route_w)) || (rc = zeros(a, s, c->vocab, &b.logits)) ||
-      (rc = zeros(a, s, (size_t)m->n_head_blocks, &b.best)) || (rc = zeros(a, s, 1, &b.head_cnt)) ||
+      (rc = zeros(a, s, (size_t)m->n_head_blocks, &b.best)) ||
       (rc = zeros(a, s, max_len, &b.seq)) || (rc = zeros(a, s, max_len, &b.argmax_hist)) ||
       (rc = zeros(a, s, ST_WORDS, &b.state)))
     return bail(rc);
@@ -357,8 +358,7 @@ struct moert_block {
     if (stream) (void)hipStreamDestroy(stream);
   }
   int enqueue() {
-    CHECK_HIP(launch_router(stream, L, dims, b, 0, false));
-    CHECK_HIP(launch_expert_up(stream, L, dims, b, 0));
+    CHECK_HIP(launch_route_up(stream, L, dims, b, 0, false));
     CHECK_HIP(launch_expert_down(stream, L, dims, b, 0, false));
     return MOERT_OK;
   }
@@ -464,7 +464,18 @@ static int model_copy_out(moert_model* m, void* dst, const void* src, size_t byt
   CHECK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, m->stream));
   return MOERT_OK;
 }
+// MOERT_GRAPH=0 launches the step's kernels one by one instead of replaying the captured graph (for tracing
+// tools that do not follow graph launches); results are the same.
+static bool use_graph() {
+  static const bool on = [] {
+    const char* v = getenv("MOERT_GRAPH");
+    return !(v && v[0] == '0');
+  }();
+  return on;
+}
+
 static int model_launch(moert_model* m) {
+  if (!use_graph()) return m->enqueue(-1, nullptr);
   CHECK_HIP(hipGraphLaunch(m->exec, m->stream));
   return MOERT_OK;
 }
@@ -611,9 +622,9 @@ static int time_steps_impl(moert_model* m, int warmup, int iters, double* ms) {
   hipEvent_t e0, e1;
   CHECK_HIP(hipEventCreate(&e0));
   CHECK_HIP(hipEventCreate(&e1));
-  for (int i = 0; i < warmup; i++) CHECK_HIP(hipGraphLaunch(m->exec, m->stream));
+  for (int i = 0; i < warmup; i++) TRY(model_launch(m));
   CHECK_HIP(hipEventRecord(e0, m->stream));
-  for (int i = 0; i < iters; i++) CHECK_HIP(hipGraphLaunch(m->exec, m->stream));
+  for (int i = 0; i < iters; i++) TRY(model_launch(m));
   CHECK_HIP(hipEventRecord(e1, m->stream));
   CHECK_HIP(hipEventSynchronize(e1));
   float t = 0.0f;
@@ -685,6 +696,7 @@ int moert_block_create(int hidden, int inter, int experts, int top_k, const moer
   CHECK_CFG(k_supported(hidden) && (inter == 128 || inter == 256 || inter == 512), "hidden %d / inter %d", hidden, inter);
   CHECK_CFG(experts >= 1 && experts <= 64 && top_k >= 1 && top_k <= 8 && top_k <= experts, "experts %d, top_k %d",
             experts, top_k);
+  CHECK_CFG(router->dtype == gate_up->dtype, "router and gate_up must share a dtype");
   moert_block* b = new moert_block;
   auto bail = [&](int rc) {
     delete b;
@@ -707,7 +719,7 @@ int moert_block_create(int hidden, int inter, int experts, int top_k, const moer
     if ((rc = upload_f32(a, s, router_bias, experts, &tmp))) return bail(rc);
     b->L.router_bias = tmp;
   }
-  if ((rc = zeros(a, s, hidden, &b->x)) || (rc = zeros(a, s, hidden, &b->b.xn)) ||
+  if ((rc = zeros(a, s, hidden, &b->x)) ||
       (rc = zeros(a, s, (size_t)top_k * inter, &b->b.act)) || (rc = zeros(a, s, top_k, &b->b.route_ids)) ||
       (rc = zeros(a, s, top_k, &b->b.route_w)) || (rc = zeros(a, s, hidden, &b->b.logits)))
     return bail(rc);
@@ -847,26 +859,25 @@ int moert_rope(float* x, int heads, int head_dim, float theta, int pos) {
 }
 
 int moert_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, int heads, int kv_heads,
-                      int head_dim, int max_len, int len, float scale, int splits, float* out) {
+                      int head_dim, int max_len, int len, float scale, int tiles_per_split, float* out) {
   CHECK_CFG(q && k_cache && v_cache && out, "null argument");
   CHECK_CFG(head_dim == 64 && heads % kv_heads == 0 && heads / kv_heads <= 4 && max_len % 64 == 0 && len >= 1 &&
-                len <= max_len && splits >= 1,
-            "attn: heads %d, kv %d, d %d, max_len %d, len %d, splits %d", heads, kv_heads, head_dim, max_len, len,
-            splits);
+                len <= max_len && tiles_per_split >= 1 && attn_splits_for(max_len, tiles_per_split) <= 64,
+            "attn: heads %d, kv %d, d %d, max_len %d, len %d, tiles_per_split %d", heads, kv_heads, head_dim, max_len,
+            len, tiles_per_split);
   Scoped sc;
   TRY(sc.init());
   float *dq, *part, *dout;
   uint16_t *dk, *dv;
-  int *cnt, *dlen;
+  int* dlen;
   size_t kvn = (size_t)kv_heads * max_len * 64;
   TRY(sc.dev(&dq, (size_t)heads * 64, q));
   TRY(sc.dev(&dk, kvn, k_cache));
   TRY(sc.dev(&dv, kvn, v_cache));
-  TRY(sc.dev(&part, (size_t)heads * splits * 66));
-  TRY(sc.dev(&cnt, kv_heads));
+  TRY(sc.dev(&part, (size_t)heads * attn_splits_for(max_len, tiles_per_split) * 66));
   TRY(sc.dev(&dlen, 1, &len));
   TRY(sc.dev(&dout, (size_t)heads * 64));
-  CHECK_HIP(launch_attn_unit(sc.s, dq, dk, dv, heads, kv_heads, max_len, dlen, scale, splits, part, cnt, dout));
+  CHECK_HIP(launch_attn_unit(sc.s, dq, dk, dv, heads, kv_heads, max_len, dlen, scale, tiles_per_split, part, dout));
   TRY(sc.get(out, dout, (size_t)heads * 64 * 4));
   return MOERT_OK;
 }

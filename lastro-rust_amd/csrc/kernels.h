@@ -25,7 +25,7 @@ struct LayerDev {
 };
 
 struct Dims {
-  int hidden, inter, heads, kv_heads, head_dim, vocab, experts, top_k, max_len, splits;
+  int hidden, inter, heads, kv_heads, head_dim, vocab, experts, top_k, max_len, tps;  // tps: attention tiles per split
   float eps, emb_mult, res_mult, attn_mult, logits_scaling;
 };
 
@@ -35,14 +35,11 @@ struct StepBufs {
   float* q;          // [heads*d]
   float* att;        // [heads*d]
   float* part;       // [heads, splits, 2 + d] split-KV partials
-  int* attn_cnt;     // [kv_heads] arrival counters (left at 0)
-  float* xn;         // [H] normalised MoE input
   float* act;        // [k, I] SwiGLU activations
   int* route_ids;    // [layers, k]
   float* route_w;    // [layers, k]
   float* logits;     // [V]
   int2* best;        // [head blocks] per-block argmax
-  int* head_cnt;     // [1]
   int* seq;          // [max_len] token of each position
   int* argmax_hist;  // [max_len] argmax produced at each position
   int* state;        // [ST_WORDS]
@@ -53,10 +50,10 @@ hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const Ste
 hipError_t launch_qkv(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
 hipError_t launch_attn(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
 hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
+// Router + gate/up of the routed experts (the router recomputed by every workgroup, workgroup 0 publishes it).
 // normalize: rmsnorm h with ln_moe first (decode step); otherwise h is the block input as is.
-hipError_t launch_router(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
-                         bool normalize);
-hipError_t launch_expert_up(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer);
+hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
+                           bool normalize);
 // accumulate: h += res * y (decode step); otherwise y is written to b.logits (standalone MoE block output).
 hipError_t launch_expert_down(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
                               bool accumulate);
@@ -72,7 +69,9 @@ hipError_t launch_topk(hipStream_t s, const float* logits, const float* bias, in
 hipError_t launch_argmax(hipStream_t s, const float* v, int n, int2* best, int* cnt, int* out);
 hipError_t launch_exp(hipStream_t s, const float* x, float* y, int n);
 hipError_t launch_attn_unit(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vc, int heads,
-                            int kv_heads, int max_len, const int* len_dev, float scale, int splits, float* part,
-                            int* cnt, float* out);
+                            int kv_heads, int max_len, const int* len_dev, float scale, int tps, float* part,
+                            float* out);
+// Splits of a cache of max_len positions with tps 64-position tiles per split.
+int attn_splits_for(int max_len, int tps);
 
 }  // namespace moert

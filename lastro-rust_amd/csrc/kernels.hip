@@ -106,30 +106,77 @@ __device__ __forceinline__ float rms_scale(const float* __restrict__ x, float ep
   return 1.0f / sqrtf(ss / (float)K + eps);
 }
 
-// P rows per lane group: all chunk loads are issued before any arithmetic. out[p] ends up in every lane of the
-// group that computed row[p].
+// Chunk registers of P rows. rows_load issues every load before any arithmetic (and before the activations are
+// ready), rows_fma does the canonical chain per row; out[p] ends up in every lane of the group owning row[p].
 template <int DT, int K, int P>
-__device__ __forceinline__ void rows_dot(const DMat& m, const size_t (&row)[P], const bool (&ok)[P],
-                                         const XReg<DT, K>& xr, int sub, float (&out)[P]) {
+struct Rows {
+  RawChunk c[P][Geo<DT, K>::NJ];
+};
+
+template <int DT, int K, int P>
+__device__ __forceinline__ void rows_load(Rows<DT, K, P>& r, const DMat& m, const size_t (&row)[P],
+                                          const bool (&ok)[P], int sub) {
   using G = Geo<DT, K>;
-  RawChunk c[P][G::NJ];
 #pragma unroll
   for (int p = 0; p < P; p++)
 #pragma unroll
     for (int jj = 0; jj < G::NJ; jj++) {
       int j = sub + G::LPR * jj;
-      if (ok[p] && j < G::NCH) c[p][jj] = load_chunk<DT>(m, row[p], j);
+      if (ok[p] && j < G::NCH) r.c[p][jj] = load_chunk<DT>(m, row[p], j);
     }
+}
+
+template <int DT, int K, int P>
+__device__ __forceinline__ void rows_fma(const Rows<DT, K, P>& r, const bool (&ok)[P], const XReg<DT, K>& xr,
+                                         int sub, float (&out)[P]) {
+  using G = Geo<DT, K>;
 #pragma unroll
   for (int p = 0; p < P; p++) {
     float acc = 0.0f;
 #pragma unroll
     for (int jj = 0; jj < G::NJ; jj++) {
       int j = sub + G::LPR * jj;
-      if (ok[p] && j < G::NCH) acc = fma_chunk<DT>(c[p][jj], xr.v[jj], acc);
+      if (ok[p] && j < G::NCH) acc = fma_chunk<DT>(r.c[p][jj], xr.v[jj], acc);
     }
     out[p] = group_sum<G::LPR>(acc);
   }
+}
+
+// Workgroup prologues: the block's activation vector in LDS, once per workgroup.
+// wg_norm: xs = lnw * (x * r), r = 1/sqrt(sum(x^2)/K + eps), the sum in the canonical order by wave 0.
+template <int K, int NT>
+__device__ __forceinline__ void wg_norm(const float* __restrict__ x, const float* __restrict__ lnw, float eps,
+                                        float* xs, float* rs) {
+  constexpr int PER = (K + NT - 1) / NT;
+  float hv[PER], wv[PER];
+#pragma unroll
+  for (int e = 0; e < PER; e++) {
+    int i = threadIdx.x + e * NT;
+    if (i < K) {
+      hv[e] = x[i];
+      wv[e] = lnw[i];
+    }
+  }
+  if (threadIdx.x < 64) {
+    float r = rms_scale<K>(x, eps, threadIdx.x);
+    if (threadIdx.x == 0) *rs = r;
+  }
+  __syncthreads();
+  const float r = *rs;
+#pragma unroll
+  for (int e = 0; e < PER; e++) {
+    int i = threadIdx.x + e * NT;
+    if (i < K) xs[i] = wv[e] * (hv[e] * r);
+  }
+  __syncthreads();
+}
+
+template <int N, int NT>
+__device__ __forceinline__ void wg_copy(const float* __restrict__ x, float* xs) {
+  static_assert(N % 4 == 0, "vector copy");
+  for (int i = threadIdx.x; i < N / 4; i += NT)
+    reinterpret_cast<float4*>(xs)[i] = reinterpret_cast<const float4*>(x)[i];
+  __syncthreads();
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -137,10 +184,9 @@ __device__ __forceinline__ void rows_dot(const DMat& m, const size_t (&row)[P], 
 template <int DT, int K, int P>
 __global__ __launch_bounds__(kBlock) void k_gemv(DMat m, const float* __restrict__ x, float* __restrict__ y) {
   using G = Geo<DT, K>;
+  __shared__ float xs[K];
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int sub = lane % G::LPR, rw = lane / G::LPR;
-  XReg<DT, K> xr;
-  load_x<DT, K>(xr, x, sub);
   size_t base = ((size_t)blockIdx.x * kWavesPerBlock + wave) * (P * G::RPW);
   size_t row[P];
   bool ok[P];
@@ -149,8 +195,13 @@ __global__ __launch_bounds__(kBlock) void k_gemv(DMat m, const float* __restrict
     row[p] = base + (size_t)p * G::RPW + rw;
     ok[p] = row[p] < (size_t)m.rows;
   }
+  Rows<DT, K, P> rr;
+  rows_load<DT, K, P>(rr, m, row, ok, sub);
+  wg_copy<K, kBlock>(x, xs);
+  XReg<DT, K> xr;
+  load_x<DT, K>(xr, xs, sub);
   float out[P];
-  rows_dot<DT, K, P>(m, row, ok, xr, sub, out);
+  rows_fma<DT, K, P>(rr, ok, xr, sub, out);
 #pragma unroll
   for (int p = 0; p < P; p++)
     if (ok[p] && sub == 0) y[row[p]] = out[p];
@@ -190,12 +241,10 @@ __global__ __launch_bounds__(kBlock) void k_qkv(DMat m, const float* __restrict_
                                                 uint16_t* __restrict__ kc, uint16_t* __restrict__ vc) {
   using G = Geo<DT, K>;
   constexpr int P = 2 * NP;
+  __shared__ float xs[K];
+  __shared__ float rs;
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int sub = lane % G::LPR, rw = lane / G::LPR;
-  float r = rms_scale<K>(h, eps, lane);
-  XReg<DT, K> xr;
-  load_xn<DT, K>(xr, h, lnw, r, sub);
-  int pos = st[ST_POS];
   int npairs = m.rows / 2;
   int wbase = (blockIdx.x * kWavesPerBlock + wave) * (NP * G::RPW);
   size_t row[P];
@@ -211,8 +260,14 @@ __global__ __launch_bounds__(kBlock) void k_qkv(DMat m, const float* __restrict_
     ok[2 * a] = v;
     ok[2 * a + 1] = v;
   }
+  Rows<DT, K, P> rr;
+  rows_load<DT, K, P>(rr, m, row, ok, sub);
+  const int pos = st[ST_POS];
+  wg_norm<K, kBlock>(h, lnw, eps, xs, &rs);
+  XReg<DT, K> xr;
+  load_x<DT, K>(xr, xs, sub);
   float out[P];
-  rows_dot<DT, K, P>(m, row, ok, xr, sub, out);
+  rows_fma<DT, K, P>(rr, ok, xr, sub, out);
   if (sub != 0) return;
   const float* cs = rope + (size_t)pos * 64;
 #pragma unroll
@@ -220,14 +275,14 @@ __global__ __launch_bounds__(kBlock) void k_qkv(DMat m, const float* __restrict_
     if (!ok[2 * a]) continue;
     int head = gp[a] / 32, jp = gp[a] % 32;
     float x1 = out[2 * a], x2 = out[2 * a + 1];
-    float c = cs[jp], s = cs[32 + jp];
+    float c = cs[jp], sn = cs[32 + jp];
     if (head < heads) {
-      q[head * 64 + jp] = x1 * c - x2 * s;
-      q[head * 64 + jp + 32] = x2 * c + x1 * s;
+      q[head * 64 + jp] = x1 * c - x2 * sn;
+      q[head * 64 + jp + 32] = x2 * c + x1 * sn;
     } else if (head < heads + kvh) {
       uint16_t* kp = kc + ((size_t)(head - heads) * max_len + pos) * 64;
-      kp[jp] = f2h(x1 * c - x2 * s);
-      kp[jp + 32] = f2h(x2 * c + x1 * s);
+      kp[jp] = f2h(x1 * c - x2 * sn);
+      kp[jp + 32] = f2h(x2 * c + x1 * sn);
     } else {
       uint16_t* vp = vc + ((size_t)(head - heads - kvh) * max_len + pos) * 64;
       vp[jp] = f2h(x1);
@@ -237,109 +292,167 @@ __global__ __launch_bounds__(kBlock) void k_qkv(DMat m, const float* __restrict_
 }
 
 // ------------------------------------------------------------------------------------------------------------
-// Split-KV GQA decode attention over the fp16 cache (attn_split + attn_combine, gpu.rs:205-292). Block (g, s)
-// serves the G query heads of KV head g against its share of the ceil(len/64) tiles; K is staged transposed and V
-// row-major in LDS as f32 and read by the G waves. The last block of a KV head to finish (arrival counter)
-// combines the partials of the used blocks in split order, so no second launch is needed.
-__global__ __launch_bounds__(kBlock) void k_attn(const float* __restrict__ q, const uint16_t* __restrict__ kc,
-                                                 const uint16_t* __restrict__ vc, const int* __restrict__ lenp,
-                                                 int len_add, int heads, int kvh, int max_len, float scale,
-                                                 int splits, float* __restrict__ part, int* __restrict__ cnt,
-                                                 float* __restrict__ out) {
-  __shared__ float KT[64][65];
-  __shared__ float Vs[64][64];
-  __shared__ float Qs[kWavesPerBlock][64];
-  __shared__ float Ps[kWavesPerBlock][64];
-  __shared__ int last;
-  int g = blockIdx.x / splits, s = blockIdx.x % splits;
-  int G = heads / kvh;
-  int len = *lenp + len_add;
-  int nb = (len + 63) / 64, per = (nb + splits - 1) / splits, used = (nb + per - 1) / per;
-  if (s >= used) return;
-  int t0 = s * per, t1 = min(t0 + per, nb);
-  int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  bool active = w < G;
-  int h = g * G + w;
-  if (active) Qs[w][lane] = q[h * 64 + lane];
+// Split-KV GQA decode attention over the fp16 cache, two kernels (attn_split + attn_combine, gpu.rs:205-292).
+// k_attn_split: one wave per (KV head g, split s) serves all G query heads of g, so each K/V byte is read once.
+// Lane i holds the K row of position i of a tile in registers (scores: lane = position); V goes straight from HBM
+// to the wave's LDS (p.v: lane = dim), double buffered: the next tile's K and V are requested before the current
+// tile's scores are computed. Partials (m, l, acc[64]) per (head, split).
+// k_attn_combine: one wave per query head merges the used splits in split order, all partials loaded at once.
+
+// A 128-byte row held in named registers (an array copied to LDS in a loop is turned into a memcpy from a stack
+// slot by the compiler).
+struct Row8 {
+  uint4 a, b, c, d, e, f, g, h;
+  __device__ __forceinline__ void load(const uint4* p) {
+    a = p[0]; b = p[1]; c = p[2]; d = p[3]; e = p[4]; f = p[5]; g = p[6]; h = p[7];
+  }
+  // member i for a compile-time i (unrolled loops)
+  __device__ __forceinline__ uint4 at(int i) const {
+    return i == 0 ? a : i == 1 ? b : i == 2 ? c : i == 3 ? d : i == 4 ? e : i == 5 ? f : i == 6 ? g : h;
+  }
+};
+
+// V rows of tile t into an LDS tile: instruction e moves rows 8e..8e+7, lane l carries 16 bytes of row 8e + l/8,
+// so each instruction reads 1 KB of consecutive cache rows and the LDS tile is row-major [64][64] fp16.
+__device__ __forceinline__ void v_tile_to_lds(const uint16_t* V, int t, int lane, uint4 (*dst)[8]) {
+  const uint16_t* src = V + ((size_t)t * 64 + (lane >> 3)) * 64 + (lane & 7) * 8;
+#pragma unroll
+  for (int e = 0; e < 8; e++) __builtin_amdgcn_global_load_lds(src + (size_t)e * 8 * 64, &dst[8 * e][0], 16, 0, 0);
+}
+
+template <int G>
+__global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ q, const uint16_t* __restrict__ kc,
+                                                   const uint16_t* __restrict__ vc, const int* __restrict__ lenp,
+                                                   int len_add, int max_len, float scale, int tps, int splits,
+                                                   float* __restrict__ part) {
+  // workgroup = G waves, wave w serves query head g*G + w; the K rows are read by every wave (L2 after the first),
+  // the V tile is moved into LDS once, each wave carrying a share of its rows
+  __shared__ uint4 Vs[2][64][8];  // fp16 V tiles, row i = position
+  __shared__ float Qs[G][64];
+  __shared__ float Ps[G][64];
+  const int g = blockIdx.x / splits, s = blockIdx.x % splits;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int h = g * G + w;
+  const float NEG_INF = __int_as_float(0xff800000);
   const uint16_t* K = kc + (size_t)g * max_len * 64;
   const uint16_t* V = vc + (size_t)g * max_len * 64;
-  const float NEG_INF = __int_as_float(0xff800000);
-  float m = NEG_INF, l = 0.0f, acc = 0.0f, alpha = 0.0f, mn = NEG_INF;
+  auto v_share = [&](int t, int buf) {
+    const uint16_t* src = V + ((size_t)t * 64 + (lane >> 3)) * 64 + (lane & 7) * 8;
+    for (int e = w; e < 8; e += G)
+      __builtin_amdgcn_global_load_lds(src + (size_t)e * 8 * 64, &Vs[buf][8 * e][0], 16, 0, 0);
+  };
+  // split s covers tiles [s*tps, s*tps + tps); its first tile is requested before the length is known (the grid
+  // only covers tiles inside the cache)
+  const int t0 = s * tps;
+  Row8 kn;
+  kn.load(reinterpret_cast<const uint4*>(K + (size_t)(t0 * 64 + lane) * 64));
+  v_share(t0, 0);
+  Qs[w][lane] = q[h * 64 + lane];
+  const int len = *lenp + len_add;
+  const int nb = (len + 63) / 64;
+  if (t0 >= nb) {
+    __builtin_amdgcn_s_waitcnt(0);  // the tile copy into LDS has finished before the wave ends
+    return;
+  }
+  const int t1 = min(t0 + tps, nb);
+  float m = NEG_INF, l = 0.0f, acc = 0.0f;
   for (int t = t0; t < t1; t++) {
-    __syncthreads();
-    for (int sg = tid; sg < 512; sg += kBlock) {
-      int i = sg >> 3, c0 = (sg & 7) * 8;
-      uint4 kv = *reinterpret_cast<const uint4*>(K + (size_t)(t * 64 + i) * 64 + c0);
-      uint4 vv = *reinterpret_cast<const uint4*>(V + (size_t)(t * 64 + i) * 64 + c0);
-      const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w};
-      const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+    const int nv = min(64, len - t * 64), buf = (t - t0) & 1;
+    const Row8 kr = kn;
+    __syncthreads();  // Qs written; every wave is done with the buffer the prefetch overwrites
+    if (t + 1 < t1) {
+      kn.load(reinterpret_cast<const uint4*>(K + (size_t)((t + 1) * 64 + lane) * 64));
+      v_share(t + 1, buf ^ 1);
+    }
+    // scores: lane = position, chain over the 64 dims in order
+    float dt = 0.0f;
 #pragma unroll
-      for (int e = 0; e < 8; e++) {
-        KT[c0 + e][i] = h2f((uint16_t)(kw[e >> 1] >> (16 * (e & 1))));
-        Vs[i][c0 + e] = h2f((uint16_t)(vw[e >> 1] >> (16 * (e & 1))));
+    for (int e = 0; e < 8; e++) {
+      const uint4 ke = kr.at(e);
+      const uint32_t wv[4] = {ke.x, ke.y, ke.z, ke.w};
+#pragma unroll
+      for (int hh = 0; hh < 2; hh++) {
+        const float4 qv = *reinterpret_cast<const float4*>(&Qs[w][8 * e + 4 * hh]);
+        const float qa[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const uint32_t word = wv[2 * hh + (c >> 1)];
+          dt = __builtin_fmaf(qa[c], h2f((uint16_t)(word >> (16 * (c & 1)))), dt);
+        }
       }
     }
-    __syncthreads();
-    int nv = min(64, len - t * 64);
-    if (active) {
-      float sc = NEG_INF;
-      if (lane < nv) {
-        float dt = 0.0f;
-#pragma unroll 16
-        for (int c = 0; c < 64; c++) dt = __builtin_fmaf(Qs[w][c], KT[c][lane], dt);
-        sc = dt * scale;
+    const float sc = lane < nv ? dt * scale : NEG_INF;
+    const float tmax = group_max<64>(sc);
+    const float mn = m > tmax ? m : tmax;
+    const float alpha = dexp(m - mn);
+    const float p = dexp(sc - mn);
+    const float ts = group_sum<64>(p);
+    l = __builtin_fmaf(l, alpha, ts);
+    Ps[w][lane] = p;
+    m = mn;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's share of the tile's V rows has landed in LDS
+    __syncthreads();                // every share has
+    // p.v: lane = dim, chain over the valid positions in order; LDS reads batched 8 positions at a time
+    const uint16_t* vcol = reinterpret_cast<const uint16_t*>(&Vs[buf][0][0]) + lane;
+    float pv = 0.0f;
+#pragma unroll
+    for (int i0 = 0; i0 < 64; i0 += 8) {
+      if (i0 < nv) {
+        float vf[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) vf[u] = h2f(vcol[(i0 + u) * 64]);
+        const float4 p0 = *reinterpret_cast<const float4*>(&Ps[w][i0]);
+        const float4 p1 = *reinterpret_cast<const float4*>(&Ps[w][i0 + 4]);
+        const float pa[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+          if (i0 + u < nv) pv = __builtin_fmaf(pa[u], vf[u], pv);
       }
-      float tmax = group_max<64>(sc);
-      mn = m > tmax ? m : tmax;
-      alpha = dexp(m - mn);
-      float p = dexp(sc - mn);
-      float ts = group_sum<64>(p);
-      l = __builtin_fmaf(l, alpha, ts);
-      Ps[w][lane] = p;
     }
-    __syncthreads();
-    if (active) {
-      float pv = 0.0f;
-      for (int i = 0; i < nv; i++) pv = __builtin_fmaf(Ps[w][i], Vs[i][lane], pv);
-      acc = __builtin_fmaf(acc, alpha, pv);
-      m = mn;
+    acc = __builtin_fmaf(acc, alpha, pv);
+  }
+  float* pp = part + ((size_t)h * splits + s) * 66;
+  if (lane == 0) {
+    pp[0] = m;
+    pp[1] = l;
+  }
+  pp[2 + lane] = acc;
+}
+
+// One wave per query head: M = max m_s; w_s = exp(m_s - M); den = fma chain of w_s * l_s; num_c = fma chain of
+// w_s * acc_sc, both over s = 0..used-1 in order; out_c = num_c / den. used <= splits <= 64.
+__global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ part, const int* __restrict__ lenp,
+                                                    int len_add, int tps, int splits, float* __restrict__ out) {
+  __shared__ float Cw[2][64];
+  const int h = blockIdx.x, lane = threadIdx.x;
+  const float NEG_INF = __int_as_float(0xff800000);
+  const float* base = part + (size_t)h * splits * 66;
+  // every split's partial is requested before the length (and so the number of used splits) is known
+  float av[64];
+#pragma unroll
+  for (int s2 = 0; s2 < 64; s2++) av[s2] = s2 < splits ? base[(size_t)s2 * 66 + 2 + lane] : 0.0f;
+  float ms = lane < splits ? base[(size_t)lane * 66] : NEG_INF;
+  float ls = lane < splits ? base[(size_t)lane * 66 + 1] : 0.0f;
+  const int len = *lenp + len_add;
+  const int nb = (len + 63) / 64, used = (nb + tps - 1) / tps;
+  if (lane >= used) {
+    ms = NEG_INF;
+    ls = 0.0f;
+  }
+  const float M = group_max<64>(ms);
+  Cw[0][lane] = lane < used ? dexp(ms - M) : 0.0f;
+  Cw[1][lane] = ls;
+  wave_lds_sync();
+  float den = 0.0f, num = 0.0f;
+#pragma unroll
+  for (int s2 = 0; s2 < 64; s2++) {
+    if (s2 < used) {
+      const float ws = Cw[0][s2];
+      den = __builtin_fmaf(ws, Cw[1][s2], den);
+      num = __builtin_fmaf(ws, av[s2], num);
     }
   }
-  if (active) {
-    float* pp = part + ((size_t)h * splits + s) * 66;
-    if (lane == 0) {
-      pp[0] = m;
-      pp[1] = l;
-    }
-    pp[2 + lane] = acc;
-  }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) last = (atomicAdd(&cnt[g], 1) == used - 1);
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  if (active) {
-    const float* base = part + (size_t)h * splits * 66;
-    float M = NEG_INF;
-    for (int s2 = 0; s2 < used; s2++) {
-      float ms = __uint_as_float(__hip_atomic_load(reinterpret_cast<const unsigned*>(base + (size_t)s2 * 66),
-                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-      M = ms > M ? ms : M;
-    }
-    float den = 0.0f, num = 0.0f;
-    for (int s2 = 0; s2 < used; s2++) {
-      const unsigned* pp = reinterpret_cast<const unsigned*>(base + (size_t)s2 * 66);
-      float ms = __uint_as_float(__hip_atomic_load(pp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-      float ls = __uint_as_float(__hip_atomic_load(pp + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-      float as = __uint_as_float(__hip_atomic_load(pp + 2 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-      float wgt = dexp(ms - M);
-      den = __builtin_fmaf(wgt, ls, den);
-      num = __builtin_fmaf(wgt, as, num);
-    }
-    out[h * 64 + lane] = num / den;
-  }
-  if (tid == 0) atomicExch(&cnt[g], 0);
+  out[h * 64 + lane] = num / den;
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -349,10 +462,9 @@ template <int DT, int K, int P>
 __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restrict__ att, float res,
                                                   float* __restrict__ h) {
   using G = Geo<DT, K>;
+  __shared__ float xs[K];
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int sub = lane % G::LPR, rw = lane / G::LPR;
-  XReg<DT, K> xr;
-  load_x<DT, K>(xr, att, sub);
   size_t base = ((size_t)blockIdx.x * kWavesPerBlock + wave) * (P * G::RPW);
   size_t row[P];
   bool ok[P];
@@ -361,103 +473,128 @@ __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restric
     row[p] = base + (size_t)p * G::RPW + rw;
     ok[p] = row[p] < (size_t)m.rows;
   }
+  Rows<DT, K, P> rr;
+  rows_load<DT, K, P>(rr, m, row, ok, sub);
+  float hold[P];
+#pragma unroll
+  for (int p = 0; p < P; p++) hold[p] = (ok[p] && sub == 0) ? h[row[p]] : 0.0f;
+  wg_copy<K, kBlock>(att, xs);
+  XReg<DT, K> xr;
+  load_x<DT, K>(xr, xs, sub);
   float out[P];
-  rows_dot<DT, K, P>(m, row, ok, xr, sub, out);
+  rows_fma<DT, K, P>(rr, ok, xr, sub, out);
 #pragma unroll
   for (int p = 0; p < P; p++)
-    if (ok[p] && sub == 0) h[row[p]] = h[row[p]] + res * out[p];
+    if (ok[p] && sub == 0) h[row[p]] = hold[p] + res * out[p];
 }
 
 // ------------------------------------------------------------------------------------------------------------
-// Top-k of one wave's logits (lane e holds expert e, e < n <= 64): repeated max of (total-order key, lower index
-// first), then w_j = exp(l_j - l_top) / sum with the sum taken left to right (Routing::from_logits,
-// block.rs:81-89; route_topk, route.rs:18-75). ids/weights written by lanes j < k.
-__device__ __forceinline__ void wave_topk(float lv, int n, int k, int lane, int* ids, float* weights) {
-  int key = lane < n ? total_key(lv) : INT_MIN;
-  int my_id = -1;
-  float my_val = 0.0f;
-  for (int j = 0; j < k; j++) {
-    int bk = key, bi = lane;
+// Top-k of n <= 64 logits held in LDS (lg), by rank: lane e counts the logits that precede it in the order
+// (total-order key descending, index ascending) and, if its rank is below k, takes that slot; then
+// w_j = exp(l_j - l_top) / sum with the sum taken left to right (Routing::from_logits, block.rs:81-89; route_topk,
+// route.rs:18-75). `slot` is 3*64 words of LDS. ids/weights written by lanes j < k.
+__device__ __forceinline__ void wave_topk(const float* lg, int n, int k, int lane, float* slot, int* ids,
+                                          float* weights) {
+  const float v = lane < n ? lg[lane] : 0.0f;
+  const int key = total_key(v);
+  int rank = 0;
+  // all 64 slots read as float4 up front (slots >= n hold stale values and are skipped)
+  float4 all[16];
 #pragma unroll
-    for (int s = 1; s < 64; s <<= 1) {
-      int ok_ = __shfl_xor(bk, s), oi = __shfl_xor(bi, s);
-      if (ok_ > bk || (ok_ == bk && oi < bi)) {
-        bk = ok_;
-        bi = oi;
-      }
+  for (int j4 = 0; j4 < 16; j4++) all[j4] = reinterpret_cast<const float4*>(lg)[j4];
+#pragma unroll
+  for (int j4 = 0; j4 < 16; j4++) {
+    const float a4[4] = {all[j4].x, all[j4].y, all[j4].z, all[j4].w};
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+      const int j = 4 * j4 + u;
+      const int kj = total_key(a4[u]);
+      rank += j < n && ((kj > key) || (kj == key && j < lane));
     }
-    float bv = __shfl(lv, bi);
-    if (lane == j) {
-      my_id = bi;
-      my_val = bv;
-    }
-    if (lane == bi) key = INT_MIN;
   }
-  float top = __shfl(my_val, 0);
-  float ex = lane < k ? dexp(my_val - top) : 0.0f;
+  float* sval = slot;
+  int* sid = reinterpret_cast<int*>(slot + 64);
+  float* sex = slot + 128;
+  if (lane < n && rank < k) {
+    sval[rank] = v;
+    sid[rank] = lane;
+  }
+  wave_lds_sync();
+  const float ex = lane < k ? dexp(sval[lane] - sval[0]) : 0.0f;
+  sex[lane] = ex;
+  wave_lds_sync();
   float sum = 0.0f;
-  for (int j = 0; j < k; j++) sum = sum + __shfl(ex, j);
+  for (int j = 0; j < k; j++) sum = sum + sex[j];
   if (lane < k) {
-    ids[lane] = my_id;
+    ids[lane] = sid[lane];
     weights[lane] = ex / sum;
   }
 }
 
-// Router of one layer, one workgroup of 16 waves: rmsnorm of h (written to xn for the experts), logits = Wr xn
-// (+ bias), then top-k and the softmax weights (forward_cpu's router part, block.rs:56-62; gemv + route_topk,
-// cuda_backend.rs:804-835). E <= 64.
-// With NORM false, h is already the block input (HostLayer::forward_cpu takes a normalised x) and is copied to xn.
-template <int DT, int K, bool NORM>
-__global__ __launch_bounds__(1024) void k_router(DMat m, const float* __restrict__ bias,
-                                                 const float* __restrict__ h, const float* __restrict__ lnw,
-                                                 float eps, int k, float* __restrict__ xn, int* __restrict__ ids,
-                                                 float* __restrict__ weights) {
+// ------------------------------------------------------------------------------------------------------------
+// Router and gate/up of the routed experts in one kernel. Every workgroup computes the router itself (its 40-65 KB
+// of weights stay in L2 after the first read): xn = rmsnorm(h) (or h as is), logits = Wr xn (+ bias), top-k and the
+// softmax weights (forward_cpu's router, block.rs:56-62; gemv + route_topk, cuda_backend.rs:804-835); workgroup 0
+// publishes ids/weights for the down kernel. Then its pairs (slot j, row r): act[j, r] = silu(gate_r . xn) *
+// (up_r . xn) for expert ids[j] (gemv_swiglu gpu.rs:46-74, grouped as moe_gate_up hits.rs:67-105; Cpu::experts
+// cpu.rs:116-137). E <= 64, k <= 8.
+constexpr int kRouteWaves = 8;
+
+template <int DT, int K, int NP, bool NORM>
+__global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, const float* __restrict__ bias, DMat gu,
+                                                               const float* __restrict__ h,
+                                                               const float* __restrict__ lnw, float eps, int k,
+                                                               int inter, int* __restrict__ ids_out,
+                                                               float* __restrict__ w_out, float* __restrict__ act) {
   using G = Geo<DT, K>;
-  __shared__ float lg[64];
+  constexpr int NT = kRouteWaves * 64;
+  constexpr int RP = (64 + kRouteWaves * G::RPW - 1) / (kRouteWaves * G::RPW);  // router passes for 64 rows
+  constexpr int P = 2 * NP;
+  __shared__ float xs[K];
+  __shared__ __align__(16) float lg[64];
+  __shared__ float slot[3 * 64];
+  __shared__ int sids[8];
+  __shared__ float sw[8];
+  __shared__ float rs;
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int sub = lane % G::LPR, rw = lane / G::LPR;
+  const int E = router.rows;
   XReg<DT, K> xr;
-  if (NORM) {
-    float r = rms_scale<K>(h, eps, lane);
-    load_xn<DT, K>(xr, h, lnw, r, sub);
-  } else {
-    load_x<DT, K>(xr, h, sub);
-  }
-  if (wave == 0 && rw == 0) {
+  {
+    size_t row[RP];
+    bool ok[RP];
 #pragma unroll
-    for (int jj = 0; jj < G::NJ; jj++) {
-      int j = sub + G::LPR * jj;
-      if (j < G::NCH)
-#pragma unroll
-        for (int e = 0; e < G::CE; e++) xn[j * G::CE + e] = xr.v[jj][e];
+    for (int p = 0; p < RP; p++) {
+      row[p] = (size_t)(p * kRouteWaves + wave) * G::RPW + rw;
+      ok[p] = row[p] < (size_t)E;
     }
-  }
-  int E = m.rows;
-  for (int base = 0; base < E; base += 16 * G::RPW) {
-    size_t row[1] = {(size_t)(base + wave * G::RPW + rw)};
-    bool ok[1] = {row[0] < (size_t)E};
-    float out[1];
-    rows_dot<DT, K, 1>(m, row, ok, xr, sub, out);
-    if (ok[0] && sub == 0) lg[row[0]] = bias ? out[0] + bias[row[0]] : out[0];
+    Rows<DT, K, RP> rr;
+    rows_load<DT, K, RP>(rr, router, row, ok, sub);
+    float bv[RP];
+#pragma unroll
+    for (int p = 0; p < RP; p++) bv[p] = (bias && ok[p]) ? bias[row[p]] : 0.0f;
+    if (NORM)
+      wg_norm<K, NT>(h, lnw, eps, xs, &rs);
+    else
+      wg_copy<K, NT>(h, xs);
+    load_x<DT, K>(xr, xs, sub);
+    float out[RP];
+    rows_fma<DT, K, RP>(rr, ok, xr, sub, out);
+#pragma unroll
+    for (int p = 0; p < RP; p++)
+      if (ok[p] && sub == 0) lg[row[p]] = bias ? out[p] + bv[p] : out[p];
   }
   __syncthreads();
-  if (wave == 0) wave_topk(lane < E ? lg[lane] : 0.0f, E, k, lane, ids, weights);
-}
-
-// ------------------------------------------------------------------------------------------------------------
-// Gate/up rows of the k routed experts with SwiGLU: act[j, r] = silu(gate_r . xn) * (up_r . xn) for expert
-// ids[j] (gemv_swiglu gpu.rs:46-74, grouped as moe_gate_up hits.rs:67-105; Cpu::experts cpu.rs:116-137).
-template <int DT, int K, int NP>
-__global__ __launch_bounds__(kBlock) void k_expert_up(DMat m, const float* __restrict__ xn, const int* __restrict__ ids,
-                                                      int k, int inter, float* __restrict__ act) {
-  using G = Geo<DT, K>;
-  constexpr int P = 2 * NP;
-  int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  int sub = lane % G::LPR, rw = lane / G::LPR;
-  XReg<DT, K> xr;
-  load_x<DT, K>(xr, xn, sub);
-  int npairs = k * inter;
-  int wbase = (blockIdx.x * kWavesPerBlock + wave) * (NP * G::RPW);
+  if (wave == 0) {
+    wave_topk(lg, E, k, lane, slot, sids, sw);
+    if (blockIdx.x == 0 && lane < k) {
+      ids_out[lane] = sids[lane];
+      w_out[lane] = sw[lane];
+    }
+  }
+  __syncthreads();
+  const int npairs = k * inter;
+  const int wbase = (blockIdx.x * kRouteWaves + wave) * (NP * G::RPW);
   size_t row[P];
   bool ok[P];
   int gp[NP];
@@ -466,14 +603,16 @@ __global__ __launch_bounds__(kBlock) void k_expert_up(DMat m, const float* __res
     gp[a] = wbase + a * G::RPW + rw;
     bool v = gp[a] < npairs;
     int j = v ? gp[a] / inter : 0, r = gp[a] % inter;
-    size_t e = (size_t)ids[j];
+    size_t e = (size_t)sids[j];
     row[2 * a] = e * 2 * inter + r;
     row[2 * a + 1] = e * 2 * inter + inter + r;
     ok[2 * a] = v;
     ok[2 * a + 1] = v;
   }
+  Rows<DT, K, P> rr;
+  rows_load<DT, K, P>(rr, gu, row, ok, sub);
   float out[P];
-  rows_dot<DT, K, P>(m, row, ok, xr, sub, out);
+  rows_fma<DT, K, P>(rr, ok, xr, sub, out);
   if (sub != 0) return;
 #pragma unroll
   for (int a = 0; a < NP; a++)
@@ -491,35 +630,41 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __r
   using G = Geo<DT, K>;
   constexpr int KMAX = 8;
   constexpr int KP = (KMAX + G::RPW - 1) / G::RPW;
+  __shared__ float xs[KMAX * K];
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int sub = lane % G::LPR, rw = lane / G::LPR;
   int r = blockIdx.x * kWavesPerBlock + wave;
-  if (r >= hidden) return;
-  XReg<DT, K> xr[KP];
+  bool rok = r < hidden;
   RawChunk c[KP][G::NJ];
 #pragma unroll
   for (int p = 0; p < KP; p++) {
     int j = p * G::RPW + rw;
-    if (j < k) {
+    if (rok && j < k) {
       size_t row = (size_t)ids[j] * hidden + r;
 #pragma unroll
       for (int jj = 0; jj < G::NJ; jj++) {
         int ch = sub + G::LPR * jj;
         if (ch < G::NCH) c[p][jj] = load_chunk<DT>(m, row, ch);
       }
-      load_x<DT, K>(xr[p], act + (size_t)j * K, sub);
     }
   }
+  float hold = (rok && lane == 0 && accumulate) ? h[r] : 0.0f;
+  for (int i = threadIdx.x; i < k * K / 4; i += kBlock)
+    reinterpret_cast<float4*>(xs)[i] = reinterpret_cast<const float4*>(act)[i];
+  __syncthreads();
+  if (!rok) return;
   float dsum[KP];
 #pragma unroll
   for (int p = 0; p < KP; p++) {
     int j = p * G::RPW + rw;
     float acc = 0.0f;
     if (j < k) {
+      XReg<DT, K> xr;
+      load_x<DT, K>(xr, xs + (size_t)j * K, sub);
 #pragma unroll
       for (int jj = 0; jj < G::NJ; jj++) {
         int ch = sub + G::LPR * jj;
-        if (ch < G::NCH) acc = fma_chunk<DT>(c[p][jj], xr[p].v[jj], acc);
+        if (ch < G::NCH) acc = fma_chunk<DT>(c[p][jj], xr.v[jj], acc);
       }
     }
     dsum[p] = group_sum<G::LPR>(acc);
@@ -530,11 +675,11 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __r
 #pragma unroll
     for (int g2 = 0; g2 < G::RPW; g2++) {
       int j = p * G::RPW + g2;
-      float dj = __shfl(dsum[p], g2 * G::LPR);
+      float dj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dsum[p]), g2 * G::LPR));
       if (j < k) y = y + wts[j] * dj;
     }
   }
-  if (lane == 0) h[r] = accumulate ? h[r] + res * y : y;
+  if (lane == 0) h[r] = accumulate ? hold + res * y : y;
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -543,50 +688,72 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __r
 // (final rmsnorm + gemv, gpu_model.rs:414-439; argmax, bin/m1b-gulosa.rs:22-24).
 __device__ __forceinline__ bool later_better(int ak, int ai, int bk, int bi) { return ak > bk || (ak == bk && ai > bi); }
 
-template <int DT, int K, int P>
+template <int S>
+__device__ __forceinline__ void argmax_stage(int& bk, int& bi) {
+  int ok_ = partner<S>(bk), oi = partner<S>(bi);
+  if (later_better(ok_, oi, bk, bi)) {
+    bk = ok_;
+    bi = oi;
+  }
+}
+
+// (key, index) maximum over the wave, the later index winning ties (max_by keeps the last maximum).
+__device__ __forceinline__ void wave_argmax(int& bk, int& bi) {
+  argmax_stage<1>(bk, bi);
+  argmax_stage<2>(bk, bi);
+  argmax_stage<4>(bk, bi);
+  argmax_stage<8>(bk, bi);
+  argmax_stage<16>(bk, bi);
+  argmax_stage<32>(bk, bi);
+}
+
+template <int DT, int K, int P, int NB>
 __global__ __launch_bounds__(kBlock) void k_head(DMat m, const float* __restrict__ h, const float* __restrict__ lnw,
-                                                 float eps, float ls, float* __restrict__ logits, int2* __restrict__ best,
-                                                 int* __restrict__ cnt, int* __restrict__ st, int* __restrict__ seq,
-                                                 int* __restrict__ hist, int max_len) {
+                                                 float eps, float ls, float* __restrict__ logits,
+                                                 int2* __restrict__ best) {
   using G = Geo<DT, K>;
+  __shared__ float xs[K];
+  __shared__ float rs;
   __shared__ int sk[kWavesPerBlock], si[kWavesPerBlock];
-  __shared__ int last;
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int sub = lane % G::LPR, rw = lane / G::LPR;
-  float r = rms_scale<K>(h, eps, lane);
-  XReg<DT, K> xr;
-  load_xn<DT, K>(xr, h, lnw, r, sub);
-  size_t base = ((size_t)blockIdx.x * kWavesPerBlock + wave) * (P * G::RPW);
-  size_t row[P];
-  bool ok[P];
+  // NB batches of P rows per wave; the next batch's loads are issued before the current batch's arithmetic
+  const size_t wbase = ((size_t)blockIdx.x * kWavesPerBlock + wave) * (NB * P * G::RPW);
+  size_t row[NB][P];
+  bool ok[NB][P];
 #pragma unroll
-  for (int p = 0; p < P; p++) {
-    row[p] = base + (size_t)p * G::RPW + rw;
-    ok[p] = row[p] < (size_t)m.rows;
-  }
-  float out[P];
-  rows_dot<DT, K, P>(m, row, ok, xr, sub, out);
+  for (int bt = 0; bt < NB; bt++)
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+      row[bt][p] = wbase + (size_t)(bt * P + p) * G::RPW + rw;
+      ok[bt][p] = row[bt][p] < (size_t)m.rows;
+    }
+  Rows<DT, K, P> cur, nxt;
+  rows_load<DT, K, P>(cur, m, row[0], ok[0], sub);
+  wg_norm<K, kBlock>(h, lnw, eps, xs, &rs);
+  XReg<DT, K> xr;
+  load_x<DT, K>(xr, xs, sub);
   int bk = INT_MIN, bi = -1;
 #pragma unroll
-  for (int p = 0; p < P; p++) {
-    if (ok[p]) {
-      float v = out[p] / ls;
-      if (sub == 0) logits[row[p]] = v;
-      int kk = total_key(v);
-      if (later_better(kk, (int)row[p], bk, bi)) {
-        bk = kk;
-        bi = (int)row[p];
+  for (int bt = 0; bt < NB; bt++) {
+    if (bt + 1 < NB) rows_load<DT, K, P>(nxt, m, row[bt + 1], ok[bt + 1], sub);
+    float out[P];
+    rows_fma<DT, K, P>(cur, ok[bt], xr, sub, out);
+#pragma unroll
+    for (int p = 0; p < P; p++) {
+      if (ok[bt][p]) {
+        float v = out[p] / ls;
+        if (sub == 0) logits[row[bt][p]] = v;
+        int kk = total_key(v);
+        if (later_better(kk, (int)row[bt][p], bk, bi)) {
+          bk = kk;
+          bi = (int)row[bt][p];
+        }
       }
     }
+    if (bt + 1 < NB) cur = nxt;
   }
-#pragma unroll
-  for (int s = 1; s < 64; s <<= 1) {
-    int ok_ = __shfl_xor(bk, s), oi = __shfl_xor(bi, s);
-    if (later_better(ok_, oi, bk, bi)) {
-      bk = ok_;
-      bi = oi;
-    }
-  }
+  wave_argmax(bk, bi);
   if (lane == 0) {
     sk[wave] = bk;
     si[wave] = bi;
@@ -600,31 +767,24 @@ __global__ __launch_bounds__(kBlock) void k_head(DMat m, const float* __restrict
       }
     best[blockIdx.x] = make_int2(bk, bi);
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) last = (atomicAdd(cnt, 1) == (int)gridDim.x - 1);
-  __syncthreads();
-  if (!last) return;
-  __threadfence();
-  bk = INT_MIN;
-  bi = -1;
-  for (int i = threadIdx.x; i < (int)gridDim.x; i += kBlock) {
-    int ck = (int)__hip_atomic_load(reinterpret_cast<const unsigned*>(&best[i].x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    int ci = (int)__hip_atomic_load(reinterpret_cast<const unsigned*>(&best[i].y), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (later_better(ck, ci, bk, bi)) {
-      bk = ck;
-      bi = ci;
+}
+
+// Greedy token from the per-block maxima of k_head (one block); records it, feeds it to the next position unless
+// that position holds a forced prompt token, and advances the position.
+__global__ __launch_bounds__(kBlock) void k_head_argmax(const int2* __restrict__ best, int nblocks,
+                                                        int* __restrict__ st, int* __restrict__ seq,
+                                                        int* __restrict__ hist, int max_len) {
+  __shared__ int sk[kWavesPerBlock], si[kWavesPerBlock];
+  int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int bk = INT_MIN, bi = -1;
+  for (int i = threadIdx.x; i < nblocks; i += kBlock) {
+    int2 c = best[i];
+    if (later_better(c.x, c.y, bk, bi)) {
+      bk = c.x;
+      bi = c.y;
     }
   }
-#pragma unroll
-  for (int s = 1; s < 64; s <<= 1) {
-    int ok_ = __shfl_xor(bk, s), oi = __shfl_xor(bi, s);
-    if (later_better(ok_, oi, bk, bi)) {
-      bk = ok_;
-      bi = oi;
-    }
-  }
-  __syncthreads();
+  wave_argmax(bk, bi);
   if (lane == 0) {
     sk[wave] = bk;
     si[wave] = bi;
@@ -641,7 +801,6 @@ __global__ __launch_bounds__(kBlock) void k_head(DMat m, const float* __restrict
     st[ST_ARGMAX] = bi;
     if (pos + 1 < max_len && pos + 1 >= st[ST_FIXED]) seq[pos + 1] = bi;
     st[ST_POS] = pos + 1;
-    atomicExch(cnt, 0);
   }
 }
 
@@ -684,16 +843,16 @@ __global__ void k_rope(float* __restrict__ x, int heads, int half, const float* 
 
 __global__ void k_topk(const float* __restrict__ logits, const float* __restrict__ bias, int n, int k,
                        int* __restrict__ ids, float* __restrict__ w) {
+  __shared__ __align__(16) float lg[64];
+  __shared__ float slot[3 * 64];
   int lane = threadIdx.x;
-  float v = 0.0f;
-  if (lane < n) v = bias ? logits[lane] + bias[lane] : logits[lane];
-  wave_topk(v, n, k, lane, ids, w);
+  if (lane < n) lg[lane] = bias ? logits[lane] + bias[lane] : logits[lane];
+  wave_lds_sync();
+  wave_topk(lg, n, k, lane, slot, ids, w);
 }
 
-__global__ __launch_bounds__(kBlock) void k_argmax(const float* __restrict__ v, int n, int2* __restrict__ best,
-                                                   int* __restrict__ cnt, int* __restrict__ outp) {
+__global__ __launch_bounds__(kBlock) void k_argmax(const float* __restrict__ v, int n, int2* __restrict__ best) {
   __shared__ int sk[kWavesPerBlock], si[kWavesPerBlock];
-  __shared__ int last;
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int bk = INT_MIN, bi = -1;
   for (int i = blockIdx.x * kBlock + threadIdx.x; i < n; i += gridDim.x * kBlock) {
@@ -703,13 +862,7 @@ __global__ __launch_bounds__(kBlock) void k_argmax(const float* __restrict__ v, 
       bi = i;
     }
   }
-  for (int s = 1; s < 64; s <<= 1) {
-    int ok_ = __shfl_xor(bk, s), oi = __shfl_xor(bi, s);
-    if (later_better(ok_, oi, bk, bi)) {
-      bk = ok_;
-      bi = oi;
-    }
-  }
+  wave_argmax(bk, bi);
   if (lane == 0) {
     sk[wave] = bk;
     si[wave] = bi;
@@ -723,24 +876,19 @@ __global__ __launch_bounds__(kBlock) void k_argmax(const float* __restrict__ v, 
       }
     best[blockIdx.x] = make_int2(bk, bi);
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) last = (atomicAdd(cnt, 1) == (int)gridDim.x - 1);
-  __syncthreads();
-  if (!last || threadIdx.x != 0) return;
-  __threadfence();
-  bk = INT_MIN;
-  bi = -1;
-  for (int i = 0; i < (int)gridDim.x; i++) {
-    int ck = (int)__hip_atomic_load(reinterpret_cast<const unsigned*>(&best[i].x), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    int ci = (int)__hip_atomic_load(reinterpret_cast<const unsigned*>(&best[i].y), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (later_better(ck, ci, bk, bi)) {
-      bk = ck;
-      bi = ci;
+}
+
+__global__ void k_argmax_final(const int2* __restrict__ best, int nblocks, int* __restrict__ outp) {
+  int bk = INT_MIN, bi = -1;
+  for (int i = threadIdx.x; i < nblocks; i += 64) {
+    int2 c = best[i];
+    if (later_better(c.x, c.y, bk, bi)) {
+      bk = c.x;
+      bi = c.y;
     }
   }
-  *outp = bi < 0 ? 0 : bi;
-  atomicExch(cnt, 0);
+  wave_argmax(bk, bi);
+  if (threadIdx.x == 0) *outp = bi < 0 ? 0 : bi;
 }
 
 __global__ void k_exp(const float* __restrict__ x, float* __restrict__ y, int n) {
@@ -779,7 +927,6 @@ static inline int cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 
 constexpr int kGemvP = 4;
 constexpr int kQkvNP = 1;
-constexpr int kUpNP = 1;
 constexpr int kHeadP = 4;
 constexpr int kOprojP = 2;
 
@@ -817,19 +964,36 @@ hipError_t launch_qkv(hipStream_t s, const LayerDev& L, const Dims& d, const Ste
   return hipGetLastError();
 }
 
-hipError_t launch_attn(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b) {
-  k_attn<<<d.kv_heads * d.splits, kBlock, 0, s>>>(b.q, L.k_cache, L.v_cache, b.state + ST_POS, 1, d.heads,
-                                                 d.kv_heads, d.max_len, d.attn_mult, d.splits, b.part,
-                                                 b.attn_cnt, b.att);
+int attn_splits_for(int max_len, int tps) { return ((max_len + 63) / 64 + tps - 1) / tps; }
+
+static hipError_t attn_dispatch(hipStream_t s, int G, int kvh, int tps, const float* q, const uint16_t* kc,
+                                const uint16_t* vc, const int* lenp, int len_add, int max_len, float scale,
+                                float* part, float* out) {
+  const int splits = attn_splits_for(max_len, tps);
+  if (splits > 64 || max_len % 64) return hipErrorInvalidValue;
+  const int blocks = kvh * splits;
+  switch (G) {
+    case 1: k_attn_split<1><<<blocks, 64, 0, s>>>(q, kc, vc, lenp, len_add, max_len, scale, tps, splits, part); break;
+    case 2: k_attn_split<2><<<blocks, 128, 0, s>>>(q, kc, vc, lenp, len_add, max_len, scale, tps, splits, part); break;
+    case 3: k_attn_split<3><<<blocks, 192, 0, s>>>(q, kc, vc, lenp, len_add, max_len, scale, tps, splits, part); break;
+    case 4: k_attn_split<4><<<blocks, 256, 0, s>>>(q, kc, vc, lenp, len_add, max_len, scale, tps, splits, part); break;
+    default: return hipErrorInvalidValue;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  k_attn_combine<<<kvh * G, 64, 0, s>>>(part, lenp, len_add, tps, splits, out);
   return hipGetLastError();
 }
 
+hipError_t launch_attn(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b) {
+  return attn_dispatch(s, d.heads / d.kv_heads, d.kv_heads, d.tps, b.q, L.k_cache, L.v_cache, b.state + ST_POS, 1,
+                       d.max_len, d.attn_mult, b.part, b.att);
+}
+
 hipError_t launch_attn_unit(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vc, int heads,
-                            int kv_heads, int max_len, const int* len_dev, float scale, int splits, float* part,
-                            int* cnt, float* out) {
-  k_attn<<<kv_heads * splits, kBlock, 0, s>>>(q, kc, vc, len_dev, 0, heads, kv_heads, max_len, scale, splits,
-                                              part, cnt, out);
-  return hipGetLastError();
+                            int kv_heads, int max_len, const int* len_dev, float scale, int tps, float* part,
+                            float* out) {
+  return attn_dispatch(s, heads / kv_heads, kv_heads, tps, q, kc, vc, len_dev, 0, max_len, scale, part, out);
 }
 
 hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b) {
@@ -843,32 +1007,25 @@ hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const S
   return hipGetLastError();
 }
 
-hipError_t launch_router(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
-                         bool normalize) {
-#define BODY(KK)                                                                                          \
-  case KK:                                                                                                \
-    if (normalize)                                                                                        \
-      k_router<DTC, KK, true><<<1, 1024, 0, s>>>(L.router, L.router_bias, b.h, L.ln_moe, d.eps, d.top_k,  \
-                                                 b.xn, b.route_ids + layer * d.top_k,                     \
-                                                 b.route_w + layer * d.top_k);                            \
-    else                                                                                                  \
-      k_router<DTC, KK, false><<<1, 1024, 0, s>>>(L.router, L.router_bias, b.h, L.ln_moe, d.eps, d.top_k, \
-                                                  b.xn, b.route_ids + layer * d.top_k,                    \
-                                                  b.route_w + layer * d.top_k);                           \
-    break;
-  MOERT_DISPATCH(L.router.dtype, L.router.cols, BODY)
-#undef BODY
-  return hipGetLastError();
-}
+constexpr int kRouteNP = 2;
 
-hipError_t launch_expert_up(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer) {
-#define BODY(KK)                                                                                         \
-  case KK: {                                                                                             \
-    constexpr int PB = kWavesPerBlock * kUpNP * Geo<DTC, KK>::RPW;                                       \
-    k_expert_up<DTC, KK, kUpNP><<<cdiv((long)d.top_k * d.inter, PB), kBlock, 0, s>>>(                   \
-        L.gate_up, b.xn, b.route_ids + layer * d.top_k, d.top_k, d.inter, b.act);                        \
+hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
+                           bool normalize) {
+  if (L.router.dtype != L.gate_up.dtype || L.router.cols != L.gate_up.cols) return hipErrorInvalidValue;
+#define BODY(KK)                                                                                           \
+  case KK: {                                                                                               \
+    constexpr int PB = kRouteWaves * kRouteNP * Geo<DTC, KK>::RPW;                                         \
+    const int blocks = cdiv((long)d.top_k * d.inter, PB);                                                  \
+    if (normalize)                                                                                         \
+      k_route_up<DTC, KK, kRouteNP, true><<<blocks, kRouteWaves * 64, 0, s>>>(                             \
+          L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter,                      \
+          b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act);                              \
+    else                                                                                                   \
+      k_route_up<DTC, KK, kRouteNP, false><<<blocks, kRouteWaves * 64, 0, s>>>(                            \
+          L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter,                      \
+          b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act);                              \
   } break;
-  MOERT_DISPATCH(L.gate_up.dtype, L.gate_up.cols, BODY)
+  MOERT_DISPATCH(L.router.dtype, L.router.cols, BODY)
 #undef BODY
   return hipGetLastError();
 }
@@ -891,24 +1048,26 @@ hipError_t launch_expert_down(hipStream_t s, const LayerDev& L, const Dims& d, c
   return hipGetLastError();
 }
 
+constexpr int kHeadNB = 4;
+
 int head_blocks(const DMat& head) {
-  int rpw;
   int ce = head.dtype == DT_Q8_0 ? 16 : head.dtype == DT_Q4_0 ? 32 : 4;
-  rpw = kWave / lanes_per_row(head.cols / ce);
-  return cdiv(head.rows, kWavesPerBlock * kHeadP * rpw);
+  int rpw = kWave / lanes_per_row(head.cols / ce);
+  return cdiv(head.rows, kWavesPerBlock * kHeadNB * kHeadP * rpw);
 }
 
 hipError_t launch_head(hipStream_t s, const DMat& head, const float* norm, const Dims& d, const StepBufs& b) {
 #define BODY(KK)                                                                                        \
   case KK: {                                                                                            \
-    constexpr int RB = rows_per_block<DTC, KK, kHeadP>();                                               \
-    k_head<DTC, KK, kHeadP><<<cdiv(head.rows, RB), kBlock, 0, s>>>(head, b.h, norm, d.eps,              \
-                                                                   d.logits_scaling, b.logits, b.best,  \
-                                                                   b.head_cnt, b.state, b.seq,          \
-                                                                   b.argmax_hist, d.max_len);           \
+    constexpr int RB = rows_per_block<DTC, KK, kHeadP>() * kHeadNB;                                     \
+    k_head<DTC, KK, kHeadP, kHeadNB><<<cdiv(head.rows, RB), kBlock, 0, s>>>(head, b.h, norm, d.eps,     \
+                                                                   d.logits_scaling, b.logits, b.best); \
   } break;
   MOERT_DISPATCH(head.dtype, head.cols, BODY)
 #undef BODY
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  k_head_argmax<<<1, kBlock, 0, s>>>(b.best, head_blocks(head), b.state, b.seq, b.argmax_hist, d.max_len);
   return hipGetLastError();
 }
 
@@ -943,7 +1102,11 @@ hipError_t launch_argmax(hipStream_t s, const float* v, int n, int2* best, int* 
   int blocks = cdiv(n, kBlock * 4);
   if (blocks > 1024) blocks = 1024;
   if (blocks < 1) blocks = 1;
-  k_argmax<<<blocks, kBlock, 0, s>>>(v, n, best, cnt, out);
+  (void)cnt;
+  k_argmax<<<blocks, kBlock, 0, s>>>(v, n, best);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  k_argmax_final<<<1, 64, 0, s>>>(best, blocks, out);
   return hipGetLastError();
 }
 

@@ -22,8 +22,8 @@ import numpy as np
 F32, Q8_0, Q4_0 = 0, 1, 2
 DTYPE_NAMES = {F32: "f32", Q8_0: "q8_0", Q4_0: "q4_0"}
 
-K_EMBED, K_QKV, K_ATTN, K_OPROJ, K_ROUTER, K_EXPERT_UP, K_EXPERT_DOWN, K_HEAD = range(8)
-KERNEL_NAMES = ["embed", "qkv", "attn", "oproj", "router", "expert_up", "expert_down", "head"]
+K_EMBED, K_QKV, K_ATTN, K_OPROJ, K_ROUTE_UP, K_EXPERT_DOWN, K_HEAD = range(7)
+KERNEL_NAMES = ["embed", "qkv", "attn", "oproj", "route_up", "expert_down", "head"]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmoert.so")
@@ -455,13 +455,13 @@ def rope(x: np.ndarray, head_dim: int, theta: float, pos: int) -> np.ndarray:
     return y
 
 
-def attn_decode(q, k_cache, v_cache, heads, kv_heads, max_len, length, scale, splits):
+def attn_decode(q, k_cache, v_cache, heads, kv_heads, max_len, length, scale, tiles_per_split):
     q = np.ascontiguousarray(q, np.float32)
     k_cache = np.ascontiguousarray(k_cache, np.uint16)
     v_cache = np.ascontiguousarray(v_cache, np.uint16)
     out = np.empty(heads * 64, np.float32)
     check(lib().moert_attn_decode(ptr(q), ptr(k_cache), ptr(v_cache), heads, kv_heads, 64, max_len, length, scale,
-                                  splits, ptr(out)))
+                                  tiles_per_split, ptr(out)))
     return out
 
 

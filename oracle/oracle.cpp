@@ -297,8 +297,8 @@ const float* h2f_table() {
 }
 
 // Split-KV decode attention (rust/moe-rt/src/gpu.rs:205-292) in the canonical order:
-//   tiles of 64 positions; nb = ceil(len/64) tiles go to `splits` blocks per head, per = ceil(nb/splits) tiles
-//   each, used = ceil(nb/per) blocks non-empty. In a block, per tile:
+//   tiles of 64 positions; split s covers tiles [s*tps, s*tps + tps) of the nb = ceil(len/64) valid ones (tps =
+//   tiles per split, fixed for a cache), used = ceil(nb/tps) splits non-empty. In a split, per tile:
 //     s_i = (fmaf chain over dims 0..d-1 of q*k_i) * scale for valid positions, -inf otherwise;
 //     m' = max(m, max_i s_i); alpha = exp(m - m'); p_i = exp(s_i - m'); ts = pairwise tree of the 64 p_i;
 //     l = fmaf(l, alpha, ts); pv_c = fmaf chain over valid i of p_i * v_ic; acc_c = fmaf(acc_c, alpha, pv_c).
@@ -306,11 +306,11 @@ const float* h2f_table() {
 //   num_c = fmaf(w, acc_sc, num_c); out_c = num_c / den.
 // The loops run across independent positions (scores) or dims (p.v) innermost, each chain in its own order.
 void attention(Pool* pool, const float* q, const uint16_t* k_cache, const uint16_t* v_cache, int heads, int kv_heads,
-               int d, int max_len, int len, float scale, int splits, float* out) {
+               int d, int max_len, int len, float scale, int tps, float* out) {
   const float* H2F = h2f_table();
   int G = heads / kv_heads;
   int nb = (len + kTile - 1) / kTile;
-  int per = (nb + splits - 1) / splits;
+  int per = tps;
   int used = (nb + per - 1) / per;
   auto one_head = [&](size_t hh) {
     int h = (int)hh, g = h / G;
@@ -533,17 +533,14 @@ void orc_moe_block(int hidden, int inter, int n_experts, int k, const moert_tens
   experts(pool, hidden, inter, gate_up, down, x, ids, weights, k, y);
 }
 
-// Split-KV decode attention (rust/moe-rt/src/gpu.rs:205-292) in the canonical order:
-//   tiles of 64 positions; nb = ceil(len/64) tiles go to `splits` blocks per head, per = ceil(nb/splits) tiles
-//   each, used = ceil(nb/per) blocks non-empty. In a block, per tile:
-//     s_i = (fmaf chain over dims 0..d-1 of q*k_i) * scale for valid positions, -inf otherwise;
-//     m' = max(m, max_i s_i); alpha = exp(m - m'); p_i = exp(s_i - m'); ts = pairwise tree of the 64 p_i;
-//     l = fmaf(l, alpha, ts); pv_c = fmaf chain over valid i of p_i * v_ic; acc_c = fmaf(acc_c, alpha, pv_c).
-//   Combine over blocks s = 0..used-1 in order: M = max m_s; w = exp(m_s - M); den = fmaf(w, l_s, den);
-//   num_c = fmaf(w, acc_sc, num_c); out_c = num_c / den.
 void orc_attention(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, int heads, int kv_heads,
-                   int d, int max_len, int len, float scale, int splits, float* out) {
-  attention(nullptr, q, k_cache, v_cache, heads, kv_heads, d, max_len, len, scale, splits, out);
+                   int d, int max_len, int len, float scale, int tiles_per_split, float* out) {
+  attention(nullptr, q, k_cache, v_cache, heads, kv_heads, d, max_len, len, scale, tiles_per_split, out);
+}
+
+int orc_tiles_per_split(int max_len, int attn_splits) {
+  int nbmax = (max_len + kTile - 1) / kTile;
+  return (nbmax + attn_splits - 1) / attn_splits;
 }
 
 // Cpu::experts_step (rust/moe-rt/src/cpu.rs:239-296): positions grouped per expert in first-appearance order,
@@ -628,7 +625,7 @@ struct orc_session {
   moert_config cfg;
   moert_model_weights w;
   std::vector<moert_layer_weights> layers;
-  int max_len, splits, pos;
+  int max_len, tps, pos;
   Pool* pool;
   std::vector<std::vector<uint16_t>> kc, vc;  // per layer [kv_heads, max_len, d]
 };
@@ -642,7 +639,7 @@ int orc_session_create(const moert_config* cfg, const moert_model_weights* w, in
   s->layers.assign(w->layers, w->layers + cfg->layers);
   s->w.layers = s->layers.data();
   s->max_len = max_len;
-  s->splits = attn_splits;
+  s->tps = orc_tiles_per_split(max_len, attn_splits);
   s->pos = 0;
   s->pool = new Pool(threads);
   size_t kv = (size_t)cfg->kv_heads * max_len * cfg->head_dim;
@@ -715,7 +712,7 @@ int orc_session_step(orc_session* s, int token, float* logits, int* route_ids, f
         s->vc[l][dst] = f2h(vv[g * d + i]);
       }
     attention(s->pool, q.data(), s->kc[l].data(), s->vc[l].data(), c.heads, c.kv_heads, d, s->max_len, s->pos + 1,
-              c.attention_multiplier, s->splits, att.data());
+              c.attention_multiplier, s->tps, att.data());
     gemv(pool, L.o.data, L.o.dtype, H, qd, att.data(), o.data());
     for (int i = 0; i < H; i++) x[i] = x[i] + c.residual_multiplier * o[i];
     orc_rmsnorm(x.data(), L.ln_moe, H, c.eps, xn.data());

@@ -52,9 +52,11 @@ void orc_moe_block(int hidden, int inter, int experts, int k, const moert_tensor
                    const moert_tensor* gate_up, const moert_tensor* down, const float* x, float* y, int* ids,
                    float* weights, int threads);
 
-/* Split-KV decode attention, canonical order (see oracle.cpp). */
+/* Split-KV decode attention, canonical order (see oracle.cpp): splits of tiles_per_split 64-position tiles. */
 void orc_attention(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, int heads, int kv_heads,
-                   int head_dim, int max_len, int len, float scale, int splits, float* out);
+                   int head_dim, int max_len, int len, float scale, int tiles_per_split, float* out);
+/* Tiles per split of a cache of max_len positions cut into at most attn_splits splits. */
+int orc_tiles_per_split(int max_len, int attn_splits);
 
 /* Cpu::experts_step: m positions, per-position top-k routing; y written for every position. */
 void orc_experts_step(int hidden, int inter, int m, int k, const moert_tensor* gate_up, const moert_tensor* down,

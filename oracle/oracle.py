@@ -44,6 +44,7 @@ def lib() -> ctypes.CDLL:
             "orc_argmax": (i, [vp, i]),
             "orc_moe_block": (None, [i, i, i, i, vp, vp, vp, vp, vp, vp, vp, vp, i]),
             "orc_attention": (None, [vp, vp, vp, i, i, i, i, i, f, i, vp]),
+            "orc_tiles_per_split": (i, [i, i]),
             "orc_experts_step": (None, [i, i, i, i, vp, vp, vp, vp, vp, vp, i]),
             "orc_session_create": (i, [vp, vp, i, i, i, ctypes.POINTER(vp)]),
             "orc_session_destroy": (None, [vp]),
@@ -166,13 +167,17 @@ def moe_block(hidden, inter, experts, k, router, gate_up, down, dtype, x, bias=N
     return y, ids, w
 
 
-def attention(q, k_cache, v_cache, heads, kv_heads, max_len, length, scale, splits):
+def attention(q, k_cache, v_cache, heads, kv_heads, max_len, length, scale, tiles_per_split):
     q = _f32(q)
     kc = np.ascontiguousarray(k_cache, np.uint16)
     vc = np.ascontiguousarray(v_cache, np.uint16)
     out = np.empty(heads * 64, np.float32)
-    lib().orc_attention(_p(q), _p(kc), _p(vc), heads, kv_heads, 64, max_len, length, scale, splits, _p(out))
+    lib().orc_attention(_p(q), _p(kc), _p(vc), heads, kv_heads, 64, max_len, length, scale, tiles_per_split, _p(out))
     return out
+
+
+def tiles_per_split(max_len, attn_splits):
+    return int(lib().orc_tiles_per_split(max_len, attn_splits))
 
 
 def experts_step(hidden, inter, m, k, gate_up, down, dtype, x, ids, weights, threads=4):

@@ -100,10 +100,12 @@ def test_argmax_is_greedy_with_the_last_index_on_ties(gpu):
 
 
 def test_split_kv_attention_is_bit_identical_at_every_slice_and_block_boundary(gpu):
-    """tests/model.rs:183-250 cases (ns=8 over 32 tiles, ns=64 over 128 tiles, amplified scores), G=2 and G=3."""
+    """tests/model.rs:183-250 cases (splits of 4 tiles over 32, of 2 over 68, of 1 over 16; amplified scores),
+    G=2 and G=3."""
     b = 64
-    configs = [(4, 2, 8, 32 * b, [1, 2, b - 1, b, b + 1, 8 * b, 8 * b + 1, 9 * b - 1, 3 * b + 7, 17 * b + 5, 32 * b - 1, 32 * b]),
-               (24, 8, 64, 68 * b, [1, b + 1, 64 * b, 64 * b + 1, 67 * b + 9, 68 * b])]
+    configs = [(4, 2, 4, 32 * b, [1, 2, b - 1, b, b + 1, 8 * b, 8 * b + 1, 9 * b - 1, 3 * b + 7, 17 * b + 5, 32 * b - 1, 32 * b]),
+               (24, 8, 2, 68 * b, [1, b + 1, 64 * b, 64 * b + 1, 67 * b + 9, 68 * b]),
+               (4, 1, 1, 16 * b, [1, b, b + 1, 16 * b])]
     for heads, kvh, ns, max_len, lens in configs:
         for amp in (False, True):
             q = moert.synth_normal(71, ns, heads * 64)
@@ -115,7 +117,7 @@ def test_split_kv_attention_is_bit_identical_at_every_slice_and_block_boundary(g
                 kf[:, mid:mid + b] *= np.float32(4.0)
             kc, vc = oracle.f2h(kf.reshape(-1)), oracle.f2h(vf)
             for length in lens:
-                say(f"attn heads={heads} kv={kvh} ns={ns} len={length} amp={amp}")
+                say(f"attn heads={heads} kv={kvh} tiles/split={ns} len={length} amp={amp}")
                 got = moert.attn_decode(q, kc, vc, heads, kvh, max_len, length, 0.125, ns)
                 want = oracle.attention(q, kc, vc, heads, kvh, max_len, length, 0.125, ns)
                 assert bits_equal(got, want), (heads, ns, length, amp)

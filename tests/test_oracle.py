@@ -265,11 +265,14 @@ def _attn_f64(q, kc, vc, heads, kvh, max_len, length, scale):
 
 
 def test_split_kv_attention_matches_float64_at_every_slice_and_block_boundary():
-    """tests/model.rs:183-250: lengths at tile and split boundaries, ns=8 over 32 tiles and ns=64 over 128 tiles,
-    with amplified scores (q x4, a middle tile x4); positions past len hold finite garbage that must stay masked."""
+    """tests/model.rs:183-250: lengths at tile and split boundaries (splits of 4 tiles over a 32-tile cache, of 2
+    tiles over 128, of 1 and 3 tiles), with amplified scores (q x4, a middle tile x4); positions past len hold finite
+    garbage that must stay masked."""
     heads, kvh, b, scale = 4, 2, 64, 0.125
-    configs = [(8, 32 * b, [1, 2, b - 1, b, b + 1, 8 * b, 8 * b + 1, 9 * b - 1, 3 * b + 7, 17 * b + 5, 32 * b - 1, 32 * b]),
-               (64, 128 * b, [1, b + 1, 64 * b, 64 * b + 1, 67 * b + 9, 128 * b])]
+    configs = [(4, 32 * b, [1, 2, b - 1, b, b + 1, 8 * b, 8 * b + 1, 9 * b - 1, 3 * b + 7, 17 * b + 5, 32 * b - 1, 32 * b]),
+               (2, 128 * b, [1, b + 1, 64 * b, 64 * b + 1, 67 * b + 9, 128 * b]),
+               (1, 16 * b, [1, b, b + 1, 16 * b]),
+               (3, 24 * b, [1, 3 * b, 3 * b + 1, 10 * b + 7, 24 * b])]
     for ns, max_len, lens in configs:
         for amp in (False, True):
             q = moert.synth_normal(31, ns, heads * 64)
