@@ -26,9 +26,10 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def kernel_bytes(kind, cfg, ctx, wd, ed):
+def kernel_bytes(kind, cfg, ctx, wd, ed, nsplit):
     """Algorithmic HBM bytes of one launch of a kernel class at `ctx` cached positions: the weights it must stream
-    (only the k routed experts for the expert kernels) and the KV it must read; activations are < 0.1% and left out."""
+    (only the k routed experts for the expert kernels), the KV it must read and the split partials the attention
+    kernels exchange; other activations are < 0.1% of a layer's bytes and left out."""
     import moert
     H, d, I = cfg.hidden, cfg.head_dim, cfg.inter
     qd, kvd = cfg.heads * d, cfg.kv_heads * d
@@ -36,12 +37,27 @@ def kernel_bytes(kind, cfg, ctx, wd, ed):
     return {
         moert.K_EMBED: b(ed, H),
         moert.K_QKV: b(wd, (qd + 2 * kvd) * H),
-        moert.K_ATTN: 2 * kvd * 2 * ctx,
+        moert.K_ATTN_SPLIT: 2 * kvd * 2 * ctx,
+        moert.K_ATTN_COMBINE: cfg.heads * nsplit * 66 * 4,
         moert.K_OPROJ: b(wd, H * qd),
         moert.K_ROUTE_UP: b(wd, cfg.experts * H) + cfg.top_k * b(wd, 2 * I * H),
         moert.K_EXPERT_DOWN: cfg.top_k * b(wd, H * I),
         moert.K_HEAD: b(ed, cfg.vocab * H),
+        moert.K_HEAD_ARGMAX: 0,
     }[kind]
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `k_<kernel>` from the committed FETCH_SIZE/WRITE_SIZE summary (calibrated against a
+    copy of known size); None when the summary has no row for it."""
+    path = os.path.join(ROOT, "profiles", "decode3b_hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) >= 5 and cells[0] == f"k_{kernel}":
+            return int(cells[4])
+    return None
 
 
 def main():
@@ -94,20 +110,26 @@ def main():
     log(f"{args.steps} steps in {wall * 1e3:.1f} ms wall ({ms_event:.3f} ms/step by events): {tok_s:.1f} tok/s")
 
     kernels = {}
+    nsplit = moert.attn_splits_for(max_len, moert.tiles_per_split(max_len, 64))
     for kind in range(len(moert.KERNEL_NAMES)):
         g.set_position(pos0)
         us, launches = g.time_kernel(kind, args.kernel_iters)
         per_step = launches // args.kernel_iters
-        nbytes = kernel_bytes(kind, cfg, pos0 + args.kernel_iters // 2, wd, ed)
+        nbytes = kernel_bytes(kind, cfg, pos0 + args.kernel_iters // 2, wd, ed, nsplit)
         kernels[moert.KERNEL_NAMES[kind]] = {
             "us": round(us, 3), "launches_per_step": per_step, "bytes": nbytes,
-            "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "us_per_step": round(us * per_step, 2)}
+            "gbs": round(nbytes / (us * 1e-6) / 1e9, 1) if nbytes else None, "us_per_step": round(us * per_step, 2)}
     dom = max(kernels, key=lambda k: kernels[k]["us_per_step"])
     dk = kernels[dom]
-    log("kernels: " + ", ".join(f"{k} {v['us']:.2f}us x{v['launches_per_step']} {v['gbs']:.0f}GB/s"
+    log("kernels: " + ", ".join(f"{k} {v['us']:.2f}us x{v['launches_per_step']} {v['gbs'] or 0:.0f}GB/s"
                                 for k, v in kernels.items()))
     moe = {k: kernels[k] for k in ("route_up", "expert_down")}
     g.close()
+    copy_bytes = 1 << 30
+    copy_us = moert.copy_probe(copy_bytes, 10)
+    hbm_copy = {"bytes_moved": 2 * copy_bytes, "us": round(copy_us, 2),
+                "gbs": round(2 * copy_bytes / (copy_us * 1e-6) / 1e9, 1)}
+    log(f"device copy of {copy_bytes >> 20} MiB: {copy_us:.1f} us, {hbm_copy['gbs']:.0f} GB/s read+write")
 
     cpu = None
     if args.cpu_steps > 0:
@@ -139,11 +161,14 @@ def main():
                                f"pre-filled to {CTX}", "layers": cfg.layers, "hidden": cfg.hidden,
                    "experts": cfg.experts, "top_k": cfg.top_k, "context_mean": ctx_mean, "parallelism": "none"},
         "roofline": {"bound": "hbm", "kernel": dom, "achieved": dk["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(dk["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
+                     "algorithmic_bytes": dk["bytes"], "us": dk["us"],
+                     "traffic_source": "profiles/decode3b_hbm_traffic.md (FETCH_SIZE x2 + WRITE_SIZE, k_copy-calibrated)"},
         "step_roofline": {"bytes": step_bytes, "achieved": round(step_bytes / (wall / args.steps) / 1e9, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
                           "frac": round(step_bytes / (wall / args.steps) / 1e9 / HBM_PEAK_GBS, 4)},
         "moe_gemv": moe,
+        "hbm_copy": hbm_copy,
         "kernels": kernels,
         "cpu_baseline": cpu,
         "device": name,

@@ -130,18 +130,21 @@ int moert_read_hidden(moert_model* m, float* h);
  * ms_per_step receives the mean. The position advances by warmup + iters. */
 int moert_time_steps(moert_model* m, int warmup, int iters, double* ms_per_step);
 
-/* Per-kernel timing: replays the step `iters` times as individual launches with a HIP event pair around every
- * launch of kernel class `kind` (see moert_kernel_kind) and returns the mean duration of one launch in
- * microseconds and the number of launches timed. Position advances by iters. */
+/* Per-kernel timing: replays the step `iters` times as individual launches; every launch of kernel class `kind`
+ * (see moert_kernel_kind) is made with start/stop events taken from its own dispatch (hipExtLaunchKernelGGL), and
+ * the mean duration of one launch in microseconds and the number of launches timed are returned. The position
+ * advances by iters. */
 typedef enum {
-  MOERT_K_EMBED = 0,       /* embedding row */
-  MOERT_K_QKV = 1,         /* rmsnorm + q/k/v + RoPE + KV write */
-  MOERT_K_ATTN = 2,        /* split-KV attention + combine */
-  MOERT_K_OPROJ = 3,       /* output projection + residual */
-  MOERT_K_ROUTE_UP = 4,    /* rmsnorm + router + top-k + gate/up + SwiGLU of the routed experts */
-  MOERT_K_EXPERT_DOWN = 5, /* down of the routed experts + weighted combine + residual */
-  MOERT_K_HEAD = 6,        /* final rmsnorm + LM head + greedy argmax */
-  MOERT_K_COUNT = 7
+  MOERT_K_EMBED = 0,        /* embedding row */
+  MOERT_K_QKV = 1,          /* rmsnorm + q/k/v + RoPE + KV write */
+  MOERT_K_ATTN_SPLIT = 2,   /* split-KV attention partials */
+  MOERT_K_ATTN_COMBINE = 3, /* combine of the split partials */
+  MOERT_K_OPROJ = 4,        /* output projection + residual */
+  MOERT_K_ROUTE_UP = 5,     /* rmsnorm + router + top-k + gate/up + SwiGLU of the routed experts */
+  MOERT_K_EXPERT_DOWN = 6,  /* down of the routed experts + weighted combine + residual */
+  MOERT_K_HEAD = 7,         /* final rmsnorm + LM head + per-block argmax */
+  MOERT_K_HEAD_ARGMAX = 8,  /* argmax over the head blocks, token and position update */
+  MOERT_K_COUNT = 9
 } moert_kernel_kind;
 int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch, int* launches);
 
@@ -187,6 +190,11 @@ int moert_rope(float* x, int heads, int head_dim, float theta, int pos);
  * (attn_split + attn_combine, rust/moe-rt/src/gpu.rs:205-292; CpuSession attention model.rs:200-222). */
 int moert_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, int heads, int kv_heads,
                       int head_dim, int max_len, int len, float scale, int tiles_per_split, float* out);
+
+/* Achievable HBM bandwidth reference: mean microseconds of one device-to-device streaming copy of `bytes`
+ * (multiple of 16) over `iters` launches, each timed by its own dispatch events. No reference counterpart (the
+ * reference measures PCIe and HBM rates with separate CUDA tools); used to calibrate the roofline. */
+int moert_copy_probe(size_t bytes, int iters, double* us_per_copy);
 
 /* Canonical exponential used by every kernel (softmax, SiLU, top-k weights), evaluated on the device. */
 int moert_exp_device(const float* x, float* y, int n);

@@ -170,42 +170,37 @@ struct moert_model {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
 
-  // Launches one decode step. With `timed` >= 0, records an event pair around every launch of that kernel class.
+  // Launches one decode step. With `timed` >= 0, every launch of that kernel class records its dispatch start and
+  // end into the next event pair of `ev`.
   int enqueue(int timed, std::vector<hipEvent_t>* ev) {
-    auto t0 = [&](int kind) {
-      if (kind == timed) (void)hipEventRecord((*ev)[ev_i], stream);
-    };
-    auto t1 = [&](int kind) {
+    ev_i = 0;
+    auto arm = [&](int kind) {
       if (kind == timed) {
-        (void)hipEventRecord((*ev)[ev_i + 1], stream);
+        arm_launch_events((*ev)[ev_i], (*ev)[ev_i + 1]);
         ev_i += 2;
       }
     };
-    ev_i = 0;
-    t0(MOERT_K_EMBED);
+    arm(MOERT_K_EMBED);
     CHECK_HIP(launch_embed(stream, embed, dims, b));
-    t1(MOERT_K_EMBED);
     for (size_t l = 0; l < layers.size(); l++) {
       const LayerDev& L = layers[l];
-      t0(MOERT_K_QKV);
+      arm(MOERT_K_QKV);
       CHECK_HIP(launch_qkv(stream, L, dims, b));
-      t1(MOERT_K_QKV);
-      t0(MOERT_K_ATTN);
-      CHECK_HIP(launch_attn(stream, L, dims, b));
-      t1(MOERT_K_ATTN);
-      t0(MOERT_K_OPROJ);
+      arm(MOERT_K_ATTN_SPLIT);
+      CHECK_HIP(launch_attn_split(stream, L, dims, b));
+      arm(MOERT_K_ATTN_COMBINE);
+      CHECK_HIP(launch_attn_combine(stream, dims, b));
+      arm(MOERT_K_OPROJ);
       CHECK_HIP(launch_oproj(stream, L, dims, b));
-      t1(MOERT_K_OPROJ);
-      t0(MOERT_K_ROUTE_UP);
+      arm(MOERT_K_ROUTE_UP);
       CHECK_HIP(launch_route_up(stream, L, dims, b, (int)l, true));
-      t1(MOERT_K_ROUTE_UP);
-      t0(MOERT_K_EXPERT_DOWN);
+      arm(MOERT_K_EXPERT_DOWN);
       CHECK_HIP(launch_expert_down(stream, L, dims, b, (int)l, true));
-      t1(MOERT_K_EXPERT_DOWN);
     }
-    t0(MOERT_K_HEAD);
+    arm(MOERT_K_HEAD);
     CHECK_HIP(launch_head(stream, embed, norm, dims, b));
-    t1(MOERT_K_HEAD);
+    arm(MOERT_K_HEAD_ARGMAX);
+    CHECK_HIP(launch_head_argmax(stream, embed, dims, b));
     return MOERT_OK;
   }
   int ev_i = 0;
@@ -649,7 +644,7 @@ int moert_time_steps(moert_model* m, int warmup, int iters, double* ms_per_step)
 }
 
 static int time_kernel_impl(moert_model* m, int kind, int iters, double* us, int* launches) {
-  int per_step = (kind == MOERT_K_EMBED || kind == MOERT_K_HEAD) ? 1 : m->cfg.layers;
+  int per_step = (kind == MOERT_K_EMBED || kind == MOERT_K_HEAD || kind == MOERT_K_HEAD_ARGMAX) ? 1 : m->cfg.layers;
   std::vector<hipEvent_t> ev(2 * per_step);
   for (auto& e : ev) CHECK_HIP(hipEventCreate(&e));
   double total = 0.0;
@@ -891,6 +886,41 @@ int moert_exp_device(const float* x, float* y, int n) {
   TRY(sc.dev(&dy, n));
   CHECK_HIP(launch_exp(sc.s, dx, dy, n));
   TRY(sc.get(y, dy, (size_t)n * 4));
+  return MOERT_OK;
+}
+
+int moert_copy_probe(size_t bytes, int iters, double* us_per_copy) {
+  CHECK_CFG(bytes >= 16 && bytes % 16 == 0 && iters >= 1 && us_per_copy, "copy_probe: bytes %zu, iters %d", bytes,
+            iters);
+  Scoped sc;
+  TRY(sc.init());
+  uint8_t *src, *dst;
+  TRY(sc.dev(&src, bytes));
+  TRY(sc.dev(&dst, bytes));
+  CHECK_HIP(launch_copy(sc.s, src, dst, bytes));  // warm-up
+  std::vector<hipEvent_t> ev(2 * iters);
+  for (auto& e : ev) CHECK_HIP(hipEventCreate(&e));
+  int rc = MOERT_OK;
+  for (int i = 0; i < iters && rc == MOERT_OK; i++) {
+    arm_launch_events(ev[2 * i], ev[2 * i + 1]);
+    if (launch_copy(sc.s, src, dst, bytes) != hipSuccess) rc = MOERT_E_DEVICE;
+  }
+  double total = 0.0;
+  if (rc == MOERT_OK && hipStreamSynchronize(sc.s) == hipSuccess) {
+    for (int i = 0; i < iters; i++) {
+      float t = 0.0f;
+      if (hipEventElapsedTime(&t, ev[2 * i], ev[2 * i + 1]) != hipSuccess) rc = MOERT_E_DEVICE;
+      total += t;
+    }
+  } else {
+    rc = MOERT_E_DEVICE;
+  }
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  if (rc) {
+    set_err("copy_probe: device error");
+    return rc;
+  }
+  *us_per_copy = total * 1000.0 / iters;
   return MOERT_OK;
 }
 

@@ -48,7 +48,8 @@ struct StepBufs {
 
 hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const StepBufs& b);
 hipError_t launch_qkv(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
-hipError_t launch_attn(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
+hipError_t launch_attn_split(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
+hipError_t launch_attn_combine(hipStream_t s, const Dims& d, const StepBufs& b);
 hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
 // Router + gate/up of the routed experts (the router recomputed by every workgroup, workgroup 0 publishes it).
 // normalize: rmsnorm h with ln_moe first (decode step); otherwise h is the block input as is.
@@ -58,7 +59,11 @@ hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, cons
 hipError_t launch_expert_down(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
                               bool accumulate);
 hipError_t launch_head(hipStream_t s, const DMat& head, const float* norm, const Dims& d, const StepBufs& b);
+hipError_t launch_head_argmax(hipStream_t s, const DMat& head, const Dims& d, const StepBufs& b);
 int head_blocks(const DMat& head);
+
+// The next kernel launched on this thread records its dispatch start/end into these events (hipExtLaunchKernelGGL).
+void arm_launch_events(hipEvent_t start, hipEvent_t stop);
 
 // Unit kernels.
 hipError_t launch_gemv(hipStream_t s, const DMat& w, const float* x, float* y);
@@ -68,6 +73,7 @@ hipError_t launch_rope(hipStream_t s, float* x, int heads, int head_dim, const f
 hipError_t launch_topk(hipStream_t s, const float* logits, const float* bias, int n, int k, int* ids, float* w);
 hipError_t launch_argmax(hipStream_t s, const float* v, int n, int2* best, int* cnt, int* out);
 hipError_t launch_exp(hipStream_t s, const float* x, float* y, int n);
+hipError_t launch_copy(hipStream_t s, const void* src, void* dst, size_t bytes);
 hipError_t launch_attn_unit(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vc, int heads,
                             int kv_heads, int max_len, const int* len_dev, float scale, int tps, float* part,
                             float* out);

@@ -1,11 +1,35 @@
 // Decode-step kernels for gfx950 (wave64). The evaluation order of every reduction is the one stated in
 // dev_math.h; the reference kernels these replace are cited on each kernel (paths relative to the reference
 // root, rust/moe-rt/src).
+#include <hip/hip_ext.h>
+
+#include <algorithm>
 #include <climits>
 
 #include "kernels.h"
 
 namespace moert {
+
+// Launch of one kernel. When an event pair has been armed on this thread (arm_launch_events), the next launch is
+// made with hipExtLaunchKernelGGL, whose start/stop events take the dispatch's own timestamps, so that the
+// measured time is the kernel's execution and not the host's enqueue of separate event markers.
+namespace {
+thread_local hipEvent_t t_armed[2] = {nullptr, nullptr};
+}
+void arm_launch_events(hipEvent_t start, hipEvent_t stop) {
+  t_armed[0] = start;
+  t_armed[1] = stop;
+}
+template <typename F, typename... Args>
+static inline void klaunch(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args... args) {
+  if (t_armed[0]) {
+    hipEvent_t a = t_armed[0], z = t_armed[1];
+    t_armed[0] = t_armed[1] = nullptr;
+    hipExtLaunchKernelGGL(kernel, grid, block, shm, s, a, z, 0u, args...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, shm, s, args...);
+  }
+}
 
 constexpr int kBlock = 256;  // 4 waves per workgroup
 constexpr int kWavesPerBlock = kBlock / kWave;
@@ -934,7 +958,7 @@ hipError_t launch_gemv(hipStream_t s, const DMat& w, const float* x, float* y) {
 #define BODY(KK)                                                                                    \
   case KK: {                                                                                        \
     constexpr int RB = rows_per_block<DTC, KK, kGemvP>();                                           \
-    k_gemv<DTC, KK, kGemvP><<<cdiv(w.rows, RB), kBlock, 0, s>>>(w, x, y);                           \
+    klaunch(k_gemv<DTC, KK, kGemvP>, cdiv(w.rows, RB), kBlock, 0, s, w, x, y);                           \
   } break;
   MOERT_DISPATCH(w.dtype, w.cols, BODY)
 #undef BODY
@@ -943,9 +967,9 @@ hipError_t launch_gemv(hipStream_t s, const DMat& w, const float* x, float* y) {
 
 hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const StepBufs& b) {
   switch (emb.dtype) {
-    case DT_Q8_0: k_embed<DT_Q8_0><<<1, kBlock, 0, s>>>(emb, b.seq, b.state, d.emb_mult, b.h); break;
-    case DT_Q4_0: k_embed<DT_Q4_0><<<1, kBlock, 0, s>>>(emb, b.seq, b.state, d.emb_mult, b.h); break;
-    case DT_F32: k_embed<DT_F32><<<1, kBlock, 0, s>>>(emb, b.seq, b.state, d.emb_mult, b.h); break;
+    case DT_Q8_0: klaunch(k_embed<DT_Q8_0>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h); break;
+    case DT_Q4_0: klaunch(k_embed<DT_Q4_0>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h); break;
+    case DT_F32: klaunch(k_embed<DT_F32>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -955,7 +979,7 @@ hipError_t launch_qkv(hipStream_t s, const LayerDev& L, const Dims& d, const Ste
 #define BODY(KK)                                                                                            \
   case KK: {                                                                                                \
     constexpr int PB = kWavesPerBlock * kQkvNP * Geo<DTC, KK>::RPW; /* pairs per block */                   \
-    k_qkv<DTC, KK, kQkvNP><<<cdiv(L.qkv.rows / 2, PB), kBlock, 0, s>>>(                                     \
+    klaunch(k_qkv<DTC, KK, kQkvNP>, cdiv(L.qkv.rows / 2, PB), kBlock, 0, s,                                      \
         L.qkv, b.h, L.ln_attn, d.eps, b.state, b.rope, d.heads, d.kv_heads, d.max_len, b.q, L.k_cache,      \
         L.v_cache);                                                                                         \
   } break;
@@ -966,41 +990,52 @@ hipError_t launch_qkv(hipStream_t s, const LayerDev& L, const Dims& d, const Ste
 
 int attn_splits_for(int max_len, int tps) { return ((max_len + 63) / 64 + tps - 1) / tps; }
 
-static hipError_t attn_dispatch(hipStream_t s, int G, int kvh, int tps, const float* q, const uint16_t* kc,
-                                const uint16_t* vc, const int* lenp, int len_add, int max_len, float scale,
-                                float* part, float* out) {
+static hipError_t attn_split_dispatch(hipStream_t s, int G, int kvh, int tps, const float* q, const uint16_t* kc,
+                                      const uint16_t* vc, const int* lenp, int len_add, int max_len, float scale,
+                                      float* part) {
   const int splits = attn_splits_for(max_len, tps);
   if (splits > 64 || max_len % 64) return hipErrorInvalidValue;
   const int blocks = kvh * splits;
   switch (G) {
-    case 1: k_attn_split<1><<<blocks, 64, 0, s>>>(q, kc, vc, lenp, len_add, max_len, scale, tps, splits, part); break;
-    case 2: k_attn_split<2><<<blocks, 128, 0, s>>>(q, kc, vc, lenp, len_add, max_len, scale, tps, splits, part); break;
-    case 3: k_attn_split<3><<<blocks, 192, 0, s>>>(q, kc, vc, lenp, len_add, max_len, scale, tps, splits, part); break;
-    case 4: k_attn_split<4><<<blocks, 256, 0, s>>>(q, kc, vc, lenp, len_add, max_len, scale, tps, splits, part); break;
+    case 1: klaunch(k_attn_split<1>, blocks, 64, 0, s, q, kc, vc, lenp, len_add, max_len, scale, tps, splits, part); break;
+    case 2: klaunch(k_attn_split<2>, blocks, 128, 0, s, q, kc, vc, lenp, len_add, max_len, scale, tps, splits, part); break;
+    case 3: klaunch(k_attn_split<3>, blocks, 192, 0, s, q, kc, vc, lenp, len_add, max_len, scale, tps, splits, part); break;
+    case 4: klaunch(k_attn_split<4>, blocks, 256, 0, s, q, kc, vc, lenp, len_add, max_len, scale, tps, splits, part); break;
     default: return hipErrorInvalidValue;
   }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  k_attn_combine<<<kvh * G, 64, 0, s>>>(part, lenp, len_add, tps, splits, out);
   return hipGetLastError();
 }
 
-hipError_t launch_attn(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b) {
-  return attn_dispatch(s, d.heads / d.kv_heads, d.kv_heads, d.tps, b.q, L.k_cache, L.v_cache, b.state + ST_POS, 1,
-                       d.max_len, d.attn_mult, b.part, b.att);
+static hipError_t attn_combine_dispatch(hipStream_t s, int heads, int tps, int max_len, const int* lenp, int len_add,
+                                        const float* part, float* out) {
+  const int splits = attn_splits_for(max_len, tps);
+  if (splits > 64 || max_len % 64) return hipErrorInvalidValue;
+  klaunch(k_attn_combine, heads, 64, 0, s, part, lenp, len_add, tps, splits, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_attn_split(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b) {
+  return attn_split_dispatch(s, d.heads / d.kv_heads, d.kv_heads, d.tps, b.q, L.k_cache, L.v_cache, b.state + ST_POS,
+                             1, d.max_len, d.attn_mult, b.part);
+}
+
+hipError_t launch_attn_combine(hipStream_t s, const Dims& d, const StepBufs& b) {
+  return attn_combine_dispatch(s, d.heads, d.tps, d.max_len, b.state + ST_POS, 1, b.part, b.att);
 }
 
 hipError_t launch_attn_unit(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vc, int heads,
                             int kv_heads, int max_len, const int* len_dev, float scale, int tps, float* part,
                             float* out) {
-  return attn_dispatch(s, heads / kv_heads, kv_heads, tps, q, kc, vc, len_dev, 0, max_len, scale, part, out);
+  hipError_t e = attn_split_dispatch(s, heads / kv_heads, kv_heads, tps, q, kc, vc, len_dev, 0, max_len, scale, part);
+  if (e != hipSuccess) return e;
+  return attn_combine_dispatch(s, heads, tps, max_len, len_dev, 0, part, out);
 }
 
 hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b) {
 #define BODY(KK)                                                                            \
   case KK: {                                                                                \
     constexpr int RB = rows_per_block<DTC, KK, kOprojP>();                                  \
-    k_oproj<DTC, KK, kOprojP><<<cdiv(L.o.rows, RB), kBlock, 0, s>>>(L.o, b.att, d.res_mult, b.h); \
+    klaunch(k_oproj<DTC, KK, kOprojP>, cdiv(L.o.rows, RB), kBlock, 0, s, L.o, b.att, d.res_mult, b.h); \
   } break;
   MOERT_DISPATCH(L.o.dtype, L.o.cols, BODY)
 #undef BODY
@@ -1017,11 +1052,11 @@ hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, cons
     constexpr int PB = kRouteWaves * kRouteNP * Geo<DTC, KK>::RPW;                                         \
     const int blocks = cdiv((long)d.top_k * d.inter, PB);                                                  \
     if (normalize)                                                                                         \
-      k_route_up<DTC, KK, kRouteNP, true><<<blocks, kRouteWaves * 64, 0, s>>>(                             \
+      klaunch(k_route_up<DTC, KK, kRouteNP, true>, blocks, kRouteWaves * 64, 0, s,                              \
           L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter,                      \
           b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act);                              \
     else                                                                                                   \
-      k_route_up<DTC, KK, kRouteNP, false><<<blocks, kRouteWaves * 64, 0, s>>>(                            \
+      klaunch(k_route_up<DTC, KK, kRouteNP, false>, blocks, kRouteWaves * 64, 0, s,                             \
           L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter,                      \
           b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act);                              \
   } break;
@@ -1034,7 +1069,7 @@ hipError_t launch_expert_down(hipStream_t s, const LayerDev& L, const Dims& d, c
                               bool accumulate) {
 #define BODY(KK)                                                                                          \
   case KK:                                                                                                \
-    k_expert_down<DTC, KK><<<cdiv(d.hidden, kWavesPerBlock), kBlock, 0, s>>>(                             \
+    klaunch(k_expert_down<DTC, KK>, cdiv(d.hidden, kWavesPerBlock), kBlock, 0, s,                              \
         L.down, b.act, b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, d.top_k, d.hidden,     \
         d.res_mult, accumulate, accumulate ? b.h : b.logits);                                             \
     break;
@@ -1060,41 +1095,43 @@ hipError_t launch_head(hipStream_t s, const DMat& head, const float* norm, const
 #define BODY(KK)                                                                                        \
   case KK: {                                                                                            \
     constexpr int RB = rows_per_block<DTC, KK, kHeadP>() * kHeadNB;                                     \
-    k_head<DTC, KK, kHeadP, kHeadNB><<<cdiv(head.rows, RB), kBlock, 0, s>>>(head, b.h, norm, d.eps,     \
+    klaunch(k_head<DTC, KK, kHeadP, kHeadNB>, cdiv(head.rows, RB), kBlock, 0, s, head, b.h, norm, d.eps,     \
                                                                    d.logits_scaling, b.logits, b.best); \
   } break;
   MOERT_DISPATCH(head.dtype, head.cols, BODY)
 #undef BODY
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  k_head_argmax<<<1, kBlock, 0, s>>>(b.best, head_blocks(head), b.state, b.seq, b.argmax_hist, d.max_len);
+  return hipGetLastError();
+}
+
+hipError_t launch_head_argmax(hipStream_t s, const DMat& head, const Dims& d, const StepBufs& b) {
+  klaunch(k_head_argmax, 1, kBlock, 0, s, b.best, head_blocks(head), b.state, b.seq, b.argmax_hist, d.max_len);
   return hipGetLastError();
 }
 
 hipError_t launch_dequant(hipStream_t s, const DMat& w, float* out) {
   size_t n;
   switch (w.dtype) {
-    case DT_Q8_0: n = (size_t)w.rows * (w.cols / 16); k_dequant<DT_Q8_0><<<cdiv(n, kBlock), kBlock, 0, s>>>(w, out); break;
-    case DT_Q4_0: n = (size_t)w.rows * (w.cols / 32); k_dequant<DT_Q4_0><<<cdiv(n, kBlock), kBlock, 0, s>>>(w, out); break;
-    case DT_F32: n = (size_t)w.rows * (w.cols / 4); k_dequant<DT_F32><<<cdiv(n, kBlock), kBlock, 0, s>>>(w, out); break;
+    case DT_Q8_0: n = (size_t)w.rows * (w.cols / 16); klaunch(k_dequant<DT_Q8_0>, cdiv(n, kBlock), kBlock, 0, s, w, out); break;
+    case DT_Q4_0: n = (size_t)w.rows * (w.cols / 32); klaunch(k_dequant<DT_Q4_0>, cdiv(n, kBlock), kBlock, 0, s, w, out); break;
+    case DT_F32: n = (size_t)w.rows * (w.cols / 4); klaunch(k_dequant<DT_F32>, cdiv(n, kBlock), kBlock, 0, s, w, out); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm(hipStream_t s, const float* x, const float* w, int n, float eps, float* out) {
-  k_rmsnorm<<<1, 64, 0, s>>>(x, w, n, eps, out);
+  klaunch(k_rmsnorm, 1, 64, 0, s, x, w, n, eps, out);
   return hipGetLastError();
 }
 
 hipError_t launch_rope(hipStream_t s, float* x, int heads, int head_dim, const float* cs) {
   int n = heads * head_dim / 2;
-  k_rope<<<cdiv(n, 256), 256, 0, s>>>(x, heads, head_dim / 2, cs);
+  klaunch(k_rope, cdiv(n, 256), 256, 0, s, x, heads, head_dim / 2, cs);
   return hipGetLastError();
 }
 
 hipError_t launch_topk(hipStream_t s, const float* logits, const float* bias, int n, int k, int* ids, float* w) {
-  k_topk<<<1, 64, 0, s>>>(logits, bias, n, k, ids, w);
+  klaunch(k_topk, 1, 64, 0, s, logits, bias, n, k, ids, w);
   return hipGetLastError();
 }
 
@@ -1103,15 +1140,28 @@ hipError_t launch_argmax(hipStream_t s, const float* v, int n, int2* best, int* 
   if (blocks > 1024) blocks = 1024;
   if (blocks < 1) blocks = 1;
   (void)cnt;
-  k_argmax<<<blocks, kBlock, 0, s>>>(v, n, best);
+  klaunch(k_argmax, blocks, kBlock, 0, s, v, n, best);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  k_argmax_final<<<1, 64, 0, s>>>(best, blocks, out);
+  klaunch(k_argmax_final, 1, 64, 0, s, best, blocks, out);
+  return hipGetLastError();
+}
+
+// Plain streaming copy (16 B per lane per iteration): the reference point for achievable HBM bandwidth and for
+// scaling the FETCH_SIZE / WRITE_SIZE counters of the other kernels.
+__global__ __launch_bounds__(256) void k_copy(const float4* __restrict__ src, float4* __restrict__ dst, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) dst[i] = src[i];
+}
+
+hipError_t launch_copy(hipStream_t s, const void* src, void* dst, size_t bytes) {
+  const size_t n = bytes / 16;
+  const int blocks = (int)std::min<size_t>((n + 255) / 256, 8192);
+  klaunch(k_copy, blocks, 256, 0, s, (const float4*)src, (float4*)dst, n);
   return hipGetLastError();
 }
 
 hipError_t launch_exp(hipStream_t s, const float* x, float* y, int n) {
-  k_exp<<<cdiv(n, 256), 256, 0, s>>>(x, y, n);
+  klaunch(k_exp, cdiv(n, 256), 256, 0, s, x, y, n);
   return hipGetLastError();
 }
 

@@ -22,8 +22,10 @@ import numpy as np
 F32, Q8_0, Q4_0 = 0, 1, 2
 DTYPE_NAMES = {F32: "f32", Q8_0: "q8_0", Q4_0: "q4_0"}
 
-K_EMBED, K_QKV, K_ATTN, K_OPROJ, K_ROUTE_UP, K_EXPERT_DOWN, K_HEAD = range(7)
-KERNEL_NAMES = ["embed", "qkv", "attn", "oproj", "route_up", "expert_down", "head"]
+(K_EMBED, K_QKV, K_ATTN_SPLIT, K_ATTN_COMBINE, K_OPROJ, K_ROUTE_UP, K_EXPERT_DOWN, K_HEAD,
+ K_HEAD_ARGMAX) = range(9)
+KERNEL_NAMES = ["embed", "qkv", "attn_split", "attn_combine", "oproj", "route_up", "expert_down", "head",
+                "head_argmax"]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmoert.so")
@@ -102,6 +104,7 @@ def lib() -> ctypes.CDLL:
             "moert_rope": (i, [vp, i, i, f, i]),
             "moert_attn_decode": (i, [vp, vp, vp, i, i, i, i, i, f, i, vp]),
             "moert_exp_device": (i, [vp, vp, i]),
+            "moert_copy_probe": (i, [sz, i, ctypes.POINTER(ctypes.c_double)]),
             "moert_quantize": (i, [vp, sz, i, vp]),
             "moert_dtype_bytes": (sz, [i, sz]),
             "moert_synth_normal": (i, [u64, u64, sz, f, f, vp]),
@@ -122,7 +125,7 @@ EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moer
             "moert_time_steps", "moert_time_kernel", "moert_block_create", "moert_block_destroy",
             "moert_block_forward", "moert_block_time", "moert_router_topk", "moert_argmax", "moert_gemv",
             "moert_dequant", "moert_rmsnorm", "moert_rope", "moert_attn_decode", "moert_exp_device",
-            "moert_quantize", "moert_dtype_bytes", "moert_synth_normal", "moert_synth_quantized",
+            "moert_copy_probe", "moert_quantize", "moert_dtype_bytes", "moert_synth_normal", "moert_synth_quantized",
             "moert_synth_fp16"]
 
 
@@ -470,6 +473,23 @@ def exp_device(x: np.ndarray) -> np.ndarray:
     y = np.empty_like(x)
     check(lib().moert_exp_device(ptr(x), ptr(y), x.size))
     return y
+
+
+def tiles_per_split(max_len: int, attn_splits: int) -> int:
+    """64-position tiles per attention split when a cache of max_len positions is cut into at most attn_splits."""
+    return (max_len // 64 + attn_splits - 1) // attn_splits
+
+
+def attn_splits_for(max_len: int, tps: int) -> int:
+    """Number of attention splits of tps tiles covering max_len positions."""
+    return ((max_len + 63) // 64 + tps - 1) // tps
+
+
+def copy_probe(nbytes: int, iters: int = 10) -> float:
+    """Mean microseconds of one device-to-device copy of nbytes (HBM bandwidth reference)."""
+    us = ctypes.c_double()
+    check(lib().moert_copy_probe(ctypes.c_size_t(nbytes), iters, ctypes.byref(us)))
+    return us.value
 
 
 def step_bytes(cfg: Config, wdtype: int, embed_dtype: int, context: int) -> int:
