@@ -60,6 +60,49 @@ def measured_traffic(kernel):
     return None
 
 
+def batched_step(cfg, seed, iters, m=16, nblocks=4):
+    """16 positions through one MoE block of the 3B shape at once (router + top-8 per position with the Zipf(1.1)
+    router bias, experts regrouped into the grouped int8 MFMA GEMM), rotating over `nblocks` blocks of separate
+    weights (400 MB of experts, beyond the 256 MB last-level cache). Reports the block step time, its kernels, the
+    expert bytes it must stream (U distinct experts x 2,506,752 B + router) and the per-position GEMV path timed on
+    the same blocks for comparison."""
+    import numpy as np
+
+    import moert
+    H, I, E, k = cfg.hidden, cfg.inter, cfg.experts, cfg.top_k
+    blocks, uniq = [], []
+    for b in range(nblocks):
+        router = moert.synth_quantized(seed + b, 900, E * H, 0.02, moert.Q8_0)
+        gu = moert.synth_quantized(seed + b, 901, E * 2 * I * H, 0.02, moert.Q8_0)
+        dn = moert.synth_quantized(seed + b, 902, E * H * I, 0.02, moert.Q8_0)
+        blk = moert.GpuBlock(H, I, E, k, router, gu, dn, moert.Q8_0, router_bias=moert.zipf_bias(E, seed + b))
+        x = moert.synth_normal(seed + b, 903, m * H).reshape(m, H)
+        blk.forward_batched(x)
+        uniq.append(blk.experts_in_step())
+        blocks.append(blk)
+    t = moert.time_batched(blocks, m, iters)
+    per_pos_us = blocks[0].time(max(4, iters)) * m
+    for blk in blocks:
+        blk.close()
+    u_mean = sum(uniq) / len(uniq)
+    expert_bytes = moert.dtype_bytes(moert.Q8_0, 3 * I * H)
+    nbytes = u_mean * expert_bytes + moert.dtype_bytes(moert.Q8_0, E * H)
+    gu_bytes = u_mean * moert.dtype_bytes(moert.Q8_0, 2 * I * H)
+    dn_bytes = u_mean * moert.dtype_bytes(moert.Q8_0, I * H)
+    flops = 2 * m * k * 3 * I * H
+    out = {"positions": m, "experts_distinct_mean": u_mean, "block_step_us": round(t["step"], 2),
+           "kernels_us": {key: round(t[key], 2) for key in ("route", "up", "down", "combine")},
+           "bytes": int(nbytes), "achieved_gbs": round(nbytes / (t["step"] * 1e-6) / 1e9, 1),
+           "up_gbs": round(gu_bytes / (t["up"] * 1e-6) / 1e9, 1),
+           "down_gbs": round(dn_bytes / (t["down"] * 1e-6) / 1e9, 1),
+           "useful_tops": round(flops / ((t["up"] + t["down"]) * 1e-6) / 1e12, 3),
+           "per_position_path_us": round(per_pos_us, 2),
+           "speedup_vs_per_position": round(per_pos_us / t["step"], 2)}
+    log(f"batched step m={m}: {t['step']:.1f} us per block ({u_mean:.1f} experts, {out['achieved_gbs']} GB/s), "
+        f"per-position path {per_pos_us:.1f} us")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -69,6 +112,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=32, help="oracle decode steps timed for the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--seed", type=int, default=3003)
+    ap.add_argument("--batched-iters", type=int, default=20,
+                    help="rounds of the 16-position grouped MoE step over 4 rotating 3B blocks (0 skips it)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this engine has no multi-GPU path (asked for --gpus {args.gpus})",
@@ -131,6 +176,8 @@ def main():
                 "gbs": round(2 * copy_bytes / (copy_us * 1e-6) / 1e9, 1)}
     log(f"device copy of {copy_bytes >> 20} MiB: {copy_us:.1f} us, {hbm_copy['gbs']:.0f} GB/s read+write")
 
+    batched = batched_step(cfg, args.seed, args.batched_iters) if args.batched_iters > 0 else None
+
     cpu = None
     if args.cpu_steps > 0:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -169,6 +216,7 @@ def main():
                           "frac": round(step_bytes / (wall / args.steps) / 1e9 / HBM_PEAK_GBS, 4)},
         "moe_gemv": moe,
         "hbm_copy": hbm_copy,
+        "batched_step": batched,
         "kernels": kernels,
         "cpu_baseline": cpu,
         "device": name,

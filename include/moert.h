@@ -162,6 +162,21 @@ int moert_block_forward(moert_block* b, const float* x, float* y, int* ids, floa
 /* Mean microseconds of one block forward over `iters` launches (inputs resident in HBM). */
 int moert_block_time(moert_block* b, int iters, double* us);
 
+/* m positions (1..32) through the block at once: per-position router + top-k, then the routed experts regrouped
+ * per expert (first-appearance order) and computed as a grouped int8 MFMA GEMM, each weight row read once for all
+ * of its member positions, and y[p] = y[p] + w * o summed in that list order. Activations enter the MFMA as
+ * 15-bit block codes (see the kernel header), so the result differs from the f32 per-position path by that
+ * rounding only. Q8_0 router and experts. x, y: [m, hidden]; ids, weights: [m, top_k] (nullable outputs).
+ * Replaces Cpu::experts_step (rust/moe-rt/src/cpu.rs:239-296) and the per-position GPU loops of the multi-position
+ * step (rust/moe-rt/src/cuda_backend.rs:751-917). */
+int moert_block_forward_batched(moert_block* b, int m, const float* x, float* y, int* ids, float* weights);
+/* Number of distinct experts routed by the last batched step on this block (the grouped GEMM's expert count). */
+int moert_block_experts_in_step(moert_block* b, int* n_experts);
+/* Times `iters` rounds of the batched step over `nblocks` blocks in turn (rotating weights beyond the caches),
+ * each block's inputs being those of its last moert_block_forward_batched. us[0] = mean microseconds of one
+ * block step; us[1..4] = mean dispatch time of the route, gate/up, down and combine kernels. */
+int moert_block_time_batched(moert_block* const* blocks, int nblocks, int m, int iters, double* us);
+
 /* ---------------------------------------------------------------------------------------------------------
  * Unit-parity entry points: one kernel on host buffers (copied in and out). For tests of each subsystem.
  * ------------------------------------------------------------------------------------------------------- */

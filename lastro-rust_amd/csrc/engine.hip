@@ -18,6 +18,7 @@
 
 #include "../../include/moert.h"
 #include "host_utils.h"
+#include "grouped.h"
 #include "kernels.h"
 
 using namespace moert;
@@ -347,6 +348,24 @@ struct moert_block {
   LayerDev L{};
   StepBufs b{};
   float* x = nullptr;
+  // multi-position (grouped) step buffers, allocated on first use
+  GroupBufs g{};
+  float* gx = nullptr;
+  float* gy = nullptr;
+  int ensure_grouped() {
+    if (gx) return MOERT_OK;
+    const int H = dims.hidden, I = dims.inter, M = kGrpMaxPos, S = kGrpMaxPos * 8;
+    int rc;
+    if ((rc = zeros(arena, stream, (size_t)M * H, &gx)) || (rc = zeros(arena, stream, (size_t)M * H, &gy)) ||
+        (rc = zeros(arena, stream, (size_t)S, &g.ids)) || (rc = zeros(arena, stream, (size_t)S, &g.w)) ||
+        (rc = zeros(arena, stream, (size_t)M * H, &g.xh)) || (rc = zeros(arena, stream, (size_t)M * H, &g.xl)) ||
+        (rc = zeros(arena, stream, (size_t)M * (H / 32), &g.xd)) || (rc = zeros(arena, stream, (size_t)GRP_WORDS, &g.grp)) ||
+        (rc = zeros(arena, stream, (size_t)S * I, &g.ah)) || (rc = zeros(arena, stream, (size_t)S * I, &g.al)) ||
+        (rc = zeros(arena, stream, (size_t)S * (I / 32), &g.ad)) || (rc = zeros(arena, stream, (size_t)S * H, &g.o)))
+      return rc;
+    CHECK_HIP(hipStreamSynchronize(stream));
+    return MOERT_OK;
+  }
   ~moert_block() {
     if (stream) (void)hipStreamSynchronize(stream);
     arena.release();
@@ -760,6 +779,79 @@ int moert_block_time(moert_block* b, int iters, double* us) {
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
   return MOERT_OK;
+}
+
+static int check_grouped(moert_block* b, int m) {
+  CHECK_CFG(m >= 1 && m <= kGrpMaxPos, "batched step: m %d outside [1, %d]", m, kGrpMaxPos);
+  CHECK_CFG(b->L.router.dtype == MOERT_Q8_0 && b->L.gate_up.dtype == MOERT_Q8_0 && b->L.down.dtype == MOERT_Q8_0,
+            "batched step: the grouped MFMA path takes Q8_0 router and experts");
+  CHECK_CFG(b->dims.hidden % 256 == 0 && (b->dims.hidden == 1024 || b->dims.hidden == 1536),
+            "batched step: hidden %d not compiled", b->dims.hidden);
+  return b->ensure_grouped();
+}
+
+int moert_block_forward_batched(moert_block* b, int m, const float* x, float* y, int* ids, float* weights) {
+  CHECK_CFG(b && x, "null argument");
+  TRY(check_grouped(b, m));
+  const Dims& d = b->dims;
+  CHECK_HIP(hipMemcpyAsync(b->gx, x, (size_t)m * d.hidden * 4, hipMemcpyHostToDevice, b->stream));
+  CHECK_HIP(launch_grouped_block(b->stream, b->L, m, d.top_k, d.inter, b->gx, b->g, b->gy));
+  if (y) CHECK_HIP(hipMemcpyAsync(y, b->gy, (size_t)m * d.hidden * 4, hipMemcpyDeviceToHost, b->stream));
+  if (ids) CHECK_HIP(hipMemcpyAsync(ids, b->g.ids, (size_t)m * d.top_k * 4, hipMemcpyDeviceToHost, b->stream));
+  if (weights) CHECK_HIP(hipMemcpyAsync(weights, b->g.w, (size_t)m * d.top_k * 4, hipMemcpyDeviceToHost, b->stream));
+  CHECK_HIP(hipStreamSynchronize(b->stream));
+  return MOERT_OK;
+}
+
+int moert_block_experts_in_step(moert_block* b, int* n_experts) {
+  CHECK_CFG(b && n_experts && b->gx, "no batched step has run on this block");
+  int nu = 0;
+  CHECK_HIP(hipMemcpy(&nu, b->g.grp + GRP_NU, 4, hipMemcpyDeviceToHost));
+  *n_experts = nu;
+  return MOERT_OK;
+}
+
+int moert_block_time_batched(moert_block* const* blocks, int nblocks, int m, int iters, double* us) {
+  CHECK_CFG(blocks && nblocks >= 1 && iters >= 1 && us, "bad argument");
+  for (int i = 0; i < nblocks; i++) {
+    CHECK_CFG(blocks[i] && blocks[i]->gx, "block %d: run moert_block_forward_batched first", i);
+    TRY(check_grouped(blocks[i], m));
+  }
+  hipStream_t s = blocks[0]->stream;
+  for (int i = 1; i < nblocks; i++) CHECK_HIP(hipStreamSynchronize(blocks[i]->stream));
+  const int n = iters * nblocks;
+  std::vector<hipEvent_t> ev(8 * n + 2);
+  for (auto& e : ev) CHECK_HIP(hipEventCreate(&e));
+  auto run = [&](bool per_kernel) -> int {
+    for (int it = 0; it < iters; it++)
+      for (int i = 0; i < nblocks; i++) {
+        moert_block* b = blocks[i];
+        const hipEvent_t* e = per_kernel ? &ev[8 * (it * nblocks + i)] : nullptr;
+        CHECK_HIP(launch_grouped_block(s, b->L, m, b->dims.top_k, b->dims.inter, b->gx, b->g, b->gy, e));
+      }
+    return MOERT_OK;
+  };
+  int rc = run(false);  // warm-up
+  if (!rc) rc = hipEventRecord(ev[8 * n], s) == hipSuccess ? run(false) : MOERT_E_DEVICE;
+  if (!rc) rc = hipEventRecord(ev[8 * n + 1], s) == hipSuccess ? run(true) : MOERT_E_DEVICE;
+  if (!rc && hipStreamSynchronize(s) != hipSuccess) rc = MOERT_E_DEVICE;
+  if (!rc) {
+    float t = 0.0f;
+    (void)hipEventElapsedTime(&t, ev[8 * n], ev[8 * n + 1]);
+    us[0] = (double)t * 1000.0 / n;
+    for (int k = 0; k < 4; k++) {
+      double tot = 0.0;
+      for (int i = 0; i < n; i++) {
+        float x = 0.0f;
+        (void)hipEventElapsedTime(&x, ev[8 * i + 2 * k], ev[8 * i + 2 * k + 1]);
+        tot += x;
+      }
+      us[1 + k] = tot * 1000.0 / n;
+    }
+  }
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  if (rc == MOERT_E_DEVICE && g_err.empty()) set_err("time_batched: device error");
+  return rc;
 }
 
 // ---- unit-parity entry points ---------------------------------------------------------------------------------

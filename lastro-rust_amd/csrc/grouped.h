@@ -1,0 +1,36 @@
+// Multi-position MoE step (grouped int8 MFMA expert GEMM): device buffers and launcher (grouped.hip).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kernels.h"
+
+namespace moert {
+
+constexpr int kGrpMaxPos = 32;  // positions per grouped step (the reference caps a step at 32, cuda_backend.rs:272-274)
+
+// Offsets (in ints) of the grouping published by k_grp_up for the down and combine kernels.
+enum { GRP_NU = 0, GRP_LIST = 1, GRP_CNT = 65, GRP_OFF = 129, GRP_UOF = 193, GRP_SLOT = 257,
+       GRP_WORDS = GRP_SLOT + kGrpMaxPos * 8 };
+
+// Device buffers of one grouped step, sized for kGrpMaxPos positions, hidden H, inter I and top-k <= 8.
+struct GroupBufs {
+  int* ids;      // [m, k] routed experts, top-k order
+  float* w;      // [m, k] routing weights
+  int8_t* xh;    // [m, H] hi codes of the block inputs
+  int8_t* xl;    // [m, H] lo codes
+  float* xd;     // [m, H/32] their block scales
+  int* grp;      // [GRP_WORDS] grouping: list of experts, member counts, offsets, slot of every entry
+  int8_t* ah;    // [m*k, I] hi codes of the SwiGLU activations, by member slot
+  int8_t* al;    // [m*k, I]
+  float* ad;     // [m*k, I/32]
+  float* o;      // [m*k, H] down outputs by member slot
+};
+
+// y[m, H] = MoE block of the m rows of x (already normalised), router + top-k per row, experts grouped.
+// Q8_0 router, gate_up and down; E <= 64, k <= 8, m <= kGrpMaxPos. With `ev` (8 events), the four kernels
+// (route, up, down, combine) record their dispatch start/end into ev[2i], ev[2i+1].
+hipError_t launch_grouped_block(hipStream_t s, const LayerDev& L, int m, int k, int inter, const float* x,
+                                GroupBufs g, float* y, const hipEvent_t* ev = nullptr);
+
+}  // namespace moert

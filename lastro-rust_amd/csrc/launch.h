@@ -1,0 +1,22 @@
+// Kernel launch helper: plain hipLaunchKernelGGL, or hipExtLaunchKernelGGL with the event pair armed on this
+// thread (arm_launch_events), whose start/stop events take the dispatch's own timestamps so that the measured
+// time is the kernel's execution and not the host's enqueue of separate event markers.
+#pragma once
+#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
+
+namespace moert {
+
+// Takes (and clears) the event pair armed on this thread; false when none is armed.
+bool take_armed_events(hipEvent_t* start, hipEvent_t* stop);
+
+template <typename F, typename... Args>
+static inline void klaunch(F kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args... args) {
+  hipEvent_t a, z;
+  if (take_armed_events(&a, &z))
+    hipExtLaunchKernelGGL(kernel, grid, block, shm, s, a, z, 0u, args...);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, shm, s, args...);
+}
+
+}  // namespace moert

@@ -96,6 +96,9 @@ def lib() -> ctypes.CDLL:
             "moert_block_destroy": (i, [vp]),
             "moert_block_forward": (i, [vp, vp, vp, vp, vp]),
             "moert_block_time": (i, [vp, i, ctypes.POINTER(ctypes.c_double)]),
+            "moert_block_forward_batched": (i, [vp, i, vp, vp, vp, vp]),
+            "moert_block_experts_in_step": (i, [vp, ip]),
+            "moert_block_time_batched": (i, [vp, i, i, i, vp]),
             "moert_router_topk": (i, [vp, i, i, vp, vp]),
             "moert_argmax": (i, [vp, i, ip]),
             "moert_gemv": (i, [ctypes.POINTER(moert_tensor), i, i, vp, vp]),
@@ -123,7 +126,8 @@ EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moer
             "moert_decode_step", "moert_generate", "moert_reset_sequence", "moert_kv_prefill_fp16",
             "moert_set_position", "moert_get_position", "moert_read_kv_fp16", "moert_read_hidden",
             "moert_time_steps", "moert_time_kernel", "moert_block_create", "moert_block_destroy",
-            "moert_block_forward", "moert_block_time", "moert_router_topk", "moert_argmax", "moert_gemv",
+            "moert_block_forward", "moert_block_time", "moert_block_forward_batched",
+            "moert_block_experts_in_step", "moert_block_time_batched", "moert_router_topk", "moert_argmax", "moert_gemv",
             "moert_dequant", "moert_rmsnorm", "moert_rope", "moert_attn_decode", "moert_exp_device",
             "moert_copy_probe", "moert_quantize", "moert_dtype_bytes", "moert_synth_normal", "moert_synth_quantized",
             "moert_synth_fp16"]
@@ -264,10 +268,7 @@ class SynthModel:
             a[f"{l}.gate_up"] = synth_quantized(s, b + 7, E * 2 * I * H, self.std, self.wdtype)
             a[f"{l}.down"] = synth_quantized(s, b + 8, E * H * I, self.std, self.wdtype)
             if self.zipf_s is not None:
-                rng = np.random.default_rng(s * 1000 + l)
-                rank = np.empty(E, np.int64)
-                rank[rng.permutation(E)] = np.arange(1, E + 1)
-                a[f"{l}.router_bias"] = (-self.zipf_s * np.log(rank)).astype(np.float32)
+                a[f"{l}.router_bias"] = zipf_bias(E, s * 1000 + l, self.zipf_s)
         self._struct = None
 
     def weights(self) -> moert_model_weights:
@@ -403,6 +404,21 @@ class GpuBlock:
         check(lib().moert_block_time(self.h, iters, ctypes.byref(us)))
         return us.value
 
+    def forward_batched(self, x: np.ndarray):
+        """m positions at once (grouped MFMA experts): (y [m, H], ids [m, k], weights [m, k])."""
+        x = np.ascontiguousarray(x, np.float32).reshape(-1, self.hidden)
+        m = x.shape[0]
+        y = np.empty((m, self.hidden), np.float32)
+        ids = np.empty((m, self.top_k), np.int32)
+        w = np.empty((m, self.top_k), np.float32)
+        check(lib().moert_block_forward_batched(self.h, m, ptr(x), ptr(y), ptr(ids), ptr(w)))
+        return y, ids, w
+
+    def experts_in_step(self) -> int:
+        n = ctypes.c_int(0)
+        check(lib().moert_block_experts_in_step(self.h, ctypes.byref(n)))
+        return n.value
+
     def close(self):
         if self.h:
             lib().moert_block_destroy(self.h)
@@ -413,6 +429,22 @@ class GpuBlock:
             self.close()
         except Exception:
             pass
+
+
+def time_batched(blocks, m: int, iters: int):
+    """Mean microseconds of one batched block step over `blocks` in turn, and of its four kernels."""
+    arr = (ctypes.c_void_p * len(blocks))(*[b.h.value if isinstance(b.h, ctypes.c_void_p) else b.h for b in blocks])
+    us = (ctypes.c_double * 5)()
+    check(lib().moert_block_time_batched(arr, len(blocks), m, iters, us))
+    return {"step": us[0], "route": us[1], "up": us[2], "down": us[3], "combine": us[4]}
+
+
+def zipf_bias(experts: int, seed: int, s: float = 1.1) -> np.ndarray:
+    """Router bias b_e = -s * ln(rank_e) over a seeded permutation of the experts (Zipf-skewed expert loads)."""
+    rng = np.random.default_rng(seed)
+    rank = np.empty(experts, np.int64)
+    rank[rng.permutation(experts)] = np.arange(1, experts + 1)
+    return (-s * np.log(rank)).astype(np.float32)
 
 
 # ---- unit-parity entry points ------------------------------------------------------------------------------------

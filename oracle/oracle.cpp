@@ -621,6 +621,154 @@ void orc_experts_step(int hidden, int inter, int m, int k, const moert_tensor* g
   });
 }
 
+// ------------------------------------------------------------------------------------------------------------
+// Grouped (multi-position) expert step in the integer order of the MFMA path. Same structure as Cpu::experts_step
+// (rust/moe-rt/src/cpu.rs:239-296): experts in first-appearance order, each weight row used by all positions that
+// route to it, y[p] = y[p] + w * o summed in list order. The arithmetic differs from the f32 path only in that
+// each activation vector is first split into 15-bit integer codes per 32-element block (orc_quant_hilo), so that
+// every block product is an exact integer:
+//   S_b = 256 * sum(q * hi) + sum(q * lo),   acc = fmaf((float)S_b, d_w(b) * d_x(b), acc) over blocks b in order.
+
+void orc_quant_hilo(const float* x, int n, int8_t* hi, int8_t* lo, float* d) {
+  for (int b = 0; b < n / 32; b++) {
+    const float* xb = x + (size_t)b * 32;
+    float amax = 0.0f;
+    for (int i = 0; i < 32; i++) {
+      float a = std::fabs(xb[i]);
+      amax = a > amax ? a : amax;
+    }
+    const float s = amax / 32639.0f;
+    d[b] = s;
+    for (int i = 0; i < 32; i++) {
+      int v = s > 0.0f ? (int)std::rint(xb[i] / s) : 0;
+      int h = (v + 128) >> 8;  // floor((v + 128) / 256)
+      hi[b * 32 + i] = (int8_t)h;
+      lo[b * 32 + i] = (int8_t)(v - 256 * h);
+    }
+  }
+}
+
+namespace {
+
+// Integer codes and fp16 scale of block b of a Q8_0 / Q4_0 row (natural element order).
+void block_codes(const void* w, int dtype, int cols, size_t row, int b, int8_t* q, float* d) {
+  const uint8_t* p = (const uint8_t*)w + row * row_bytes(dtype, cols);
+  if (dtype == MOERT_Q8_0) {
+    const uint8_t* blk = p + (size_t)b * 34;
+    *d = h2f((uint16_t)(blk[0] | (blk[1] << 8)));
+    for (int i = 0; i < 32; i++) q[i] = (int8_t)blk[2 + i];
+  } else {
+    const uint8_t* blk = p + (size_t)b * 18;
+    *d = h2f((uint16_t)(blk[0] | (blk[1] << 8)));
+    for (int i = 0; i < 16; i++) {
+      q[i] = (int8_t)((int)(blk[2 + i] & 15) - 8);
+      q[16 + i] = (int8_t)((int)(blk[2 + i] >> 4) - 8);
+    }
+  }
+}
+
+float dot_hilo(const void* w, int dtype, int cols, size_t row, const int8_t* hi, const int8_t* lo, const float* dx) {
+  float acc = 0.0f;
+  int8_t q[32];
+  for (int b = 0; b < cols / 32; b++) {
+    float dw;
+    block_codes(w, dtype, cols, row, b, q, &dw);
+    int32_t sh = 0, sl = 0;
+    for (int i = 0; i < 32; i++) {
+      sh += (int32_t)q[i] * hi[b * 32 + i];
+      sl += (int32_t)q[i] * lo[b * 32 + i];
+    }
+    const int32_t S = 256 * sh + sl;
+    acc = std::fmaf((float)S, dw * dx[b], acc);
+  }
+  return acc;
+}
+
+}  // namespace
+
+float orc_dot_hilo(const void* w, int dtype, int cols, size_t row, const int8_t* hi, const int8_t* lo,
+                   const float* dx) {
+  return dot_hilo(w, dtype, cols, row, hi, lo, dx);
+}
+
+void orc_experts_grouped(int hidden, int inter, int m, int k, const moert_tensor* gate_up, const moert_tensor* down,
+                         const float* x, const int* ids, const float* weights, float* y, int threads) {
+  Pool pool(threads);
+  std::vector<int> list;                                  // experts in first-appearance order
+  std::vector<std::vector<std::pair<int, float>>> members;  // (position, weight), position order
+  for (int p = 0; p < m; p++)
+    for (int j = 0; j < k; j++) {
+      int e = ids[p * k + j];
+      size_t idx = 0;
+      while (idx < list.size() && list[idx] != e) idx++;
+      if (idx == list.size()) {
+        list.push_back(e);
+        members.emplace_back();
+      }
+      members[idx].push_back({p, weights[p * k + j]});
+    }
+  const size_t ne = list.size();
+  std::vector<size_t> off(ne);
+  size_t tot = 0;
+  for (size_t e = 0; e < ne; e++) {
+    off[e] = tot;
+    tot += members[e].size();
+  }
+  const int HB = hidden / 32, IB = inter / 32;
+  std::vector<int8_t> xh((size_t)m * hidden), xl((size_t)m * hidden);
+  std::vector<float> xd((size_t)m * HB);
+  for (int p = 0; p < m; p++)
+    orc_quant_hilo(x + (size_t)p * hidden, hidden, &xh[(size_t)p * hidden], &xl[(size_t)p * hidden], &xd[(size_t)p * HB]);
+  std::vector<float> a(tot * inter);
+  size_t per = (size_t)(inter + kRowsPerTask - 1) / kRowsPerTask;
+  pool.run(ne * per, [&](size_t t) {
+    size_t e = t / per, c = t % per;
+    size_t base = (size_t)list[e] * 2 * inter;
+    int r0 = (int)(c * kRowsPerTask), r1 = r0 + kRowsPerTask < inter ? r0 + kRowsPerTask : inter;
+    for (int r = r0; r < r1; r++)
+      for (size_t j = 0; j < members[e].size(); j++) {
+        size_t p = (size_t)members[e][j].first;
+        float g = dot_hilo(gate_up->data, gate_up->dtype, hidden, base + r, &xh[p * hidden], &xl[p * hidden], &xd[p * HB]);
+        float u = dot_hilo(gate_up->data, gate_up->dtype, hidden, base + inter + r, &xh[p * hidden], &xl[p * hidden],
+                           &xd[p * HB]);
+        a[(off[e] + j) * inter + r] = (g / (1.0f + orc_exp(-g))) * u;
+      }
+  });
+  std::vector<int8_t> ah(tot * inter), al(tot * inter);
+  std::vector<float> ad(tot * IB);
+  for (size_t i = 0; i < tot; i++) orc_quant_hilo(&a[i * inter], inter, &ah[i * inter], &al[i * inter], &ad[i * IB]);
+  size_t tasks = (size_t)(hidden + kRowsPerTask - 1) / kRowsPerTask;
+  pool.run(tasks, [&](size_t t) {
+    thread_local std::vector<float> acc;
+    acc.assign(m, 0.0f);
+    int r0 = (int)(t * kRowsPerTask), r1 = r0 + kRowsPerTask < hidden ? r0 + kRowsPerTask : hidden;
+    for (int r = r0; r < r1; r++) {
+      for (int p = 0; p < m; p++) acc[p] = 0.0f;
+      for (size_t e = 0; e < ne; e++)
+        for (size_t j = 0; j < members[e].size(); j++) {
+          size_t i = off[e] + j;
+          float o = dot_hilo(down->data, down->dtype, inter, (size_t)list[e] * hidden + r, &ah[i * inter],
+                             &al[i * inter], &ad[i * IB]);
+          int p = members[e][j].first;
+          float tw = members[e][j].second * o;
+          acc[p] = acc[p] + tw;
+        }
+      for (int p = 0; p < m; p++) y[(size_t)p * hidden + r] = acc[p];
+    }
+  });
+}
+
+void orc_moe_block_batched(int hidden, int inter, int experts, int k, const moert_tensor* router, const float* bias,
+                           const moert_tensor* gate_up, const moert_tensor* down, int m, const float* x, float* y,
+                           int* ids, float* weights, int threads) {
+  std::vector<float> logits(experts);
+  for (int p = 0; p < m; p++) {
+    orc_gemv(router->data, router->dtype, experts, hidden, x + (size_t)p * hidden, logits.data(), 1);
+    orc_route(logits.data(), bias, experts, k, ids + (size_t)p * k, weights + (size_t)p * k);
+  }
+  orc_experts_grouped(hidden, inter, m, k, gate_up, down, x, ids, weights, y, threads);
+}
+
 struct orc_session {
   moert_config cfg;
   moert_model_weights w;

@@ -62,6 +62,22 @@ int orc_tiles_per_split(int max_len, int attn_splits);
 void orc_experts_step(int hidden, int inter, int m, int k, const moert_tensor* gate_up, const moert_tensor* down,
                       const float* x, const int* ids, const float* weights, float* y, int threads);
 
+/* Split of x (n multiple of 32) into 15-bit integer codes per 32-element block: d = amax/32639,
+ * v = rint(x/d) = 256*hi + lo with lo in [-128, 127] (d = 0 and v = 0 for an all-zero block). */
+void orc_quant_hilo(const float* x, int n, int8_t* hi, int8_t* lo, float* d);
+/* Row `row` of a Q8_0/Q4_0 matrix against hi/lo codes: per block the exact integer product, then
+ * acc = fmaf((float)S, d_w * d_x, acc) in block order. */
+float orc_dot_hilo(const void* w, int dtype, int cols, size_t row, const int8_t* hi, const int8_t* lo,
+                   const float* dx);
+/* experts_step (first-appearance grouping, list-order combine) in the integer block order of the grouped MFMA
+ * path; Q8_0/Q4_0 weights. */
+void orc_experts_grouped(int hidden, int inter, int m, int k, const moert_tensor* gate_up, const moert_tensor* down,
+                         const float* x, const int* ids, const float* weights, float* y, int threads);
+/* m positions through one MoE block: per-position router + top-k (canonical order), then orc_experts_grouped. */
+void orc_moe_block_batched(int hidden, int inter, int experts, int k, const moert_tensor* router, const float* bias,
+                           const moert_tensor* gate_up, const moert_tensor* down, int m, const float* x, float* y,
+                           int* ids, float* weights, int threads);
+
 /* CpuSession. */
 int orc_session_create(const moert_config* cfg, const moert_model_weights* w, int max_len, int attn_splits,
                        int threads, orc_session** out);

@@ -46,6 +46,10 @@ def lib() -> ctypes.CDLL:
             "orc_attention": (None, [vp, vp, vp, i, i, i, i, i, f, i, vp]),
             "orc_tiles_per_split": (i, [i, i]),
             "orc_experts_step": (None, [i, i, i, i, vp, vp, vp, vp, vp, vp, i]),
+            "orc_quant_hilo": (None, [vp, i, vp, vp, vp]),
+            "orc_dot_hilo": (f, [vp, i, i, sz, vp, vp, vp]),
+            "orc_experts_grouped": (None, [i, i, i, i, vp, vp, vp, vp, vp, vp, i]),
+            "orc_moe_block_batched": (None, [i, i, i, i, vp, vp, vp, vp, i, vp, vp, vp, vp, i]),
             "orc_session_create": (i, [vp, vp, i, i, i, ctypes.POINTER(vp)]),
             "orc_session_destroy": (None, [vp]),
             "orc_session_step": (i, [vp, i, vp, vp, vp, vp]),
@@ -190,6 +194,46 @@ def experts_step(hidden, inter, m, k, gate_up, down, dtype, x, ids, weights, thr
     lib().orc_experts_step(hidden, inter, m, k, ctypes.byref(gu), ctypes.byref(dn), _p(x), _p(ids), _p(weights),
                            _p(y), threads)
     return y.reshape(m, hidden)
+
+
+def quant_hilo(x):
+    """15-bit block codes of x: (hi int8, lo int8, d f32 per 32-block) with x ~ (256*hi + lo) * d."""
+    x = _f32(x)
+    hi = np.empty(x.size, np.int8)
+    lo = np.empty(x.size, np.int8)
+    d = np.empty(x.size // 32, np.float32)
+    lib().orc_quant_hilo(_p(x), x.size, _p(hi), _p(lo), _p(d))
+    return hi, lo, d
+
+
+def dot_hilo(w, dtype, cols, row, hi, lo, d):
+    return float(lib().orc_dot_hilo(w.ctypes.data, dtype, cols, row, _p(hi), _p(lo), _p(d)))
+
+
+def experts_grouped(hidden, inter, m, k, gate_up, down, dtype, x, ids, weights, threads=4):
+    mt = _moert()
+    gu, dn = mt.moert_tensor(gate_up.ctypes.data, dtype), mt.moert_tensor(down.ctypes.data, dtype)
+    x = _f32(x)
+    ids = np.ascontiguousarray(ids, np.int32)
+    weights = _f32(weights)
+    y = np.empty(m * hidden, np.float32)
+    lib().orc_experts_grouped(hidden, inter, m, k, ctypes.byref(gu), ctypes.byref(dn), _p(x), _p(ids), _p(weights),
+                              _p(y), threads)
+    return y.reshape(m, hidden)
+
+
+def moe_block_batched(hidden, inter, experts, k, router, gate_up, down, dtype, x, bias=None, threads=4):
+    """m = len(x) // hidden positions through one MoE block in the grouped integer order: (y, ids, weights)."""
+    mt = _moert()
+    r, gu, dn = (mt.moert_tensor(a.ctypes.data, dtype) for a in (router, gate_up, down))
+    x = _f32(x)
+    m = x.size // hidden
+    y = np.empty(m * hidden, np.float32)
+    ids = np.empty(m * k, np.int32)
+    w = np.empty(m * k, np.float32)
+    lib().orc_moe_block_batched(hidden, inter, experts, k, ctypes.byref(r), _p(None if bias is None else _f32(bias)),
+                                ctypes.byref(gu), ctypes.byref(dn), m, _p(x), _p(y), _p(ids), _p(w), threads)
+    return y.reshape(m, hidden), ids.reshape(m, k), w.reshape(m, k)
 
 
 class CpuSession:

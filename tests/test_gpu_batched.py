@@ -1,0 +1,92 @@
+"""Multi-position MoE step (grouped int8 MFMA experts) through the C ABI, against the oracle's grouped integer order
+bit for bit, and against the single-position GPU block for the routing."""
+import numpy as np
+import pytest
+
+import moert
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+SHAPES = [(1024, 512, 32, 8), (1536, 512, 40, 8), (1024, 128, 6, 2), (1536, 256, 64, 4)]
+
+
+@pytest.mark.parametrize("hidden,inter,experts,k", SHAPES)
+def test_batched_block_is_bit_identical_to_the_grouped_oracle(gpu, hidden, inter, experts, k):
+    router = moert.synth_quantized(101, hidden, experts * hidden, 0.02, moert.Q8_0)
+    gate_up = moert.synth_quantized(102, hidden, experts * 2 * inter * hidden, 0.02, moert.Q8_0)
+    down = moert.synth_quantized(103, hidden, experts * hidden * inter, 0.02, moert.Q8_0)
+    for zipf in (False, True):
+        bias = moert.zipf_bias(experts, 7) if zipf else None
+        blk = moert.GpuBlock(hidden, inter, experts, k, router, gate_up, down, moert.Q8_0, router_bias=bias)
+        for m in (1, 3, 16, 17, 32):
+            say(f"batched block hidden={hidden} inter={inter} E={experts} k={k} zipf={zipf} m={m}")
+            x = moert.synth_normal(104, m, m * hidden).reshape(m, hidden)
+            y, ids, w = blk.forward_batched(x)
+            oy, oi, ow = oracle.moe_block_batched(hidden, inter, experts, k, router, gate_up, down, moert.Q8_0, x,
+                                                  bias=bias)
+            assert ids.tolist() == oi.tolist(), m
+            assert bits_equal(w, ow), m
+            assert bits_equal(y, oy), m
+            assert blk.experts_in_step() == len(np.unique(oi))
+        blk.close()
+
+
+def test_batched_block_with_every_position_on_the_same_experts(gpu):
+    """All positions identical: every routed expert has m members (the widest member tile), and positions with
+    zero input (all-zero activation blocks, scale 0)."""
+    hidden, inter, experts, k = 1536, 512, 40, 8
+    router = moert.synth_quantized(111, 0, experts * hidden, 0.02, moert.Q8_0)
+    gate_up = moert.synth_quantized(112, 0, experts * 2 * inter * hidden, 0.02, moert.Q8_0)
+    down = moert.synth_quantized(113, 0, experts * hidden * inter, 0.02, moert.Q8_0)
+    blk = moert.GpuBlock(hidden, inter, experts, k, router, gate_up, down, moert.Q8_0)
+    for m, zero in ((16, False), (32, False), (5, True)):
+        say(f"batched block identical positions m={m} zero={zero}")
+        row = np.zeros(hidden, np.float32) if zero else moert.synth_normal(114, 0, hidden)
+        x = np.tile(row, (m, 1))
+        y, ids, w = blk.forward_batched(x)
+        oy, oi, ow = oracle.moe_block_batched(hidden, inter, experts, k, router, gate_up, down, moert.Q8_0, x)
+        assert ids.tolist() == oi.tolist() and bits_equal(w, ow) and bits_equal(y, oy)
+        assert blk.experts_in_step() == k
+        assert (y == y[0]).all()
+    blk.close()
+
+
+def test_batched_routing_equals_the_single_position_gpu_block(gpu):
+    hidden, inter, experts, k, m = 1536, 512, 40, 8, 16
+    router = moert.synth_quantized(121, 0, experts * hidden, 0.02, moert.Q8_0)
+    gate_up = moert.synth_quantized(122, 0, experts * 2 * inter * hidden, 0.02, moert.Q8_0)
+    down = moert.synth_quantized(123, 0, experts * hidden * inter, 0.02, moert.Q8_0)
+    bias = moert.zipf_bias(experts, 9)
+    blk = moert.GpuBlock(hidden, inter, experts, k, router, gate_up, down, moert.Q8_0, router_bias=bias)
+    x = moert.synth_normal(124, 0, m * hidden).reshape(m, hidden)
+    say("batched vs single-position routing")
+    yb, ids, w = blk.forward_batched(x)
+    for p in range(m):
+        y1, i1, w1 = blk.forward(x[p])
+        assert ids[p].tolist() == i1.tolist() and bits_equal(w[p], w1)
+        # the two paths differ only by the 15-bit activation codes of the grouped path
+        assert np.linalg.norm(yb[p] - y1) <= 2e-4 * np.linalg.norm(y1)
+    blk.close()
+
+
+def test_batched_block_refuses_bad_sizes(gpu):
+    hidden, inter, experts, k = 1024, 128, 6, 2
+    router = moert.synth_quantized(131, 0, experts * hidden, 0.02, moert.Q8_0)
+    gate_up = moert.synth_quantized(132, 0, experts * 2 * inter * hidden, 0.02, moert.Q8_0)
+    down = moert.synth_quantized(133, 0, experts * hidden * inter, 0.02, moert.Q8_0)
+    blk = moert.GpuBlock(hidden, inter, experts, k, router, gate_up, down, moert.Q8_0)
+    with pytest.raises(moert.MoertError):
+        blk.forward_batched(np.zeros((33, hidden), np.float32))
+    blk.close()

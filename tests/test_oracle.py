@@ -340,6 +340,79 @@ def test_batched_experts_step_matches_the_per_position_path():
         assert np.abs(got - per).max() <= 1e-5 * np.abs(per).max(), m
 
 
+# ---- grouped (multi-position) integer path ---------------------------------------------------------------------------
+def test_hilo_codes_reconstruct_every_block_within_half_a_step():
+    """v = 256*hi + lo with lo in [-128, 127], |x - v*d| <= d/2 (plus the f32 rounding of x/d, below 32639 * 2^-24)
+    and the block maximum at +-32639; zero blocks give d = 0 and zero codes."""
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal(32 * 400) * np.exp(rng.uniform(-20, 8, 32 * 400))).astype(np.float32)
+    x[:32] = 0.0
+    x[64:96] = np.float32(-3.5)
+    hi, lo, d = oracle.quant_hilo(x)
+    v = 256 * hi.astype(np.int64) + lo.astype(np.int64)
+    assert lo.min() >= -128 and lo.max() <= 127 and np.abs(hi).max() <= 127
+    blk = x.reshape(-1, 32).astype(np.float64)
+    assert d[0] == 0.0 and not v[:32].any()
+    rec = v.reshape(-1, 32) * d[:, None].astype(np.float64)
+    assert np.all(np.abs(rec - blk) <= (0.5 + 2.0 ** -8) * d[:, None])
+    amax_idx = np.abs(blk).argmax(axis=1)
+    nz = d > 0
+    assert np.all(np.abs(v.reshape(-1, 32)[np.arange(len(d)), amax_idx][nz]) == 32639)
+    assert np.all(v[64:96] == -32639)
+
+
+@pytest.mark.parametrize("dtype", [moert.Q8_0, moert.Q4_0])
+def test_integer_block_dot_equals_the_float64_dot_of_the_codes(dtype):
+    """The hi/lo block product is exact: the result equals float64 sum_b dw_b*dx_b*(q . v)_b up to the f32
+    accumulation, and differs from the dot with the unrounded x by at most sum |w| * d / 2."""
+    cols = 1536
+    w = moert.synth_quantized(71, dtype, 6 * cols, 0.02, dtype)
+    deq = oracle.dequant(w, dtype, 6 * cols).reshape(6, cols).astype(np.float64)
+    for t in range(4):
+        x = moert.synth_normal(72, t, cols, 1.0 + 10 * t)
+        hi, lo, d = oracle.quant_hilo(x)
+        xq = ((256 * hi.astype(np.float64) + lo) .reshape(-1, 32) * d[:, None]).reshape(-1)
+        for r in range(6):
+            got = oracle.dot_hilo(w, dtype, cols, r, hi, lo, d)
+            exact = float(deq[r] @ xq)
+            scale = float(np.abs(deq[r]) @ np.abs(xq))
+            assert abs(got - exact) <= 48 * 2 ** -23 * scale, (t, r, got, exact)
+            bound = float(np.abs(deq[r]).reshape(-1, 32).sum(axis=1) @ d) / 2
+            assert abs(got - float(deq[r] @ x.astype(np.float64))) <= bound + 48 * 2 ** -23 * scale
+
+
+def test_grouped_experts_step_agrees_with_the_f32_path():
+    """orc_experts_grouped (integer block products of 15-bit activation codes) against Cpu::experts_step in f32
+    (cpu.rs:239-296): the 3B expert shape, 16 positions with Zipf-skewed routing; rel-L2 per position < 2e-4."""
+    hidden, inter, experts, k, m = 1536, 512, 40, 8, 16
+    router = moert.synth_quantized(81, 0, experts * hidden, 0.02, moert.Q8_0)
+    gate_up = moert.synth_quantized(82, 0, experts * 2 * inter * hidden, 0.02, moert.Q8_0)
+    down = moert.synth_quantized(83, 0, experts * hidden * inter, 0.02, moert.Q8_0)
+    bias = moert.zipf_bias(experts, 5)
+    x = moert.synth_normal(84, 0, m * hidden).reshape(m, hidden)
+    y, ids, w = oracle.moe_block_batched(hidden, inter, experts, k, router, gate_up, down, moert.Q8_0, x, bias=bias)
+    ref = oracle.experts_step(hidden, inter, m, k, gate_up, down, moert.Q8_0, x, ids, w)
+    rel = np.linalg.norm(y - ref, axis=1) / np.linalg.norm(ref, axis=1)
+    assert rel.max() < 2e-4, rel
+    assert len(np.unique(ids)) < experts  # the skew leaves some experts unused
+
+
+def test_batched_block_routes_every_position_like_the_single_position_block():
+    """Per-position router + top-k of the batched block equals HostLayer::forward_cpu's (block.rs:56-62), bit for
+    bit, with and without the router bias."""
+    hidden, inter, experts, k, m = 1024, 128, 32, 8, 9
+    router = moert.synth_quantized(91, 0, experts * hidden, 0.02, moert.Q8_0)
+    gate_up = moert.synth_quantized(92, 0, experts * 2 * inter * hidden, 0.02, moert.Q8_0)
+    down = moert.synth_quantized(93, 0, experts * hidden * inter, 0.02, moert.Q8_0)
+    x = moert.synth_normal(94, 0, m * hidden).reshape(m, hidden)
+    for bias in (None, moert.zipf_bias(experts, 3)):
+        _, ids, w = oracle.moe_block_batched(hidden, inter, experts, k, router, gate_up, down, moert.Q8_0, x, bias=bias)
+        for p in range(m):
+            _, i1, w1 = oracle.moe_block(hidden, inter, experts, k, router, gate_up, down, moert.Q8_0, x[p], bias=bias)
+            assert ids[p].tolist() == i1.tolist()
+            assert np.array_equal(w[p].view(np.uint32), w1.view(np.uint32))
+
+
 # ---- whole model ----------------------------------------------------------------------------------------------------
 def _granite_golden():
     import make_granite_golden as g
