@@ -9,9 +9,11 @@ namespace moert {
 
 constexpr int kGrpMaxPos = 32;  // positions per grouped step (the reference caps a step at 32, cuda_backend.rs:272-274)
 
-// Offsets (in ints) of the grouping published by k_grp_up for the down and combine kernels.
-enum { GRP_NU = 0, GRP_LIST = 1, GRP_CNT = 65, GRP_OFF = 129, GRP_UOF = 193, GRP_SLOT = 257,
-       GRP_WORDS = GRP_SLOT + kGrpMaxPos * 8 };
+// Offsets (in ints) of the step plan published by the gate/up kernel: number of distinct experts, then per list
+// index u (first-appearance order) the expert, its member count, its first member slot and its member positions as
+// a bit mask; then per position p its k member slots and routing weights (as float bits) in list order.
+enum { GRP_NU = 0, GRP_LIST = 1, GRP_CNT = 65, GRP_OFF = 129, GRP_BITS = 193, GRP_ORD_SLOT = 257,
+       GRP_ORD_W = GRP_ORD_SLOT + kGrpMaxPos * 8, GRP_WORDS = GRP_ORD_W + kGrpMaxPos * 8 };
 
 // Device buffers of one grouped step, sized for kGrpMaxPos positions, hidden H, inter I and top-k <= 8.
 struct GroupBufs {
@@ -20,7 +22,7 @@ struct GroupBufs {
   int8_t* xh;    // [m, H] hi codes of the block inputs
   int8_t* xl;    // [m, H] lo codes
   float* xd;     // [m, H/32] their block scales
-  int* grp;      // [GRP_WORDS] grouping: list of experts, member counts, offsets, slot of every entry
+  int* grp;      // [GRP_WORDS] the step plan (see GRP_*)
   int8_t* ah;    // [m*k, I] hi codes of the SwiGLU activations, by member slot
   int8_t* al;    // [m*k, I]
   float* ad;     // [m*k, I/32]

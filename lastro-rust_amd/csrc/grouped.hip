@@ -11,10 +11,11 @@
 // y[p] = y[p] + w * o accumulates the experts in list order, as the reference does.
 //
 // Kernels (one stream, in order):
-//   k_grp_route   grid m:            router logits + top-k per position, hi/lo codes of x
-//   k_grp_up      grid (U, I/32):    grouping, gate/up MFMA of expert u for its members, SwiGLU, hi/lo codes of act
-//   k_grp_down    grid (U, H/64):    down MFMA of expert u for its members -> o[member slot]
-//   k_grp_combine grid (m, H/256):   y[p] = ordered sum over p's experts of w * o
+//   k_grp_route   grid m:            router + top-k of position p, hi/lo codes of x_p
+//   k_grp_up      grid (U, I/32):    grouping (every workgroup), gate/up MFMA of list expert u for its members,
+//                                    SwiGLU, hi/lo codes of act; workgroup (0, 0) publishes the plan
+//   k_grp_down    grid (U, H/64):    down MFMA of list expert u for its members -> o[member slot]
+//   k_grp_combine grid (m, H/256):   y[p] = sum over p's experts in list order of w * o
 #include <climits>
 
 #include "dev_rows.h"
@@ -28,13 +29,14 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr int kRouteThreads = 512;
 
 // ------------------------------------------------------------------------------------------------------------
-// Per-position router (canonical dot, optional bias), top-k, and the hi/lo split of x_p.
+// Per-position router (canonical dot, optional bias), top-k, and the hi/lo codes of x_p: workgroup p.
 template <int DT, int H>
 __global__ __launch_bounds__(kRouteThreads) void k_grp_route(DMat router, const float* __restrict__ bias,
                                                              const float* __restrict__ x, int k, GroupBufs g) {
   using G = Geo<DT, H>;
   constexpr int NW = kRouteThreads / 64;
   constexpr int RP = (64 + NW * G::RPW - 1) / (NW * G::RPW);
+  constexpr int NB = H / 32;
   __shared__ float xs[H];
   __shared__ __align__(16) float lg[64];
   __shared__ float slot[3 * 64];
@@ -63,15 +65,15 @@ __global__ __launch_bounds__(kRouteThreads) void k_grp_route(DMat router, const 
   for (int q = 0; q < RP; q++)
     if (ok[q] && sub == 0) lg[row[q]] = bias ? out[q] + bv[q] : out[q];
   // hi/lo codes: 8 lanes per 32-element block, 4 elements per lane
-  {
-    const int t = threadIdx.x, b = t >> 3, part = t & 7;
-    const bool valid = b < H / 32;
+  for (int base = 0; base < NB; base += kRouteThreads / 8) {
+    const int b = base + (threadIdx.x >> 3), part = threadIdx.x & 7;
+    const bool valid = b < NB;
     float v[4];
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       v[i] = valid ? xs[32 * b + 4 * part + i] : 0.0f;
-      float a = fabsf(v[i]);
+      const float a = fabsf(v[i]);
       amax = a > amax ? a : amax;
     }
     amax = group_max<8>(amax);
@@ -79,15 +81,15 @@ __global__ __launch_bounds__(kRouteThreads) void k_grp_route(DMat router, const 
     uint32_t hw = 0, lw = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      int q = d > 0.0f ? (int)__builtin_rintf(v[i] / d) : 0;
-      int h = (q + 128) >> 8;
+      const int q = d > 0.0f ? (int)__builtin_rintf(v[i] / d) : 0;
+      const int h = (q + 128) >> 8;
       hw |= (uint32_t)(uint8_t)(int8_t)h << (8 * i);
       lw |= (uint32_t)(uint8_t)(int8_t)(q - 256 * h) << (8 * i);
     }
     if (valid) {
       reinterpret_cast<uint32_t*>(g.xh + (size_t)p * H)[8 * b + part] = hw;
       reinterpret_cast<uint32_t*>(g.xl + (size_t)p * H)[8 * b + part] = lw;
-      if (part == 0) g.xd[(size_t)p * (H / 32) + b] = d;
+      if (part == 0) g.xd[(size_t)p * NB + b] = d;
     }
   }
   __syncthreads();
@@ -95,59 +97,76 @@ __global__ __launch_bounds__(kRouteThreads) void k_grp_route(DMat router, const 
 }
 
 // ------------------------------------------------------------------------------------------------------------
-// Grouping of the m*k routed (position, expert) entries, in LDS: experts in first-appearance order (list index u),
-// member counts and offsets. Every thread of the workgroup takes part.
-struct GroupLds {
-  int se[kGrpMaxPos * 8];  // expert of entry i = p*k + j
-  int first[64];           // first entry of expert e (INT_MAX if absent)
-  int cnt[64];             // entries of expert e
+// Grouping of the m*k (position, expert) entries, computed in LDS by every workgroup of the gate/up kernel:
+//   list order   experts sorted by their first entry p*k + j (first appearance, as experts_step builds its list)
+//   members      positions routing to the expert, as a bit mask (member index = set bits below the position)
+//   slots        member slot = offset of the expert + member index (rows of the act / o buffers)
+struct Plan {
+  int se[kGrpMaxPos * 8];  // expert of entry p*k + j
+  int first[64];           // first entry of expert e (INT_MAX when unused)
+  unsigned bits[64];       // member positions of expert e
+  int uof[64], offe[64];   // list index and first member slot of expert e
   int list[64];            // expert of list index u
-  int uof[64];             // list index of expert e
-  int cntu[64];            // member count of list index u
-  int offu[64];            // first member slot of list index u
   int nu;
 };
 
 template <int NT>
-__device__ __forceinline__ void group_entries(const int* __restrict__ ids, int n, GroupLds& s) {
-  const int t = threadIdx.x;
-  for (int i = t; i < n; i += NT) s.se[i] = ids[i];
+__device__ __forceinline__ void make_plan(const int* __restrict__ ids, int m, int k, Plan& s) {
+  const int t = threadIdx.x, n = m * k;
+  const int mine = t < n ? ids[t] : 0;
   if (t < 64) {
     s.first[t] = INT_MAX;
-    s.cnt[t] = 0;
-  }
-  if (t == 0) s.nu = 0;
-  __syncthreads();
-  for (int i = t; i < n; i += NT) {
-    atomicMin(&s.first[s.se[i]], i);
-    atomicAdd(&s.cnt[s.se[i]], 1);
+    s.bits[t] = 0u;
   }
   __syncthreads();
-  if (t < 64 && s.cnt[t] > 0) {
-    int u = 0;
-    for (int e = 0; e < 64; e++) u += (s.cnt[e] > 0 && s.first[e] < s.first[t]) ? 1 : 0;
-    s.list[u] = t;
-    s.uof[t] = u;
-    s.cntu[u] = s.cnt[t];
-    atomicAdd(&s.nu, 1);
+  if (t < n) {
+    s.se[t] = mine;
+    atomicMin(&s.first[mine], t);
+    atomicOr(&s.bits[mine], 1u << (t / k));
   }
   __syncthreads();
-  if (t < s.nu) {
-    int o = 0;
-    for (int u = 0; u < t; u++) o += s.cntu[u];
-    s.offu[t] = o;
+  if (t < 64) {
+    // lane e: rank of expert e in first-appearance order and the members of the experts before it
+    const int key = s.bits[t] ? s.first[t] : INT_MAX;
+    const int cnt = __popc(s.bits[t]);
+    int u = 0, off = 0, nu = 0;
+    for (int e = 0; e < 64; e++) {
+      const int ke = __shfl(key, e), ce = __shfl(cnt, e);
+      nu += ke != INT_MAX;
+      if (ke < key) {
+        u++;
+        off += ce;
+      }
+    }
+    if (key != INT_MAX) {
+      s.uof[t] = u;
+      s.offe[t] = off;
+      s.list[u] = t;
+    }
+    if (t == 0) s.nu = nu;
   }
   __syncthreads();
 }
 
-// Positions whose top-k holds expert e, in position order (its members): mp[0, count). Wave 0 only, m <= 32.
-__device__ __forceinline__ void member_positions(const GroupLds& s, int e, int m, int k, int* mp) {
-  const int lane = threadIdx.x & 63;
-  bool has = false;
-  if (lane < m)
-    for (int j = 0; j < k; j++) has |= s.se[lane * k + j] == e;
-  const unsigned long long mask = __ballot(has);
-  if (has) mp[__popcll(mask & ((1ull << lane) - 1ull))] = lane;
+// The plan in global memory for the down and combine kernels (written once, by one workgroup).
+template <int NT>
+__device__ __forceinline__ void publish_plan(const Plan& s, const float* __restrict__ w, int m, int k, int* grp) {
+  const int t = threadIdx.x, n = m * k;
+  if (t == 0) grp[GRP_NU] = s.nu;
+  if (t < s.nu) {
+    const int e = s.list[t];
+    grp[GRP_LIST + t] = e;
+    grp[GRP_CNT + t] = __popc(s.bits[e]);
+    grp[GRP_OFF + t] = s.offe[e];
+    grp[GRP_BITS + t] = (int)s.bits[e];
+  }
+  for (int i = t; i < n; i += NT) {
+    const int p = i / k, e = s.se[i];
+    int rank = 0;
+    for (int j = 0; j < k; j++) rank += s.uof[s.se[p * k + j]] < s.uof[e];
+    grp[GRP_ORD_SLOT + p * 8 + rank] = s.offe[e] + __popc(s.bits[e] & ((1u << p) - 1u));
+    grp[GRP_ORD_W + p * 8 + rank] = __float_as_int(w[i]);
+  }
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -191,69 +210,129 @@ __device__ __forceinline__ void mfma_tile(const uint2 (&a)[NB], const int8_t* bh
   }
 }
 
-// Loads the 8-byte A-operand pieces of NB blocks of one weight row (Q8_0 payload plane) and stages the row's fp16
-// scales into LDS transposed ([b][row-in-tile]).
+// Operands of one wave's 16 weight rows and of the member activations, fetched in the order scales, activations,
+// weights, so that writing the first two into LDS waits only for them while the weight stream is still in flight.
 template <int NB>
-__device__ __forceinline__ void load_rows_q8(const DMat& m, size_t row, int r16, uint2 (&a)[NB], uint16_t* sdt) {
+struct RowScales {
+  uint16_t v[(NB + 3) / 4];
+};
+
+// Scales of the row this lane loads for (row r16 of the tile), blocks grp, grp + 4, ...
+template <int NB>
+__device__ __forceinline__ void fetch_scales(const DMat& m, size_t row, RowScales<NB>& sc) {
+  const int grp = (threadIdx.x & 63) >> 4;
+  const uint16_t* p = m.d + row * (size_t)(m.cols / 32);
+#pragma unroll
+  for (int q = 0; q < (NB + 3) / 4; q++)
+    if (grp + 4 * q < NB) sc.v[q] = p[grp + 4 * q];
+}
+template <int NB>
+__device__ __forceinline__ void store_scales(const RowScales<NB>& sc, int r16, uint16_t* sdt) {
+  const int grp = (threadIdx.x & 63) >> 4;
+#pragma unroll
+  for (int q = 0; q < (NB + 3) / 4; q++)
+    if (grp + 4 * q < NB) sdt[(grp + 4 * q) * 16 + r16] = sc.v[q];
+}
+
+// The 8-byte A-operand pieces of NB blocks of one Q8_0 row: elements 8*(lane/16) .. +8 of each block.
+template <int NB>
+__device__ __forceinline__ void fetch_rows_q8(const DMat& m, size_t row, uint2 (&a)[NB]) {
   const int grp = (threadIdx.x & 63) >> 4;
   const uint8_t* base = m.q + row * (size_t)m.cols + 8 * grp;
 #pragma unroll
   for (int b = 0; b < NB; b++) a[b] = *reinterpret_cast<const uint2*>(base + 32 * b);
-  const uint16_t* sc = m.d + row * (size_t)(m.cols / 32);
-  for (int b = grp; b < NB; b += 4) sdt[b * 16 + r16] = sc[b];
 }
 
-// Member activations into LDS: rows [0, ne) of hi/lo (row length K, padded stride) and their block scales.
+// Member activations: rows row(c) for c in [0, ne) of the hi/lo planes (row length K) and their K/32 block scales;
+// row(c) = off + c (member slots, contiguous) or the c-th set bit of `bits` (member positions).
 template <int K, int NM, int NT>
-__device__ __forceinline__ void load_members(const int8_t* __restrict__ srch, const int8_t* __restrict__ srcl,
-                                             const float* __restrict__ srcd, const int* rows, int ne, int8_t* bh,
-                                             int8_t* bl, int stride, float* dx) {
-  constexpr int C16 = K / 16;  // 16-byte chunks per row
-  for (int i = threadIdx.x; i < NM * C16; i += NT) {
-    const int c = i / C16, j = i % C16;
-    uint4 vh = {0, 0, 0, 0}, vl = {0, 0, 0, 0};
-    if (c < ne) {
-      const size_t r = (size_t)rows[c];
-      vh = reinterpret_cast<const uint4*>(srch + r * K)[j];
-      vl = reinterpret_cast<const uint4*>(srcl + r * K)[j];
+struct Members {
+  static constexpr int C16 = K / 16;
+  static constexpr int PER = (NM * C16 + NT - 1) / NT;
+  static constexpr int PERD = (NM * (K / 32) + NT - 1) / NT;
+  uint4 h[PER], l[PER];
+  float d[PERD];
+};
+
+__device__ __forceinline__ int nth_set_bit(unsigned bits, int c) {
+  for (int i = 0; i < c; i++) bits &= bits - 1u;
+  return __ffs(bits) - 1;
+}
+
+template <int K, int NM, int NT, bool CONTIG>
+__device__ __forceinline__ void fetch_members(const int8_t* __restrict__ srch, const int8_t* __restrict__ srcl,
+                                              const float* __restrict__ srcd, unsigned bits, int off, int ne,
+                                              Members<K, NM, NT>& mb) {
+  using M = Members<K, NM, NT>;
+#pragma unroll
+  for (int q = 0; q < M::PER; q++) {
+    const int i = threadIdx.x + q * NT, c = i / M::C16, j = i % M::C16;
+    mb.h[q] = make_uint4(0, 0, 0, 0);
+    mb.l[q] = make_uint4(0, 0, 0, 0);
+    if (i < NM * M::C16 && c < ne) {
+      const size_t r = CONTIG ? (size_t)(off + c) : (size_t)nth_set_bit(bits, c);
+      mb.h[q] = reinterpret_cast<const uint4*>(srch + r * K)[j];
+      mb.l[q] = reinterpret_cast<const uint4*>(srcl + r * K)[j];
     }
-    *reinterpret_cast<uint4*>(bh + (size_t)c * stride + 16 * j) = vh;
-    *reinterpret_cast<uint4*>(bl + (size_t)c * stride + 16 * j) = vl;
   }
-  for (int i = threadIdx.x; i < NM * (K / 32); i += NT) {
-    const int c = i / (K / 32), b = i % (K / 32);
-    dx[i] = c < ne ? srcd[(size_t)rows[c] * (K / 32) + b] : 0.0f;
+#pragma unroll
+  for (int q = 0; q < M::PERD; q++) {
+    const int i = threadIdx.x + q * NT, c = i / (K / 32), b = i % (K / 32);
+    mb.d[q] = 0.0f;
+    if (i < NM * (K / 32) && c < ne) mb.d[q] = srcd[(CONTIG ? (size_t)(off + c) : (size_t)nth_set_bit(bits, c)) * (K / 32) + b];
+  }
+}
+
+template <int K, int NM, int NT>
+__device__ __forceinline__ void store_members(const Members<K, NM, NT>& mb, int8_t* bh, int8_t* bl, int stride,
+                                              float* dx) {
+  using M = Members<K, NM, NT>;
+#pragma unroll
+  for (int q = 0; q < M::PER; q++) {
+    const int i = threadIdx.x + q * NT, c = i / M::C16, j = i % M::C16;
+    if (i < NM * M::C16) {
+      *reinterpret_cast<uint4*>(bh + (size_t)c * stride + 16 * j) = mb.h[q];
+      *reinterpret_cast<uint4*>(bl + (size_t)c * stride + 16 * j) = mb.l[q];
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < M::PERD; q++) {
+    const int i = threadIdx.x + q * NT;
+    if (i < NM * (K / 32)) dx[i] = mb.d[q];
   }
 }
 
 // ------------------------------------------------------------------------------------------------------------
 // Gate/up of list expert u = blockIdx.x for its members, rows [32t, 32t+32) of gate and of up (t = blockIdx.y):
 // wave w computes 16 rows (w & 1) of gate (w < 2) or up (w >= 2). Then act = silu(g)*u and its hi/lo codes (the
-// 32 rows are one block of the act vector). Workgroup (0, 0) also publishes the grouping for the later kernels.
+// 32 rows are one block of the act vector), written to the members' slots.
 template <int H, int NM>
 __global__ __launch_bounds__(256) void k_grp_up(DMat gu, int m, int k, int inter, GroupBufs g) {
   constexpr int NB = H / 32;
   constexpr int STR = H + 16;
-  __shared__ GroupLds s;
-  __shared__ int mp[kGrpMaxPos];
+  __shared__ Plan plan;
   __shared__ __align__(16) int8_t bh[NM * STR];
   __shared__ __align__(16) int8_t bl[NM * STR];
   __shared__ float dx[NM * NB];
   __shared__ __align__(16) uint16_t sdt[4][NB * 16];
   __shared__ float gout[2][32][NM + 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int n = m * k;
-  group_entries<256>(g.ids, n, s);
   const int u = blockIdx.x, tile = blockIdx.y;
-  if (u >= s.nu) return;
-  const int e = s.list[u], ne = s.cntu[u];
+  make_plan<256>(g.ids, m, k, plan);
+  if (u >= plan.nu) return;
+  const int e = plan.list[u], off = plan.offe[e];
+  const unsigned bits = plan.bits[e];
+  const int ne = __popc(bits);
   const int r16 = lane & 15;
   const size_t row = (size_t)e * 2 * inter + (size_t)(wave >> 1) * inter + 32 * tile + 16 * (wave & 1) + r16;
+  RowScales<NB> sc;
+  fetch_scales<NB>(gu, row, sc);
+  Members<H, NM, 256> mb;
+  fetch_members<H, NM, 256, false>(g.xh, g.xl, g.xd, bits, 0, ne, mb);
   uint2 a[NB];
-  load_rows_q8<NB>(gu, row, r16, a, sdt[wave]);
-  if (wave == 0) member_positions(s, e, m, k, mp);
-  __syncthreads();
-  load_members<H, NM, 256>(g.xh, g.xl, g.xd, mp, ne, bh, bl, STR, dx);
+  fetch_rows_q8<NB>(gu, row, a);
+  store_scales<NB>(sc, r16, sdt[wave]);
+  store_members<H, NM, 256>(mb, bh, bl, STR, dx);
   __syncthreads();
   float acc[NM / 16][4];
   mfma_tile<NB, NM>(a, bh, bl, STR, sdt[wave], dx, acc);
@@ -287,30 +366,13 @@ __global__ __launch_bounds__(256) void k_grp_up(DMat gu, int m, int k, int inter
       lw |= (uint32_t)(uint8_t)(int8_t)(q - 256 * h) << (8 * i);
     }
     if (valid) {
-      const size_t slot = (size_t)(s.offu[u] + j);
-      reinterpret_cast<uint32_t*>(g.ah + slot * inter + 32 * tile)[part] = hw;
-      reinterpret_cast<uint32_t*>(g.al + slot * inter + 32 * tile)[part] = lw;
-      if (part == 0) g.ad[slot * (inter / 32) + tile] = d;
+      const size_t slotv = (size_t)(off + j);
+      reinterpret_cast<uint32_t*>(g.ah + slotv * inter + 32 * tile)[part] = hw;
+      reinterpret_cast<uint32_t*>(g.al + slotv * inter + 32 * tile)[part] = lw;
+      if (part == 0) g.ad[slotv * (inter / 32) + tile] = d;
     }
   }
-  if (u == 0 && tile == 0) {
-    // grouping for k_grp_down / k_grp_combine: list, counts, offsets, and the member slot of every entry
-    const int t = threadIdx.x;
-    if (t == 0) g.grp[GRP_NU] = s.nu;
-    if (t < 64) {
-      g.grp[GRP_LIST + t] = t < s.nu ? s.list[t] : 0;
-      g.grp[GRP_CNT + t] = t < s.nu ? s.cntu[t] : 0;
-      g.grp[GRP_OFF + t] = t < s.nu ? s.offu[t] : 0;
-      g.grp[GRP_UOF + t] = s.cnt[t] > 0 ? s.uof[t] : 0;
-    }
-    for (int i = t; i < n; i += 256) {
-      const int ee = s.se[i], p = i / k;
-      int before = 0;  // earlier positions that also route to ee
-      for (int q = 0; q < p; q++)
-        for (int jj = 0; jj < k; jj++) before += s.se[q * k + jj] == ee;
-      g.grp[GRP_SLOT + i] = s.offu[s.uof[ee]] + before;
-    }
-  }
+  if (u == 0 && tile == 0) publish_plan<256>(plan, g.w, m, k, g.grp);
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -319,7 +381,6 @@ template <int I, int NM>
 __global__ __launch_bounds__(256) void k_grp_down(DMat dn, int hidden, GroupBufs g) {
   constexpr int NB = I / 32;
   constexpr int STR = I + 16;
-  __shared__ int slots[kGrpMaxPos];
   __shared__ __align__(16) int8_t bh[NM * STR];
   __shared__ __align__(16) int8_t bl[NM * STR];
   __shared__ float dx[NM * NB];
@@ -330,11 +391,15 @@ __global__ __launch_bounds__(256) void k_grp_down(DMat dn, int hidden, GroupBufs
   const int e = g.grp[GRP_LIST + u], ne = g.grp[GRP_CNT + u], off = g.grp[GRP_OFF + u];
   const int r16 = lane & 15;
   const int r = 64 * tile + 16 * wave + r16;
+  const size_t row = (size_t)e * hidden + r;
+  RowScales<NB> sc;
+  fetch_scales<NB>(dn, row, sc);
+  Members<I, NM, 256> mb;
+  fetch_members<I, NM, 256, true>(g.ah, g.al, g.ad, 0u, off, ne, mb);
   uint2 a[NB];
-  load_rows_q8<NB>(dn, (size_t)e * hidden + r, r16, a, sdt[wave]);
-  if (threadIdx.x < kGrpMaxPos) slots[threadIdx.x] = off + threadIdx.x;
-  __syncthreads();
-  load_members<I, NM, 256>(g.ah, g.al, g.ad, slots, ne, bh, bl, STR, dx);
+  fetch_rows_q8<NB>(dn, row, a);
+  store_scales<NB>(sc, r16, sdt[wave]);
+  store_members<I, NM, 256>(mb, bh, bl, STR, dx);
   __syncthreads();
   float acc[NM / 16][4];
   mfma_tile<NB, NM>(a, bh, bl, STR, sdt[wave], dx, acc);
@@ -353,32 +418,26 @@ __global__ __launch_bounds__(256) void k_grp_down(DMat dn, int hidden, GroupBufs
 // ------------------------------------------------------------------------------------------------------------
 // y[p][r] = sum over p's experts in list order of w * o[slot][r] (the reference's acc[p] += w * o).
 __global__ __launch_bounds__(256) void k_grp_combine(int k, int hidden, GroupBufs g, float* __restrict__ y) {
-  __shared__ int ord_slot[8];
-  __shared__ float ord_w[8];
-  const int p = blockIdx.x, t = threadIdx.x;
-  if (t == 0) {
-    int us[8], sl[8];
-    float ws[8];
-    for (int j = 0; j < k; j++) {
-      us[j] = g.grp[GRP_UOF + g.ids[p * k + j]];
-      sl[j] = g.grp[GRP_SLOT + p * k + j];
-      ws[j] = g.w[p * k + j];
-    }
-    for (int j = 0; j < k; j++) {  // rank by list index (distinct)
-      int rank = 0;
-      for (int q = 0; q < k; q++) rank += us[q] < us[j];
-      ord_slot[rank] = sl[j];
-      ord_w[rank] = ws[j];
-    }
+  const int p = blockIdx.x;
+  const int r = blockIdx.y * 256 + threadIdx.x;
+  int sl[8];
+  float wt[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) {
+    sl[j] = j < k ? g.grp[GRP_ORD_SLOT + p * 8 + j] : 0;
+    wt[j] = j < k ? __int_as_float(g.grp[GRP_ORD_W + p * 8 + j]) : 0.0f;
   }
-  __syncthreads();
-  const int r = blockIdx.y * 256 + t;
   if (r >= hidden) return;
+  float ov[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) ov[j] = j < k ? g.o[(size_t)sl[j] * hidden + r] : 0.0f;
   float acc = 0.0f;
-  for (int j = 0; j < k; j++) {
-    const float tw = ord_w[j] * g.o[(size_t)ord_slot[j] * hidden + r];
-    acc = acc + tw;
-  }
+#pragma unroll
+  for (int j = 0; j < 8; j++)
+    if (j < k) {
+      const float tw = wt[j] * ov[j];
+      acc = acc + tw;
+    }
   y[(size_t)p * hidden + r] = acc;
 }
 
