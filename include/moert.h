@@ -97,6 +97,22 @@ int moert_model_create(const moert_config* cfg, const moert_model_weights* w, in
                        moert_model** out);
 int moert_model_destroy(moert_model* m);
 
+/* Same model with the experts served from an expert cache: every expert of every layer lives in pinned host memory
+ * and `slots` of them at a time in an HBM pool (top_k <= slots <= min(4096, layers*experts)). Each layer step
+ * routes on the device, then applies the LRU rule of the reference's LruSync cache: every requested expert already
+ * in the pool is pinned for the step, each miss (in top-k order) takes the first free slot or else the least
+ * recently used slot not used in this step (lowest slot index on ties), and is copied in from host memory by a
+ * device kernel before the experts run. No host synchronisation per layer: a step stays one graph. Outputs are
+ * identical to moert_model_create's. Replaces GpuModel::upload_cached + ExpertCache (rust/moe-rt/src/gpu_model.rs:
+ * 197-200, rust/moe-rt/src/cache.rs:140-354, LRU rule of rust/moe-rt/tests/model.rs:380-412). */
+int moert_model_create_cached(const moert_config* cfg, const moert_model_weights* w, int max_len, int attn_splits,
+                              int slots, moert_model** out);
+/* Cache counters since creation or the last clear: requests served from the pool, and copies from host memory
+ * (CacheStats::{hits, sync_copies}, rust/moe-rt/src/cache.rs:112-124). */
+int moert_cache_stats(moert_model* m, unsigned long long* hits, unsigned long long* copies);
+/* Empties the pool and zeroes the counters (ExpertCache::clear, rust/moe-rt/src/cache.rs:216-220). */
+int moert_cache_clear(moert_model* m);
+
 /* One token at the current position: logits of the next position (vocab floats, divided by logits_scaling),
  * the router decision of every layer (layers*top_k ids and weights, top-k order) and the greedy argmax.
  * Any output pointer may be NULL. Replaces GpuModel::step (rust/moe-rt/src/gpu_model.rs:251-267). */
@@ -144,7 +160,9 @@ typedef enum {
   MOERT_K_EXPERT_DOWN = 6,  /* down of the routed experts + weighted combine + residual */
   MOERT_K_HEAD = 7,         /* final rmsnorm + LM head + per-block argmax */
   MOERT_K_HEAD_ARGMAX = 8,  /* argmax over the head blocks, token and position update */
-  MOERT_K_COUNT = 9
+  MOERT_K_ROUTE_LRU = 9,    /* expert cache: rmsnorm + router + top-k + LRU decision (cached models) */
+  MOERT_K_FILL = 10,        /* expert cache: copy of the misses from host memory into the pool (cached models) */
+  MOERT_K_COUNT = 11
 } moert_kernel_kind;
 int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch, int* launches);
 

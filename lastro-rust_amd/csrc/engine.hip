@@ -18,6 +18,7 @@
 
 #include "../../include/moert.h"
 #include "host_utils.h"
+#include "cache.h"
 #include "grouped.h"
 #include "kernels.h"
 
@@ -74,6 +75,34 @@ struct Arena {
 
 bool valid_dtype(int dt) { return dt == MOERT_F32 || dt == MOERT_Q8_0 || dt == MOERT_Q4_0; }
 
+size_t payload_bytes(int dtype, int cols) {
+  return dtype == MOERT_Q8_0 ? (size_t)cols : dtype == MOERT_Q4_0 ? (size_t)cols / 2 : (size_t)cols * 4;
+}
+
+// Rows [row0, row0 + n) of a GGML blob ([*, cols] of dtype) into a payload plane (n * payload_bytes) and a scale
+// plane (n * cols/32 fp16; untouched for f32).
+void repack_rows(const void* src_, int dtype, int cols, size_t row0, size_t n, uint8_t* q, uint16_t* d) {
+  const uint8_t* src = (const uint8_t*)src_;
+  const size_t nb = n * (cols / 32);
+  if (dtype == MOERT_F32) {
+    std::memcpy(q, src + row0 * cols * 4, n * cols * 4);
+  } else if (dtype == MOERT_Q8_0) {
+    src += row0 * (cols / 32) * 34;
+    for (size_t b = 0; b < nb; b++) {
+      const uint8_t* blk = src + b * 34;
+      d[b] = (uint16_t)(blk[0] | (blk[1] << 8));
+      std::memcpy(q + b * 32, blk + 2, 32);
+    }
+  } else {
+    src += row0 * (cols / 32) * 18;
+    for (size_t b = 0; b < nb; b++) {
+      const uint8_t* blk = src + b * 18;
+      d[b] = (uint16_t)(blk[0] | (blk[1] << 8));
+      std::memcpy(q + b * 16, blk + 2, 16);
+    }
+  }
+}
+
 // Repacks `parts` (each [rows_i, cols] of one dtype, GGML blocks) into one SoA device matrix.
 struct Part {
   const void* data;
@@ -87,7 +116,7 @@ int upload_matrix(Arena& a, hipStream_t s, const std::vector<Part>& parts, int d
     CHECK_CFG(p.data != nullptr, "missing weight tensor");
     rows += (size_t)p.rows;
   }
-  size_t plane = dtype == MOERT_Q8_0 ? rows * cols : dtype == MOERT_Q4_0 ? rows * cols / 2 : rows * cols * 4;
+  size_t plane = rows * payload_bytes(dtype, cols);
   size_t scales = dtype == MOERT_F32 ? 0 : rows * (cols / 32) * 2;
   void* dev;
   int rc = a.alloc(&dev, align256(plane) + scales);
@@ -96,27 +125,8 @@ int upload_matrix(Arena& a, hipStream_t s, const std::vector<Part>& parts, int d
   std::vector<uint16_t> d(scales / 2);
   size_t r0 = 0;
   for (const Part& p : parts) {
-    const uint8_t* src = (const uint8_t*)p.data;
-    size_t nb = (size_t)p.rows * (cols / 32);
-    if (dtype == MOERT_F32) {
-      std::memcpy(q.data() + r0 * cols * 4, src, (size_t)p.rows * cols * 4);
-    } else if (dtype == MOERT_Q8_0) {
-      uint8_t* qd = q.data() + r0 * cols;
-      uint16_t* dd = d.data() + r0 * (cols / 32);
-      for (size_t b = 0; b < nb; b++) {
-        const uint8_t* blk = src + b * 34;
-        dd[b] = (uint16_t)(blk[0] | (blk[1] << 8));
-        std::memcpy(qd + b * 32, blk + 2, 32);
-      }
-    } else {
-      uint8_t* qd = q.data() + r0 * cols / 2;
-      uint16_t* dd = d.data() + r0 * (cols / 32);
-      for (size_t b = 0; b < nb; b++) {
-        const uint8_t* blk = src + b * 18;
-        dd[b] = (uint16_t)(blk[0] | (blk[1] << 8));
-        std::memcpy(qd + b * 16, blk + 2, 16);
-      }
-    }
+    repack_rows(p.data, dtype, cols, 0, (size_t)p.rows, q.data() + r0 * payload_bytes(dtype, cols),
+                d.empty() ? nullptr : d.data() + r0 * (cols / 32));
     r0 += (size_t)p.rows;
   }
   CHECK_HIP(hipMemcpyAsync(dev, q.data(), plane, hipMemcpyHostToDevice, s));
@@ -170,6 +180,11 @@ struct moert_model {
   int n_head_blocks = 0;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  // expert cache (ExpertCache, rust/moe-rt/src/cache.rs): experts live in the pinned host store, `cache.slots` of
+  // them at a time in the HBM pool
+  bool cached = false;
+  CacheDev cache{};
+  void* host_store = nullptr;
 
   // Launches one decode step. With `timed` >= 0, every launch of that kernel class records its dispatch start and
   // end into the next event pair of `ev`.
@@ -193,10 +208,21 @@ struct moert_model {
       CHECK_HIP(launch_attn_combine(stream, dims, b));
       arm(MOERT_K_OPROJ);
       CHECK_HIP(launch_oproj(stream, L, dims, b));
-      arm(MOERT_K_ROUTE_UP);
-      CHECK_HIP(launch_route_up(stream, L, dims, b, (int)l, true));
-      arm(MOERT_K_EXPERT_DOWN);
-      CHECK_HIP(launch_expert_down(stream, L, dims, b, (int)l, true));
+      if (cached) {
+        arm(MOERT_K_ROUTE_LRU);
+        CHECK_HIP(launch_route_lru(stream, L, dims, b, (int)l, cache));
+        arm(MOERT_K_FILL);
+        CHECK_HIP(launch_fill(stream, cache, dims.top_k));
+        arm(MOERT_K_ROUTE_UP);
+        CHECK_HIP(launch_up_routed(stream, cache.pool_gu, L.ln_moe, dims, b, (int)l, cache.route_slot));
+        arm(MOERT_K_EXPERT_DOWN);
+        CHECK_HIP(launch_expert_down_slots(stream, cache.pool_dn, dims, b, (int)l, cache.route_slot));
+      } else {
+        arm(MOERT_K_ROUTE_UP);
+        CHECK_HIP(launch_route_up(stream, L, dims, b, (int)l, true));
+        arm(MOERT_K_EXPERT_DOWN);
+        CHECK_HIP(launch_expert_down(stream, L, dims, b, (int)l, true));
+      }
     }
     arm(MOERT_K_HEAD);
     CHECK_HIP(launch_head(stream, embed, norm, dims, b));
@@ -234,17 +260,98 @@ struct moert_model {
     return MOERT_OK;
   }
 
+  // Empties the pool and zeroes the clock and the counters (ExpertCache::clear, rust/moe-rt/src/cache.rs:216-220).
+  int cache_clear() {
+    CHECK_HIP(hipMemsetAsync(cache.slot_key, 0xff, (size_t)cache.slots * 4, stream));
+    CHECK_HIP(hipMemsetAsync(cache.slot_last, 0, (size_t)cache.slots * 4, stream));
+    CHECK_HIP(hipMemsetAsync(cache.key_slot, 0xff, (size_t)cfg.layers * cfg.experts * 4, stream));
+    CHECK_HIP(hipMemsetAsync(cache.clock, 0, 4, stream));
+    CHECK_HIP(hipMemsetAsync(cache.stats, 0, CS_WORDS * 8, stream));
+    CHECK_HIP(hipStreamSynchronize(stream));
+    return MOERT_OK;
+  }
+
   ~moert_model() {
     if (stream) (void)hipStreamSynchronize(stream);
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
     arena.release();
+    if (host_store) (void)hipHostFree(host_store);
     if (stream) (void)hipStreamDestroy(stream);
   }
 };
 
+// Experts of every layer into a pinned host store of records [gu payload | gu scales | down payload | down scales]
+// (key = layer * E + expert) and an HBM pool of `slots` records as two SoA matrices; LRU tables emptied.
+static int cache_create(moert_model* m, const moert_model_weights* w, int slots) {
+  const moert_config& c = m->cfg;
+  const int H = c.hidden, I = c.inter, E = c.experts, L = c.layers;
+  const int dt = w->layers[0].gate_up.dtype;
+  for (int l = 0; l < L; l++)
+    CHECK_CFG(w->layers[l].gate_up.dtype == dt && w->layers[l].down.dtype == dt,
+              "expert cache: every layer's experts must share one dtype");
+  CHECK_CFG(slots >= c.top_k && slots <= kCacheMaxSlots && slots <= L * E,
+            "expert cache: %d slots outside [top_k, min(%d, layers*experts)]", slots, kCacheMaxSlots);
+  CacheDev& cd = m->cache;
+  const size_t gu_rows = 2 * (size_t)I, dn_rows = H;
+  cd.gu_q = gu_rows * payload_bytes(dt, H);
+  cd.gu_d = dt == MOERT_F32 ? 0 : gu_rows * (H / 32) * 2;
+  cd.dn_q = dn_rows * payload_bytes(dt, I);
+  const size_t dn_d = dt == MOERT_F32 ? 0 : dn_rows * (I / 32) * 2;
+  cd.record_bytes = cd.gu_q + cd.gu_d + cd.dn_q + dn_d;
+  CHECK_CFG(cd.gu_q % 16 == 0 && cd.gu_d % 16 == 0 && cd.dn_q % 16 == 0 && dn_d % 16 == 0,
+            "expert cache: record pieces must be multiples of 16 bytes");
+  const size_t total = cd.record_bytes * (size_t)L * E;
+  CHECK_HIP(hipHostMalloc(&m->host_store, total, hipHostMallocMapped | hipHostMallocNonCoherent));
+  uint8_t* hs = (uint8_t*)m->host_store;
+  for (int l = 0; l < L; l++) {
+    const moert_layer_weights& W = w->layers[l];
+    CHECK_CFG(W.gate_up.data && W.down.data, "layer %d: missing experts", l);
+    for (int e = 0; e < E; e++) {
+      uint8_t* r = hs + ((size_t)l * E + e) * cd.record_bytes;
+      repack_rows(W.gate_up.data, dt, H, (size_t)e * gu_rows, gu_rows, r, (uint16_t*)(r + cd.gu_q));
+      uint8_t* rd = r + cd.gu_q + cd.gu_d;
+      repack_rows(W.down.data, dt, I, (size_t)e * dn_rows, dn_rows, rd, (uint16_t*)(rd + cd.dn_q));
+    }
+  }
+  void* dev_host = nullptr;
+  CHECK_HIP(hipHostGetDevicePointer(&dev_host, m->host_store, 0));
+  cd.host = (const uint8_t*)dev_host;
+  Arena& a = m->arena;
+  void* p;
+  int rc;
+  auto mat = [&](size_t rows, int cols, DMat* out) -> int {
+    const size_t plane = rows * payload_bytes(dt, cols), sc = dt == MOERT_F32 ? 0 : rows * (cols / 32) * 2;
+    int r = a.alloc(&p, align256(plane) + sc);
+    if (r) return r;
+    *out = DMat{(const uint8_t*)p, sc ? (const uint16_t*)((uint8_t*)p + align256(plane)) : nullptr, dt, (int)rows, cols};
+    return MOERT_OK;
+  };
+  if ((rc = mat((size_t)slots * gu_rows, H, &cd.pool_gu)) || (rc = mat((size_t)slots * dn_rows, I, &cd.pool_dn)))
+    return rc;
+  // the pool's slot pieces must start where the fill kernel writes them: payload planes are contiguous per slot
+  cd.slots = slots;
+  cd.experts = E;
+  if ((rc = a.alloc(&p, (size_t)slots * 4))) return rc;
+  cd.slot_key = (int*)p;
+  if ((rc = a.alloc(&p, (size_t)slots * 4))) return rc;
+  cd.slot_last = (int*)p;
+  if ((rc = a.alloc(&p, (size_t)L * E * 4))) return rc;
+  cd.key_slot = (int*)p;
+  if ((rc = a.alloc(&p, 256))) return rc;
+  cd.clock = (int*)p;
+  if ((rc = a.alloc(&p, CS_WORDS * 8))) return rc;
+  cd.stats = (unsigned long long*)p;
+  if ((rc = a.alloc(&p, 8 * 4))) return rc;
+  cd.route_slot = (int*)p;
+  if ((rc = a.alloc(&p, (1 + 2 * 8) * 4))) return rc;
+  cd.miss = (int*)p;
+  m->cached = true;
+  return m->cache_clear();
+}
+
 static int model_create(const moert_config* c, const moert_model_weights* w, int max_len, int splits,
-                        moert_model** out) {
+                        int cache_slots, moert_model** out) {
   CHECK_CFG(c && w && out, "null argument");
   *out = nullptr;
   CHECK_CFG(c->head_dim == 64, "head_dim %d: the attention kernels are built for 64", c->head_dim);
@@ -300,8 +407,10 @@ static int model_create(const moert_config* c, const moert_model_weights* w, int
       if ((rc = upload_f32(a, s, W.router_bias, E, &tmp))) return bail(rc);
       L.router_bias = tmp;
     }
-    if ((rc = upload_matrix(a, s, {{W.gate_up.data, E * 2 * I}}, W.gate_up.dtype, H, &L.gate_up))) return bail(rc);
-    if ((rc = upload_matrix(a, s, {{W.down.data, E * H}}, W.down.dtype, I, &L.down))) return bail(rc);
+    if (cache_slots == 0) {
+      if ((rc = upload_matrix(a, s, {{W.gate_up.data, E * 2 * I}}, W.gate_up.dtype, H, &L.gate_up))) return bail(rc);
+      if ((rc = upload_matrix(a, s, {{W.down.data, E * H}}, W.down.dtype, I, &L.down))) return bail(rc);
+    }
     if ((rc = zeros(a, s, (size_t)c->kv_heads * max_len * d, &L.k_cache))) return bail(rc);
     if ((rc = zeros(a, s, (size_t)c->kv_heads * max_len * d, &L.v_cache))) return bail(rc);
   }
@@ -334,6 +443,7 @@ static int model_create(const moert_config* c, const moert_model_weights* w, int
     set_err("upload failed");
     return bail(MOERT_E_DEVICE);
   }
+  if (cache_slots > 0 && (rc = cache_create(m, w, cache_slots))) return bail(rc);
   if ((rc = m->build_graph())) return bail(rc);
   *out = m;
   return MOERT_OK;
@@ -444,7 +554,13 @@ int moert_device_info(int* count, char* name, int name_len) {
 
 int moert_model_create(const moert_config* cfg, const moert_model_weights* w, int max_len, int attn_splits,
                        moert_model** out) {
-  return model_create(cfg, w, max_len, attn_splits, out);
+  return model_create(cfg, w, max_len, attn_splits, 0, out);
+}
+
+int moert_model_create_cached(const moert_config* cfg, const moert_model_weights* w, int max_len, int attn_splits,
+                              int slots, moert_model** out) {
+  CHECK_CFG(slots >= 1, "expert cache: %d slots", slots);
+  return model_create(cfg, w, max_len, attn_splits, slots, out);
 }
 
 int moert_model_destroy(moert_model* m) {
@@ -698,6 +814,23 @@ int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch
   int st[2] = {m->host_pos, 0};
   MTRY(m, model_copy_in(m, m->b.state, st, sizeof st));
   MTRY(m, time_kernel_impl(m, kind, iters, us_per_launch, launches));
+  return MOERT_OK;
+}
+
+int moert_cache_stats(moert_model* m, unsigned long long* hits, unsigned long long* copies) {
+  MODEL_OK(m);
+  CHECK_CFG(m->cached, "model has no expert cache");
+  unsigned long long st[CS_WORDS];
+  MTRY(m, model_copy_out(m, st, m->cache.stats, sizeof st));
+  if (hits) *hits = st[CS_HITS];
+  if (copies) *copies = st[CS_COPIES];
+  return MOERT_OK;
+}
+
+int moert_cache_clear(moert_model* m) {
+  MODEL_OK(m);
+  CHECK_CFG(m->cached, "model has no expert cache");
+  MTRY(m, m->cache_clear());
   return MOERT_OK;
 }
 

@@ -343,12 +343,15 @@ __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restric
 // cpu.rs:116-137). E <= 64, k <= 8.
 constexpr int kRouteWaves = 8;
 
-template <int DT, int K, int NP, bool NORM>
+// ROUTED: the routing is already made (expert-cache path): slots_in holds the k slot ids of the routed experts in
+// gu and w_out their weights; the router is skipped.
+template <int DT, int K, int NP, bool NORM, bool ROUTED>
 __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, const float* __restrict__ bias, DMat gu,
                                                                const float* __restrict__ h,
                                                                const float* __restrict__ lnw, float eps, int k,
                                                                int inter, int* __restrict__ ids_out,
-                                                               float* __restrict__ w_out, float* __restrict__ act) {
+                                                               float* __restrict__ w_out, float* __restrict__ act,
+                                                               const int* __restrict__ slots_in) {
   using G = Geo<DT, K>;
   constexpr int NT = kRouteWaves * 64;
   constexpr int RP = (64 + kRouteWaves * G::RPW - 1) / (kRouteWaves * G::RPW);  // router passes for 64 rows
@@ -363,7 +366,17 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
   int sub = lane % G::LPR, rw = lane / G::LPR;
   const int E = router.rows;
   XReg<DT, K> xr;
-  {
+  if (ROUTED) {
+    if (threadIdx.x < k) {
+      sids[threadIdx.x] = slots_in[threadIdx.x];
+      sw[threadIdx.x] = w_out[threadIdx.x];
+    }
+    if (NORM)
+      wg_norm<K, NT>(h, lnw, eps, xs, &rs);
+    else
+      wg_copy<K, NT>(h, xs);
+    load_x<DT, K>(xr, xs, sub);
+  } else {
     size_t row[RP];
     bool ok[RP];
 #pragma unroll
@@ -388,7 +401,7 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
       if (ok[p] && sub == 0) lg[row[p]] = bias ? out[p] + bv[p] : out[p];
   }
   __syncthreads();
-  if (wave == 0) {
+  if (!ROUTED && wave == 0) {
     wave_topk(lg, E, k, lane, slot, sids, sw);
     if (blockIdx.x == 0 && lane < k) {
       ids_out[lane] = sids[lane];
@@ -702,26 +715,6 @@ __global__ void k_exp(const float* __restrict__ x, float* __restrict__ y, int n)
 // ------------------------------------------------------------------------------------------------------------
 // Launchers. Row lengths are compile-time; the switch covers the shapes of the Granite-MoE family and the small
 // test models.
-#define MOERT_K_CASES(X) X(128) X(256) X(512) X(1024) X(1536)
-#define MOERT_KDOWN_CASES(X) X(128) X(256) X(512)
-
-#define MOERT_DISPATCH(dt, K, BODY)                                   \
-  switch (dt) {                                                       \
-    case DT_Q8_0: {                                                   \
-      constexpr int DTC = DT_Q8_0;                                    \
-      switch (K) { MOERT_K_CASES(BODY) default: return hipErrorInvalidValue; } \
-    } break;                                                          \
-    case DT_Q4_0: {                                                   \
-      constexpr int DTC = DT_Q4_0;                                    \
-      switch (K) { MOERT_K_CASES(BODY) default: return hipErrorInvalidValue; } \
-    } break;                                                          \
-    case DT_F32: {                                                    \
-      constexpr int DTC = DT_F32;                                     \
-      switch (K) { MOERT_K_CASES(BODY) default: return hipErrorInvalidValue; } \
-    } break;                                                          \
-    default:                                                          \
-      return hipErrorInvalidValue;                                    \
-  }
 
 template <int DT, int K, int P>
 constexpr int rows_per_block() { return kWavesPerBlock * P * Geo<DT, K>::RPW; }
@@ -831,15 +824,47 @@ hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, cons
     constexpr int PB = kRouteWaves * kRouteNP * Geo<DTC, KK>::RPW;                                         \
     const int blocks = cdiv((long)d.top_k * d.inter, PB);                                                  \
     if (normalize)                                                                                         \
-      klaunch(k_route_up<DTC, KK, kRouteNP, true>, blocks, kRouteWaves * 64, 0, s,                              \
+      klaunch(k_route_up<DTC, KK, kRouteNP, true, false>, blocks, kRouteWaves * 64, 0, s,                       \
           L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter,                      \
-          b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act);                              \
+          b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, (const int*)nullptr);         \
     else                                                                                                   \
-      klaunch(k_route_up<DTC, KK, kRouteNP, false>, blocks, kRouteWaves * 64, 0, s,                             \
+      klaunch(k_route_up<DTC, KK, kRouteNP, false, false>, blocks, kRouteWaves * 64, 0, s,                      \
           L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter,                      \
-          b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act);                              \
+          b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, (const int*)nullptr);         \
   } break;
   MOERT_DISPATCH(L.router.dtype, L.router.cols, BODY)
+#undef BODY
+  return hipGetLastError();
+}
+
+hipError_t launch_up_routed(hipStream_t s, const DMat& gu, const float* lnw, const Dims& d, const StepBufs& b,
+                            int layer, const int* slots) {
+#define BODY(KK)                                                                                           \
+  case KK: {                                                                                               \
+    constexpr int PB = kRouteWaves * kRouteNP * Geo<DTC, KK>::RPW;                                         \
+    const int blocks = cdiv((long)d.top_k * d.inter, PB);                                                  \
+    klaunch(k_route_up<DTC, KK, kRouteNP, true, true>, blocks, kRouteWaves * 64, 0, s, gu, (const float*)nullptr, \
+            gu, b.h, lnw, d.eps, d.top_k, d.inter, b.route_ids + layer * d.top_k,                          \
+            b.route_w + layer * d.top_k, b.act, slots);                                                    \
+  } break;
+  MOERT_DISPATCH(gu.dtype, gu.cols, BODY)
+#undef BODY
+  return hipGetLastError();
+}
+
+hipError_t launch_expert_down_slots(hipStream_t s, const DMat& down, const Dims& d, const StepBufs& b, int layer,
+                                   const int* slots) {
+#define BODY(KK)                                                                                          \
+  case KK:                                                                                                \
+    klaunch(k_expert_down<DTC, KK>, cdiv(d.hidden, kWavesPerBlock), kBlock, 0, s, down, b.act, slots,      \
+            b.route_w + layer * d.top_k, d.top_k, d.hidden, d.res_mult, true, b.h);                       \
+    break;
+  switch (down.dtype) {
+    case DT_Q8_0: { constexpr int DTC = DT_Q8_0; switch (down.cols) { MOERT_KDOWN_CASES(BODY) default: return hipErrorInvalidValue; } } break;
+    case DT_Q4_0: { constexpr int DTC = DT_Q4_0; switch (down.cols) { MOERT_KDOWN_CASES(BODY) default: return hipErrorInvalidValue; } } break;
+    case DT_F32: { constexpr int DTC = DT_F32; switch (down.cols) { MOERT_KDOWN_CASES(BODY) default: return hipErrorInvalidValue; } } break;
+    default: return hipErrorInvalidValue;
+  }
 #undef BODY
   return hipGetLastError();
 }

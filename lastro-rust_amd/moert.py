@@ -23,9 +23,10 @@ F32, Q8_0, Q4_0 = 0, 1, 2
 DTYPE_NAMES = {F32: "f32", Q8_0: "q8_0", Q4_0: "q4_0"}
 
 (K_EMBED, K_QKV, K_ATTN_SPLIT, K_ATTN_COMBINE, K_OPROJ, K_ROUTE_UP, K_EXPERT_DOWN, K_HEAD,
- K_HEAD_ARGMAX) = range(9)
+ K_HEAD_ARGMAX, K_ROUTE_LRU, K_FILL) = range(11)
 KERNEL_NAMES = ["embed", "qkv", "attn_split", "attn_combine", "oproj", "route_up", "expert_down", "head",
-                "head_argmax"]
+                "head_argmax"]   # the resident model's kernel classes
+CACHE_KERNEL_NAMES = ["route_lru", "fill"]
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmoert.so")
@@ -81,6 +82,10 @@ def lib() -> ctypes.CDLL:
             "moert_model_create": (i, [ctypes.POINTER(moert_config), ctypes.POINTER(moert_model_weights), i, i,
                                        ctypes.POINTER(vp)]),
             "moert_model_destroy": (i, [vp]),
+            "moert_model_create_cached": (i, [ctypes.POINTER(moert_config), ctypes.POINTER(moert_model_weights), i,
+                                              i, i, ctypes.POINTER(vp)]),
+            "moert_cache_stats": (i, [vp, ctypes.POINTER(ctypes.c_ulonglong), ctypes.POINTER(ctypes.c_ulonglong)]),
+            "moert_cache_clear": (i, [vp]),
             "moert_decode_step": (i, [vp, i, vp, vp, vp, ip]),
             "moert_generate": (i, [vp, vp, i, i, vp, vp]),
             "moert_reset_sequence": (i, [vp]),
@@ -123,6 +128,7 @@ def lib() -> ctypes.CDLL:
 
 
 EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moert_model_destroy",
+            "moert_model_create_cached", "moert_cache_stats", "moert_cache_clear",
             "moert_decode_step", "moert_generate", "moert_reset_sequence", "moert_kv_prefill_fp16",
             "moert_set_position", "moert_get_position", "moert_read_kv_fp16", "moert_read_hidden",
             "moert_time_steps", "moert_time_kernel", "moert_block_create", "moert_block_destroy",
@@ -294,14 +300,30 @@ class SynthModel:
 
 
 class GpuModel:
-    """All weights resident in HBM (GpuModel::upload, gpu_model.rs:191-194) and an fp16 KV cache of max_len."""
+    """All weights resident in HBM (GpuModel::upload, gpu_model.rs:191-194) and an fp16 KV cache of max_len; with
+    cache_slots, the experts are served from an expert cache of that many HBM slots over a pinned host store
+    (GpuModel::upload_cached, gpu_model.rs:197-200)."""
 
-    def __init__(self, model: SynthModel, max_len: int, attn_splits: int = 64):
+    def __init__(self, model: SynthModel, max_len: int, attn_splits: int = 64, cache_slots: Optional[int] = None):
         self.model, self.cfg, self.max_len = model, model.cfg, max_len
+        self.cache_slots = cache_slots
         h = ctypes.c_void_p()
-        check(lib().moert_model_create(ctypes.byref(model.cfg.c()), ctypes.byref(model.weights()), max_len,
-                                       attn_splits, ctypes.byref(h)))
+        if cache_slots is None:
+            check(lib().moert_model_create(ctypes.byref(model.cfg.c()), ctypes.byref(model.weights()), max_len,
+                                           attn_splits, ctypes.byref(h)))
+        else:
+            check(lib().moert_model_create_cached(ctypes.byref(model.cfg.c()), ctypes.byref(model.weights()),
+                                                  max_len, attn_splits, int(cache_slots), ctypes.byref(h)))
         self.h = h
+
+    def cache_stats(self):
+        """(hits, copies) of the expert cache since creation or the last clear."""
+        hi, co = ctypes.c_ulonglong(0), ctypes.c_ulonglong(0)
+        check(lib().moert_cache_stats(self.h, ctypes.byref(hi), ctypes.byref(co)))
+        return hi.value, co.value
+
+    def cache_clear(self):
+        check(lib().moert_cache_clear(self.h))
 
     def close(self):
         if self.h:

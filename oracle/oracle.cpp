@@ -769,6 +769,54 @@ void orc_moe_block_batched(int hidden, int inter, int experts, int k, const moer
   orc_experts_grouped(hidden, inter, m, k, gate_up, down, x, ids, weights, y, threads);
 }
 
+// ------------------------------------------------------------------------------------------------------------
+// LRU expert cache replay (the LruSync rule of ExpertCache, rust/moe-rt/src/cache.rs:249-354, as stated by
+// reference_lru in rust/moe-rt/tests/model.rs:380-412): one clock tick per (step, layer); every requested key that
+// is resident is touched first (pinned for the tick); then, in top-k order, a resident key is a hit, and a missing
+// key takes the first free slot, else the slot with the oldest last use among those not used in this tick (lowest
+// index on ties), else goes to the CPU. out = {hits, copies, cpu}.
+void orc_lru_replay(const int* routes, int steps, int layers, int k, int experts, int slots,
+                    unsigned long long* out) {
+  std::vector<int> skey(slots, -1);
+  std::vector<unsigned long long> last(slots, 0);
+  std::vector<int> where((size_t)layers * experts, -1);
+  unsigned long long clock = 0, hits = 0, copies = 0, cpu = 0;
+  for (int st = 0; st < steps; st++)
+    for (int l = 0; l < layers; l++) {
+      clock++;
+      const int* r = routes + ((size_t)st * layers + l) * k;
+      for (int j = 0; j < k; j++) {
+        int sl = where[(size_t)l * experts + r[j]];
+        if (sl >= 0) last[sl] = clock;
+      }
+      for (int j = 0; j < k; j++) {
+        const int key = l * experts + r[j];
+        if (where[key] >= 0) {
+          hits++;
+          continue;
+        }
+        int v = -1;
+        for (int i = 0; i < slots && v < 0; i++)
+          if (skey[i] < 0) v = i;
+        if (v < 0)
+          for (int i = 0; i < slots; i++)
+            if (last[i] < clock && (v < 0 || last[i] < last[v])) v = i;
+        if (v < 0) {
+          cpu++;
+          continue;
+        }
+        if (skey[v] >= 0) where[skey[v]] = -1;
+        skey[v] = key;
+        last[v] = clock;
+        where[key] = v;
+        copies++;
+      }
+    }
+  out[0] = hits;
+  out[1] = copies;
+  out[2] = cpu;
+}
+
 struct orc_session {
   moert_config cfg;
   moert_model_weights w;

@@ -78,6 +78,10 @@ void orc_moe_block_batched(int hidden, int inter, int experts, int k, const moer
                            const moert_tensor* gate_up, const moert_tensor* down, int m, const float* x, float* y,
                            int* ids, float* weights, int threads);
 
+/* LRU expert cache (LruSync rule) replayed over routes [steps][layers][k]: out = {hits, copies, cpu}. */
+void orc_lru_replay(const int* routes, int steps, int layers, int k, int experts, int slots,
+                    unsigned long long* out);
+
 /* CpuSession. */
 int orc_session_create(const moert_config* cfg, const moert_model_weights* w, int max_len, int attn_splits,
                        int threads, orc_session** out);

@@ -50,6 +50,7 @@ def lib() -> ctypes.CDLL:
             "orc_dot_hilo": (f, [vp, i, i, sz, vp, vp, vp]),
             "orc_experts_grouped": (None, [i, i, i, i, vp, vp, vp, vp, vp, vp, i]),
             "orc_moe_block_batched": (None, [i, i, i, i, vp, vp, vp, vp, i, vp, vp, vp, vp, i]),
+            "orc_lru_replay": (None, [vp, i, i, i, i, i, vp]),
             "orc_session_create": (i, [vp, vp, i, i, i, ctypes.POINTER(vp)]),
             "orc_session_destroy": (None, [vp]),
             "orc_session_step": (i, [vp, i, vp, vp, vp, vp]),
@@ -234,6 +235,44 @@ def moe_block_batched(hidden, inter, experts, k, router, gate_up, down, dtype, x
     lib().orc_moe_block_batched(hidden, inter, experts, k, ctypes.byref(r), _p(None if bias is None else _f32(bias)),
                                 ctypes.byref(gu), ctypes.byref(dn), m, _p(x), _p(y), _p(ids), _p(w), threads)
     return y.reshape(m, hidden), ids.reshape(m, k), w.reshape(m, k)
+
+
+def lru_replay(routes, experts, slots):
+    """(hits, copies, cpu) of the LRU expert cache over routes [steps, layers, k] (C restatement)."""
+    r = np.ascontiguousarray(routes, np.int32)
+    steps, layers, k = r.shape
+    out = np.zeros(3, np.uint64)
+    lib().orc_lru_replay(_p(r), steps, layers, k, experts, slots, _p(out))
+    return tuple(int(v) for v in out)
+
+
+def lru_reference(routes, experts, cap):
+    """The same rule written as rust/moe-rt/tests/model.rs:380-412 states it (list scans), for small traces:
+    slots hold (key, last use) or None; the requested keys are touched first, then each missing key takes the
+    first free slot or else the oldest slot used before this tick (first such on ties)."""
+    slots = [None] * cap
+    clock = hits = copies = cpu = 0
+    for step in routes:
+        for l, chosen in enumerate(step):
+            clock += 1
+            keys = [l * experts + int(e) for e in chosen]
+            for i, s in enumerate(slots):
+                if s is not None and s[0] in keys:
+                    slots[i] = (s[0], clock)
+            for key in keys:
+                if any(s is not None and s[0] == key for s in slots):
+                    hits += 1
+                    continue
+                victim = next((i for i, s in enumerate(slots) if s is None), None)
+                if victim is None:
+                    old = [(s[1], i) for i, s in enumerate(slots) if s[1] < clock]
+                    victim = min(old)[1] if old else None
+                if victim is None:
+                    cpu += 1
+                else:
+                    slots[victim] = (key, clock)
+                    copies += 1
+    return hits, copies, cpu
 
 
 class CpuSession:

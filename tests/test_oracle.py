@@ -413,6 +413,44 @@ def test_batched_block_routes_every_position_like_the_single_position_block():
             assert np.array_equal(w[p].view(np.uint32), w1.view(np.uint32))
 
 
+# ---- expert cache (LRU) -----------------------------------------------------------------------------------------------
+def test_lru_known_answers():
+    """Hand-worked traces of the LruSync rule (tests/model.rs:380-412): a 2-slot cache over 4 tokens; the pin rule
+    (a hit that comes after a miss in top-k order is still protected: without it the answer would be 0 hits,
+    4 copies); and a cache smaller than k, whose extra miss goes to the CPU."""
+    trace = [[[0, 1]], [[2, 0]], [[1, 2]], [[0, 3]]]
+    assert oracle.lru_replay(np.array(trace), 4, 2) == (2, 6, 0)
+    pin = [[[0, 1]], [[2, 0]]]
+    assert oracle.lru_replay(np.array(pin), 3, 2) == (1, 3, 0)
+    small = [[[0, 1, 2]]]
+    assert oracle.lru_replay(np.array(small), 4, 2) == (0, 2, 1)
+    for t in (trace, pin, small):
+        assert oracle.lru_reference(t, 4, 2) == oracle.lru_replay(np.array(t), 4, 2)
+
+
+def test_lru_table_replay_equals_the_list_statement_and_keeps_its_invariants():
+    """The C replay (slot tables) against the list-scan statement on random and skewed traces, plus invariants:
+    every request is a hit, a copy or a CPU miss; a cache holding every key copies each key exactly once."""
+    rng = np.random.default_rng(21)
+    for trial in range(40):
+        layers, experts = int(rng.integers(1, 5)), int(rng.integers(3, 12))
+        k = int(rng.integers(1, min(experts, 4) + 1))
+        steps = int(rng.integers(1, 30))
+        p = rng.zipf(1.3, size=experts).astype(np.float64) if trial % 2 else np.ones(experts)
+        p = p / p.sum()
+        routes = np.stack([np.stack([rng.choice(experts, size=k, replace=False, p=p) for _ in range(layers)])
+                           for _ in range(steps)]).astype(np.int32)
+        for cap in sorted({1, k, k + 1, layers * experts // 2 + 1, layers * experts}):
+            got = oracle.lru_replay(routes, experts, cap)
+            assert got == oracle.lru_reference(routes.tolist(), experts, cap), (trial, cap)
+            assert sum(got) == steps * layers * k
+            if cap >= layers * experts:
+                distinct = len({(l, int(e)) for st in routes for l, ch in enumerate(st) for e in ch})
+                assert got[1] == distinct and got[2] == 0
+            if cap >= k:
+                assert got[2] == 0
+
+
 # ---- whole model ----------------------------------------------------------------------------------------------------
 def _granite_golden():
     import make_granite_golden as g
