@@ -103,6 +103,63 @@ def batched_step(cfg, seed, iters, m=16, nblocks=4):
     return out
 
 
+def expert_cache(cfg, seed, steps, frac=0.25):
+    """The 3B shape with Q4_0 weights and the Zipf(1.1) router bias, experts served from an HBM pool holding 25% of
+    the 1280 experts (320 slots) over pinned host memory: `steps` greedy tokens from an empty pool, one graph per
+    token (routing, LRU and the host->pool copies all on the device). Reports tok/s, the hit rate, the bytes copied
+    per token, the copy kernel's PCIe rate, and the same model fully resident for comparison."""
+    import numpy as np
+
+    import moert
+    m = moert.SynthModel(cfg, seed=seed + 5, wdtype=moert.Q4_0, embed_dtype=moert.Q4_0, zipf_s=1.1)
+    slots = int(cfg.layers * cfg.experts * frac)
+    max_len = (steps + 2 + 63) // 64 * 64
+    record = moert.dtype_bytes(moert.Q4_0, 3 * cfg.inter * cfg.hidden)
+    tok = int(np.random.default_rng(seed).integers(0, cfg.vocab))
+    g = moert.GpuModel(m, max_len, attn_splits=64, cache_slots=slots)
+    g.step(tok, want_logits=False)
+    g.cache_clear()
+    g.reset()
+    g.step(tok, want_logits=False)
+    t0 = time.perf_counter()
+    g.time_steps(0, steps - 1)
+    wall = time.perf_counter() - t0
+    hits, copies = g.cache_stats()
+    n = steps * cfg.layers * cfg.top_k
+    tok_s = (steps - 1) / wall
+    # the same positions with a forced stream of random tokens (greedy decoding of a random-init model settles on
+    # one token, and so on one set of experts per layer); one graph replay per token, no host synchronisation
+    forced = np.random.default_rng(seed + 1).integers(0, cfg.vocab, steps)
+    g.cache_clear()
+    g.reset()
+    t0 = time.perf_counter()
+    g.generate(forced, 1)
+    fwall = time.perf_counter() - t0
+    fhits, fcopies = g.cache_stats()
+    g.close()
+    probe_bytes = 256 << 20
+    pk, pm = moert.h2d_probe(probe_bytes, 4)
+    r = moert.GpuModel(m, max_len, attn_splits=64)
+    r.step(tok, want_logits=False)
+    res_ms = r.time_steps(2, 64)
+    r.close()
+    out = {"slots": slots, "experts_total": cfg.layers * cfg.experts, "steps": steps, "tok_s": round(tok_s, 2),
+           "ms_per_step": round(wall * 1e3 / (steps - 1), 4), "hits": hits, "copies": copies,
+           "hit_rate": round(hits / max(1, hits + copies), 4), "requests": n,
+           "copied_bytes_per_token": round(copies * record / steps),
+           "forced_tokens": {"tok_s": round((steps + 1) / fwall, 2), "hits": fhits, "copies": fcopies,
+                             "hit_rate": round(fhits / max(1, fhits + fcopies), 4),
+                             "copied_bytes_per_token": round(fcopies * record / steps),
+                             "pcie_gbs_end_to_end": round(fcopies * record / fwall / 1e9, 2)},
+           "h2d_probe": {"bytes": probe_bytes, "kernel_copy_gbs": round(probe_bytes / (pk * 1e-6) / 1e9, 2),
+                         "hipmemcpy_gbs": round(probe_bytes / (pm * 1e-6) / 1e9, 2)},
+           "resident_tok_s": round(1e3 / res_ms, 2)}
+    log(f"expert cache {slots}/{cfg.layers * cfg.experts} slots: {tok_s:.1f} tok/s, hit rate {out['hit_rate']:.3f}, "
+        f"{out['copied_bytes_per_token'] / 1e6:.1f} MB copied per token; resident {out['resident_tok_s']} tok/s; "
+        f"forced tokens {out['forced_tokens']}")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -112,6 +169,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=32, help="oracle decode steps timed for the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--seed", type=int, default=3003)
+    ap.add_argument("--cache-steps", type=int, default=512,
+                    help="greedy steps of the 3B Q4_0 model served from a 25%% expert cache (0 skips it)")
     ap.add_argument("--batched-iters", type=int, default=20,
                     help="rounds of the 16-position grouped MoE step over 4 rotating 3B blocks (0 skips it)")
     args = ap.parse_args()
@@ -177,6 +236,7 @@ def main():
     log(f"device copy of {copy_bytes >> 20} MiB: {copy_us:.1f} us, {hbm_copy['gbs']:.0f} GB/s read+write")
 
     batched = batched_step(cfg, args.seed, args.batched_iters) if args.batched_iters > 0 else None
+    cache = expert_cache(cfg, args.seed, args.cache_steps) if args.cache_steps > 0 else None
 
     cpu = None
     if args.cpu_steps > 0:
@@ -217,6 +277,7 @@ def main():
         "moe_gemv": moe,
         "hbm_copy": hbm_copy,
         "batched_step": batched,
+        "expert_cache": cache,
         "kernels": kernels,
         "cpu_baseline": cpu,
         "device": name,

@@ -229,6 +229,12 @@ int moert_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v
  * reference measures PCIe and HBM rates with separate CUDA tools); used to calibrate the roofline. */
 int moert_copy_probe(size_t bytes, int iters, double* us_per_copy);
 
+/* PCIe reference for the expert cache: mean microseconds of one copy of `bytes` (multiple of 16) from pinned,
+ * device-mapped host memory into HBM, by a copy kernel (the way the cache fills its pool) and by hipMemcpyAsync
+ * (the DMA engines). The analogue of the reference's PCIe measurement programs (tools/llama-forcado/banda.cu,
+ * qual-runs/PCIE-X8-20261031/banda2.cu), which are not on its runtime path. */
+int moert_h2d_probe(size_t bytes, int iters, double* kernel_us, double* memcpy_us);
+
 /* Canonical exponential used by every kernel (softmax, SiLU, top-k weights), evaluated on the device. */
 int moert_exp_device(const float* x, float* y, int n);
 

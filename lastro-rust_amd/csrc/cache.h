@@ -37,5 +37,7 @@ hipError_t launch_route_lru(hipStream_t s, const LayerDev& L, const Dims& d, con
                             const CacheDev& c);
 // Copies the current miss list from the host store into the pool (PCIe reads by the kernel).
 hipError_t launch_fill(hipStream_t s, const CacheDev& c, int k);
+// Kernel copy of `bytes` (multiple of 16) from device-mapped pinned host memory to device memory.
+hipError_t launch_h2d_copy(hipStream_t s, const void* src, void* dst, size_t bytes);
 
 }  // namespace moert

@@ -167,6 +167,32 @@ __global__ __launch_bounds__(kFillThreads) void k_fill(CacheDev c) {
   }
 }
 
+// Plain copy of `bytes` (multiple of 16) from pinned host memory into device memory by a kernel: the transfer the
+// fill kernel makes, without the pool addressing (PCIe rate reference).
+__global__ __launch_bounds__(kFillThreads) void k_h2d_copy(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                                           size_t n) {
+  constexpr int PER = kFillChunk / 16 / kFillThreads;
+  const size_t base = (size_t)blockIdx.x * (kFillChunk / 16) + threadIdx.x;
+  uint4 buf[PER];
+#pragma unroll
+  for (int q = 0; q < PER; q++) {
+    const size_t i = base + (size_t)q * kFillThreads;
+    buf[q] = i < n ? src[i] : make_uint4(0, 0, 0, 0);
+  }
+#pragma unroll
+  for (int q = 0; q < PER; q++) {
+    const size_t i = base + (size_t)q * kFillThreads;
+    if (i < n) dst[i] = buf[q];
+  }
+}
+
+hipError_t launch_h2d_copy(hipStream_t s, const void* src, void* dst, size_t bytes) {
+  const size_t n = bytes / 16;
+  const int blocks = (int)((bytes + kFillChunk - 1) / kFillChunk);
+  klaunch(k_h2d_copy, blocks, kFillThreads, 0, s, (const uint4*)src, (uint4*)dst, n);
+  return hipGetLastError();
+}
+
 hipError_t launch_route_lru(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
                             const CacheDev& c) {
   if (c.slots < d.top_k || c.slots > kCacheMaxSlots || L.router.rows > 64 || d.top_k > 8) return hipErrorInvalidValue;

@@ -1149,6 +1149,51 @@ int moert_copy_probe(size_t bytes, int iters, double* us_per_copy) {
   return MOERT_OK;
 }
 
+int moert_h2d_probe(size_t bytes, int iters, double* kernel_us, double* memcpy_us) {
+  CHECK_CFG(bytes >= 16 && bytes % 16 == 0 && iters >= 1 && kernel_us && memcpy_us, "h2d_probe: bytes %zu", bytes);
+  Scoped sc;
+  TRY(sc.init());
+  uint8_t* dst;
+  TRY(sc.dev(&dst, bytes));
+  void* host = nullptr;
+  CHECK_HIP(hipHostMalloc(&host, bytes, hipHostMallocMapped | hipHostMallocNonCoherent));
+  std::memset(host, 1, bytes);
+  void* dev_host = nullptr;
+  int rc = MOERT_OK;
+  std::vector<hipEvent_t> ev(2 * iters + 2);
+  for (auto& e : ev)
+    if (hipEventCreate(&e) != hipSuccess) rc = MOERT_E_DEVICE;
+  if (!rc && hipHostGetDevicePointer(&dev_host, host, 0) != hipSuccess) rc = MOERT_E_DEVICE;
+  if (!rc && launch_h2d_copy(sc.s, dev_host, dst, bytes) != hipSuccess) rc = MOERT_E_DEVICE;  // warm-up
+  for (int i = 0; i < iters && !rc; i++) {
+    arm_launch_events(ev[2 * i], ev[2 * i + 1]);
+    if (launch_h2d_copy(sc.s, dev_host, dst, bytes) != hipSuccess) rc = MOERT_E_DEVICE;
+  }
+  if (!rc && hipMemcpyAsync(dst, host, bytes, hipMemcpyHostToDevice, sc.s) != hipSuccess) rc = MOERT_E_DEVICE;
+  if (!rc && hipEventRecord(ev[2 * iters], sc.s) != hipSuccess) rc = MOERT_E_DEVICE;
+  for (int i = 0; i < iters && !rc; i++)
+    if (hipMemcpyAsync(dst, host, bytes, hipMemcpyHostToDevice, sc.s) != hipSuccess) rc = MOERT_E_DEVICE;
+  if (!rc && hipEventRecord(ev[2 * iters + 1], sc.s) != hipSuccess) rc = MOERT_E_DEVICE;
+  if (!rc && hipStreamSynchronize(sc.s) != hipSuccess) rc = MOERT_E_DEVICE;
+  if (!rc) {
+    double tk = 0.0;
+    for (int i = 0; i < iters; i++) {
+      float t = 0.0f;
+      (void)hipEventElapsedTime(&t, ev[2 * i], ev[2 * i + 1]);
+      tk += t;
+    }
+    float tm = 0.0f;
+    (void)hipEventElapsedTime(&tm, ev[2 * iters], ev[2 * iters + 1]);
+    *kernel_us = tk * 1000.0 / iters;
+    *memcpy_us = (double)tm * 1000.0 / iters;
+  }
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  (void)hipStreamSynchronize(sc.s);
+  (void)hipHostFree(host);
+  if (rc) set_err("h2d_probe: device error");
+  return rc;
+}
+
 // ---- host utilities --------------------------------------------------------------------------------------------
 int moert_quantize(const float* x, size_t n, int dtype, void* out) {
   CHECK_CFG(x && out && valid_dtype(dtype) && n % 32 == 0, "quantize: n %zu, dtype %d", n, dtype);
