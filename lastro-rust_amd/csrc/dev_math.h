@@ -137,10 +137,11 @@ template <> struct Fmt<DT_F32> {
   __device__ static size_t row_bytes(int cols) { return (size_t)cols * 4; }
 };
 
-// One 16-byte chunk j of a row, loaded raw, with its scale.
+// One 16-byte chunk j of a row, loaded raw, with the raw bits of its fp16 scale (converted where it is used, so
+// that a run of chunk loads is not broken by a wait for each scale).
 struct RawChunk {
   uint4 v;
-  float d;
+  uint32_t d;
 };
 
 template <int DT>
@@ -149,35 +150,38 @@ __device__ __forceinline__ RawChunk load_chunk(const DMat& m, size_t row, int j)
   const uint8_t* base = m.q + row * Fmt<DT>::row_bytes(m.cols);
   c.v = *reinterpret_cast<const uint4*>(base + (size_t)j * 16);
   if (DT == DT_Q8_0)
-    c.d = h2f(m.d[row * (size_t)(m.cols / 32) + (j >> 1)]);
+    c.d = m.d[row * (size_t)(m.cols / 32) + (j >> 1)];
   else if (DT == DT_Q4_0)
-    c.d = h2f(m.d[row * (size_t)(m.cols / 32) + j]);
+    c.d = m.d[row * (size_t)(m.cols / 32) + j];
   else
-    c.d = 1.0f;
+    c.d = 0x3c00u;  // 1.0
   return c;
 }
+
+__device__ __forceinline__ float chunk_scale(const RawChunk& c) { return h2f((uint16_t)c.d); }
 
 // acc = fma chain over the chunk's elements in index order; x holds the chunk's Fmt<DT>::kElems activations.
 template <int DT>
 __device__ __forceinline__ float fma_chunk(const RawChunk& c, const float* x, float acc) {
   const uint32_t w[4] = {c.v.x, c.v.y, c.v.z, c.v.w};
+  const float d = chunk_scale(c);
   if (DT == DT_Q8_0) {
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       float q = (float)(int8_t)(w[i >> 2] >> (8 * (i & 3)));
-      acc = __builtin_fmaf(q * c.d, x[i], acc);
+      acc = __builtin_fmaf(q * d, x[i], acc);
     }
   } else if (DT == DT_Q4_0) {
     // GGML Q4_0: byte b holds element b (low nibble) and element b + 16 (high nibble).
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       float q = (float)((int)((w[i >> 2] >> (8 * (i & 3))) & 15u) - 8);
-      acc = __builtin_fmaf(q * c.d, x[i], acc);
+      acc = __builtin_fmaf(q * d, x[i], acc);
     }
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       float q = (float)((int)((w[i >> 2] >> (8 * (i & 3) + 4)) & 15u) - 8);
-      acc = __builtin_fmaf(q * c.d, x[16 + i], acc);
+      acc = __builtin_fmaf(q * d, x[16 + i], acc);
     }
   } else {
 #pragma unroll
@@ -190,10 +194,10 @@ __device__ __forceinline__ float fma_chunk(const RawChunk& c, const float* x, fl
 template <int DT>
 __device__ __forceinline__ float chunk_elem(const RawChunk& c, int i) {
   const uint32_t w[4] = {c.v.x, c.v.y, c.v.z, c.v.w};
-  if (DT == DT_Q8_0) return (float)(int8_t)(w[i >> 2] >> (8 * (i & 3))) * c.d;
+  if (DT == DT_Q8_0) return (float)(int8_t)(w[i >> 2] >> (8 * (i & 3))) * chunk_scale(c);
   if (DT == DT_Q4_0) {
     int b = i & 15, sh = 8 * (b & 3) + (i >= 16 ? 4 : 0);
-    return (float)((int)((w[b >> 2] >> sh) & 15u) - 8) * c.d;
+    return (float)((int)((w[b >> 2] >> sh) & 15u) - 8) * chunk_scale(c);
   }
   return __uint_as_float(w[i]);
 }

@@ -111,6 +111,8 @@ struct Rows {
   RawChunk c[P][Geo<DT, K>::NJ];
 };
 
+// Loads are unconditional (a row that is not used loads row 0, a chunk past the row end loads the last chunk) so
+// that they form one straight run of independent loads; rows_fma skips what is not used.
 template <int DT, int K, int P>
 __device__ __forceinline__ void rows_load(Rows<DT, K, P>& r, const DMat& m, const size_t (&row)[P],
                                           const bool (&ok)[P], int sub) {
@@ -119,8 +121,8 @@ __device__ __forceinline__ void rows_load(Rows<DT, K, P>& r, const DMat& m, cons
   for (int p = 0; p < P; p++)
 #pragma unroll
     for (int jj = 0; jj < G::NJ; jj++) {
-      int j = sub + G::LPR * jj;
-      if (ok[p] && j < G::NCH) r.c[p][jj] = load_chunk<DT>(m, row[p], j);
+      const int j = sub + G::LPR * jj;
+      r.c[p][jj] = load_chunk<DT>(m, ok[p] ? row[p] : 0, j < G::NCH ? j : G::NCH - 1);
     }
 }
 
@@ -140,82 +142,141 @@ __device__ __forceinline__ void rows_fma(const Rows<DT, K, P>& r, const bool (&o
   }
 }
 
-// Workgroup prologues: the block's activation vector in LDS, once per workgroup.
-// wg_norm: xs = lnw * (x * r), r = 1/sqrt(sum(x^2)/K + eps), the sum in the canonical order by wave 0.
+// Workgroup prologues: the block's activation vector in LDS, once per workgroup. Each comes as a fetch, which only
+// issues the loads and is placed before a kernel's weight loads, and a finish, which uses them: loads complete in
+// issue order, so the prologue then waits only for the activation while the weights are still streaming.
+//
+// Norm: xs = lnw * (x * r), r = 1/sqrt(sum(x^2)/K + eps), the sum in the canonical order by wave 0 (16-element
+// chunks, chunk j in lane j % 64) over x staged in LDS. Fetch loads are unconditional (clamped indices) so that no
+// branch join forces an early wait.
 template <int K, int NT>
-__device__ __forceinline__ void wg_norm(const float* __restrict__ x, const float* __restrict__ lnw, float eps,
-                                        float* xs, float* rs) {
-  constexpr int PER = (K + NT - 1) / NT;
+struct NormIn {
+  static constexpr int PER = (K + NT - 1) / NT;
   float hv[PER], wv[PER];
+};
+
+template <int K, int NT>
+__device__ __forceinline__ void norm_fetch(const float* __restrict__ x, const float* __restrict__ lnw,
+                                           NormIn<K, NT>& in) {
 #pragma unroll
-  for (int e = 0; e < PER; e++) {
-    int i = threadIdx.x + e * NT;
-    if (i < K) {
-      hv[e] = x[i];
-      wv[e] = lnw[i];
-    }
+  for (int e = 0; e < NormIn<K, NT>::PER; e++) {
+    const int i = threadIdx.x + e * NT;
+    in.hv[e] = x[i < K ? i : K - 1];
+    in.wv[e] = lnw[i < K ? i : K - 1];
   }
+  __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the kernel's weight loads
+}
+
+template <int K, int NT>
+__device__ __forceinline__ void norm_finish(const NormIn<K, NT>& in, float eps, float* xs, float* rs) {
+  constexpr int NCH = K / 16;
+#pragma unroll
+  for (int e = 0; e < NormIn<K, NT>::PER; e++) {
+    const int i = threadIdx.x + e * NT;
+    if (i < K) xs[i] = in.hv[e];
+  }
+  __syncthreads();
   if (threadIdx.x < 64) {
-    float r = rms_scale<K>(x, eps, threadIdx.x);
-    if (threadIdx.x == 0) *rs = r;
+    float acc = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < (NCH + 63) / 64; jj++) {
+      const int j = threadIdx.x + 64 * jj;
+      if (j < NCH) {
+        const float4* p = reinterpret_cast<const float4*>(xs + 16 * j);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          const float4 t = p[e];
+          acc = __builtin_fmaf(t.x, t.x, acc);
+          acc = __builtin_fmaf(t.y, t.y, acc);
+          acc = __builtin_fmaf(t.z, t.z, acc);
+          acc = __builtin_fmaf(t.w, t.w, acc);
+        }
+      }
+    }
+    const float ss = group_sum<64>(acc);
+    if (threadIdx.x == 0) *rs = 1.0f / sqrtf(ss / (float)K + eps);
   }
   __syncthreads();
   const float r = *rs;
 #pragma unroll
-  for (int e = 0; e < PER; e++) {
-    int i = threadIdx.x + e * NT;
-    if (i < K) xs[i] = wv[e] * (hv[e] * r);
+  for (int e = 0; e < NormIn<K, NT>::PER; e++) {
+    const int i = threadIdx.x + e * NT;
+    if (i < K) xs[i] = in.wv[e] * (in.hv[e] * r);
+  }
+  __syncthreads();
+}
+
+template <int K, int NT>
+__device__ __forceinline__ void wg_norm(const float* __restrict__ x, const float* __restrict__ lnw, float eps,
+                                        float* xs, float* rs) {
+  NormIn<K, NT> in;
+  norm_fetch<K, NT>(x, lnw, in);
+  norm_finish<K, NT>(in, eps, xs, rs);
+}
+
+// Copy: xs = x[0, N).
+template <int N, int NT>
+struct CopyIn {
+  static constexpr int PER = (N / 4 + NT - 1) / NT;
+  float4 v[PER];
+};
+
+template <int N, int NT>
+__device__ __forceinline__ void copy_fetch(const float* __restrict__ x, CopyIn<N, NT>& in) {
+  static_assert(N % 4 == 0, "vector copy");
+#pragma unroll
+  for (int e = 0; e < CopyIn<N, NT>::PER; e++) {
+    const int i = threadIdx.x + e * NT;
+    in.v[e] = reinterpret_cast<const float4*>(x)[i < N / 4 ? i : 0];
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the kernel's weight loads
+}
+
+template <int N, int NT>
+__device__ __forceinline__ void copy_finish(const CopyIn<N, NT>& in, float* xs) {
+#pragma unroll
+  for (int e = 0; e < CopyIn<N, NT>::PER; e++) {
+    const int i = threadIdx.x + e * NT;
+    if (i < N / 4) reinterpret_cast<float4*>(xs)[i] = in.v[e];
   }
   __syncthreads();
 }
 
 template <int N, int NT>
 __device__ __forceinline__ void wg_copy(const float* __restrict__ x, float* xs) {
-  static_assert(N % 4 == 0, "vector copy");
-  for (int i = threadIdx.x; i < N / 4; i += NT)
-    reinterpret_cast<float4*>(xs)[i] = reinterpret_cast<const float4*>(x)[i];
-  __syncthreads();
+  CopyIn<N, NT> in;
+  copy_fetch<N, NT>(x, in);
+  copy_finish<N, NT>(in, xs);
 }
 
-// Top-k of n <= 64 logits held in LDS (lg), by rank: lane e counts the logits that precede it in the order
-// (total-order key descending, index ascending) and, if its rank is below k, takes that slot; then
-// w_j = exp(l_j - l_top) / sum with the sum taken left to right (Routing::from_logits, block.rs:81-89; route_topk,
-// route.rs:18-75). `slot` is 3*64 words of LDS. ids/weights written by lanes j < k.
-__device__ __forceinline__ void wave_topk(const float* lg, int n, int k, int lane, float* slot, int* ids,
-                                          float* weights) {
+// Top-k of n <= 64 logits held in LDS (lg), by one wave, in registers: lane e holds logit e and counts the logits
+// that precede it in the order (total-order key descending, index ascending); a lane whose rank is below k is
+// selected. Then w_j = exp(l_j - l_top) / sum with the sum taken left to right in rank order (Routing::from_logits,
+// block.rs:81-89; route_topk, route.rs:18-75). ids[r] / weights[r] are written by the lane of rank r.
+__device__ __forceinline__ void wave_topk(const float* lg, int n, int k, int lane, int* ids, float* weights) {
   const float v = lane < n ? lg[lane] : 0.0f;
-  const int key = total_key(v);
+  // (key, 63 - index) as one unsigned 64-bit number: larger means earlier in the order
+  const unsigned long long mine =
+      ((unsigned long long)((unsigned)total_key(v) ^ 0x80000000u) << 6) | (unsigned)(63 - lane);
+  const unsigned mlo = (unsigned)mine, mhi = (unsigned)(mine >> 32);
   int rank = 0;
-  // all 64 slots read as float4 up front (slots >= n hold stale values and are skipped)
-  float4 all[16];
-#pragma unroll
-  for (int j4 = 0; j4 < 16; j4++) all[j4] = reinterpret_cast<const float4*>(lg)[j4];
-#pragma unroll
-  for (int j4 = 0; j4 < 16; j4++) {
-    const float a4[4] = {all[j4].x, all[j4].y, all[j4].z, all[j4].w};
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-      const int j = 4 * j4 + u;
-      const int kj = total_key(a4[u]);
-      rank += j < n && ((kj > key) || (kj == key && j < lane));
-    }
+  for (int j = 0; j < n; j++) {
+    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)mlo, j);
+    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)mhi, j);
+    rank += (((unsigned long long)hi << 32) | lo) > mine;
   }
-  float* sval = slot;
-  int* sid = reinterpret_cast<int*>(slot + 64);
-  float* sex = slot + 128;
-  if (lane < n && rank < k) {
-    sval[rank] = v;
-    sid[rank] = lane;
-  }
-  wave_lds_sync();
-  const float ex = lane < k ? dexp(sval[lane] - sval[0]) : 0.0f;
-  sex[lane] = ex;
-  wave_lds_sync();
+  const bool sel = lane < n && rank < k;
+  const int top = __ffsll((long long)__ballot(sel && rank == 0)) - 1;
+  const float vtop = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), top));
+  const float ex = sel ? dexp(v - vtop) : 0.0f;
   float sum = 0.0f;
-  for (int j = 0; j < k; j++) sum = sum + sex[j];
-  if (lane < k) {
-    ids[lane] = sid[lane];
-    weights[lane] = ex / sum;
+  for (int r = 0; r < k; r++) {
+    const int lr = __ffsll((long long)__ballot(sel && rank == r)) - 1;
+    sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), lr));
+  }
+  if (sel) {
+    ids[rank] = lane;
+    weights[rank] = ex / sum;
   }
 }
 

@@ -41,9 +41,11 @@ __global__ __launch_bounds__(kBlock) void k_gemv(DMat m, const float* __restrict
     row[p] = base + (size_t)p * G::RPW + rw;
     ok[p] = row[p] < (size_t)m.rows;
   }
+  CopyIn<K, kBlock> xin;
+  copy_fetch<K, kBlock>(x, xin);
   Rows<DT, K, P> rr;
   rows_load<DT, K, P>(rr, m, row, ok, sub);
-  wg_copy<K, kBlock>(x, xs);
+  copy_finish<K, kBlock>(xin, xs);
   XReg<DT, K> xr;
   load_x<DT, K>(xr, xs, sub);
   float out[P];
@@ -106,10 +108,12 @@ __global__ __launch_bounds__(kBlock) void k_qkv(DMat m, const float* __restrict_
     ok[2 * a] = v;
     ok[2 * a + 1] = v;
   }
+  NormIn<K, kBlock> hin;
+  norm_fetch<K, kBlock>(h, lnw, hin);
+  const int pos = st[ST_POS];
   Rows<DT, K, P> rr;
   rows_load<DT, K, P>(rr, m, row, ok, sub);
-  const int pos = st[ST_POS];
-  wg_norm<K, kBlock>(h, lnw, eps, xs, &rs);
+  norm_finish<K, kBlock>(hin, eps, xs, &rs);
   XReg<DT, K> xr;
   load_x<DT, K>(xr, xs, sub);
   float out[P];
@@ -319,12 +323,14 @@ __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restric
     row[p] = base + (size_t)p * G::RPW + rw;
     ok[p] = row[p] < (size_t)m.rows;
   }
-  Rows<DT, K, P> rr;
-  rows_load<DT, K, P>(rr, m, row, ok, sub);
+  CopyIn<K, kBlock> ain;
+  copy_fetch<K, kBlock>(att, ain);
   float hold[P];
 #pragma unroll
   for (int p = 0; p < P; p++) hold[p] = (ok[p] && sub == 0) ? h[row[p]] : 0.0f;
-  wg_copy<K, kBlock>(att, xs);
+  Rows<DT, K, P> rr;
+  rows_load<DT, K, P>(rr, m, row, ok, sub);
+  copy_finish<K, kBlock>(ain, xs);
   XReg<DT, K> xr;
   load_x<DT, K>(xr, xs, sub);
   float out[P];
@@ -358,7 +364,6 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
   constexpr int P = 2 * NP;
   __shared__ float xs[K];
   __shared__ __align__(16) float lg[64];
-  __shared__ float slot[3 * 64];
   __shared__ int sids[8];
   __shared__ float sw[8];
   __shared__ float rs;
@@ -366,15 +371,21 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
   int sub = lane % G::LPR, rw = lane / G::LPR;
   const int E = router.rows;
   XReg<DT, K> xr;
+  NormIn<K, NT> hin;
+  CopyIn<K, NT> cin;
+  if (NORM)
+    norm_fetch<K, NT>(h, lnw, hin);
+  else
+    copy_fetch<K, NT>(h, cin);
   if (ROUTED) {
     if (threadIdx.x < k) {
       sids[threadIdx.x] = slots_in[threadIdx.x];
       sw[threadIdx.x] = w_out[threadIdx.x];
     }
     if (NORM)
-      wg_norm<K, NT>(h, lnw, eps, xs, &rs);
+      norm_finish<K, NT>(hin, eps, xs, &rs);
     else
-      wg_copy<K, NT>(h, xs);
+      copy_finish<K, NT>(cin, xs);
     load_x<DT, K>(xr, xs, sub);
   } else {
     size_t row[RP];
@@ -390,9 +401,9 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
 #pragma unroll
     for (int p = 0; p < RP; p++) bv[p] = (bias && ok[p]) ? bias[row[p]] : 0.0f;
     if (NORM)
-      wg_norm<K, NT>(h, lnw, eps, xs, &rs);
+      norm_finish<K, NT>(hin, eps, xs, &rs);
     else
-      wg_copy<K, NT>(h, xs);
+      copy_finish<K, NT>(cin, xs);
     load_x<DT, K>(xr, xs, sub);
     float out[RP];
     rows_fma<DT, K, RP>(rr, ok, xr, sub, out);
@@ -402,7 +413,7 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
   }
   __syncthreads();
   if (!ROUTED && wave == 0) {
-    wave_topk(lg, E, k, lane, slot, sids, sw);
+    wave_topk(lg, E, k, lane, sids, sw);
     if (blockIdx.x == 0 && lane < k) {
       ids_out[lane] = sids[lane];
       w_out[lane] = sw[lane];
@@ -451,22 +462,38 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __r
   int sub = lane % G::LPR, rw = lane / G::LPR;
   int r = blockIdx.x * kWavesPerBlock + wave;
   bool rok = r < hidden;
+  // routed ids, then activations (loads complete in issue order, so waiting for the ids does not wait for the
+  // activations), then the expert rows, then the activations into LDS
+  int idj[KP];
+#pragma unroll
+  for (int p = 0; p < KP; p++) {
+    const int j = p * G::RPW + rw;
+    idj[p] = ids[j < k ? j : 0];
+  }
+  constexpr int AP = (KMAX * K / 4 + kBlock - 1) / kBlock;
+  float4 av[AP];
+#pragma unroll
+  for (int q = 0; q < AP; q++) {
+    const int i = threadIdx.x + q * kBlock;
+    av[q] = reinterpret_cast<const float4*>(act)[i < k * K / 4 ? i : 0];
+  }
+  float hold = (rok && lane == 0 && accumulate) ? h[r] : 0.0f;
+  __builtin_amdgcn_sched_barrier(0);  // ids and activations ahead of the expert rows
   RawChunk c[KP][G::NJ];
 #pragma unroll
   for (int p = 0; p < KP; p++) {
-    int j = p * G::RPW + rw;
-    if (rok && j < k) {
-      size_t row = (size_t)ids[j] * hidden + r;
+    const size_t row = (size_t)idj[p] * hidden + (rok ? r : 0);
 #pragma unroll
-      for (int jj = 0; jj < G::NJ; jj++) {
-        int ch = sub + G::LPR * jj;
-        if (ch < G::NCH) c[p][jj] = load_chunk<DT>(m, row, ch);
-      }
+    for (int jj = 0; jj < G::NJ; jj++) {
+      const int ch = sub + G::LPR * jj;
+      c[p][jj] = load_chunk<DT>(m, row, ch < G::NCH ? ch : G::NCH - 1);
     }
   }
-  float hold = (rok && lane == 0 && accumulate) ? h[r] : 0.0f;
-  for (int i = threadIdx.x; i < k * K / 4; i += kBlock)
-    reinterpret_cast<float4*>(xs)[i] = reinterpret_cast<const float4*>(act)[i];
+#pragma unroll
+  for (int q = 0; q < AP; q++) {
+    const int i = threadIdx.x + q * kBlock;
+    if (i < k * K / 4) reinterpret_cast<float4*>(xs)[i] = av[q];
+  }
   __syncthreads();
   if (!rok) return;
   float dsum[KP];
@@ -544,9 +571,11 @@ __global__ __launch_bounds__(kBlock) void k_head(DMat m, const float* __restrict
       row[bt][p] = wbase + (size_t)(bt * P + p) * G::RPW + rw;
       ok[bt][p] = row[bt][p] < (size_t)m.rows;
     }
+  NormIn<K, kBlock> hin;
+  norm_fetch<K, kBlock>(h, lnw, hin);
   Rows<DT, K, P> cur, nxt;
   rows_load<DT, K, P>(cur, m, row[0], ok[0], sub);
-  wg_norm<K, kBlock>(h, lnw, eps, xs, &rs);
+  norm_finish<K, kBlock>(hin, eps, xs, &rs);
   XReg<DT, K> xr;
   load_x<DT, K>(xr, xs, sub);
   int bk = INT_MIN, bi = -1;
@@ -660,11 +689,10 @@ __global__ void k_rope(float* __restrict__ x, int heads, int half, const float* 
 __global__ void k_topk(const float* __restrict__ logits, const float* __restrict__ bias, int n, int k,
                        int* __restrict__ ids, float* __restrict__ w) {
   __shared__ __align__(16) float lg[64];
-  __shared__ float slot[3 * 64];
   int lane = threadIdx.x;
   if (lane < n) lg[lane] = bias ? logits[lane] + bias[lane] : logits[lane];
   wave_lds_sync();
-  wave_topk(lg, n, k, lane, slot, ids, w);
+  wave_topk(lg, n, k, lane, ids, w);
 }
 
 __global__ __launch_bounds__(kBlock) void k_argmax(const float* __restrict__ v, int n, int2* __restrict__ best) {
