@@ -111,12 +111,14 @@ def expert_cache(cfg, seed, steps, frac=0.25):
     import numpy as np
 
     import moert
+    log("expert cache: building the 3B Q4_0 model")
     m = moert.SynthModel(cfg, seed=seed + 5, wdtype=moert.Q4_0, embed_dtype=moert.Q4_0, zipf_s=1.1)
     slots = int(cfg.layers * cfg.experts * frac)
     max_len = (steps + 2 + 63) // 64 * 64
     record = moert.dtype_bytes(moert.Q4_0, 3 * cfg.inter * cfg.hidden)
     tok = int(np.random.default_rng(seed).integers(0, cfg.vocab))
     g = moert.GpuModel(m, max_len, attn_splits=64, cache_slots=slots)
+    log(f"expert cache: pinned host store and {slots}-slot pool ready; greedy run")
     g.step(tok, want_logits=False)
     g.cache_clear()
     g.reset()
@@ -129,6 +131,7 @@ def expert_cache(cfg, seed, steps, frac=0.25):
     tok_s = (steps - 1) / wall
     # the same positions with a forced stream of random tokens (greedy decoding of a random-init model settles on
     # one token, and so on one set of experts per layer); one graph replay per token, no host synchronisation
+    log("expert cache: forced-token run")
     forced = np.random.default_rng(seed + 1).integers(0, cfg.vocab, steps)
     g.cache_clear()
     g.reset()
@@ -139,6 +142,7 @@ def expert_cache(cfg, seed, steps, frac=0.25):
     g.close()
     probe_bytes = 256 << 20
     pk, pm = moert.h2d_probe(probe_bytes, 4)
+    log("expert cache: resident comparison")
     r = moert.GpuModel(m, max_len, attn_splits=64)
     r.step(tok, want_logits=False)
     res_ms = r.time_steps(2, 64)
