@@ -37,6 +37,7 @@ __global__ __launch_bounds__(kLruThreads) void k_route_lru(DMat router, const fl
   constexpr int RP = (64 + NW * G::RPW - 1) / (NW * G::RPW);
   __shared__ float xs[K];
   __shared__ __align__(16) float lg[64];
+  __shared__ __align__(16) TopkLds tk;
   __shared__ int sids[8];
   __shared__ float sw[8];
   __shared__ float rs;
@@ -72,7 +73,7 @@ __global__ __launch_bounds__(kLruThreads) void k_route_lru(DMat router, const fl
     if (ok[q] && sub == 0) lg[row[q]] = bias ? out[q] + bv[q] : out[q];
   __syncthreads();
   if (wave == 0) {
-    wave_topk(lg, E, k, lane, sids, sw);
+    wave_topk(lg, E, k, lane, tk, sids, sw);
     wave_lds_sync();
     int key = 0, s0 = -1;
     if (lane < k) {

@@ -249,31 +249,46 @@ __device__ __forceinline__ void wg_copy(const float* __restrict__ x, float* xs) 
   copy_finish<N, NT>(in, xs);
 }
 
-// Top-k of n <= 64 logits held in LDS (lg), by one wave, in registers: lane e holds logit e and counts the logits
-// that precede it in the order (total-order key descending, index ascending); a lane whose rank is below k is
-// selected. Then w_j = exp(l_j - l_top) / sum with the sum taken left to right in rank order (Routing::from_logits,
-// block.rs:81-89; route_topk, route.rs:18-75). ids[r] / weights[r] are written by the lane of rank r.
-__device__ __forceinline__ void wave_topk(const float* lg, int n, int k, int lane, int* ids, float* weights) {
+// Top-k of n <= 64 logits held in LDS (lg), by one wave. Lane e holds logit e as one 64-bit sort key
+// (total-order key, then 63 - e, so that larger means earlier: descending value, ties to the lower index); the keys
+// are broadcast through LDS and each lane counts the keys above its own, which is its rank; a lane whose rank is
+// below k is selected. Then w_j = exp(l_j - l_top) / sum with the sum taken left to right in rank order
+// (Routing::from_logits, block.rs:81-89; route_topk, route.rs:18-75). ids[r] / weights[r] are written by the lane of
+// rank r (k <= 8).
+struct TopkLds {
+  unsigned long long keys[64];
+  float val[8];
+  float ex[8];
+};
+
+__device__ __forceinline__ void wave_topk(const float* lg, int n, int k, int lane, TopkLds& t, int* ids,
+                                          float* weights) {
   const float v = lane < n ? lg[lane] : 0.0f;
-  // (key, 63 - index) as one unsigned 64-bit number: larger means earlier in the order
   const unsigned long long mine =
       ((unsigned long long)((unsigned)total_key(v) ^ 0x80000000u) << 6) | (unsigned)(63 - lane);
-  const unsigned mlo = (unsigned)mine, mhi = (unsigned)(mine >> 32);
+  t.keys[lane] = lane < n ? mine : 0ull;
+  if (lane < 8) t.ex[lane] = 0.0f;
+  wave_lds_sync();
   int rank = 0;
-  for (int j = 0; j < n; j++) {
-    const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)mlo, j);
-    const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)mhi, j);
-    rank += (((unsigned long long)hi << 32) | lo) > mine;
+#pragma unroll
+  for (int j2 = 0; j2 < 32; j2++) {
+    const ulonglong2 kk = reinterpret_cast<const ulonglong2*>(t.keys)[j2];
+    rank += kk.x > mine;
+    rank += kk.y > mine;
   }
   const bool sel = lane < n && rank < k;
-  const int top = __ffsll((long long)__ballot(sel && rank == 0)) - 1;
-  const float vtop = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), top));
-  const float ex = sel ? dexp(v - vtop) : 0.0f;
+  if (sel) t.val[rank] = v;
+  wave_lds_sync();
+  const float ex = sel ? dexp(v - t.val[0]) : 0.0f;
+  if (sel) t.ex[rank] = ex;
+  wave_lds_sync();
+  const float4 e0 = *reinterpret_cast<const float4*>(&t.ex[0]);
+  const float4 e1 = *reinterpret_cast<const float4*>(&t.ex[4]);
+  const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
   float sum = 0.0f;
-  for (int r = 0; r < k; r++) {
-    const int lr = __ffsll((long long)__ballot(sel && rank == r)) - 1;
-    sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), lr));
-  }
+#pragma unroll
+  for (int r = 0; r < 8; r++)
+    if (r < k) sum = sum + ev[r];
   if (sel) {
     ids[rank] = lane;
     weights[rank] = ex / sum;

@@ -39,6 +39,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_grp_route(DMat router, const 
   constexpr int NB = H / 32;
   __shared__ float xs[H];
   __shared__ __align__(16) float lg[64];
+  __shared__ __align__(16) TopkLds tk;
   const int p = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane % G::LPR, rw = lane / G::LPR;
@@ -92,7 +93,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_grp_route(DMat router, const 
     }
   }
   __syncthreads();
-  if (wave == 0) wave_topk(lg, E, k, lane, g.ids + (size_t)p * k, g.w + (size_t)p * k);
+  if (wave == 0) wave_topk(lg, E, k, lane, tk, g.ids + (size_t)p * k, g.w + (size_t)p * k);
 }
 
 // ------------------------------------------------------------------------------------------------------------

@@ -364,6 +364,7 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
   constexpr int P = 2 * NP;
   __shared__ float xs[K];
   __shared__ __align__(16) float lg[64];
+  __shared__ __align__(16) TopkLds tk;
   __shared__ int sids[8];
   __shared__ float sw[8];
   __shared__ float rs;
@@ -413,7 +414,7 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
   }
   __syncthreads();
   if (!ROUTED && wave == 0) {
-    wave_topk(lg, E, k, lane, sids, sw);
+    wave_topk(lg, E, k, lane, tk, sids, sw);
     if (blockIdx.x == 0 && lane < k) {
       ids_out[lane] = sids[lane];
       w_out[lane] = sw[lane];
@@ -689,10 +690,11 @@ __global__ void k_rope(float* __restrict__ x, int heads, int half, const float* 
 __global__ void k_topk(const float* __restrict__ logits, const float* __restrict__ bias, int n, int k,
                        int* __restrict__ ids, float* __restrict__ w) {
   __shared__ __align__(16) float lg[64];
+  __shared__ __align__(16) TopkLds tk;
   int lane = threadIdx.x;
   if (lane < n) lg[lane] = bias ? logits[lane] + bias[lane] : logits[lane];
   wave_lds_sync();
-  wave_topk(lg, n, k, lane, ids, w);
+  wave_topk(lg, n, k, lane, tk, ids, w);
 }
 
 __global__ __launch_bounds__(kBlock) void k_argmax(const float* __restrict__ v, int n, int2* __restrict__ best) {
