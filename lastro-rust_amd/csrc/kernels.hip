@@ -108,9 +108,20 @@ __global__ __launch_bounds__(kBlock) void k_qkv(DMat m, const float* __restrict_
     ok[2 * a] = v;
     ok[2 * a + 1] = v;
   }
+  // position first, then the activation, then this lane's cos/sin (they depend only on the position), then the
+  // weights: each wait below covers only what was issued before the thing waited for
+  const int pos = st[ST_POS];
   NormIn<K, kBlock> hin;
   norm_fetch<K, kBlock>(h, lnw, hin);
-  const int pos = st[ST_POS];
+  const float* cs = rope + (size_t)pos * 64;
+  float cv[NP], sv[NP];
+#pragma unroll
+  for (int a = 0; a < NP; a++) {
+    const int jp = gp[a] % 32;
+    cv[a] = cs[jp];
+    sv[a] = cs[32 + jp];
+  }
+  __builtin_amdgcn_sched_barrier(0);
   Rows<DT, K, P> rr;
   rows_load<DT, K, P>(rr, m, row, ok, sub);
   norm_finish<K, kBlock>(hin, eps, xs, &rs);
@@ -119,13 +130,12 @@ __global__ __launch_bounds__(kBlock) void k_qkv(DMat m, const float* __restrict_
   float out[P];
   rows_fma<DT, K, P>(rr, ok, xr, sub, out);
   if (sub != 0) return;
-  const float* cs = rope + (size_t)pos * 64;
 #pragma unroll
   for (int a = 0; a < NP; a++) {
     if (!ok[2 * a]) continue;
     int head = gp[a] / 32, jp = gp[a] % 32;
     float x1 = out[2 * a], x2 = out[2 * a + 1];
-    float c = cs[jp], sn = cs[32 + jp];
+    float c = cv[a], sn = sv[a];
     if (head < heads) {
       q[head * 64 + jp] = x1 * c - x2 * sn;
       q[head * 64 + jp + 32] = x2 * c + x1 * sn;
@@ -170,6 +180,12 @@ __device__ __forceinline__ void v_tile_to_lds(const uint16_t* V, int t, int lane
   for (int e = 0; e < 8; e++) __builtin_amdgcn_global_load_lds(src + (size_t)e * 8 * 64, &dst[8 * e][0], 16, 0, 0);
 }
 
+// The instructions e0, e0 + step, ... of v_tile_to_lds: the share of one of `step` waves that move a tile together.
+__device__ __forceinline__ void v_share_to_lds(const uint16_t* V, int t, int lane, int e0, int step, uint4 (*dst)[8]) {
+  const uint16_t* src = V + ((size_t)t * 64 + (lane >> 3)) * 64 + (lane & 7) * 8;
+  for (int e = e0; e < 8; e += step) __builtin_amdgcn_global_load_lds(src + (size_t)e * 8 * 64, &dst[8 * e][0], 16, 0, 0);
+}
+
 template <int G>
 __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ q, const uint16_t* __restrict__ kc,
                                                    const uint16_t* __restrict__ vc, const int* __restrict__ lenp,
@@ -194,11 +210,14 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ q,
   // split s covers tiles [s*tps, s*tps + tps); its first tile is requested before the length is known (the grid
   // only covers tiles inside the cache)
   const int t0 = s * tps;
+  // q and the length first (loads complete in issue order), then the first tile's K rows and V shares
+  const float qv = q[h * 64 + lane];
+  const int len = *lenp + len_add;
+  __builtin_amdgcn_sched_barrier(0);
   Row8 kn;
   kn.load(reinterpret_cast<const uint4*>(K + (size_t)(t0 * 64 + lane) * 64));
   v_share(t0, 0);
-  Qs[w][lane] = q[h * 64 + lane];
-  const int len = *lenp + len_add;
+  Qs[w][lane] = qv;
   const int nb = (len + 63) / 64;
   if (t0 >= nb) {
     __builtin_amdgcn_s_waitcnt(0);  // the tile copy into LDS has finished before the wave ends
@@ -260,6 +279,122 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ q,
       }
     }
     acc = __builtin_fmaf(acc, alpha, pv);
+  }
+  float* pp = part + ((size_t)h * splits + s) * 66;
+  if (lane == 0) {
+    pp[0] = m;
+    pp[1] = l;
+  }
+  pp[2 + lane] = acc;
+}
+
+// Tile-parallel form of k_attn_split for a split of exactly T tiles: workgroup = G x T waves, wave (wh, wt) takes
+// query head g*G + wh and tile t0 + wt. Every wave computes its tile's scores and tile max at once; the running max
+// m_{t-1} each tile's online-softmax step needs is the max of the earlier tiles' maxima (exchanged through LDS), so
+// alpha_t = exp(m_{t-1} - m_t), p_t = exp(s - m_t), the tile sum and p.v are formed in parallel; the first wave of
+// each head then applies l = fma(l, alpha_t, sum_t) and acc = fma(acc, alpha_t, pv_t) over the tiles in order.
+// Every operation and its order are those of the sequential kernel, so the partials are the same bit for bit.
+template <int G, int T>
+__global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restrict__ q, const uint16_t* __restrict__ kc,
+                                                          const uint16_t* __restrict__ vc, const int* __restrict__ lenp,
+                                                          int len_add, int max_len, float scale, int splits,
+                                                          float* __restrict__ part) {
+  __shared__ uint4 Vs[T][64][8];  // fp16 V tiles, row i = position
+  __shared__ float Qs[G][64];
+  __shared__ float Ps[G][T][64];
+  __shared__ float Pv[G][T][64];
+  __shared__ float Tm[G][T], Al[G][T], Ts[G][T];
+  const int g = blockIdx.x / splits, s = blockIdx.x % splits;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int wh = wid % G, wt = wid / G;
+  const int h = g * G + wh;
+  const float NEG_INF = __int_as_float(0xff800000);
+  const uint16_t* K = kc + (size_t)g * max_len * 64;
+  const uint16_t* V = vc + (size_t)g * max_len * 64;
+  const int t0 = s * T, t = t0 + wt;
+  // the tile's rows are requested before the length is known; a tile past the end of the cache (last split, when
+  // T does not divide the tile count) reads the cache's last tile instead and is never used
+  const int tl = min(t, max_len / 64 - 1);
+  // q and the length first (loads complete in issue order), then this tile's K rows and its share of the V tile
+  const float qv = q[h * 64 + lane];
+  const int len = *lenp + len_add;
+  __builtin_amdgcn_sched_barrier(0);
+  Row8 kr;
+  kr.load(reinterpret_cast<const uint4*>(K + (size_t)(tl * 64 + lane) * 64));
+  v_share_to_lds(V, tl, lane, wh, G, Vs[wt]);
+  if (wt == 0) Qs[wh][lane] = qv;
+  const int nb = (len + 63) / 64;
+  const int used = min(T, nb - t0);  // tiles of this split inside the length (>= 1 when the split is used)
+  const bool active = wt < used;
+  const int nv = active ? min(64, len - t * 64) : 0;
+  __syncthreads();  // Qs
+  // scores: lane = position, chain over the 64 dims in order
+  float sc = NEG_INF;
+  if (active) {
+    float dt = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const uint4 ke = kr.at(e);
+      const uint32_t wv[4] = {ke.x, ke.y, ke.z, ke.w};
+#pragma unroll
+      for (int hh = 0; hh < 2; hh++) {
+        const float4 qq = *reinterpret_cast<const float4*>(&Qs[wh][8 * e + 4 * hh]);
+        const float qa[4] = {qq.x, qq.y, qq.z, qq.w};
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const uint32_t word = wv[2 * hh + (c >> 1)];
+          dt = __builtin_fmaf(qa[c], h2f((uint16_t)(word >> (16 * (c & 1)))), dt);
+        }
+      }
+    }
+    sc = lane < nv ? dt * scale : NEG_INF;
+  }
+  const float tmax = group_max<64>(sc);
+  if (lane == 0) Tm[wh][wt] = tmax;
+  __syncthreads();  // tile maxima
+  float pv = 0.0f;
+  if (active) {
+    float mprev = NEG_INF;
+    for (int u = 0; u < wt; u++) mprev = mprev > Tm[wh][u] ? mprev : Tm[wh][u];
+    const float mn = mprev > tmax ? mprev : tmax;
+    const float alpha = dexp(mprev - mn);
+    const float p = dexp(sc - mn);
+    const float ts = group_sum<64>(p);
+    Ps[wh][wt][lane] = p;
+    if (lane == 0) {
+      Al[wh][wt] = alpha;
+      Ts[wh][wt] = ts;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's share of its V tile has landed in LDS
+  __syncthreads();                // every share has; P written
+  if (active) {
+    // p.v: lane = dim, chain over the valid positions in order; LDS reads batched 8 positions at a time
+    const uint16_t* vcol = reinterpret_cast<const uint16_t*>(&Vs[wt][0][0]) + lane;
+#pragma unroll
+    for (int i0 = 0; i0 < 64; i0 += 8) {
+      if (i0 < nv) {
+        float vf[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) vf[u] = h2f(vcol[(i0 + u) * 64]);
+        const float4 p0 = *reinterpret_cast<const float4*>(&Ps[wh][wt][i0]);
+        const float4 p1 = *reinterpret_cast<const float4*>(&Ps[wh][wt][i0 + 4]);
+        const float pa[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+          if (i0 + u < nv) pv = __builtin_fmaf(pa[u], vf[u], pv);
+      }
+    }
+    if (wt > 0) Pv[wh][wt][lane] = pv;
+  }
+  __syncthreads();  // p.v of every tile
+  if (wt != 0 || used <= 0) return;
+  float m = NEG_INF, l = 0.0f, acc = 0.0f;
+  for (int u = 0; u < used; u++) {
+    const float a = Al[wh][u];
+    l = __builtin_fmaf(l, a, Ts[wh][u]);
+    acc = __builtin_fmaf(acc, a, u == 0 ? pv : Pv[wh][u][lane]);
+    m = m > Tm[wh][u] ? m : Tm[wh][u];
   }
   float* pp = part + ((size_t)h * splits + s) * 66;
   if (lane == 0) {
@@ -798,6 +933,15 @@ static hipError_t attn_split_dispatch(hipStream_t s, int G, int kvh, int tps, co
   const int splits = attn_splits_for(max_len, tps);
   if (splits > 64 || max_len % 64) return hipErrorInvalidValue;
   const int blocks = kvh * splits;
+#define TILES_CASE(GG, TT)                                                                                    \
+  if (G == GG && tps == TT) {                                                                                 \
+    klaunch(k_attn_tiles<GG, TT>, blocks, GG * TT * 64, 0, s, q, kc, vc, lenp, len_add, max_len, scale, splits, part); \
+    return hipGetLastError();                                                                                 \
+  }
+  TILES_CASE(1, 1) TILES_CASE(2, 1) TILES_CASE(3, 1) TILES_CASE(4, 1)
+  TILES_CASE(1, 2) TILES_CASE(2, 2) TILES_CASE(3, 2) TILES_CASE(4, 2)
+  TILES_CASE(1, 4) TILES_CASE(2, 4) TILES_CASE(3, 4) TILES_CASE(4, 4)
+#undef TILES_CASE
   switch (G) {
     case 1: klaunch(k_attn_split<1>, blocks, 64, 0, s, q, kc, vc, lenp, len_add, max_len, scale, tps, splits, part); break;
     case 2: klaunch(k_attn_split<2>, blocks, 128, 0, s, q, kc, vc, lenp, len_add, max_len, scale, tps, splits, part); break;

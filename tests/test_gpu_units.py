@@ -101,11 +101,15 @@ def test_argmax_is_greedy_with_the_last_index_on_ties(gpu):
 
 def test_split_kv_attention_is_bit_identical_at_every_slice_and_block_boundary(gpu):
     """tests/model.rs:183-250 cases (splits of 4 tiles over 32, of 2 over 68, of 1 over 16; amplified scores),
-    G=2 and G=3."""
+    G=2 and G=3; plus splits whose tile count does not divide the cache (30 tiles by 4), and splits of 3 and 8 tiles,
+    which take the sequential-tile kernel instead of the tile-parallel one."""
     b = 64
     configs = [(4, 2, 4, 32 * b, [1, 2, b - 1, b, b + 1, 8 * b, 8 * b + 1, 9 * b - 1, 3 * b + 7, 17 * b + 5, 32 * b - 1, 32 * b]),
                (24, 8, 2, 68 * b, [1, b + 1, 64 * b, 64 * b + 1, 67 * b + 9, 68 * b]),
-               (4, 1, 1, 16 * b, [1, b, b + 1, 16 * b])]
+               (4, 1, 1, 16 * b, [1, b, b + 1, 16 * b]),
+               (8, 2, 4, 30 * b, [1, 5 * b + 3, 28 * b, 28 * b + 1, 29 * b + 7, 30 * b]),
+               (6, 2, 3, 20 * b, [1, b + 1, 7 * b, 19 * b + 5, 20 * b]),
+               (4, 4, 8, 40 * b, [1, 9 * b, 33 * b + 2, 40 * b])]
     for heads, kvh, ns, max_len, lens in configs:
         for amp in (False, True):
             q = moert.synth_normal(71, ns, heads * 64)
