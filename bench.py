@@ -173,6 +173,8 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=32, help="oracle decode steps timed for the CPU baseline")
     ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
     ap.add_argument("--seed", type=int, default=3003)
+    ap.add_argument("--attn-splits", type=int, default=32,
+                    help="KV splits requested for decode attention (tiles per split = ceil(tiles / splits))")
     ap.add_argument("--cache-steps", type=int, default=512,
                     help="greedy steps of the 3B Q4_0 model served from a 25%% expert cache (0 skips it)")
     ap.add_argument("--batched-iters", type=int, default=20,
@@ -198,7 +200,7 @@ def main():
     model = moert.SynthModel(cfg, seed=args.seed, wdtype=wd, embed_dtype=ed)
     log(f"weights {model.weight_bytes() / 1e9:.2f} GB in {time.time() - t:.1f} s")
     max_len = (CTX + 1 + args.warmup + args.steps + 63) // 64 * 64
-    g = moert.GpuModel(model, max_len, attn_splits=64)
+    g = moert.GpuModel(model, max_len, attn_splits=args.attn_splits)
     kv = [moert.kv_prefill_data(cfg, args.seed, l, CTX) for l in range(cfg.layers)]
     for l, (k, v) in enumerate(kv):
         g.kv_prefill(l, k, v)
@@ -218,7 +220,7 @@ def main():
     log(f"{args.steps} steps in {wall * 1e3:.1f} ms wall ({ms_event:.3f} ms/step by events): {tok_s:.1f} tok/s")
 
     kernels = {}
-    nsplit = moert.attn_splits_for(max_len, moert.tiles_per_split(max_len, 64))
+    nsplit = moert.attn_splits_for(max_len, moert.tiles_per_split(max_len, args.attn_splits))
     for kind in range(len(moert.KERNEL_NAMES)):
         g.set_position(pos0)
         us, launches = g.time_kernel(kind, args.kernel_iters)
@@ -246,7 +248,7 @@ def main():
     if args.cpu_steps > 0:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle
-        s = oracle.CpuSession(model, max_len, attn_splits=64, threads=args.cpu_threads)
+        s = oracle.CpuSession(model, max_len, attn_splits=args.attn_splits, threads=args.cpu_threads)
         for l, (k, v) in enumerate(kv):
             s.kv_prefill(l, k, v)
         s.set_position(CTX)

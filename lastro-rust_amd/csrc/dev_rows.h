@@ -236,8 +236,10 @@ template <int N, int NT>
 __device__ __forceinline__ void copy_finish(const CopyIn<N, NT>& in, float* xs) {
 #pragma unroll
   for (int e = 0; e < CopyIn<N, NT>::PER; e++) {
+    // unconditional store: a thread past the end holds x[0..3] (the clamped fetch) and writes it where thread 0
+    // writes the same values; a conditional store would let the compiler sink the fetch below the weight loads
     const int i = threadIdx.x + e * NT;
-    if (i < N / 4) reinterpret_cast<float4*>(xs)[i] = in.v[e];
+    reinterpret_cast<float4*>(xs)[i < N / 4 ? i : 0] = in.v[e];
   }
   __syncthreads();
 }

@@ -172,20 +172,6 @@ struct Row8 {
   }
 };
 
-// V rows of tile t into an LDS tile: instruction e moves rows 8e..8e+7, lane l carries 16 bytes of row 8e + l/8,
-// so each instruction reads 1 KB of consecutive cache rows and the LDS tile is row-major [64][64] fp16.
-__device__ __forceinline__ void v_tile_to_lds(const uint16_t* V, int t, int lane, uint4 (*dst)[8]) {
-  const uint16_t* src = V + ((size_t)t * 64 + (lane >> 3)) * 64 + (lane & 7) * 8;
-#pragma unroll
-  for (int e = 0; e < 8; e++) __builtin_amdgcn_global_load_lds(src + (size_t)e * 8 * 64, &dst[8 * e][0], 16, 0, 0);
-}
-
-// The instructions e0, e0 + step, ... of v_tile_to_lds: the share of one of `step` waves that move a tile together.
-__device__ __forceinline__ void v_share_to_lds(const uint16_t* V, int t, int lane, int e0, int step, uint4 (*dst)[8]) {
-  const uint16_t* src = V + ((size_t)t * 64 + (lane >> 3)) * 64 + (lane & 7) * 8;
-  for (int e = e0; e < 8; e += step) __builtin_amdgcn_global_load_lds(src + (size_t)e * 8 * 64, &dst[8 * e][0], 16, 0, 0);
-}
-
 template <int G>
 __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ q, const uint16_t* __restrict__ kc,
                                                    const uint16_t* __restrict__ vc, const int* __restrict__ lenp,
@@ -288,6 +274,40 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ q,
   pp[2 + lane] = acc;
 }
 
+// One wave's share of a V tile moved into LDS through registers, by the G waves that serve the same tile: piece e
+// (e = wave, wave + G, ...) is rows 8e..8e+7, lane l carrying 16 bytes of row 8e + l/8, so each piece reads 1 KB of
+// consecutive cache rows and the LDS tile is row-major [64][64] fp16. Plain loads (not LDS DMA) keep the wait for
+// the tile separate from the waits for the kernel's other loads. A piece index past 7 (only for G = 3) loads piece
+// 7 again and stores it into rows 64..71 of the tile, which are padding and never read.
+template <int G>
+struct VShare {
+  static constexpr int N = (8 + G - 1) / G;
+  uint4 a, b, c, d, e, f, g, h;  // pieces 0..N-1 of this wave (named members: no private array)
+  __device__ __forceinline__ void load(const uint16_t* V, int t, int lane, int wave) {
+    const uint4* src = reinterpret_cast<const uint4*>(V + ((size_t)t * 64 + (lane >> 3)) * 64 + (lane & 7) * 8);
+    auto at = [&](int i) { return src[(size_t)min(wave + G * i, 7) * 64]; };
+    a = at(0);
+    if (N > 1) b = at(1);
+    if (N > 2) c = at(2);
+    if (N > 3) d = at(3);
+    if (N > 4) e = at(4);
+    if (N > 5) f = at(5);
+    if (N > 6) g = at(6);
+    if (N > 7) h = at(7);
+  }
+  __device__ __forceinline__ void store(uint4 (*dst)[8], int lane, int wave) const {
+    auto put = [&](int i, const uint4& v) { dst[8 * (wave + G * i) + (lane >> 3)][lane & 7] = v; };
+    put(0, a);
+    if (N > 1) put(1, b);
+    if (N > 2) put(2, c);
+    if (N > 3) put(3, d);
+    if (N > 4) put(4, e);
+    if (N > 5) put(5, f);
+    if (N > 6) put(6, g);
+    if (N > 7) put(7, h);
+  }
+};
+
 // Tile-parallel form of k_attn_split for a split of exactly T tiles: workgroup = G x T waves, wave (wh, wt) takes
 // query head g*G + wh and tile t0 + wt. Every wave computes its tile's scores and tile max at once; the running max
 // m_{t-1} each tile's online-softmax step needs is the max of the earlier tiles' maxima (exchanged through LDS), so
@@ -299,7 +319,7 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
                                                           const uint16_t* __restrict__ vc, const int* __restrict__ lenp,
                                                           int len_add, int max_len, float scale, int splits,
                                                           float* __restrict__ part) {
-  __shared__ uint4 Vs[T][64][8];  // fp16 V tiles, row i = position
+  __shared__ uint4 Vs[T][72][8];  // fp16 V tiles, row i = position (rows 64..71: padding for VShare)
   __shared__ float Qs[G][64];
   __shared__ float Ps[G][T][64];
   __shared__ float Pv[G][T][64];
@@ -321,16 +341,19 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
   __builtin_amdgcn_sched_barrier(0);
   Row8 kr;
   kr.load(reinterpret_cast<const uint4*>(K + (size_t)(tl * 64 + lane) * 64));
-  v_share_to_lds(V, tl, lane, wh, G, Vs[wt]);
-  if (wt == 0) Qs[wh][lane] = qv;
+  __builtin_amdgcn_sched_barrier(0);  // K (needed first) ahead of V
+  VShare<G> vsh;
+  vsh.load(V, tl, lane, wh);
+  Qs[wh][lane] = qv;  // every wave of head wh stores the same q (an unconditional store keeps the q load first)
   const int nb = (len + 63) / 64;
   const int used = min(T, nb - t0);  // tiles of this split inside the length (>= 1 when the split is used)
   const bool active = wt < used;
   const int nv = active ? min(64, len - t * 64) : 0;
   __syncthreads();  // Qs
-  // scores: lane = position, chain over the 64 dims in order
-  float sc = NEG_INF;
-  if (active) {
+  // scores: lane = position, chain over the 64 dims in order (computed by every wave, so that no branch lets the
+  // compiler sink the K loads below the barrier; an inactive tile's scores are discarded)
+  float sc;
+  {
     float dt = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; e++) {
@@ -347,7 +370,7 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
         }
       }
     }
-    sc = lane < nv ? dt * scale : NEG_INF;
+    sc = lane < nv ? dt * scale : NEG_INF;  // nv = 0 for an inactive tile
   }
   const float tmax = group_max<64>(sc);
   if (lane == 0) Tm[wh][wt] = tmax;
@@ -366,23 +389,42 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
       Ts[wh][wt] = ts;
     }
   }
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's share of its V tile has landed in LDS
-  __syncthreads();                // every share has; P written
+  vsh.store(Vs[wt], lane, wh);
+  __syncthreads();  // every share of every V tile stored; P written
   if (active) {
-    // p.v: lane = dim, chain over the valid positions in order; LDS reads batched 8 positions at a time
+    // p.v: lane = dim, chain over the positions in order, without branches so that every LDS read can be issued
+    // ahead of the chain. A position past the length has p = exp(-inf) = 0 and its V element is replaced by 0, so
+    // its step fma(0, 0, pv) returns pv unchanged (pv starts at +0 and an exact zero sum is +0, so pv is never -0):
+    // the chain equals the one over the valid positions only, bit for bit.
     const uint16_t* vcol = reinterpret_cast<const uint16_t*>(&Vs[wt][0][0]) + lane;
+    if constexpr (G * T < 16) {
 #pragma unroll
-    for (int i0 = 0; i0 < 64; i0 += 8) {
-      if (i0 < nv) {
-        float vf[8];
+      for (int i0 = 0; i0 < 64; i0 += 4) {
+        const float4 p4 = *reinterpret_cast<const float4*>(&Ps[wh][wt][i0]);
+        const float pa[4] = {p4.x, p4.y, p4.z, p4.w};
 #pragma unroll
-        for (int u = 0; u < 8; u++) vf[u] = h2f(vcol[(i0 + u) * 64]);
-        const float4 p0 = *reinterpret_cast<const float4*>(&Ps[wh][wt][i0]);
-        const float4 p1 = *reinterpret_cast<const float4*>(&Ps[wh][wt][i0 + 4]);
-        const float pa[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        for (int u = 0; u < 4; u++) {
+          // masked bits rather than a conditional read, which would become a branch around each LDS read
+          const uint32_t hv = vcol[(i0 + u) * 64];
+          const float vf = h2f((uint16_t)(hv & (i0 + u < nv ? 0xffffu : 0u)));
+          pv = __builtin_fmaf(pa[u], vf, pv);
+        }
+      }
+    } else {
+      // 16 waves leave 128 VGPRs a lane, too few to hoist every read: batches of 8 positions, valid ones only
 #pragma unroll
-        for (int u = 0; u < 8; u++)
-          if (i0 + u < nv) pv = __builtin_fmaf(pa[u], vf[u], pv);
+      for (int i0 = 0; i0 < 64; i0 += 8) {
+        if (i0 < nv) {
+          float vf[8];
+#pragma unroll
+          for (int u = 0; u < 8; u++) vf[u] = h2f(vcol[(i0 + u) * 64]);
+          const float4 p0 = *reinterpret_cast<const float4*>(&Ps[wh][wt][i0]);
+          const float4 p1 = *reinterpret_cast<const float4*>(&Ps[wh][wt][i0 + 4]);
+          const float pa[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+          for (int u = 0; u < 8; u++)
+            if (i0 + u < nv) pv = __builtin_fmaf(pa[u], vf[u], pv);
+        }
       }
     }
     if (wt > 0) Pv[wh][wt][lane] = pv;
@@ -627,8 +669,10 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __r
   }
 #pragma unroll
   for (int q = 0; q < AP; q++) {
+    // unconditional store (past the end: act[0..3] again, where thread 0 writes it), so that the activation
+    // loads stay ahead of the expert rows instead of being sunk into a branch below them
     const int i = threadIdx.x + q * kBlock;
-    if (i < k * K / 4) reinterpret_cast<float4*>(xs)[i] = av[q];
+    reinterpret_cast<float4*>(xs)[i < k * K / 4 ? i : 0] = av[q];
   }
   __syncthreads();
   if (!rok) return;
@@ -933,13 +977,14 @@ static hipError_t attn_split_dispatch(hipStream_t s, int G, int kvh, int tps, co
   const int splits = attn_splits_for(max_len, tps);
   if (splits > 64 || max_len % 64) return hipErrorInvalidValue;
   const int blocks = kvh * splits;
-#define TILES_CASE(GG, TT)                                                                                    \
-  if (G == GG && tps == TT) {                                                                                 \
+#define TILES_CASE(GG, TT)                                                                                   \
+  if (G == GG && tps == TT) {                                                                                \
     klaunch(k_attn_tiles<GG, TT>, blocks, GG * TT * 64, 0, s, q, kc, vc, lenp, len_add, max_len, scale, splits, part); \
-    return hipGetLastError();                                                                                 \
+    return hipGetLastError();                                                                                \
   }
   TILES_CASE(1, 1) TILES_CASE(2, 1) TILES_CASE(3, 1) TILES_CASE(4, 1)
   TILES_CASE(1, 2) TILES_CASE(2, 2) TILES_CASE(3, 2) TILES_CASE(4, 2)
+  TILES_CASE(1, 3) TILES_CASE(2, 3) TILES_CASE(3, 3) TILES_CASE(4, 3)
   TILES_CASE(1, 4) TILES_CASE(2, 4) TILES_CASE(3, 4) TILES_CASE(4, 4)
 #undef TILES_CASE
   switch (G) {

@@ -127,6 +127,26 @@ def test_split_kv_attention_is_bit_identical_at_every_slice_and_block_boundary(g
                 assert bits_equal(got, want), (heads, ns, length, amp)
 
 
+def test_split_kv_attention_ignores_cache_rows_past_the_length(gpu):
+    """Cache rows at and after the length hold fp16 NaN and infinity: no output may depend on them."""
+    b = 64
+    for heads, kvh, ns, max_len, length in [(24, 8, 2, 8 * b, 3 * b + 5), (4, 2, 4, 8 * b, 5 * b + 1),
+                                            (8, 2, 4, 8 * b, 2 * b), (6, 2, 3, 8 * b, b + 9)]:
+        q = moert.synth_normal(74, 1, heads * 64)
+        kc = oracle.f2h(moert.synth_normal(75, 1, kvh * max_len * 64)).reshape(kvh, max_len, 64)
+        vc = oracle.f2h(moert.synth_normal(76, 1, kvh * max_len * 64)).reshape(kvh, max_len, 64)
+        kc[:, length:, ::2] = 0x7E00   # NaN
+        kc[:, length:, 1::2] = 0x7C00  # +inf
+        vc[:, length:, ::2] = 0xFC00   # -inf
+        vc[:, length:, 1::2] = 0x7E00
+        kc, vc = kc.reshape(-1), vc.reshape(-1)
+        say(f"attn past-length poison heads={heads} kv={kvh} tiles/split={ns} len={length}")
+        got = moert.attn_decode(q, kc, vc, heads, kvh, max_len, length, 0.125, ns)
+        want = oracle.attention(q, kc, vc, heads, kvh, max_len, length, 0.125, ns)
+        assert np.isfinite(got).all()
+        assert bits_equal(got, want), (heads, ns, length)
+
+
 @pytest.mark.parametrize("dtype", [moert.Q8_0, moert.Q4_0, moert.F32])
 def test_moe_block_is_bit_identical(gpu, dtype):
     """The 1B MoE block (router 1024->32, top-8, experts 1024->512->1024) and a small one."""
