@@ -251,6 +251,54 @@ __device__ __forceinline__ void wg_copy(const float* __restrict__ x, float* xs) 
   copy_finish<N, NT>(in, xs);
 }
 
+// Ranks of n <= 64 logits held in LDS (lg, visible to the whole workgroup), by all NW waves: wave w counts, for
+// every lane e, the 64-bit sort keys of logits [w * 64 / NW, (w + 1) * 64 / NW) above lane e's key (total-order key,
+// then 63 - e: descending value, ties to the lower index); the counts meet in LDS and every wave adds them in wave
+// order. Returns the rank of lane e's logit (the same in every wave); contains a workgroup barrier.
+template <int NW>
+__device__ __forceinline__ int wg_rank(const float* lg, int n, int lane, int wave, int (*part)[NW]) {
+  constexpr int PER = 64 / NW;
+  static_assert(64 % NW == 0, "waves must divide 64");
+  auto key = [&](int e) -> unsigned long long {
+    return e < n ? (((unsigned long long)((unsigned)total_key(lg[e]) ^ 0x80000000u) << 6) | (unsigned)(63 - e)) : 0ull;
+  };
+  const unsigned long long mine = key(lane);
+  int cnt = 0;
+#pragma unroll
+  for (int u = 0; u < PER; u++) cnt += key(wave * PER + u) > mine;
+  part[lane][wave] = cnt;
+  __syncthreads();
+  int rank = 0;
+#pragma unroll
+  for (int w = 0; w < NW; w++) rank += part[lane][w];
+  return rank;
+}
+
+// The ids of ranks 0..k-1 (k <= 8) as wave-uniform values: id[r] = the lane whose rank is r.
+__device__ __forceinline__ void ids_by_rank(bool sel, int rank, int k, int (&id)[8]) {
+#pragma unroll
+  for (int r = 0; r < 8; r++) {
+    const unsigned long long b = __ballot(sel && rank == r);
+    id[r] = r < k && b ? __ffsll((long long)b) - 1 : 0;
+  }
+}
+
+// Routing weights of the selected lanes: w = exp(l - l_top) / sum, the sum over ranks 0..k-1 left to right
+// (Routing::from_logits, block.rs:81-89); the lane of rank r writes ids[r] and weights[r].
+__device__ __forceinline__ void route_weights(const float* lg, bool sel, int rank, int k, int lane,
+                                              const int (&id)[8], int* ids, float* weights) {
+  const float v = lg[lane];
+  const float ex = sel ? dexp(v - lg[id[0]]) : 0.0f;
+  float sum = 0.0f;
+#pragma unroll
+  for (int r = 0; r < 8; r++)
+    if (r < k) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), id[r]));
+  if (sel) {
+    ids[rank] = lane;
+    weights[rank] = ex / sum;
+  }
+}
+
 // Top-k of n <= 64 logits held in LDS (lg), by one wave. Lane e holds logit e as one 64-bit sort key
 // (total-order key, then 63 - e, so that larger means earlier: descending value, ties to the lower index); the keys
 // are broadcast through LDS and each lane counts the keys above its own, which is its rank; a lane whose rank is

@@ -541,9 +541,8 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
   constexpr int P = 2 * NP;
   __shared__ float xs[K];
   __shared__ __align__(16) float lg[64];
-  __shared__ __align__(16) TopkLds tk;
+  __shared__ int part[64][kRouteWaves];
   __shared__ int sids[8];
-  __shared__ float sw[8];
   __shared__ float rs;
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int sub = lane % G::LPR, rw = lane / G::LPR;
@@ -556,10 +555,7 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
   else
     copy_fetch<K, NT>(h, cin);
   if (ROUTED) {
-    if (threadIdx.x < k) {
-      sids[threadIdx.x] = slots_in[threadIdx.x];
-      sw[threadIdx.x] = w_out[threadIdx.x];
-    }
+    if (threadIdx.x < k) sids[threadIdx.x] = slots_in[threadIdx.x];
     if (NORM)
       norm_finish<K, NT>(hin, eps, xs, &rs);
     else
@@ -590,14 +586,17 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
       if (ok[p] && sub == 0) lg[row[p]] = bias ? out[p] + bv[p] : out[p];
   }
   __syncthreads();
-  if (!ROUTED && wave == 0) {
-    wave_topk(lg, E, k, lane, tk, sids, sw);
-    if (blockIdx.x == 0 && lane < k) {
-      ids_out[lane] = sids[lane];
-      w_out[lane] = sw[lane];
-    }
+  // routed ids as wave-uniform values: ranked by all waves (ROUTED: the given slots)
+  int eid[8];
+  if (!ROUTED) {
+    const int rank = wg_rank<kRouteWaves>(lg, E, lane, wave, part);
+    const bool sel = lane < E && rank < k;
+    ids_by_rank(sel, rank, k, eid);
+    if (blockIdx.x == 0 && wave == 0) route_weights(lg, sel, rank, k, lane, eid, ids_out, w_out);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 8; r++) eid[r] = r < k ? sids[r] : 0;
   }
-  __syncthreads();
   const int npairs = k * inter;
   const int wbase = (blockIdx.x * kRouteWaves + wave) * (NP * G::RPW);
   size_t row[P];
@@ -608,7 +607,10 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
     gp[a] = wbase + a * G::RPW + rw;
     bool v = gp[a] < npairs;
     int j = v ? gp[a] / inter : 0, r = gp[a] % inter;
-    size_t e = (size_t)sids[j];
+    int ej = eid[0];
+#pragma unroll
+    for (int q = 1; q < 8; q++) ej = j == q ? eid[q] : ej;
+    size_t e = (size_t)ej;
     row[2 * a] = e * 2 * inter + r;
     row[2 * a + 1] = e * 2 * inter + inter + r;
     ok[2 * a] = v;
