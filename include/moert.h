@@ -101,9 +101,9 @@ int moert_model_destroy(moert_model* m);
  * and `slots` of them at a time in an HBM pool (top_k <= slots <= min(4096, layers*experts)). Each layer step
  * routes on the device, then applies the LRU rule of the reference's LruSync cache: every requested expert already
  * in the pool is pinned for the step, each miss (in top-k order) takes the first free slot or else the least
- * recently used slot not used in this step (lowest slot index on ties), and is copied in from host memory by a
- * device kernel before the experts run. No host synchronisation per layer: a step stays one graph. Outputs are
- * identical to moert_model_create's. Replaces GpuModel::upload_cached + ExpertCache (rust/moe-rt/src/gpu_model.rs:
+ * recently used slot not used in this step (lowest slot index on ties). The kernels that use a missed expert read
+ * it from host memory and write it into its slot as they go. No host synchronisation per layer: a step stays one
+ * graph of the same kernels as moert_model_create's, and its outputs are identical to that model's. Replaces GpuModel::upload_cached + ExpertCache (rust/moe-rt/src/gpu_model.rs:
  * 197-200, rust/moe-rt/src/cache.rs:140-354, LRU rule of rust/moe-rt/tests/model.rs:380-412). */
 int moert_model_create_cached(const moert_config* cfg, const moert_model_weights* w, int max_len, int attn_splits,
                               int slots, moert_model** out);
@@ -156,13 +156,11 @@ typedef enum {
   MOERT_K_ATTN_SPLIT = 2,   /* split-KV attention partials */
   MOERT_K_ATTN_COMBINE = 3, /* combine of the split partials */
   MOERT_K_OPROJ = 4,        /* output projection + residual */
-  MOERT_K_ROUTE_UP = 5,     /* rmsnorm + router + top-k + gate/up + SwiGLU of the routed experts */
+  MOERT_K_ROUTE_UP = 5,     /* rmsnorm + router + top-k (+ LRU decision) + gate/up + SwiGLU of the routed experts */
   MOERT_K_EXPERT_DOWN = 6,  /* down of the routed experts + weighted combine + residual */
   MOERT_K_HEAD = 7,         /* final rmsnorm + LM head + per-block argmax */
   MOERT_K_HEAD_ARGMAX = 8,  /* argmax over the head blocks, token and position update */
-  MOERT_K_ROUTE_LRU = 9,    /* expert cache: rmsnorm + router + top-k + LRU decision (cached models) */
-  MOERT_K_FILL = 10,        /* expert cache: copy of the misses from host memory into the pool (cached models) */
-  MOERT_K_COUNT = 11
+  MOERT_K_COUNT = 9
 } moert_kernel_kind;
 int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch, int* launches);
 
@@ -230,7 +228,7 @@ int moert_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v
 int moert_copy_probe(size_t bytes, int iters, double* us_per_copy);
 
 /* PCIe reference for the expert cache: mean microseconds of one copy of `bytes` (multiple of 16) from pinned,
- * device-mapped host memory into HBM, by a copy kernel (the way the cache fills its pool) and by hipMemcpyAsync
+ * device-mapped host memory into HBM, by a copy kernel (the way the cached kernels read missed experts) and by hipMemcpyAsync
  * (the DMA engines). The analogue of the reference's PCIe measurement programs (tools/llama-forcado/banda.cu,
  * qual-runs/PCIE-X8-20261031/banda2.cu), which are not on its runtime path. */
 int moert_h2d_probe(size_t bytes, int iters, double* kernel_us, double* memcpy_us);

@@ -1,5 +1,8 @@
-// Expert cache on the device (cache.hip): an HBM pool of `slots` experts filled from a pinned host store, with
-// the LRU bookkeeping done by a kernel so that a whole decode step stays one graph with no host round trip.
+// Expert cache on the device: an HBM pool of `slots` experts over a pinned host store. Every workgroup of the
+// cached gate/up kernel makes the LRU decision of its layer step itself, from the same slot tables, and workgroup 0
+// writes the result; an expert that misses is read from the host store by the kernels that use it (gate/up, then
+// down), which also write it into its slot. So a whole decode step, copies included, stays one graph of the same
+// six kernels per layer as the resident model, with no host round trip.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -17,27 +20,30 @@ struct CacheDev {
   DMat pool_gu;           // [slots * 2I, H]: slot s holds rows [s*2I, s*2I + 2I) (gate rows, then up rows)
   DMat pool_dn;           // [slots * H, I]
   const uint8_t* host;    // pinned store, one record per key = layer * E + expert: [gu payload | gu scales |
-                          // down payload | down scales], record_bytes each
+                          // down payload | down scales], record_bytes each (device address of the mapping)
   size_t record_bytes, gu_q, gu_d, dn_q;  // record size and its first three piece sizes (dn_d is the rest)
   int slots;
   int experts;
-  int* slot_key;          // [slots] key held by the slot, -1 when free
-  int* slot_last;         // [slots] clock of the slot's last use
-  int* key_slot;          // [layers * E] slot of a resident key, -1 otherwise
-  int* clock;             // [1] one tick per layer step
+  // Two copies of the slot tables and the clock: a layer step reads copy `*cur` and workgroup 0 of the gate/up
+  // kernel writes the updated tables into the other copy; the down kernel then switches `*cur`. No kernel writes
+  // the copy it reads, so the workgroups of one launch all decide from the same tables.
+  int* slot_key;          // [2][slots] key held by the slot, -1 when free
+  int* slot_last;         // [2][slots] clock of the slot's last use
+  int* clock;             // [2] one tick per layer step
+  int* cur;               // [1] the current copy (0 or 1)
   unsigned long long* stats;  // [CS_WORDS]
-  int* route_slot;        // [k] slots of the current layer's routed experts, top-k order
-  int* miss;              // [1 + 2k]: count, then (slot, key) pairs to copy in
+  int* route;             // [16] the current layer step: slot of each routed expert in top-k order, then its host
+                          // key when it missed (read from the host store by the down kernel), -1 when it hit
 };
 
-// Router of layer `layer` (rmsnorm of h, GEMV, optional bias), top-k into b.route_ids / b.route_w of the layer,
-// then the LRU decision for its k keys: hits are pinned, misses take the first free slot or else the least
-// recently used slot not used in this layer step.
-hipError_t launch_route_lru(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
-                            const CacheDev& c);
-// Copies the current miss list from the host store into the pool (PCIe reads by the kernel).
-hipError_t launch_fill(hipStream_t s, const CacheDev& c, int k);
-// Kernel copy of `bytes` (multiple of 16) from device-mapped pinned host memory to device memory.
+// The MoE half of a layer step of a cached model: rmsnorm + router + top-k + LRU decision + gate/up + SwiGLU of the
+// routed experts (k_route_up, cached mode), then down + combine + residual (k_expert_down, cached mode).
+hipError_t launch_route_up_cached(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
+                                  const CacheDev& c);
+hipError_t launch_expert_down_cached(hipStream_t s, const Dims& d, const StepBufs& b, int layer, const CacheDev& c);
+
+// Kernel copy of `bytes` (multiple of 16) from device-mapped pinned host memory to device memory (the PCIe rate
+// the cached kernels' host reads are bounded by).
 hipError_t launch_h2d_copy(hipStream_t s, const void* src, void* dst, size_t bytes);
 
 }  // namespace moert

@@ -126,6 +126,42 @@ __device__ __forceinline__ void rows_load(Rows<DT, K, P>& r, const DMat& m, cons
     }
 }
 
+// rows_load with a matrix per row (rows of routed experts that live in different places).
+template <int DT, int K, int P>
+__device__ __forceinline__ void rows_load_from(Rows<DT, K, P>& r, const DMat (&m)[P], const size_t (&row)[P],
+                                               const bool (&ok)[P], int sub) {
+  using G = Geo<DT, K>;
+#pragma unroll
+  for (int p = 0; p < P; p++)
+#pragma unroll
+    for (int jj = 0; jj < G::NJ; jj++) {
+      const int j = sub + G::LPR * jj;
+      r.c[p][jj] = load_chunk<DT>(m[p], ok[p] ? row[p] : 0, j < G::NCH ? j : G::NCH - 1);
+    }
+}
+
+// Writes the lane's chunks of row p back, as loaded, into row dst_row[p] of `dst` where put[p] (the chunk payload
+// and its scale; for Q8_0 the even chunk of a block writes the block's scale).
+template <int DT, int K, int P>
+__device__ __forceinline__ void rows_store(const Rows<DT, K, P>& r, const DMat& dst, const size_t (&dst_row)[P],
+                                           const bool (&put)[P], int sub) {
+  using G = Geo<DT, K>;
+#pragma unroll
+  for (int p = 0; p < P; p++) {
+    if (!put[p]) continue;
+#pragma unroll
+    for (int jj = 0; jj < G::NJ; jj++) {
+      const int j = sub + G::LPR * jj;
+      if (j >= G::NCH) continue;
+      uint8_t* base = const_cast<uint8_t*>(dst.q) + dst_row[p] * Fmt<DT>::row_bytes(dst.cols);
+      *reinterpret_cast<uint4*>(base + (size_t)j * 16) = r.c[p][jj].v;
+      uint16_t* sc = const_cast<uint16_t*>(dst.d) + dst_row[p] * (size_t)(dst.cols / 32);
+      if (DT == DT_Q8_0 && (j & 1) == 0) sc[j >> 1] = (uint16_t)r.c[p][jj].d;
+      if (DT == DT_Q4_0) sc[j] = (uint16_t)r.c[p][jj].d;
+    }
+  }
+}
+
 template <int DT, int K, int P>
 __device__ __forceinline__ void rows_fma(const Rows<DT, K, P>& r, const bool (&ok)[P], const XReg<DT, K>& xr,
                                          int sub, float (&out)[P]) {

@@ -209,14 +209,10 @@ struct moert_model {
       arm(MOERT_K_OPROJ);
       CHECK_HIP(launch_oproj(stream, L, dims, b));
       if (cached) {
-        arm(MOERT_K_ROUTE_LRU);
-        CHECK_HIP(launch_route_lru(stream, L, dims, b, (int)l, cache));
-        arm(MOERT_K_FILL);
-        CHECK_HIP(launch_fill(stream, cache, dims.top_k));
         arm(MOERT_K_ROUTE_UP);
-        CHECK_HIP(launch_up_routed(stream, cache.pool_gu, L.ln_moe, dims, b, (int)l, cache.route_slot));
+        CHECK_HIP(launch_route_up_cached(stream, L, dims, b, (int)l, cache));
         arm(MOERT_K_EXPERT_DOWN);
-        CHECK_HIP(launch_expert_down_slots(stream, cache.pool_dn, dims, b, (int)l, cache.route_slot));
+        CHECK_HIP(launch_expert_down_cached(stream, dims, b, (int)l, cache));
       } else {
         arm(MOERT_K_ROUTE_UP);
         CHECK_HIP(launch_route_up(stream, L, dims, b, (int)l, true));
@@ -260,12 +256,13 @@ struct moert_model {
     return MOERT_OK;
   }
 
-  // Empties the pool and zeroes the clock and the counters (ExpertCache::clear, rust/moe-rt/src/cache.rs:216-220).
+  // Empties the pool and zeroes the clock and the counters (ExpertCache::clear, rust/moe-rt/src/cache.rs:216-220):
+  // both copies of the slot tables, copy 0 current.
   int cache_clear() {
-    CHECK_HIP(hipMemsetAsync(cache.slot_key, 0xff, (size_t)cache.slots * 4, stream));
-    CHECK_HIP(hipMemsetAsync(cache.slot_last, 0, (size_t)cache.slots * 4, stream));
-    CHECK_HIP(hipMemsetAsync(cache.key_slot, 0xff, (size_t)cfg.layers * cfg.experts * 4, stream));
-    CHECK_HIP(hipMemsetAsync(cache.clock, 0, 4, stream));
+    CHECK_HIP(hipMemsetAsync(cache.slot_key, 0xff, 2 * (size_t)cache.slots * 4, stream));
+    CHECK_HIP(hipMemsetAsync(cache.slot_last, 0, 2 * (size_t)cache.slots * 4, stream));
+    CHECK_HIP(hipMemsetAsync(cache.clock, 0, 2 * 4, stream));
+    CHECK_HIP(hipMemsetAsync(cache.cur, 0, 4, stream));
     CHECK_HIP(hipMemsetAsync(cache.stats, 0, CS_WORDS * 8, stream));
     CHECK_HIP(hipStreamSynchronize(stream));
     return MOERT_OK;
@@ -329,23 +326,20 @@ static int cache_create(moert_model* m, const moert_model_weights* w, int slots)
   };
   if ((rc = mat((size_t)slots * gu_rows, H, &cd.pool_gu)) || (rc = mat((size_t)slots * dn_rows, I, &cd.pool_dn)))
     return rc;
-  // the pool's slot pieces must start where the fill kernel writes them: payload planes are contiguous per slot
   cd.slots = slots;
   cd.experts = E;
-  if ((rc = a.alloc(&p, (size_t)slots * 4))) return rc;
+  if ((rc = a.alloc(&p, 2 * (size_t)slots * 4))) return rc;
   cd.slot_key = (int*)p;
-  if ((rc = a.alloc(&p, (size_t)slots * 4))) return rc;
+  if ((rc = a.alloc(&p, 2 * (size_t)slots * 4))) return rc;
   cd.slot_last = (int*)p;
-  if ((rc = a.alloc(&p, (size_t)L * E * 4))) return rc;
-  cd.key_slot = (int*)p;
-  if ((rc = a.alloc(&p, 256))) return rc;
+  if ((rc = a.alloc(&p, 2 * 4))) return rc;
   cd.clock = (int*)p;
+  if ((rc = a.alloc(&p, 4))) return rc;
+  cd.cur = (int*)p;
   if ((rc = a.alloc(&p, CS_WORDS * 8))) return rc;
   cd.stats = (unsigned long long*)p;
-  if ((rc = a.alloc(&p, 8 * 4))) return rc;
-  cd.route_slot = (int*)p;
-  if ((rc = a.alloc(&p, (1 + 2 * 8) * 4))) return rc;
-  cd.miss = (int*)p;
+  if ((rc = a.alloc(&p, 16 * 4))) return rc;
+  cd.route = (int*)p;
   m->cached = true;
   return m->cache_clear();
 }

@@ -58,12 +58,6 @@ hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, cons
 // accumulate: h += res * y (decode step); otherwise y is written to b.logits (standalone MoE block output).
 hipError_t launch_expert_down(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
                               bool accumulate);
-// Expert-cache path: gate/up (with rmsnorm of h by lnw) and down of the k routed experts held in the slots
-// slots[0, k) of the pool matrices gu [S*2I, H] and down [S*H, I]; weights from b.route_w of the layer.
-hipError_t launch_up_routed(hipStream_t s, const DMat& gu, const float* lnw, const Dims& d, const StepBufs& b,
-                            int layer, const int* slots);
-hipError_t launch_expert_down_slots(hipStream_t s, const DMat& down, const Dims& d, const StepBufs& b, int layer,
-                                   const int* slots);
 hipError_t launch_head(hipStream_t s, const DMat& head, const float* norm, const Dims& d, const StepBufs& b);
 hipError_t launch_head_argmax(hipStream_t s, const DMat& head, const Dims& d, const StepBufs& b);
 int head_blocks(const DMat& head);

@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <climits>
 
+#include "cache_dev.h"
 #include "dev_rows.h"
 #include "kernels.h"
 #include "launch.h"
@@ -526,23 +527,29 @@ __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restric
 // cpu.rs:116-137). E <= 64, k <= 8.
 constexpr int kRouteWaves = 8;
 
-// ROUTED: the routing is already made (expert-cache path): slots_in holds the k slot ids of the routed experts in
-// gu and w_out their weights; the router is skipped.
-template <int DT, int K, int NP, bool NORM, bool ROUTED>
+// CACHED (expert-cache path): after the top-k, wave 0 of every workgroup makes the layer step's LRU decision from
+// the current copy of the slot tables (all workgroups read the same copy, so they all decide alike); workgroup 0
+// writes the updated tables into the other copy, the counters and the routed slots for the down kernel. Rows of a
+// routed expert come from its pool slot, or, when it missed, from its record in the host store; those rows are also
+// written into the slot.
+template <int DT, int K, int NP, bool NORM, bool CACHED>
 __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, const float* __restrict__ bias, DMat gu,
                                                                const float* __restrict__ h,
                                                                const float* __restrict__ lnw, float eps, int k,
-                                                               int inter, int* __restrict__ ids_out,
+                                                               int inter, int layer, int* __restrict__ ids_out,
                                                                float* __restrict__ w_out, float* __restrict__ act,
-                                                               const int* __restrict__ slots_in) {
+                                                               CacheDev c) {
   using G = Geo<DT, K>;
   constexpr int NT = kRouteWaves * 64;
   constexpr int RP = (64 + kRouteWaves * G::RPW - 1) / (kRouteWaves * G::RPW);  // router passes for 64 rows
   constexpr int P = 2 * NP;
+  constexpr int SMAX = CACHED ? kCacheMaxSlots : 1;
   __shared__ float xs[K];
   __shared__ __align__(16) float lg[64];
   __shared__ int part[64][kRouteWaves];
-  __shared__ int sids[8];
+  __shared__ int skey[SMAX];
+  __shared__ int slast[SMAX];
+  __shared__ int lslot[8], lmiss[8], lfound[8];
   __shared__ float rs;
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int sub = lane % G::LPR, rw = lane / G::LPR;
@@ -554,14 +561,7 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
     norm_fetch<K, NT>(h, lnw, hin);
   else
     copy_fetch<K, NT>(h, cin);
-  if (ROUTED) {
-    if (threadIdx.x < k) sids[threadIdx.x] = slots_in[threadIdx.x];
-    if (NORM)
-      norm_finish<K, NT>(hin, eps, xs, &rs);
-    else
-      copy_finish<K, NT>(cin, xs);
-    load_x<DT, K>(xr, xs, sub);
-  } else {
+  {
     size_t row[RP];
     bool ok[RP];
 #pragma unroll
@@ -574,6 +574,13 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
     float bv[RP];
 #pragma unroll
     for (int p = 0; p < RP; p++) bv[p] = (bias && ok[p]) ? bias[row[p]] : 0.0f;
+    if (CACHED) {
+      const int cur = *c.cur, S = c.slots;
+      for (int i = threadIdx.x; i < S; i += NT) {
+        skey[i] = c.slot_key[cur * S + i];
+        slast[i] = c.slot_last[cur * S + i];
+      }
+    }
     if (NORM)
       norm_finish<K, NT>(hin, eps, xs, &rs);
     else
@@ -586,40 +593,88 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
       if (ok[p] && sub == 0) lg[row[p]] = bias ? out[p] + bv[p] : out[p];
   }
   __syncthreads();
-  // routed ids as wave-uniform values: ranked by all waves (ROUTED: the given slots)
+  // routed ids as wave-uniform values, ranked by all waves
   int eid[8];
-  if (!ROUTED) {
-    const int rank = wg_rank<kRouteWaves>(lg, E, lane, wave, part);
-    const bool sel = lane < E && rank < k;
-    ids_by_rank(sel, rank, k, eid);
-    if (blockIdx.x == 0 && wave == 0) route_weights(lg, sel, rank, k, lane, eid, ids_out, w_out);
-  } else {
+  const int rank = wg_rank<kRouteWaves>(lg, E, lane, wave, part);
+  const bool sel = lane < E && rank < k;
+  ids_by_rank(sel, rank, k, eid);
+  if (blockIdx.x == 0 && wave == 0) route_weights(lg, sel, rank, k, lane, eid, ids_out, w_out);
+  // expert-cache path: slots of the routed experts (eid becomes slot ids) and the keys of the misses
+  int mk[8];
 #pragma unroll
-    for (int r = 0; r < 8; r++) eid[r] = r < k ? sids[r] : 0;
+  for (int r = 0; r < 8; r++) mk[r] = -1;
+  if (CACHED) {
+    const int cur = *c.cur, S = c.slots;
+    if (wave == 0) {
+      int key = 0;
+#pragma unroll
+      for (int r = 0; r < 8; r++) key = lane == r ? layer * c.experts + eid[r] : key;
+      const int clock = c.clock[cur] + 1;
+      int slot, miss_key, hits, misses;
+      lru_decide(skey, slast, lfound, S, clock, k, lane, key, slot, miss_key, hits, misses);
+      if (lane < k) {
+        lslot[lane] = slot;
+        lmiss[lane] = miss_key;
+      }
+      if (blockIdx.x == 0) {
+        if (lane < k) {
+          c.route[lane] = slot;
+          c.route[8 + lane] = miss_key;
+        }
+        if (lane == 0) {
+          c.clock[cur ^ 1] = clock;
+          c.stats[CS_HITS] += (unsigned long long)hits;
+          c.stats[CS_COPIES] += (unsigned long long)misses;
+        }
+      }
+    }
+    __syncthreads();
+    if (blockIdx.x == 0)
+      for (int i = threadIdx.x; i < S; i += NT) {
+        c.slot_key[(cur ^ 1) * S + i] = skey[i];
+        c.slot_last[(cur ^ 1) * S + i] = slast[i];
+      }
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      eid[r] = r < k ? lslot[r] : 0;
+      mk[r] = r < k ? lmiss[r] : -1;
+    }
   }
   const int npairs = k * inter;
   const int wbase = (blockIdx.x * kRouteWaves + wave) * (NP * G::RPW);
-  size_t row[P];
-  bool ok[P];
+  size_t row[P], prow[P];
+  bool ok[P], put[P];
+  DMat src[P];
   int gp[NP];
 #pragma unroll
   for (int a = 0; a < NP; a++) {
     gp[a] = wbase + a * G::RPW + rw;
     bool v = gp[a] < npairs;
     int j = v ? gp[a] / inter : 0, r = gp[a] % inter;
-    int ej = eid[0];
+    int ej = eid[0], mj = mk[0];
 #pragma unroll
-    for (int q = 1; q < 8; q++) ej = j == q ? eid[q] : ej;
-    size_t e = (size_t)ej;
-    row[2 * a] = e * 2 * inter + r;
-    row[2 * a + 1] = e * 2 * inter + inter + r;
+    for (int q = 1; q < 8; q++) {
+      ej = j == q ? eid[q] : ej;
+      mj = j == q ? mk[q] : mj;
+    }
+    size_t r0 = (size_t)ej * 2 * inter;
+    src[2 * a] = src[2 * a + 1] = CACHED ? expert_source(c, 0, ej, mj, r0) : gu;
+    row[2 * a] = r0 + r;
+    row[2 * a + 1] = r0 + inter + r;
+    prow[2 * a] = (size_t)ej * 2 * inter + r;
+    prow[2 * a + 1] = prow[2 * a] + inter;
     ok[2 * a] = v;
     ok[2 * a + 1] = v;
+    put[2 * a] = put[2 * a + 1] = CACHED && v && mj >= 0;
   }
   Rows<DT, K, P> rr;
-  rows_load<DT, K, P>(rr, gu, row, ok, sub);
+  if (CACHED)
+    rows_load_from<DT, K, P>(rr, src, row, ok, sub);
+  else
+    rows_load<DT, K, P>(rr, gu, row, ok, sub);
   float out[P];
   rows_fma<DT, K, P>(rr, ok, xr, sub, out);
+  if (CACHED) rows_store<DT, K, P>(rr, c.pool_gu, prow, put, sub);  // a missed expert's rows into its slot
   if (sub != 0) return;
 #pragma unroll
   for (int a = 0; a < NP; a++)
@@ -629,11 +684,13 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
 // Down rows of the k routed experts, combined in top-k order, residual in the epilogue:
 // h[r] = h[r] + res * sum_j w_j * (down_{ids[j]}[r] . act_j) (gemv_axpby gpu.rs:80-103 / moe_down hits.rs:109-148;
 // Cpu::experts cpu.rs:138-148). One output row per wave; expert slot j = pass * RPW + group.
-template <int DT, int K>
+// CACHED: expert j's rows come from pool slot c.route[j], or, when it missed, from its record c.route[8 + j] in the
+// host store (and are written into the slot); workgroup 0 then makes the other copy of the slot tables current.
+template <int DT, int K, bool CACHED>
 __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __restrict__ act,
                                                         const int* __restrict__ ids, const float* __restrict__ wts,
                                                         int k, int hidden, float res, bool accumulate,
-                                                        float* __restrict__ h) {
+                                                        float* __restrict__ h, CacheDev c) {
   using G = Geo<DT, K>;
   constexpr int KMAX = 8;
   constexpr int KP = (KMAX + G::RPW - 1) / G::RPW;
@@ -644,11 +701,12 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __r
   bool rok = r < hidden;
   // routed ids, then activations (loads complete in issue order, so waiting for the ids does not wait for the
   // activations), then the expert rows, then the activations into LDS
-  int idj[KP];
+  int idj[KP], mkj[KP];
 #pragma unroll
   for (int p = 0; p < KP; p++) {
     const int j = p * G::RPW + rw;
-    idj[p] = ids[j < k ? j : 0];
+    idj[p] = CACHED ? c.route[j < k ? j : 0] : ids[j < k ? j : 0];
+    mkj[p] = CACHED ? c.route[8 + (j < k ? j : 0)] : -1;
   }
   constexpr int AP = (KMAX * K / 4 + kBlock - 1) / kBlock;
   float4 av[AP];
@@ -659,16 +717,20 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __r
   }
   float hold = (rok && lane == 0 && accumulate) ? h[r] : 0.0f;
   __builtin_amdgcn_sched_barrier(0);  // ids and activations ahead of the expert rows
-  RawChunk c[KP][G::NJ];
+  Rows<DT, K, KP> rows;
+  size_t srow[KP], prow[KP];
+  bool all[KP], put[KP];
+  DMat src[KP];
 #pragma unroll
   for (int p = 0; p < KP; p++) {
-    const size_t row = (size_t)idj[p] * hidden + (rok ? r : 0);
-#pragma unroll
-    for (int jj = 0; jj < G::NJ; jj++) {
-      const int ch = sub + G::LPR * jj;
-      c[p][jj] = load_chunk<DT>(m, row, ch < G::NCH ? ch : G::NCH - 1);
-    }
+    size_t r0 = (size_t)idj[p] * hidden;
+    src[p] = CACHED ? expert_source(c, 1, idj[p], mkj[p], r0) : m;
+    srow[p] = r0 + (rok ? r : 0);
+    prow[p] = (size_t)idj[p] * hidden + (rok ? r : 0);
+    all[p] = true;
+    put[p] = CACHED && rok && mkj[p] >= 0 && p * G::RPW + rw < k;
   }
+  rows_load_from<DT, K, KP>(rows, src, srow, all, sub);
 #pragma unroll
   for (int q = 0; q < AP; q++) {
     // unconditional store (past the end: act[0..3] again, where thread 0 writes it), so that the activation
@@ -677,6 +739,10 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __r
     reinterpret_cast<float4*>(xs)[i < k * K / 4 ? i : 0] = av[q];
   }
   __syncthreads();
+  if (CACHED) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) *c.cur ^= 1;
+    rows_store<DT, K, KP>(rows, c.pool_dn, prow, put, sub);  // a missed expert's rows into its slot
+  }
   if (!rok) return;
   float dsum[KP];
 #pragma unroll
@@ -689,7 +755,7 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __r
 #pragma unroll
       for (int jj = 0; jj < G::NJ; jj++) {
         int ch = sub + G::LPR * jj;
-        if (ch < G::NCH) acc = fma_chunk<DT>(c[p][jj], xr.v[jj], acc);
+        if (ch < G::NCH) acc = fma_chunk<DT>(rows.c[p][jj], xr.v[jj], acc);
       }
     }
     dsum[p] = group_sum<G::LPR>(acc);
@@ -1040,73 +1106,76 @@ constexpr int kRouteNP = 2;
 hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
                            bool normalize) {
   if (L.router.dtype != L.gate_up.dtype || L.router.cols != L.gate_up.cols) return hipErrorInvalidValue;
+  const CacheDev none{};
 #define BODY(KK)                                                                                           \
   case KK: {                                                                                               \
     constexpr int PB = kRouteWaves * kRouteNP * Geo<DTC, KK>::RPW;                                         \
     const int blocks = cdiv((long)d.top_k * d.inter, PB);                                                  \
     if (normalize)                                                                                         \
       klaunch(k_route_up<DTC, KK, kRouteNP, true, false>, blocks, kRouteWaves * 64, 0, s,                       \
-          L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter,                      \
-          b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, (const int*)nullptr);         \
+          L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter, layer,               \
+          b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, none);                        \
     else                                                                                                   \
       klaunch(k_route_up<DTC, KK, kRouteNP, false, false>, blocks, kRouteWaves * 64, 0, s,                      \
-          L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter,                      \
-          b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, (const int*)nullptr);         \
+          L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter, layer,               \
+          b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, none);                        \
   } break;
   MOERT_DISPATCH(L.router.dtype, L.router.cols, BODY)
 #undef BODY
   return hipGetLastError();
 }
 
-hipError_t launch_up_routed(hipStream_t s, const DMat& gu, const float* lnw, const Dims& d, const StepBufs& b,
-                            int layer, const int* slots) {
+hipError_t launch_route_up_cached(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
+                                  const CacheDev& c) {
+  if (L.router.dtype != c.pool_gu.dtype || L.router.cols != c.pool_gu.cols || c.slots < d.top_k ||
+      c.slots > kCacheMaxSlots || L.router.rows > 64 || d.top_k > 8)
+    return hipErrorInvalidValue;
 #define BODY(KK)                                                                                           \
   case KK: {                                                                                               \
     constexpr int PB = kRouteWaves * kRouteNP * Geo<DTC, KK>::RPW;                                         \
     const int blocks = cdiv((long)d.top_k * d.inter, PB);                                                  \
-    klaunch(k_route_up<DTC, KK, kRouteNP, true, true>, blocks, kRouteWaves * 64, 0, s, gu, (const float*)nullptr, \
-            gu, b.h, lnw, d.eps, d.top_k, d.inter, b.route_ids + layer * d.top_k,                          \
-            b.route_w + layer * d.top_k, b.act, slots);                                                    \
+    klaunch(k_route_up<DTC, KK, kRouteNP, true, true>, blocks, kRouteWaves * 64, 0, s, L.router,           \
+            L.router_bias, c.pool_gu, b.h, L.ln_moe, d.eps, d.top_k, d.inter, layer,                       \
+            b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, c);                         \
   } break;
-  MOERT_DISPATCH(gu.dtype, gu.cols, BODY)
+  MOERT_DISPATCH(L.router.dtype, L.router.cols, BODY)
 #undef BODY
   return hipGetLastError();
 }
 
-hipError_t launch_expert_down_slots(hipStream_t s, const DMat& down, const Dims& d, const StepBufs& b, int layer,
-                                   const int* slots) {
+#define DOWN_DISPATCH(dt, cols, BODY)                                                                     \
+  switch (dt) {                                                                                           \
+    case DT_Q8_0: { constexpr int DTC = DT_Q8_0; switch (cols) { MOERT_KDOWN_CASES(BODY) default: return hipErrorInvalidValue; } } break; \
+    case DT_Q4_0: { constexpr int DTC = DT_Q4_0; switch (cols) { MOERT_KDOWN_CASES(BODY) default: return hipErrorInvalidValue; } } break; \
+    case DT_F32: { constexpr int DTC = DT_F32; switch (cols) { MOERT_KDOWN_CASES(BODY) default: return hipErrorInvalidValue; } } break;   \
+    default: return hipErrorInvalidValue;                                                                 \
+  }
+
+hipError_t launch_expert_down_cached(hipStream_t s, const Dims& d, const StepBufs& b, int layer, const CacheDev& c) {
 #define BODY(KK)                                                                                          \
   case KK:                                                                                                \
-    klaunch(k_expert_down<DTC, KK>, cdiv(d.hidden, kWavesPerBlock), kBlock, 0, s, down, b.act, slots,      \
-            b.route_w + layer * d.top_k, d.top_k, d.hidden, d.res_mult, true, b.h);                       \
+    klaunch(k_expert_down<DTC, KK, true>, cdiv(d.hidden, kWavesPerBlock), kBlock, 0, s, c.pool_dn, b.act,  \
+            (const int*)nullptr, b.route_w + layer * d.top_k, d.top_k, d.hidden, d.res_mult, true, b.h, c); \
     break;
-  switch (down.dtype) {
-    case DT_Q8_0: { constexpr int DTC = DT_Q8_0; switch (down.cols) { MOERT_KDOWN_CASES(BODY) default: return hipErrorInvalidValue; } } break;
-    case DT_Q4_0: { constexpr int DTC = DT_Q4_0; switch (down.cols) { MOERT_KDOWN_CASES(BODY) default: return hipErrorInvalidValue; } } break;
-    case DT_F32: { constexpr int DTC = DT_F32; switch (down.cols) { MOERT_KDOWN_CASES(BODY) default: return hipErrorInvalidValue; } } break;
-    default: return hipErrorInvalidValue;
-  }
+  DOWN_DISPATCH(c.pool_dn.dtype, c.pool_dn.cols, BODY)
 #undef BODY
   return hipGetLastError();
 }
 
 hipError_t launch_expert_down(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
                               bool accumulate) {
+  const CacheDev none{};
 #define BODY(KK)                                                                                          \
   case KK:                                                                                                \
-    klaunch(k_expert_down<DTC, KK>, cdiv(d.hidden, kWavesPerBlock), kBlock, 0, s,                              \
+    klaunch(k_expert_down<DTC, KK, false>, cdiv(d.hidden, kWavesPerBlock), kBlock, 0, s,                      \
         L.down, b.act, b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, d.top_k, d.hidden,     \
-        d.res_mult, accumulate, accumulate ? b.h : b.logits);                                             \
+        d.res_mult, accumulate, accumulate ? b.h : b.logits, none);                                       \
     break;
-  switch (L.down.dtype) {
-    case DT_Q8_0: { constexpr int DTC = DT_Q8_0; switch (L.down.cols) { MOERT_KDOWN_CASES(BODY) default: return hipErrorInvalidValue; } } break;
-    case DT_Q4_0: { constexpr int DTC = DT_Q4_0; switch (L.down.cols) { MOERT_KDOWN_CASES(BODY) default: return hipErrorInvalidValue; } } break;
-    case DT_F32: { constexpr int DTC = DT_F32; switch (L.down.cols) { MOERT_KDOWN_CASES(BODY) default: return hipErrorInvalidValue; } } break;
-    default: return hipErrorInvalidValue;
-  }
+  DOWN_DISPATCH(L.down.dtype, L.down.cols, BODY)
 #undef BODY
   return hipGetLastError();
 }
+#undef DOWN_DISPATCH
 
 constexpr int kHeadNB = 4;
 

@@ -23,10 +23,9 @@ F32, Q8_0, Q4_0 = 0, 1, 2
 DTYPE_NAMES = {F32: "f32", Q8_0: "q8_0", Q4_0: "q4_0"}
 
 (K_EMBED, K_QKV, K_ATTN_SPLIT, K_ATTN_COMBINE, K_OPROJ, K_ROUTE_UP, K_EXPERT_DOWN, K_HEAD,
- K_HEAD_ARGMAX, K_ROUTE_LRU, K_FILL) = range(11)
+ K_HEAD_ARGMAX) = range(9)
 KERNEL_NAMES = ["embed", "qkv", "attn_split", "attn_combine", "oproj", "route_up", "expert_down", "head",
-                "head_argmax"]   # the resident model's kernel classes
-CACHE_KERNEL_NAMES = ["route_lru", "fill"]
+                "head_argmax"]   # kernel classes of a decode step (the same for a cached model)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmoert.so")
