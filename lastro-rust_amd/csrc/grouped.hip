@@ -12,9 +12,9 @@
 //
 // Kernels (one stream, in order):
 //   k_grp_route   grid m:            router + top-k of position p, hi/lo codes of x_p
-//   k_grp_up      grid (U, I/32):    grouping (every workgroup), gate/up MFMA of list expert u for its members,
+//   k_grp_up      grid (I/64, U):    grouping (every workgroup), gate/up MFMA of list expert u for its members,
 //                                    SwiGLU, hi/lo codes of act; workgroup (0, 0) publishes the plan
-//   k_grp_down    grid (U, H/64):    down MFMA of list expert u for its members -> o[member slot]
+//   k_grp_down    grid (H/64, U):    down MFMA of list expert u for its members -> o[member slot]
 //   k_grp_combine grid (m, H/256):   y[p] = sum over p's experts in list order of w * o
 #include <climits>
 
@@ -102,47 +102,63 @@ __global__ __launch_bounds__(kRouteThreads) void k_grp_route(DMat router, const 
 //   members      positions routing to the expert, as a bit mask (member index = set bits below the position)
 //   slots        member slot = offset of the expert + member index (rows of the act / o buffers)
 struct Plan {
-  int se[kGrpMaxPos * 8];  // expert of entry p*k + j
+  int8_t se[kGrpMaxPos * 8];  // expert of entry p*k + j (< 64)
   int first[64];           // first entry of expert e (INT_MAX when unused)
   unsigned bits[64];       // member positions of expert e
   int uof[64], offe[64];   // list index and first member slot of expert e
   int list[64];            // expert of list index u
+  unsigned long long fmask[kGrpMaxPos * 8 / 64];  // entries that are the first entry of their expert
   int nu;
 };
 
 template <int NT>
 __device__ __forceinline__ void make_plan(const int* __restrict__ ids, int m, int k, Plan& s) {
+  constexpr int NWORD = kGrpMaxPos * 8 / 64;
   const int t = threadIdx.x, n = m * k;
   const int mine = t < n ? ids[t] : 0;
   if (t < 64) {
     s.first[t] = INT_MAX;
     s.bits[t] = 0u;
   }
+  if (t < NWORD) s.fmask[t] = 0ull;
   __syncthreads();
   if (t < n) {
-    s.se[t] = mine;
+    s.se[t] = (int8_t)mine;
     atomicMin(&s.first[mine], t);
     atomicOr(&s.bits[mine], 1u << (t / k));
   }
   __syncthreads();
+  if (t < n && s.first[mine] == t) atomicOr(&s.fmask[t >> 6], 1ull << (t & 63));
+  __syncthreads();
   if (t < 64) {
-    // lane e: rank of expert e in first-appearance order and the members of the experts before it
-    const int key = s.bits[t] ? s.first[t] : INT_MAX;
-    const int cnt = __popc(s.bits[t]);
-    int u = 0, off = 0, nu = 0;
-    for (int e = 0; e < 64; e++) {
-      const int ke = __shfl(key, e), ce = __shfl(cnt, e);
-      nu += ke != INT_MAX;
-      if (ke < key) {
-        u++;
-        off += ce;
-      }
+    // lane e: list index of expert e = the first entries below its own (first-appearance order); then the
+    // member offsets as an exclusive prefix sum of the member counts in list order
+    const bool present = s.bits[t] != 0u;
+    const int key = present ? s.first[t] : 0;
+    int u = 0, nu = 0;
+#pragma unroll
+    for (int w = 0; w < NWORD; w++) {
+      const unsigned long long word = s.fmask[w];
+      nu += __popcll(word);
+      const int lo = 64 * w;
+      if (key >= lo + 64)
+        u += __popcll(word);
+      else if (key > lo)
+        u += __popcll(word & ((1ull << (key - lo)) - 1ull));
     }
-    if (key != INT_MAX) {
+    if (present) {
       s.uof[t] = u;
-      s.offe[t] = off;
       s.list[u] = t;
     }
+    wave_lds_sync();
+    const int cnt = t < nu ? __popc(s.bits[s.list[t]]) : 0;
+    int incl = cnt;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(incl, d);
+      if (t >= d) incl += o;
+    }
+    if (t < nu) s.offe[s.list[t]] = incl - cnt;
     if (t == 0) s.nu = nu;
   }
   __syncthreads();
@@ -303,36 +319,40 @@ __device__ __forceinline__ void store_members(const Members<K, NM, NT>& mb, int8
 }
 
 // ------------------------------------------------------------------------------------------------------------
-// Gate/up of list expert u = blockIdx.x for its members, rows [32t, 32t+32) of gate and of up (t = blockIdx.y):
-// wave w computes 16 rows (w & 1) of gate (w < 2) or up (w >= 2). Then act = silu(g)*u and its hi/lo codes (the
-// 32 rows are one block of the act vector), written to the members' slots.
+// Gate/up of list expert u = blockIdx.y for its members, rows [64t, 64t+64) of gate and of up (t = blockIdx.x):
+// wave w computes 16 rows (w & 3) of gate (w < 4) or up (w >= 4), so the members' codes staged in LDS serve 8
+// waves and one workgroup per CU covers the step. Then act = silu(g)*u and its hi/lo codes (each 32 rows are one
+// block of the act vector), written to the members' slots.
+constexpr int kGrpUpThreads = 512;
+
 template <int H, int NM>
-__global__ __launch_bounds__(256) void k_grp_up(DMat gu, int m, int k, int inter, GroupBufs g) {
+__global__ __launch_bounds__(kGrpUpThreads) void k_grp_up(DMat gu, int m, int k, int inter, GroupBufs g) {
   constexpr int NB = H / 32;
   constexpr int STR = H + 16;
+  constexpr int NT = kGrpUpThreads;
   __shared__ Plan plan;
   __shared__ __align__(16) int8_t bh[NM * STR];
   __shared__ __align__(16) int8_t bl[NM * STR];
   __shared__ float dx[NM * NB];
-  __shared__ __align__(16) uint16_t sdt[4][NB * 16];
-  __shared__ float gout[2][32][NM + 1];
+  __shared__ __align__(16) uint16_t sdt[NT / 64][NB * 16];
+  __shared__ float gout[2][64][NM + 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int u = blockIdx.x, tile = blockIdx.y;
-  make_plan<256>(g.ids, m, k, plan);
+  const int u = blockIdx.y, tile = blockIdx.x;
+  make_plan<NT>(g.ids, m, k, plan);
   if (u >= plan.nu) return;
   const int e = plan.list[u], off = plan.offe[e];
   const unsigned bits = plan.bits[e];
   const int ne = __popc(bits);
   const int r16 = lane & 15;
-  const size_t row = (size_t)e * 2 * inter + (size_t)(wave >> 1) * inter + 32 * tile + 16 * (wave & 1) + r16;
+  const size_t row = (size_t)e * 2 * inter + (size_t)(wave >> 2) * inter + 64 * tile + 16 * (wave & 3) + r16;
   RowScales<NB> sc;
   fetch_scales<NB>(gu, row, sc);
-  Members<H, NM, 256> mb;
-  fetch_members<H, NM, 256, false>(g.xh, g.xl, g.xd, bits, 0, ne, mb);
+  Members<H, NM, NT> mb;
+  fetch_members<H, NM, NT, false>(g.xh, g.xl, g.xd, bits, 0, ne, mb);
   uint2 a[NB];
   fetch_rows_q8<NB>(gu, row, a);
   store_scales<NB>(sc, r16, sdt[wave]);
-  store_members<H, NM, 256>(mb, bh, bl, STR, dx);
+  store_members<H, NM, NT>(mb, bh, bl, STR, dx);
   __syncthreads();
   float acc[NM / 16][4];
   mfma_tile<NB, NM>(a, bh, bl, STR, sdt[wave], dx, acc);
@@ -340,18 +360,19 @@ __global__ __launch_bounds__(256) void k_grp_up(DMat gu, int m, int k, int inter
 #pragma unroll
   for (int ct = 0; ct < NM / 16; ct++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) gout[wave >> 1][16 * (wave & 1) + 4 * grp + i][16 * ct + (lane & 15)] = acc[ct][i];
+    for (int i = 0; i < 4; i++) gout[wave >> 2][16 * (wave & 3) + 4 * grp + i][16 * ct + (lane & 15)] = acc[ct][i];
   __syncthreads();
-  // act = silu(gate) * up for 32 rows x NM members; 8 lanes per member, 4 rows per lane
-  for (int base = 0; base < NM; base += 32) {
-    const int j = base + (threadIdx.x >> 3), part = threadIdx.x & 7;
-    const bool valid = j < ne;
+  // act = silu(gate) * up for 64 rows (two 32-row blocks) x NM members; 8 lanes per (block, member), 4 rows a lane
+  for (int base = 0; base < 2 * NM; base += NT / 8) {
+    const int pi = base + (threadIdx.x >> 3), part = threadIdx.x & 7;
+    const int bi = pi / NM, j = pi % NM;
+    const bool valid = pi < 2 * NM && j < ne;
     float av[4];
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int r = 4 * part + i;
-      av[i] = valid ? silu_mul(gout[0][r][j < NM ? j : 0], gout[1][r][j < NM ? j : 0]) : 0.0f;
+      const int r = (32 * bi + 4 * part + i) & 63;
+      av[i] = valid ? silu_mul(gout[0][r][j], gout[1][r][j]) : 0.0f;
       const float aa = fabsf(av[i]);
       amax = aa > amax ? aa : amax;
     }
@@ -367,18 +388,19 @@ __global__ __launch_bounds__(256) void k_grp_up(DMat gu, int m, int k, int inter
     }
     if (valid) {
       const size_t slotv = (size_t)(off + j);
-      reinterpret_cast<uint32_t*>(g.ah + slotv * inter + 32 * tile)[part] = hw;
-      reinterpret_cast<uint32_t*>(g.al + slotv * inter + 32 * tile)[part] = lw;
-      if (part == 0) g.ad[slotv * (inter / 32) + tile] = d;
+      const int blk = 2 * tile + bi;
+      reinterpret_cast<uint32_t*>(g.ah + slotv * inter + 32 * blk)[part] = hw;
+      reinterpret_cast<uint32_t*>(g.al + slotv * inter + 32 * blk)[part] = lw;
+      if (part == 0) g.ad[slotv * (inter / 32) + blk] = d;
     }
   }
-  if (u == 0 && tile == 0) publish_plan<256>(plan, g.w, m, k, g.grp);
+  if (u == 0 && tile == 0) publish_plan<NT>(plan, g.w, m, k, g.grp);
 }
 
 // ------------------------------------------------------------------------------------------------------------
-// Down of list expert u = blockIdx.x for its members, output rows [64t, 64t+64): o[slot][row].
+// Down of list expert u = blockIdx.y for its members, output rows [64t, 64t+64): o[slot][row].
 template <int I, int NM>
-__global__ __launch_bounds__(256) void k_grp_down(DMat dn, int hidden, GroupBufs g) {
+__global__ __launch_bounds__(256, NM == 16 ? 2 : 1) void k_grp_down(DMat dn, int hidden, GroupBufs g) {
   constexpr int NB = I / 32;
   constexpr int STR = I + 16;
   __shared__ __align__(16) int8_t bh[NM * STR];
@@ -386,7 +408,7 @@ __global__ __launch_bounds__(256) void k_grp_down(DMat dn, int hidden, GroupBufs
   __shared__ float dx[NM * NB];
   __shared__ __align__(16) uint16_t sdt[4][NB * 16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int u = blockIdx.x, tile = blockIdx.y;
+  const int u = blockIdx.y, tile = blockIdx.x;
   if (u >= g.grp[GRP_NU]) return;
   const int e = g.grp[GRP_LIST + u], ne = g.grp[GRP_CNT + u], off = g.grp[GRP_OFF + u];
   const int r16 = lane & 15;
@@ -461,17 +483,19 @@ hipError_t launch_grouped_block(hipStream_t s, const LayerDev& L, int m, int k, 
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const dim3 gu_grid(U, inter / 32);
+  // u is the slow grid index, so the workgroups of list indices past the step's expert count (which end at once)
+  // are dispatched last
+  const dim3 gu_grid(inter / 64, U);
   arm(1);
   if (H == 1024) {
-    if (wide) klaunch(k_grp_up<1024, 32>, gu_grid, 256, 0, s, L.gate_up, m, k, inter, g);
-    else klaunch(k_grp_up<1024, 16>, gu_grid, 256, 0, s, L.gate_up, m, k, inter, g);
+    if (wide) klaunch(k_grp_up<1024, 32>, gu_grid, kGrpUpThreads, 0, s, L.gate_up, m, k, inter, g);
+    else klaunch(k_grp_up<1024, 16>, gu_grid, kGrpUpThreads, 0, s, L.gate_up, m, k, inter, g);
   } else {
-    if (wide) klaunch(k_grp_up<1536, 32>, gu_grid, 256, 0, s, L.gate_up, m, k, inter, g);
-    else klaunch(k_grp_up<1536, 16>, gu_grid, 256, 0, s, L.gate_up, m, k, inter, g);
+    if (wide) klaunch(k_grp_up<1536, 32>, gu_grid, kGrpUpThreads, 0, s, L.gate_up, m, k, inter, g);
+    else klaunch(k_grp_up<1536, 16>, gu_grid, kGrpUpThreads, 0, s, L.gate_up, m, k, inter, g);
   }
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  const dim3 dn_grid(U, H / 64);
+  const dim3 dn_grid(H / 64, U);
   arm(2);
   switch (inter) {
 #define DOWN_CASE(II)                                                                               \
