@@ -277,9 +277,10 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ q,
 
 // One wave's share of a V tile moved into LDS through registers, by the G waves that serve the same tile: piece e
 // (e = wave, wave + G, ...) is rows 8e..8e+7, lane l carrying 16 bytes of row 8e + l/8, so each piece reads 1 KB of
-// consecutive cache rows and the LDS tile is row-major [64][64] fp16. Plain loads (not LDS DMA) keep the wait for
-// the tile separate from the waits for the kernel's other loads. A piece index past 7 (only for G = 3) loads piece
-// 7 again and stores it into rows 64..71 of the tile, which are padding and never read.
+// consecutive cache rows. The LDS tile is row-major [64][64] f32, converted once for the G heads, with the rows at
+// and past the tile's valid length `nv` stored as +0. Plain loads (not LDS DMA) keep the wait for the tile separate
+// from the waits for the kernel's other loads. A piece index past 7 (only for G = 3) loads piece 7 again and stores
+// it into rows 64..71 of the tile, which are padding and never read.
 template <int G>
 struct VShare {
   static constexpr int N = (8 + G - 1) / G;
@@ -296,8 +297,18 @@ struct VShare {
     if (N > 6) g = at(6);
     if (N > 7) h = at(7);
   }
-  __device__ __forceinline__ void store(uint4 (*dst)[8], int lane, int wave) const {
-    auto put = [&](int i, const uint4& v) { dst[8 * (wave + G * i) + (lane >> 3)][lane & 7] = v; };
+  __device__ __forceinline__ void store(float (*dst)[64], int lane, int wave, int nv) const {
+    auto put = [&](int i, const uint4& v) {
+      const int row = 8 * (wave + G * i) + (lane >> 3);
+      const bool z = row >= nv;
+      float4* o = reinterpret_cast<float4*>(&dst[row][(lane & 7) * 8]);
+      o[0] = z ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
+               : make_float4(h2f((uint16_t)(v.x & 0xffffu)), h2f((uint16_t)(v.x >> 16)), h2f((uint16_t)(v.y & 0xffffu)),
+                             h2f((uint16_t)(v.y >> 16)));
+      o[1] = z ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
+               : make_float4(h2f((uint16_t)(v.z & 0xffffu)), h2f((uint16_t)(v.z >> 16)), h2f((uint16_t)(v.w & 0xffffu)),
+                             h2f((uint16_t)(v.w >> 16)));
+    };
     put(0, a);
     if (N > 1) put(1, b);
     if (N > 2) put(2, c);
@@ -320,7 +331,7 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
                                                           const uint16_t* __restrict__ vc, const int* __restrict__ lenp,
                                                           int len_add, int max_len, float scale, int splits,
                                                           float* __restrict__ part) {
-  __shared__ uint4 Vs[T][72][8];  // fp16 V tiles, row i = position (rows 64..71: padding for VShare)
+  __shared__ float Vs[T][72][64];  // V tiles in f32, row i = position (rows 64..71: padding for VShare)
   __shared__ float Qs[G][64];
   __shared__ float Ps[G][T][64];
   __shared__ float Pv[G][T][64];
@@ -390,26 +401,21 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
       Ts[wh][wt] = ts;
     }
   }
-  vsh.store(Vs[wt], lane, wh);
+  vsh.store(Vs[wt], lane, wh, nv);
   __syncthreads();  // every share of every V tile stored; P written
   if (active) {
     // p.v: lane = dim, chain over the positions in order, without branches so that every LDS read can be issued
-    // ahead of the chain. A position past the length has p = exp(-inf) = 0 and its V element is replaced by 0, so
+    // ahead of the chain. A position past the length has p = exp(-inf) = 0 and its V element is stored as 0, so
     // its step fma(0, 0, pv) returns pv unchanged (pv starts at +0 and an exact zero sum is +0, so pv is never -0):
     // the chain equals the one over the valid positions only, bit for bit.
-    const uint16_t* vcol = reinterpret_cast<const uint16_t*>(&Vs[wt][0][0]) + lane;
+    const float* vcol = &Vs[wt][0][lane];
     if constexpr (G * T < 16) {
 #pragma unroll
       for (int i0 = 0; i0 < 64; i0 += 4) {
         const float4 p4 = *reinterpret_cast<const float4*>(&Ps[wh][wt][i0]);
         const float pa[4] = {p4.x, p4.y, p4.z, p4.w};
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-          // masked bits rather than a conditional read, which would become a branch around each LDS read
-          const uint32_t hv = vcol[(i0 + u) * 64];
-          const float vf = h2f((uint16_t)(hv & (i0 + u < nv ? 0xffffu : 0u)));
-          pv = __builtin_fmaf(pa[u], vf, pv);
-        }
+        for (int u = 0; u < 4; u++) pv = __builtin_fmaf(pa[u], vcol[(i0 + u) * 64], pv);
       }
     } else {
       // 16 waves leave 128 VGPRs a lane, too few to hoist every read: batches of 8 positions, valid ones only
@@ -418,7 +424,7 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
         if (i0 < nv) {
           float vf[8];
 #pragma unroll
-          for (int u = 0; u < 8; u++) vf[u] = h2f(vcol[(i0 + u) * 64]);
+          for (int u = 0; u < 8; u++) vf[u] = vcol[(i0 + u) * 64];
           const float4 p0 = *reinterpret_cast<const float4*>(&Ps[wh][wt][i0]);
           const float4 p1 = *reinterpret_cast<const float4*>(&Ps[wh][wt][i0 + 4]);
           const float pa[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
