@@ -297,11 +297,12 @@ struct VShare {
     if (N > 6) g = at(6);
     if (N > 7) h = at(7);
   }
-  __device__ __forceinline__ void store(float (*dst)[64], int lane, int wave, int nv) const {
+  template <int STRIDE>
+  __device__ __forceinline__ void store(float* dst, int lane, int wave, int nv) const {
     auto put = [&](int i, const uint4& v) {
       const int row = 8 * (wave + G * i) + (lane >> 3);
       const bool z = row >= nv;
-      float4* o = reinterpret_cast<float4*>(&dst[row][(lane & 7) * 8]);
+      float4* o = reinterpret_cast<float4*>(dst + row * STRIDE + (lane & 7) * 8);
       o[0] = z ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
                : make_float4(h2f((uint16_t)(v.x & 0xffffu)), h2f((uint16_t)(v.x >> 16)), h2f((uint16_t)(v.y & 0xffffu)),
                              h2f((uint16_t)(v.y >> 16)));
@@ -331,7 +332,10 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
                                                           const uint16_t* __restrict__ vc, const int* __restrict__ lenp,
                                                           int len_add, int max_len, float scale, int splits,
                                                           float* __restrict__ part) {
-  __shared__ float Vs[T][72][64];  // V tiles in f32, row i = position (rows 64..71: padding for VShare)
+  constexpr int TR = 8 % G == 0 ? 64 : 72;  // tile rows (64..71: padding for VShare when G does not divide 8)
+  constexpr int KS = 68;                     // K row stride in floats: 16-byte rows, conflict-free row reads
+  __shared__ __align__(16) float Vs[T][TR][64];  // V tiles in f32, row i = position
+  __shared__ __align__(16) float Ks[T][TR][KS];  // K tiles in f32, row i = position
   __shared__ float Qs[G][64];
   __shared__ float Ps[G][T][64];
   __shared__ float Pv[G][T][64];
@@ -347,12 +351,13 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
   // the tile's rows are requested before the length is known; a tile past the end of the cache (last split, when
   // T does not divide the tile count) reads the cache's last tile instead and is never used
   const int tl = min(t, max_len / 64 - 1);
-  // q and the length first (loads complete in issue order), then this tile's K rows and its share of the V tile
+  // q and the length first (loads complete in issue order), then this wave's shares of the tile's K and V (the G
+  // waves of a tile move it together, each element is loaded and converted once)
   const float qv = q[h * 64 + lane];
   const int len = *lenp + len_add;
   __builtin_amdgcn_sched_barrier(0);
-  Row8 kr;
-  kr.load(reinterpret_cast<const uint4*>(K + (size_t)(tl * 64 + lane) * 64));
+  VShare<G> ksh;
+  ksh.load(K, tl, lane, wh);
   __builtin_amdgcn_sched_barrier(0);  // K (needed first) ahead of V
   VShare<G> vsh;
   vsh.load(V, tl, lane, wh);
@@ -361,26 +366,21 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
   const int used = min(T, nb - t0);  // tiles of this split inside the length (>= 1 when the split is used)
   const bool active = wt < used;
   const int nv = active ? min(64, len - t * 64) : 0;
-  __syncthreads();  // Qs
-  // scores: lane = position, chain over the 64 dims in order (computed by every wave, so that no branch lets the
-  // compiler sink the K loads below the barrier; an inactive tile's scores are discarded)
+  ksh.template store<KS>(&Ks[wt][0][0], lane, wh, nv);
+  __syncthreads();  // Qs, K tiles
+  // scores: lane = position, chain over the 64 dims in order (an inactive tile's scores are discarded)
   float sc;
   {
     float dt = 0.0f;
+    const float* krow = &Ks[wt][lane][0];
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      const uint4 ke = kr.at(e);
-      const uint32_t wv[4] = {ke.x, ke.y, ke.z, ke.w};
-#pragma unroll
-      for (int hh = 0; hh < 2; hh++) {
-        const float4 qq = *reinterpret_cast<const float4*>(&Qs[wh][8 * e + 4 * hh]);
-        const float qa[4] = {qq.x, qq.y, qq.z, qq.w};
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-          const uint32_t word = wv[2 * hh + (c >> 1)];
-          dt = __builtin_fmaf(qa[c], h2f((uint16_t)(word >> (16 * (c & 1)))), dt);
-        }
-      }
+    for (int d4 = 0; d4 < 16; d4++) {
+      const float4 kk = *reinterpret_cast<const float4*>(krow + 4 * d4);
+      const float4 qq = *reinterpret_cast<const float4*>(&Qs[wh][4 * d4]);
+      dt = __builtin_fmaf(qq.x, kk.x, dt);
+      dt = __builtin_fmaf(qq.y, kk.y, dt);
+      dt = __builtin_fmaf(qq.z, kk.z, dt);
+      dt = __builtin_fmaf(qq.w, kk.w, dt);
     }
     sc = lane < nv ? dt * scale : NEG_INF;  // nv = 0 for an inactive tile
   }
@@ -401,7 +401,7 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
       Ts[wh][wt] = ts;
     }
   }
-  vsh.store(Vs[wt], lane, wh, nv);
+  vsh.template store<64>(&Vs[wt][0][0], lane, wh, nv);
   __syncthreads();  // every share of every V tile stored; P written
   if (active) {
     // p.v: lane = dim, chain over the positions in order, without branches so that every LDS read can be issued
