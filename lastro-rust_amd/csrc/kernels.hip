@@ -455,18 +455,21 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
 
 // One wave per query head: M = max m_s; w_s = exp(m_s - M); den = fma chain of w_s * l_s; num_c = fma chain of
 // w_s * acc_sc, both over s = 0..used-1 in order; out_c = num_c / den. used <= splits <= 64.
+template <int SP>
 __global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ part, const int* __restrict__ lenp,
                                                     int len_add, int tps, int splits, float* __restrict__ out) {
   __shared__ float Cw[2][64];
   const int h = blockIdx.x, lane = threadIdx.x;
   const float NEG_INF = __int_as_float(0xff800000);
   const float* base = part + (size_t)h * splits * 66;
-  // every split's partial is requested before the length (and so the number of used splits) is known
-  float av[64];
+  // every split's partial is requested before the length (and so the number of used splits) is known; indices
+  // are clamped instead of guarded (SP >= splits), so the loads form one straight run
+  float av[SP];
 #pragma unroll
-  for (int s2 = 0; s2 < 64; s2++) av[s2] = s2 < splits ? base[(size_t)s2 * 66 + 2 + lane] : 0.0f;
-  float ms = lane < splits ? base[(size_t)lane * 66] : NEG_INF;
-  float ls = lane < splits ? base[(size_t)lane * 66 + 1] : 0.0f;
+  for (int s2 = 0; s2 < SP; s2++) av[s2] = base[(size_t)min(s2, splits - 1) * 66 + 2 + lane];
+  const int sl = min(lane, splits - 1);
+  float ms = base[(size_t)sl * 66];
+  float ls = base[(size_t)sl * 66 + 1];
   const int len = *lenp + len_add;
   const int nb = (len + 63) / 64, used = (nb + tps - 1) / tps;
   if (lane >= used) {
@@ -479,7 +482,7 @@ __global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ p
   wave_lds_sync();
   float den = 0.0f, num = 0.0f;
 #pragma unroll
-  for (int s2 = 0; s2 < 64; s2++) {
+  for (int s2 = 0; s2 < SP; s2++) {
     if (s2 < used) {
       const float ws = Cw[0][s2];
       den = __builtin_fmaf(ws, Cw[1][s2], den);
@@ -1075,7 +1078,14 @@ static hipError_t attn_combine_dispatch(hipStream_t s, int heads, int tps, int m
                                         const float* part, float* out) {
   const int splits = attn_splits_for(max_len, tps);
   if (splits > 64 || max_len % 64) return hipErrorInvalidValue;
-  klaunch(k_attn_combine, heads, 64, 0, s, part, lenp, len_add, tps, splits, out);
+  if (splits <= 8)
+    klaunch(k_attn_combine<8>, heads, 64, 0, s, part, lenp, len_add, tps, splits, out);
+  else if (splits <= 16)
+    klaunch(k_attn_combine<16>, heads, 64, 0, s, part, lenp, len_add, tps, splits, out);
+  else if (splits <= 32)
+    klaunch(k_attn_combine<32>, heads, 64, 0, s, part, lenp, len_add, tps, splits, out);
+  else
+    klaunch(k_attn_combine<64>, heads, 64, 0, s, part, lenp, len_add, tps, splits, out);
   return hipGetLastError();
 }
 
