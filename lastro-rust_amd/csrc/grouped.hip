@@ -55,7 +55,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_grp_route(DMat router, const 
   rows_load<DT, H, RP>(rr, router, row, ok, sub);
   float bv[RP];
 #pragma unroll
-  for (int q = 0; q < RP; q++) bv[q] = (bias && ok[q]) ? bias[row[q]] : 0.0f;
+  for (int q = 0; q < RP; q++) bv[q] = bias ? bias[ok[q] ? row[q] : 0] : 0.0f;  // clamped, not guarded: one run of loads
   wg_copy<H, kRouteThreads>(x + (size_t)p * H, xs);
   XReg<DT, H> xr;
   load_x<DT, H>(xr, xs, sub);

@@ -534,7 +534,10 @@ __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restric
 // publishes ids/weights for the down kernel. Then its pairs (slot j, row r): act[j, r] = silu(gate_r . xn) *
 // (up_r . xn) for expert ids[j] (gemv_swiglu gpu.rs:46-74, grouped as moe_gate_up hits.rs:67-105; Cpu::experts
 // cpu.rs:116-137). E <= 64, k <= 8.
-constexpr int kRouteWaves = 8;
+// Waves per workgroup: 16 (4 per SIMD, so that the router's FMA chains of the 4 waves of a SIMD interleave); 8 for
+// f32 rows, whose registers would not fit 16 waves. Rows per wave (NP pairs) make 16 pairs per workgroup either way.
+__host__ __device__ constexpr int route_waves(int dt) { return dt == DT_F32 ? 8 : 16; }
+__host__ __device__ constexpr int route_np(int dt) { return 16 / route_waves(dt); }
 
 // CACHED (expert-cache path): after the top-k, wave 0 of every workgroup makes the layer step's LRU decision from
 // the current copy of the slot tables (all workgroups read the same copy, so they all decide alike); workgroup 0
@@ -542,20 +545,21 @@ constexpr int kRouteWaves = 8;
 // routed expert come from its pool slot, or, when it missed, from its record in the host store; those rows are also
 // written into the slot.
 template <int DT, int K, int NP, bool NORM, bool CACHED>
-__global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, const float* __restrict__ bias, DMat gu,
+__global__ __launch_bounds__(route_waves(DT) * 64) void k_route_up(DMat router, const float* __restrict__ bias, DMat gu,
                                                                const float* __restrict__ h,
                                                                const float* __restrict__ lnw, float eps, int k,
                                                                int inter, int layer, int* __restrict__ ids_out,
                                                                float* __restrict__ w_out, float* __restrict__ act,
                                                                CacheDev c) {
   using G = Geo<DT, K>;
-  constexpr int NT = kRouteWaves * 64;
-  constexpr int RP = (64 + kRouteWaves * G::RPW - 1) / (kRouteWaves * G::RPW);  // router passes for 64 rows
+  constexpr int NW = route_waves(DT);
+  constexpr int NT = NW * 64;
+  constexpr int RP = (64 + NW * G::RPW - 1) / (NW * G::RPW);  // router passes for 64 rows
   constexpr int P = 2 * NP;
   constexpr int SMAX = CACHED ? kCacheMaxSlots : 1;
   __shared__ float xs[K];
   __shared__ __align__(16) float lg[64];
-  __shared__ int part[64][kRouteWaves];
+  __shared__ int part[64][NW];
   __shared__ int skey[SMAX];
   __shared__ int slast[SMAX];
   __shared__ int lslot[8], lmiss[8], lfound[8];
@@ -575,14 +579,14 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
     bool ok[RP];
 #pragma unroll
     for (int p = 0; p < RP; p++) {
-      row[p] = (size_t)(p * kRouteWaves + wave) * G::RPW + rw;
+      row[p] = (size_t)(p * NW + wave) * G::RPW + rw;
       ok[p] = row[p] < (size_t)E;
     }
     Rows<DT, K, RP> rr;
     rows_load<DT, K, RP>(rr, router, row, ok, sub);
     float bv[RP];
 #pragma unroll
-    for (int p = 0; p < RP; p++) bv[p] = (bias && ok[p]) ? bias[row[p]] : 0.0f;
+    for (int p = 0; p < RP; p++) bv[p] = bias ? bias[ok[p] ? row[p] : 0] : 0.0f;  // clamped, not guarded: one run of loads
     if (CACHED) {
       const int cur = *c.cur, S = c.slots;
       for (int i = threadIdx.x; i < S; i += NT) {
@@ -604,7 +608,7 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
   __syncthreads();
   // routed ids as wave-uniform values, ranked by all waves
   int eid[8];
-  const int rank = wg_rank<kRouteWaves>(lg, E, lane, wave, part);
+  const int rank = wg_rank<NW>(lg, E, lane, wave, part);
   const bool sel = lane < E && rank < k;
   ids_by_rank(sel, rank, k, eid);
   if (blockIdx.x == 0 && wave == 0) route_weights(lg, sel, rank, k, lane, eid, ids_out, w_out);
@@ -650,7 +654,7 @@ __global__ __launch_bounds__(kRouteWaves * 64) void k_route_up(DMat router, cons
     }
   }
   const int npairs = k * inter;
-  const int wbase = (blockIdx.x * kRouteWaves + wave) * (NP * G::RPW);
+  const int wbase = (blockIdx.x * NW + wave) * (NP * G::RPW);
   size_t row[P], prow[P];
   bool ok[P], put[P];
   DMat src[P];
@@ -1117,7 +1121,6 @@ hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const S
   return hipGetLastError();
 }
 
-constexpr int kRouteNP = 2;
 
 hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
                            bool normalize) {
@@ -1125,14 +1128,14 @@ hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, cons
   const CacheDev none{};
 #define BODY(KK)                                                                                           \
   case KK: {                                                                                               \
-    constexpr int PB = kRouteWaves * kRouteNP * Geo<DTC, KK>::RPW;                                         \
+    constexpr int NW = route_waves(DTC), NP = route_np(DTC), PB = NW * NP * Geo<DTC, KK>::RPW;             \
     const int blocks = cdiv((long)d.top_k * d.inter, PB);                                                  \
     if (normalize)                                                                                         \
-      klaunch(k_route_up<DTC, KK, kRouteNP, true, false>, blocks, kRouteWaves * 64, 0, s,                       \
+      klaunch(k_route_up<DTC, KK, NP, true, false>, blocks, NW * 64, 0, s,                                      \
           L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter, layer,               \
           b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, none);                        \
     else                                                                                                   \
-      klaunch(k_route_up<DTC, KK, kRouteNP, false, false>, blocks, kRouteWaves * 64, 0, s,                      \
+      klaunch(k_route_up<DTC, KK, NP, false, false>, blocks, NW * 64, 0, s,                                     \
           L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter, layer,               \
           b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, none);                        \
   } break;
@@ -1148,9 +1151,9 @@ hipError_t launch_route_up_cached(hipStream_t s, const LayerDev& L, const Dims& 
     return hipErrorInvalidValue;
 #define BODY(KK)                                                                                           \
   case KK: {                                                                                               \
-    constexpr int PB = kRouteWaves * kRouteNP * Geo<DTC, KK>::RPW;                                         \
+    constexpr int NW = route_waves(DTC), NP = route_np(DTC), PB = NW * NP * Geo<DTC, KK>::RPW;             \
     const int blocks = cdiv((long)d.top_k * d.inter, PB);                                                  \
-    klaunch(k_route_up<DTC, KK, kRouteNP, true, true>, blocks, kRouteWaves * 64, 0, s, L.router,           \
+    klaunch(k_route_up<DTC, KK, NP, true, true>, blocks, NW * 64, 0, s, L.router,                          \
             L.router_bias, c.pool_gu, b.h, L.ln_moe, d.eps, d.top_k, d.inter, layer,                       \
             b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, c);                         \
   } break;
