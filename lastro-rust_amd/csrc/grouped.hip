@@ -26,7 +26,7 @@ namespace moert {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-constexpr int kRouteThreads = 512;
+constexpr int kRouteThreads = 1024;
 
 // ------------------------------------------------------------------------------------------------------------
 // Per-position router (canonical dot, optional bias), top-k, and the hi/lo codes of x_p: workgroup p.

@@ -78,13 +78,15 @@ __global__ __launch_bounds__(kBlock) void k_embed(DMat e, const int* __restrict_
   }
 }
 
+constexpr int kQkvWaves = 8;  // waves per workgroup of k_qkv
+
 // ------------------------------------------------------------------------------------------------------------
 // Attention block input: rmsnorm -> [q; k; v] GEMV -> rotate_half RoPE of q and k -> q to `q` (f32), k and v to
 // row `pos` of the fp16 KV cache. Replaces rmsnorm + gemv q/k/v + rope + the two KV copies
 // (gpu_model.rs:341-378) and rope_kv / gemv_row (gpu.rs:151-197). A wave owns NP*RPW row pairs (j, j+32) of
 // a head, so both halves of a rotation meet in the same lanes.
 template <int DT, int K, int NP>
-__global__ __launch_bounds__(kBlock) void k_qkv(DMat m, const float* __restrict__ h, const float* __restrict__ lnw,
+__global__ __launch_bounds__(kQkvWaves * 64) void k_qkv(DMat m, const float* __restrict__ h, const float* __restrict__ lnw,
                                                 float eps, const int* __restrict__ st, const float* __restrict__ rope,
                                                 int heads, int kvh, int max_len, float* __restrict__ q,
                                                 uint16_t* __restrict__ kc, uint16_t* __restrict__ vc) {
@@ -95,7 +97,7 @@ __global__ __launch_bounds__(kBlock) void k_qkv(DMat m, const float* __restrict_
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int sub = lane % G::LPR, rw = lane / G::LPR;
   int npairs = m.rows / 2;
-  int wbase = (blockIdx.x * kWavesPerBlock + wave) * (NP * G::RPW);
+  int wbase = (blockIdx.x * kQkvWaves + wave) * (NP * G::RPW);
   size_t row[P];
   bool ok[P];
   int gp[NP];
@@ -112,8 +114,8 @@ __global__ __launch_bounds__(kBlock) void k_qkv(DMat m, const float* __restrict_
   // position first, then the activation, then this lane's cos/sin (they depend only on the position), then the
   // weights: each wait below covers only what was issued before the thing waited for
   const int pos = st[ST_POS];
-  NormIn<K, kBlock> hin;
-  norm_fetch<K, kBlock>(h, lnw, hin);
+  NormIn<K, (kQkvWaves * 64)> hin;
+  norm_fetch<K, (kQkvWaves * 64)>(h, lnw, hin);
   const float* cs = rope + (size_t)pos * 64;
   float cv[NP], sv[NP];
 #pragma unroll
@@ -125,7 +127,7 @@ __global__ __launch_bounds__(kBlock) void k_qkv(DMat m, const float* __restrict_
   __builtin_amdgcn_sched_barrier(0);
   Rows<DT, K, P> rr;
   rows_load<DT, K, P>(rr, m, row, ok, sub);
-  norm_finish<K, kBlock>(hin, eps, xs, &rs);
+  norm_finish<K, (kQkvWaves * 64)>(hin, eps, xs, &rs);
   XReg<DT, K> xr;
   load_x<DT, K>(xr, xs, sub);
   float out[P];
@@ -1040,8 +1042,8 @@ hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const Ste
 hipError_t launch_qkv(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b) {
 #define BODY(KK)                                                                                            \
   case KK: {                                                                                                \
-    constexpr int PB = kWavesPerBlock * kQkvNP * Geo<DTC, KK>::RPW; /* pairs per block */                   \
-    klaunch(k_qkv<DTC, KK, kQkvNP>, cdiv(L.qkv.rows / 2, PB), kBlock, 0, s,                                      \
+    constexpr int PB = kQkvWaves * kQkvNP * Geo<DTC, KK>::RPW; /* pairs per block */                   \
+    klaunch(k_qkv<DTC, KK, kQkvNP>, cdiv(L.qkv.rows / 2, PB), kQkvWaves * 64, 0, s,                                      \
         L.qkv, b.h, L.ln_attn, d.eps, b.state, b.rope, d.heads, d.kv_heads, d.max_len, b.q, L.k_cache,      \
         L.v_cache);                                                                                         \
   } break;
