@@ -46,6 +46,31 @@ def test_cached_model_equals_the_resident_model_and_counts_like_the_lru_oracle(g
     cac.close()
 
 
+WIDE = dict(hidden=256, inter=128, layers=4, heads=4, kv_heads=2, head_dim=64, vocab=97, experts=64, top_k=8)
+
+
+@pytest.mark.parametrize("slots", [8, 100, 200])
+def test_pool_of_more_slots_than_a_wave_has_lanes(gpu, slots):
+    """64 experts x 4 layers = 256 keys: the slot tables span several passes of a wave (slots > 64)."""
+    cfg = moert.Config(**WIDE)
+    m = moert.SynthModel(cfg, seed=21, wdtype=moert.Q4_0, embed_dtype=moert.F32, std=0.1, zipf_s=1.1)
+    res = moert.GpuModel(m, 64, attn_splits=4)
+    cac = moert.GpuModel(m, 64, attn_splits=4, cache_slots=slots)
+    toks = np.random.default_rng(77).integers(0, cfg.vocab, 40)
+    routes = []
+    for t, tok in enumerate(toks):
+        say(f"wide cache slots={slots} pos={t}")
+        lg, ids, w, am = res.step(int(tok))
+        clg, cids, cw, cam = cac.step(int(tok))
+        assert bits_equal(lg, clg) and np.array_equal(ids, cids) and bits_equal(w, cw) and am == cam, t
+        routes.append(ids)
+    hits, copies, cpu = oracle.lru_replay(np.array(routes), cfg.experts, slots)
+    assert cpu == 0
+    assert cac.cache_stats() == (hits, copies)
+    res.close()
+    cac.close()
+
+
 def test_cache_clear_restarts_from_an_empty_pool(gpu):
     cfg = moert.Config(**TINY8)
     m = moert.SynthModel(cfg, seed=14, wdtype=moert.Q4_0, embed_dtype=moert.F32, std=0.1)
