@@ -467,6 +467,18 @@ struct moert_block {
         (rc = zeros(arena, stream, (size_t)S * I, &g.ah)) || (rc = zeros(arena, stream, (size_t)S * I, &g.al)) ||
         (rc = zeros(arena, stream, (size_t)S * (I / 32), &g.ad)) || (rc = zeros(arena, stream, (size_t)S * H, &g.o)))
       return rc;
+    // the experts in the tiled layout of the MFMA kernels, copied once from the resident matrices
+    auto tiled = [&](const DMat& src, TMat* dst) -> int {
+      uint8_t* q;
+      uint16_t* d;
+      const size_t n = (size_t)src.rows * src.cols;
+      int r;
+      if ((r = arena.alloc((void**)&q, n)) || (r = arena.alloc((void**)&d, n / 32 * 2))) return r;
+      CHECK_HIP(launch_tile_q8(stream, src, q, d));
+      *dst = TMat{q, d, src.rows, src.cols};
+      return MOERT_OK;
+    };
+    if ((rc = tiled(L.gate_up, &g.gu)) || (rc = tiled(L.down, &g.dn))) return rc;
     CHECK_HIP(hipStreamSynchronize(stream));
     return MOERT_OK;
   }

@@ -15,6 +15,16 @@ constexpr int kGrpMaxPos = 32;  // positions per grouped step (the reference cap
 enum { GRP_NU = 0, GRP_LIST = 1, GRP_CNT = 65, GRP_OFF = 129, GRP_BITS = 193, GRP_ORD_SLOT = 257,
        GRP_ORD_W = GRP_ORD_SLOT + kGrpMaxPos * 8, GRP_WORDS = GRP_ORD_W + kGrpMaxPos * 8 };
 
+// A Q8_0 matrix (rows % 16 == 0, cols % 64 == 0) in the tiled layout of the grouped MFMA kernels. Payload: per
+// 16-row tile t and 64-column span p, one 1 KB piece in which lane l holds 16 bytes: elements 8*(l/16) .. +8 of
+// row 16t + l%16 in block 2p, then the same elements of block 2p + 1 (the A operands of two MFMA K-steps, so a
+// wave's load is 1 KB of consecutive bytes). Scales: per tile t and block b the 16 rows' fp16 scales [t][b][16].
+struct TMat {
+  const uint8_t* q;
+  const uint16_t* d;
+  int rows, cols;
+};
+
 // Device buffers of one grouped step, sized for kGrpMaxPos positions, hidden H, inter I and top-k <= 8.
 struct GroupBufs {
   int* ids;      // [m, k] routed experts, top-k order
@@ -27,7 +37,11 @@ struct GroupBufs {
   int8_t* al;    // [m*k, I]
   float* ad;     // [m*k, I/32]
   float* o;      // [m*k, H] down outputs by member slot
+  TMat gu, dn;   // gate_up [E*2I, H] and down [E*H, I] of the block in the tiled layout
 };
+
+// Tiled copy (TMat layout) of the Q8_0 matrix src into q [rows*cols] and d [rows*cols/32].
+hipError_t launch_tile_q8(hipStream_t s, const DMat& src, uint8_t* q, uint16_t* d);
 
 // y[m, H] = MoE block of the m rows of x (already normalised), router + top-k per row, experts grouped.
 // Q8_0 router, gate_up and down; E <= 64, k <= 8, m <= kGrpMaxPos. With `ev` (8 events), the four kernels

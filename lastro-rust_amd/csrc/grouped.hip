@@ -114,6 +114,7 @@ struct Plan {
 template <int NT>
 __device__ __forceinline__ void make_plan(const int* __restrict__ ids, int m, int k, Plan& s) {
   constexpr int NWORD = kGrpMaxPos * 8 / 64;
+  static_assert(NT >= kGrpMaxPos * 8, "one thread per entry");
   const int t = threadIdx.x, n = m * k;
   const int mine = t < n ? ids[t] : 0;
   if (t < 64) {
@@ -186,14 +187,39 @@ __device__ __forceinline__ void publish_plan(const Plan& s, const float* __restr
 }
 
 // ------------------------------------------------------------------------------------------------------------
+// Tiled copy of a Q8_0 matrix (TMat layout): thread i writes the 16-byte piece i = (tile, span, lane) and, for
+// lanes below 32, the scale of row lane%16 in block 2*span + lane/16.
+__global__ __launch_bounds__(256) void k_tile_q8(DMat src, uint8_t* __restrict__ q, uint16_t* __restrict__ d) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  const int NP = src.cols / 64, NB = src.cols / 32;
+  if (i >= (size_t)src.rows / 16 * NP * 64) return;
+  const int l = (int)(i % 64), p = (int)(i / 64 % NP);
+  const size_t t = i / 64 / NP, r = 16 * t + (l & 15);
+  const uint8_t* sp = src.q + r * src.cols + 64 * p + 8 * (l >> 4);
+  const uint2 lo = *reinterpret_cast<const uint2*>(sp), hi = *reinterpret_cast<const uint2*>(sp + 32);
+  reinterpret_cast<uint4*>(q)[i] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+  if (l < 32) {
+    const int b = 2 * p + (l >> 4);
+    d[(t * NB + b) * 16 + (l & 15)] = src.d[r * NB + b];
+  }
+}
+
+hipError_t launch_tile_q8(hipStream_t s, const DMat& src, uint8_t* q, uint16_t* d) {
+  if (src.dtype != DT_Q8_0 || src.rows % 16 || src.cols % 64) return hipErrorInvalidValue;
+  const size_t n = (size_t)src.rows / 16 * (src.cols / 64) * 64;
+  klaunch(k_tile_q8, (unsigned)((n + 255) / 256), 256, 0, s, src, q, d);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------------------
 // MFMA tile of one wave: 16 weight rows x NM member columns over NB 32-element blocks.
-//   a[b]  : this lane's 8 weight codes of block b (row lane%16, elements 8*(lane/16) .. +8)
+//   a[p]  : this lane's weight codes of blocks 2p and 2p+1 (row lane%16, elements 8*(lane/16) .. +8 of each)
 //   bh/bl : LDS [NM][stride] hi / lo codes of the members
-//   sdt   : LDS [NB][16] fp16 scales of the 16 rows, transposed
+//   sdt   : LDS [NB][16] fp16 scales of the 16 rows
 //   dx    : LDS [NM][NB] activation scales
 // acc[ct][i] = output (row 4*(lane/16) + i, column 16*ct + lane%16).
 template <int NB, int NM>
-__device__ __forceinline__ void mfma_tile(const uint2 (&a)[NB], const int8_t* bh, const int8_t* bl, int stride,
+__device__ __forceinline__ void mfma_tile(const uint4 (&a)[NB / 2], const int8_t* bh, const int8_t* bl, int stride,
                                           const uint16_t* sdt, const float* dx, float (&acc)[NM / 16][4]) {
   const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
 #pragma unroll
@@ -202,7 +228,9 @@ __device__ __forceinline__ void mfma_tile(const uint2 (&a)[NB], const int8_t* bh
     for (int i = 0; i < 4; i++) acc[ct][i] = 0.0f;
 #pragma unroll
   for (int b = 0; b < NB; b++) {
-    const long av = (long)(((unsigned long long)a[b].y << 32) | a[b].x);
+    const uint4& ap = a[b / 2];
+    const long av = (b & 1) ? (long)(((unsigned long long)ap.w << 32) | ap.z)
+                            : (long)(((unsigned long long)ap.y << 32) | ap.x);
     const uint2 s4 = *reinterpret_cast<const uint2*>(sdt + b * 16 + 4 * grp);
     const float dw[4] = {h2f((uint16_t)(s4.x & 0xffff)), h2f((uint16_t)(s4.x >> 16)), h2f((uint16_t)(s4.y & 0xffff)),
                          h2f((uint16_t)(s4.y >> 16))};
@@ -226,37 +254,38 @@ __device__ __forceinline__ void mfma_tile(const uint2 (&a)[NB], const int8_t* bh
   }
 }
 
-// Operands of one wave's 16 weight rows and of the member activations, fetched in the order scales, activations,
-// weights, so that writing the first two into LDS waits only for them while the weight stream is still in flight.
+// Operands of one wave's 16-row weight tile and of the member activations, fetched in the order scales,
+// activations, weights, so that writing the first two into LDS waits only for them while the weight stream is
+// still in flight.
 template <int NB>
-struct RowScales {
-  uint16_t v[(NB + 3) / 4];
+struct TileScales {
+  static constexpr int N = (4 * NB + 63) / 64;  // 8-byte pieces (4 scales) per lane
+  uint2 v[N];
 };
 
-// Scales of the row this lane loads for (row r16 of the tile), blocks grp, grp + 4, ...
+// The [NB][16] scales of tile t16, 8 bytes a lane.
 template <int NB>
-__device__ __forceinline__ void fetch_scales(const DMat& m, size_t row, RowScales<NB>& sc) {
-  const int grp = (threadIdx.x & 63) >> 4;
-  const uint16_t* p = m.d + row * (size_t)(m.cols / 32);
+__device__ __forceinline__ void fetch_scales(const TMat& m, size_t t16, TileScales<NB>& sc) {
+  const int lane = threadIdx.x & 63;
+  const uint2* p = reinterpret_cast<const uint2*>(m.d + t16 * NB * 16);
 #pragma unroll
-  for (int q = 0; q < (NB + 3) / 4; q++)
-    if (grp + 4 * q < NB) sc.v[q] = p[grp + 4 * q];
+  for (int q = 0; q < TileScales<NB>::N; q++)
+    if (4 * NB % 64 == 0 || lane + 64 * q < 4 * NB) sc.v[q] = p[lane + 64 * q];
 }
 template <int NB>
-__device__ __forceinline__ void store_scales(const RowScales<NB>& sc, int r16, uint16_t* sdt) {
-  const int grp = (threadIdx.x & 63) >> 4;
+__device__ __forceinline__ void store_scales(const TileScales<NB>& sc, uint16_t* sdt) {
+  const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int q = 0; q < (NB + 3) / 4; q++)
-    if (grp + 4 * q < NB) sdt[(grp + 4 * q) * 16 + r16] = sc.v[q];
+  for (int q = 0; q < TileScales<NB>::N; q++)
+    if (4 * NB % 64 == 0 || lane + 64 * q < 4 * NB) reinterpret_cast<uint2*>(sdt)[lane + 64 * q] = sc.v[q];
 }
 
-// The 8-byte A-operand pieces of NB blocks of one Q8_0 row: elements 8*(lane/16) .. +8 of each block.
+// This lane's A operands of tile t16: one 16-byte load per pair of blocks, 1 KB of consecutive bytes per wave.
 template <int NB>
-__device__ __forceinline__ void fetch_rows_q8(const DMat& m, size_t row, uint2 (&a)[NB]) {
-  const int grp = (threadIdx.x & 63) >> 4;
-  const uint8_t* base = m.q + row * (size_t)m.cols + 8 * grp;
+__device__ __forceinline__ void fetch_tile_q8(const TMat& m, size_t t16, uint4 (&a)[NB / 2]) {
+  const uint4* p = reinterpret_cast<const uint4*>(m.q) + t16 * (NB / 2) * 64 + (threadIdx.x & 63);
 #pragma unroll
-  for (int b = 0; b < NB; b++) a[b] = *reinterpret_cast<const uint2*>(base + 32 * b);
+  for (int q = 0; q < NB / 2; q++) a[q] = p[q * 64];
 }
 
 // Member activations: rows row(c) for c in [0, ne) of the hi/lo planes (row length K) and their K/32 block scales;
@@ -319,23 +348,25 @@ __device__ __forceinline__ void store_members(const Members<K, NM, NT>& mb, int8
 }
 
 // ------------------------------------------------------------------------------------------------------------
-// Gate/up of list expert u = blockIdx.y for its members, rows [64t, 64t+64) of gate and of up (t = blockIdx.x):
-// wave w computes 16 rows (w & 3) of gate (w < 4) or up (w >= 4), so the members' codes staged in LDS serve 8
-// waves and one workgroup per CU covers the step. Then act = silu(g)*u and its hi/lo codes (each 32 rows are one
-// block of the act vector), written to the members' slots.
+// Gate/up of list expert u = blockIdx.y for its members, rows [RT t, RT t + RT) of gate and of up (t = blockIdx.x,
+// RT = 16 * NT / 128): the first half of the waves computes 16 gate rows each, the second half the same up rows, so
+// the members' codes staged in LDS serve every wave. Then act = silu(g)*u and its hi/lo codes (each 32 rows are
+// one block of the act vector), written to the members' slots.
 constexpr int kGrpUpThreads = 512;
 
-template <int H, int NM>
-__global__ __launch_bounds__(kGrpUpThreads) void k_grp_up(DMat gu, int m, int k, int inter, GroupBufs g) {
+template <int H, int NM, int NT>
+__global__ __launch_bounds__(NT) void k_grp_up(int m, int k, int inter, GroupBufs g) {
   constexpr int NB = H / 32;
   constexpr int STR = H + 16;
-  constexpr int NT = kGrpUpThreads;
+  constexpr int WH = NT / 128;  // waves per half (gate or up)
+  constexpr int RT = 16 * WH;   // gate (and up) rows of the workgroup
+  static_assert(RT % 32 == 0, "whole act blocks per workgroup");
   __shared__ Plan plan;
   __shared__ __align__(16) int8_t bh[NM * STR];
   __shared__ __align__(16) int8_t bl[NM * STR];
   __shared__ float dx[NM * NB];
   __shared__ __align__(16) uint16_t sdt[NT / 64][NB * 16];
-  __shared__ float gout[2][64][NM + 1];
+  __shared__ float gout[2][RT][NM + 1];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int u = blockIdx.y, tile = blockIdx.x;
   make_plan<NT>(g.ids, m, k, plan);
@@ -343,15 +374,15 @@ __global__ __launch_bounds__(kGrpUpThreads) void k_grp_up(DMat gu, int m, int k,
   const int e = plan.list[u], off = plan.offe[e];
   const unsigned bits = plan.bits[e];
   const int ne = __popc(bits);
-  const int r16 = lane & 15;
-  const size_t row = (size_t)e * 2 * inter + (size_t)(wave >> 2) * inter + 64 * tile + 16 * (wave & 3) + r16;
-  RowScales<NB> sc;
-  fetch_scales<NB>(gu, row, sc);
+  // this wave's 16 rows: gate (first half) or up (second half) rows [RT tile + 16 (wave % WH), +16) of expert e
+  const size_t t16 = ((size_t)e * 2 * inter + (size_t)(wave / WH) * inter + RT * tile + 16 * (wave % WH)) / 16;
+  TileScales<NB> sc;
+  fetch_scales<NB>(g.gu, t16, sc);
   Members<H, NM, NT> mb;
   fetch_members<H, NM, NT, false>(g.xh, g.xl, g.xd, bits, 0, ne, mb);
-  uint2 a[NB];
-  fetch_rows_q8<NB>(gu, row, a);
-  store_scales<NB>(sc, r16, sdt[wave]);
+  uint4 a[NB / 2];
+  fetch_tile_q8<NB>(g.gu, t16, a);
+  store_scales<NB>(sc, sdt[wave]);
   store_members<H, NM, NT>(mb, bh, bl, STR, dx);
   __syncthreads();
   float acc[NM / 16][4];
@@ -360,18 +391,18 @@ __global__ __launch_bounds__(kGrpUpThreads) void k_grp_up(DMat gu, int m, int k,
 #pragma unroll
   for (int ct = 0; ct < NM / 16; ct++)
 #pragma unroll
-    for (int i = 0; i < 4; i++) gout[wave >> 2][16 * (wave & 3) + 4 * grp + i][16 * ct + (lane & 15)] = acc[ct][i];
+    for (int i = 0; i < 4; i++) gout[wave / WH][16 * (wave % WH) + 4 * grp + i][16 * ct + (lane & 15)] = acc[ct][i];
   __syncthreads();
-  // act = silu(gate) * up for 64 rows (two 32-row blocks) x NM members; 8 lanes per (block, member), 4 rows a lane
-  for (int base = 0; base < 2 * NM; base += NT / 8) {
+  // act = silu(gate) * up for RT rows (RT/32 blocks) x NM members; 8 lanes per (block, member), 4 rows a lane
+  for (int base = 0; base < RT / 32 * NM; base += NT / 8) {
     const int pi = base + (threadIdx.x >> 3), part = threadIdx.x & 7;
     const int bi = pi / NM, j = pi % NM;
-    const bool valid = pi < 2 * NM && j < ne;
+    const bool valid = pi < RT / 32 * NM && j < ne;
     float av[4];
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-      const int r = (32 * bi + 4 * part + i) & 63;
+      const int r = (32 * bi + 4 * part + i) & (RT - 1);
       av[i] = valid ? silu_mul(gout[0][r][j], gout[1][r][j]) : 0.0f;
       const float aa = fabsf(av[i]);
       amax = aa > amax ? aa : amax;
@@ -388,7 +419,7 @@ __global__ __launch_bounds__(kGrpUpThreads) void k_grp_up(DMat gu, int m, int k,
     }
     if (valid) {
       const size_t slotv = (size_t)(off + j);
-      const int blk = 2 * tile + bi;
+      const int blk = RT / 32 * tile + bi;
       reinterpret_cast<uint32_t*>(g.ah + slotv * inter + 32 * blk)[part] = hw;
       reinterpret_cast<uint32_t*>(g.al + slotv * inter + 32 * blk)[part] = lw;
       if (part == 0) g.ad[slotv * (inter / 32) + blk] = d;
@@ -400,7 +431,7 @@ __global__ __launch_bounds__(kGrpUpThreads) void k_grp_up(DMat gu, int m, int k,
 // ------------------------------------------------------------------------------------------------------------
 // Down of list expert u = blockIdx.y for its members, output rows [64t, 64t+64): o[slot][row].
 template <int I, int NM>
-__global__ __launch_bounds__(256, NM == 16 ? 2 : 1) void k_grp_down(DMat dn, int hidden, GroupBufs g) {
+__global__ __launch_bounds__(256, NM == 16 ? 2 : 1) void k_grp_down(int hidden, GroupBufs g) {
   constexpr int NB = I / 32;
   constexpr int STR = I + 16;
   __shared__ __align__(16) int8_t bh[NM * STR];
@@ -411,16 +442,14 @@ __global__ __launch_bounds__(256, NM == 16 ? 2 : 1) void k_grp_down(DMat dn, int
   const int u = blockIdx.y, tile = blockIdx.x;
   if (u >= g.grp[GRP_NU]) return;
   const int e = g.grp[GRP_LIST + u], ne = g.grp[GRP_CNT + u], off = g.grp[GRP_OFF + u];
-  const int r16 = lane & 15;
-  const int r = 64 * tile + 16 * wave + r16;
-  const size_t row = (size_t)e * hidden + r;
-  RowScales<NB> sc;
-  fetch_scales<NB>(dn, row, sc);
+  const size_t t16 = ((size_t)e * hidden + 64 * tile + 16 * wave) / 16;  // this wave's 16 output rows
+  TileScales<NB> sc;
+  fetch_scales<NB>(g.dn, t16, sc);
   Members<I, NM, 256> mb;
   fetch_members<I, NM, 256, true>(g.ah, g.al, g.ad, 0u, off, ne, mb);
-  uint2 a[NB];
-  fetch_rows_q8<NB>(dn, row, a);
-  store_scales<NB>(sc, r16, sdt[wave]);
+  uint4 a[NB / 2];
+  fetch_tile_q8<NB>(g.dn, t16, a);
+  store_scales<NB>(sc, sdt[wave]);
   store_members<I, NM, 256>(mb, bh, bl, STR, dx);
   __syncthreads();
   float acc[NM / 16][4];
@@ -471,7 +500,9 @@ hipError_t launch_grouped_block(hipStream_t s, const LayerDev& L, int m, int k, 
   };
   const int H = L.gate_up.cols, E = L.router.rows;
   if (m < 1 || m > kGrpMaxPos || k < 1 || k > 8 || E > 64 || L.gate_up.dtype != DT_Q8_0 ||
-      L.down.dtype != DT_Q8_0 || L.router.dtype != DT_Q8_0 || L.down.cols != inter || inter % 32 || H % 256)
+      L.down.dtype != DT_Q8_0 || L.router.dtype != DT_Q8_0 || L.down.cols != inter || inter % 64 || H % 256 ||
+      !g.gu.q || !g.dn.q || g.gu.rows != L.gate_up.rows || g.gu.cols != H || g.dn.rows != L.down.rows ||
+      g.dn.cols != inter)
     return hipErrorInvalidValue;
   const int U = m * k < E ? m * k : E;
   const bool wide = m > 16;
@@ -485,14 +516,15 @@ hipError_t launch_grouped_block(hipStream_t s, const LayerDev& L, int m, int k, 
   if (e != hipSuccess) return e;
   // u is the slow grid index, so the workgroups of list indices past the step's expert count (which end at once)
   // are dispatched last
-  const dim3 gu_grid(inter / 64, U);
+  constexpr int NT = kGrpUpThreads, RT = 16 * NT / 128;
+  const dim3 gu_grid(inter / RT, U);
   arm(1);
   if (H == 1024) {
-    if (wide) klaunch(k_grp_up<1024, 32>, gu_grid, kGrpUpThreads, 0, s, L.gate_up, m, k, inter, g);
-    else klaunch(k_grp_up<1024, 16>, gu_grid, kGrpUpThreads, 0, s, L.gate_up, m, k, inter, g);
+    if (wide) klaunch(k_grp_up<1024, 32, NT>, gu_grid, NT, 0, s, m, k, inter, g);
+    else klaunch(k_grp_up<1024, 16, NT>, gu_grid, NT, 0, s, m, k, inter, g);
   } else {
-    if (wide) klaunch(k_grp_up<1536, 32>, gu_grid, kGrpUpThreads, 0, s, L.gate_up, m, k, inter, g);
-    else klaunch(k_grp_up<1536, 16>, gu_grid, kGrpUpThreads, 0, s, L.gate_up, m, k, inter, g);
+    if (wide) klaunch(k_grp_up<1536, 32, NT>, gu_grid, NT, 0, s, m, k, inter, g);
+    else klaunch(k_grp_up<1536, 16, NT>, gu_grid, NT, 0, s, m, k, inter, g);
   }
   if ((e = hipGetLastError()) != hipSuccess) return e;
   const dim3 dn_grid(H / 64, U);
@@ -500,8 +532,8 @@ hipError_t launch_grouped_block(hipStream_t s, const LayerDev& L, int m, int k, 
   switch (inter) {
 #define DOWN_CASE(II)                                                                               \
   case II:                                                                                          \
-    if (wide) klaunch(k_grp_down<II, 32>, dn_grid, 256, 0, s, L.down, H, g);                        \
-    else klaunch(k_grp_down<II, 16>, dn_grid, 256, 0, s, L.down, H, g);                             \
+    if (wide) klaunch(k_grp_down<II, 32>, dn_grid, 256, 0, s, H, g);                            \
+    else klaunch(k_grp_down<II, 16>, dn_grid, 256, 0, s, H, g);                                 \
     break;
     DOWN_CASE(128)
     DOWN_CASE(256)
