@@ -287,7 +287,7 @@ __device__ __forceinline__ void wg_copy(const float* __restrict__ x, float* xs) 
   copy_finish<N, NT>(in, xs);
 }
 
-// Ranks of n <= 64 logits held in LDS (lg, visible to the whole workgroup), by all NW waves: wave w counts, for
+// Ranks of n <= 64 logits held in LDS (lg[64], visible to the whole workgroup), by all NW waves: wave w counts, for
 // every lane e, the 64-bit sort keys of logits [w * 64 / NW, (w + 1) * 64 / NW) above lane e's key (total-order key,
 // then 63 - e: descending value, ties to the lower index); the counts meet in LDS and every wave adds them in wave
 // order. Returns the rank of lane e's logit (the same in every wave); contains a workgroup barrier.
@@ -295,8 +295,12 @@ template <int NW>
 __device__ __forceinline__ int wg_rank(const float* lg, int n, int lane, int wave, int (*part)[NW]) {
   constexpr int PER = 64 / NW;
   static_assert(64 % NW == 0, "waves must divide 64");
+  // lg[e] is read for every e < 64 and the entries at and past n are discarded afterwards: a read under the
+  // condition would be a branch and a wait of its own per key
   auto key = [&](int e) -> unsigned long long {
-    return e < n ? (((unsigned long long)((unsigned)total_key(lg[e]) ^ 0x80000000u) << 6) | (unsigned)(63 - e)) : 0ull;
+    const unsigned long long kv =
+        ((unsigned long long)((unsigned)total_key(lg[e]) ^ 0x80000000u) << 6) | (unsigned)(63 - e);
+    return e < n ? kv : 0ull;
   };
   const unsigned long long mine = key(lane);
   int cnt = 0;
@@ -335,7 +339,7 @@ __device__ __forceinline__ void route_weights(const float* lg, bool sel, int ran
   }
 }
 
-// Top-k of n <= 64 logits held in LDS (lg), by one wave. Lane e holds logit e as one 64-bit sort key
+// Top-k of n <= 64 logits held in LDS (lg[64]), by one wave. Lane e holds logit e as one 64-bit sort key
 // (total-order key, then 63 - e, so that larger means earlier: descending value, ties to the lower index); the keys
 // are broadcast through LDS and each lane counts the keys above its own, which is its rank; a lane whose rank is
 // below k is selected. Then w_j = exp(l_j - l_top) / sum with the sum taken left to right in rank order
@@ -349,18 +353,25 @@ struct TopkLds {
 
 __device__ __forceinline__ void wave_topk(const float* lg, int n, int k, int lane, TopkLds& t, int* ids,
                                           float* weights) {
-  const float v = lane < n ? lg[lane] : 0.0f;
+  const float lv = lg[lane];  // read unconditionally (lg holds 64 entries), discarded past n
+  const float v = lane < n ? lv : 0.0f;
   const unsigned long long mine =
       ((unsigned long long)((unsigned)total_key(v) ^ 0x80000000u) << 6) | (unsigned)(63 - lane);
   t.keys[lane] = lane < n ? mine : 0ull;
   if (lane < 8) t.ex[lane] = 0.0f;
   wave_lds_sync();
+  // the 64 keys in 4 batches of 8 independent 16-byte reads (one round trip per batch, not per read)
   int rank = 0;
 #pragma unroll
-  for (int j2 = 0; j2 < 32; j2++) {
-    const ulonglong2 kk = reinterpret_cast<const ulonglong2*>(t.keys)[j2];
-    rank += kk.x > mine;
-    rank += kk.y > mine;
+  for (int b = 0; b < 4; b++) {
+    ulonglong2 kk[8];
+#pragma unroll
+    for (int j2 = 0; j2 < 8; j2++) kk[j2] = reinterpret_cast<const ulonglong2*>(t.keys)[8 * b + j2];
+#pragma unroll
+    for (int j2 = 0; j2 < 8; j2++) {
+      rank += kk[j2].x > mine;
+      rank += kk[j2].y > mine;
+    }
   }
   const bool sel = lane < n && rank < k;
   if (sel) t.val[rank] = v;
