@@ -240,6 +240,13 @@ def main():
     hbm_copy = {"bytes_moved": 2 * copy_bytes, "us": round(copy_us, 2),
                 "gbs": round(2 * copy_bytes / (copy_us * 1e-6) / 1e9, 1)}
     log(f"device copy of {copy_bytes >> 20} MiB: {copy_us:.1f} us, {hbm_copy['gbs']:.0f} GB/s read+write")
+    # cold streaming reads: the achievable read rate of a long stream, and of one of the size of a grouped gate/up
+    # launch at 16 positions (40 MiB), which includes the ramp-up every launch pays
+    hbm_read = []
+    for rb in (1 << 30, 40 << 20):
+        r_us = moert.read_probe(rb, 10)
+        hbm_read.append({"bytes": rb, "us": round(r_us, 2), "gbs": round(rb / (r_us * 1e-6) / 1e9, 1)})
+        log(f"cold read of {rb >> 20} MiB: {r_us:.1f} us, {hbm_read[-1]['gbs']:.0f} GB/s")
 
     batched = batched_step(cfg, args.seed, args.batched_iters) if args.batched_iters > 0 else None
     cache = expert_cache(cfg, args.seed, args.cache_steps) if args.cache_steps > 0 else None
@@ -282,6 +289,7 @@ def main():
                           "frac": round(step_bytes / (wall / args.steps) / 1e9 / HBM_PEAK_GBS, 4)},
         "moe_gemv": moe,
         "hbm_copy": hbm_copy,
+        "hbm_read": hbm_read,
         "batched_step": batched,
         "expert_cache": cache,
         "kernels": kernels,

@@ -227,6 +227,11 @@ int moert_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v
  * reference measures PCIe and HBM rates with separate CUDA tools); used to calibrate the roofline. */
 int moert_copy_probe(size_t bytes, int iters, double* us_per_copy);
 
+/* Achievable HBM read bandwidth reference: mean microseconds of one streaming read of `bytes` (multiple of 16) over
+ * `iters` launches, each reading its own window of a buffer larger than the last-level cache and timed by its own
+ * dispatch events. No reference counterpart; the ceiling a weight-streaming kernel of that size can reach. */
+int moert_read_probe(size_t bytes, int iters, double* us_per_read);
+
 /* PCIe reference for the expert cache: mean microseconds of one copy of `bytes` (multiple of 16) from pinned,
  * device-mapped host memory into HBM, by a copy kernel (the way the cached kernels read missed experts) and by hipMemcpyAsync
  * (the DMA engines). The analogue of the reference's PCIe measurement programs (tools/llama-forcado/banda.cu,

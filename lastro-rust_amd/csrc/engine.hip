@@ -1155,6 +1155,45 @@ int moert_copy_probe(size_t bytes, int iters, double* us_per_copy) {
   return MOERT_OK;
 }
 
+int moert_read_probe(size_t bytes, int iters, double* us_per_read) {
+  CHECK_CFG(bytes >= 16 && bytes % 16 == 0 && iters >= 1 && us_per_read, "read_probe: bytes %zu, iters %d", bytes,
+            iters);
+  // each launch reads its own window of a buffer larger than the 256 MB last-level cache, so every read is cold
+  const size_t span = std::max<size_t>(bytes, (size_t)1 << 30);
+  const size_t windows = std::max<size_t>(span / bytes, 1);
+  Scoped sc;
+  TRY(sc.init());
+  uint8_t* src;
+  unsigned* out;
+  TRY(sc.dev(&src, span));
+  TRY(sc.dev(&out, (size_t)read_probe_blocks(bytes) * 256));
+  CHECK_HIP(launch_read(sc.s, src + (windows - 1) % windows * bytes, bytes, out));  // warm-up (code, queues)
+  std::vector<hipEvent_t> ev(2 * iters);
+  for (auto& e : ev) CHECK_HIP(hipEventCreate(&e));
+  int rc = MOERT_OK;
+  for (int i = 0; i < iters && rc == MOERT_OK; i++) {
+    arm_launch_events(ev[2 * i], ev[2 * i + 1]);
+    if (launch_read(sc.s, src + (size_t)i % windows * bytes, bytes, out) != hipSuccess) rc = MOERT_E_DEVICE;
+  }
+  double total = 0.0;
+  if (rc == MOERT_OK && hipStreamSynchronize(sc.s) == hipSuccess) {
+    for (int i = 0; i < iters; i++) {
+      float t = 0.0f;
+      if (hipEventElapsedTime(&t, ev[2 * i], ev[2 * i + 1]) != hipSuccess) rc = MOERT_E_DEVICE;
+      total += t;
+    }
+  } else {
+    rc = MOERT_E_DEVICE;
+  }
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  if (rc) {
+    set_err("read_probe: device error");
+    return rc;
+  }
+  *us_per_read = total * 1000.0 / iters;
+  return MOERT_OK;
+}
+
 int moert_h2d_probe(size_t bytes, int iters, double* kernel_us, double* memcpy_us) {
   CHECK_CFG(bytes >= 16 && bytes % 16 == 0 && iters >= 1 && kernel_us && memcpy_us, "h2d_probe: bytes %zu", bytes);
   Scoped sc;

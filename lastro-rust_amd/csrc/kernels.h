@@ -74,6 +74,9 @@ hipError_t launch_topk(hipStream_t s, const float* logits, const float* bias, in
 hipError_t launch_argmax(hipStream_t s, const float* v, int n, int2* best, int* cnt, int* out);
 hipError_t launch_exp(hipStream_t s, const float* x, float* y, int n);
 hipError_t launch_copy(hipStream_t s, const void* src, void* dst, size_t bytes);
+// Streaming read of `bytes` (multiple of 16) into read_probe_blocks(bytes) * 256 words of out.
+hipError_t launch_read(hipStream_t s, const void* src, size_t bytes, unsigned* out);
+int read_probe_blocks(size_t bytes);
 hipError_t launch_attn_unit(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vc, int heads,
                             int kv_heads, int max_len, const int* len_dev, float scale, int tps, float* part,
                             float* out);

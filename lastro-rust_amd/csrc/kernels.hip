@@ -1275,6 +1275,27 @@ hipError_t launch_copy(hipStream_t s, const void* src, void* dst, size_t bytes) 
   return hipGetLastError();
 }
 
+// Streaming read of n 16-byte words (four loads in flight per thread and pass), one word of output per thread so
+// that the loads are live.
+__global__ __launch_bounds__(256) void k_read(const uint4* __restrict__ src, size_t n, unsigned* __restrict__ out) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  unsigned acc = 0;
+  for (; i + 3 * stride < n; i += 4 * stride) {
+    const uint4 a = src[i], b = src[i + stride], c = src[i + 2 * stride], d = src[i + 3 * stride];
+    acc ^= a.x ^ b.y ^ c.z ^ d.w;
+  }
+  for (; i < n; i += stride) acc ^= src[i].x;
+  out[(size_t)blockIdx.x * 256 + threadIdx.x] = acc;
+}
+
+int read_probe_blocks(size_t bytes) { return bytes >= ((size_t)256 << 20) ? 256 : 1024; }
+
+hipError_t launch_read(hipStream_t s, const void* src, size_t bytes, unsigned* out) {
+  klaunch(k_read, read_probe_blocks(bytes), 256, 0, s, (const uint4*)src, bytes / 16, out);
+  return hipGetLastError();
+}
+
 hipError_t launch_exp(hipStream_t s, const float* x, float* y, int n) {
   klaunch(k_exp, cdiv(n, 256), 256, 0, s, x, y, n);
   return hipGetLastError();

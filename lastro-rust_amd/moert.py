@@ -112,6 +112,7 @@ def lib() -> ctypes.CDLL:
             "moert_attn_decode": (i, [vp, vp, vp, i, i, i, i, i, f, i, vp]),
             "moert_exp_device": (i, [vp, vp, i]),
             "moert_copy_probe": (i, [sz, i, ctypes.POINTER(ctypes.c_double)]),
+            "moert_read_probe": (i, [sz, i, ctypes.POINTER(ctypes.c_double)]),
             "moert_h2d_probe": (i, [sz, i, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)]),
             "moert_quantize": (i, [vp, sz, i, vp]),
             "moert_dtype_bytes": (sz, [i, sz]),
@@ -135,7 +136,7 @@ EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moer
             "moert_block_forward", "moert_block_time", "moert_block_forward_batched",
             "moert_block_experts_in_step", "moert_block_time_batched", "moert_router_topk", "moert_argmax", "moert_gemv",
             "moert_dequant", "moert_rmsnorm", "moert_rope", "moert_attn_decode", "moert_exp_device",
-            "moert_copy_probe", "moert_h2d_probe", "moert_quantize", "moert_dtype_bytes", "moert_synth_normal", "moert_synth_quantized",
+            "moert_copy_probe", "moert_read_probe", "moert_h2d_probe", "moert_quantize", "moert_dtype_bytes", "moert_synth_normal", "moert_synth_quantized",
             "moert_synth_fp16"]
 
 
@@ -543,6 +544,13 @@ def copy_probe(nbytes: int, iters: int = 10) -> float:
     """Mean microseconds of one device-to-device copy of nbytes (HBM bandwidth reference)."""
     us = ctypes.c_double()
     check(lib().moert_copy_probe(ctypes.c_size_t(nbytes), iters, ctypes.byref(us)))
+    return us.value
+
+
+def read_probe(nbytes: int, iters: int = 10) -> float:
+    """Mean microseconds of one cold streaming read of nbytes from HBM (achievable read-bandwidth reference)."""
+    us = ctypes.c_double()
+    check(lib().moert_read_probe(ctypes.c_size_t(nbytes), iters, ctypes.byref(us)))
     return us.value
 
 
