@@ -125,6 +125,21 @@ int moert_decode_step(moert_model* m, int token, float* logits, int* route_ids, 
  * Replaces the prompt + generation loop of rust/moe-rt/src/bin/m1b-gulosa.rs:85-105. */
 int moert_generate(moert_model* m, const int* prompt, int n_prompt, int n_new, int* out_tokens, float* gaps);
 
+/* Multi-position step: tokens[0..n) at positions pos .. pos + n - 1 (n <= 32) in one pass per layer, every weight row
+ * read once for the block of positions. Appends their KV rows; logits (nullable, vocab floats) and argmax are
+ * those of the last position, which becomes the next token of the sequence; the position advances by n. The
+ * result equals n decode steps bit for bit (KV rows, hidden state, logits). Replaces the block step of the model
+ * mode: CudaBackend::begin_step_tokens (rust/moe-rt/src/cuda_backend.rs:499-516) and the per-position loops of
+ * the step (cuda_backend.rs:751-917, Dense::begin_step cuda_dense.rs:236-288); limit 1..=32 as
+ * cuda_backend.rs:272-274. Resident models only (MOERT_E_CONFIG on a cached one). */
+int moert_step_batched(moert_model* m, const int* tokens, int n, float* logits, int* argmax);
+
+/* Reads n tokens from the current position in blocks of at most 32 positions (moert_step_batched each; the block
+ * plan of plano_blocos, rust/moe-rt/src/motor/leitura.rs:53-60), as
+ * le_ids (rust/moe-rt/src/motor/leitura.rs:79-85, validation leitura.rs:62-76): the tokens are checked and the
+ * cache bound (MOERT_E_FULL) before any block runs; logits / argmax of the last position. */
+int moert_prefill(moert_model* m, const int* tokens, int n, float* logits, int* argmax);
+
 /* Back to position 0 (old KV stays, masked by the length). Replaces GpuModel::reset
  * (rust/moe-rt/src/gpu_model.rs:245-247) and CudaBackend::reset_sequence (cuda_backend.rs:555-558). */
 int moert_reset_sequence(moert_model* m);

@@ -21,6 +21,7 @@
 #include "cache.h"
 #include "grouped.h"
 #include "kernels.h"
+#include "prefill.h"
 
 using namespace moert;
 
@@ -245,6 +246,39 @@ struct moert_model {
     CHECK_HIP(e);
     graph = g;
     CHECK_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+    return MOERT_OK;
+  }
+
+  // multi-position step buffers, allocated on first use
+  PfBufs pf{};
+  int ensure_pf() {
+    if (pf.h) return MOERT_OK;
+    const int H = dims.hidden, qd = dims.heads * 64, I = dims.inter, M = kPfMaxPos, K8 = 8;
+    const size_t parts = (size_t)M * dims.heads * attn_splits_for(max_len, dims.tps) * 66;
+    int rc;
+    if ((rc = zeros(arena, stream, (size_t)M, &pf.toks)) || (rc = zeros(arena, stream, (size_t)1, &pf.pos0)) ||
+        (rc = zeros(arena, stream, (size_t)M * H, &pf.h)) || (rc = zeros(arena, stream, (size_t)M * qd, &pf.q)) ||
+        (rc = zeros(arena, stream, (size_t)M * qd, &pf.att)) || (rc = zeros(arena, stream, parts, &pf.part)) ||
+        (rc = zeros(arena, stream, (size_t)M * H, &pf.xn)) || (rc = zeros(arena, stream, (size_t)M * K8, &pf.ids)) ||
+        (rc = zeros(arena, stream, (size_t)M * K8, &pf.w)) ||
+        (rc = zeros(arena, stream, (size_t)M * K8 * I, &pf.act)) ||
+        (rc = zeros(arena, stream, (size_t)M * K8 * H, &pf.o)))
+      return rc;
+    CHECK_HIP(hipStreamSynchronize(stream));
+    return MOERT_OK;
+  }
+
+  // Positions pos0 .. pos0 + nv - 1 through every layer, then the final norm, head and argmax of the last one (the
+  // device state already holds pos = pos0 + nv - 1, fixed = pos0 + nv and *pf.pos0 = pos0); its hidden state is
+  // left in b.h, as after a decode step.
+  int enqueue_batched(int pos0, int nv) {
+    CHECK_HIP(launch_embed_b(stream, embed, dims, pf, nv));
+    for (const LayerDev& L : layers) CHECK_HIP(launch_layer_b(stream, L, dims, pf, pf.pos0, pos0, nv, b.rope));
+    StepBufs bl = b;
+    bl.h = pf.h + (size_t)(nv - 1) * dims.hidden;
+    CHECK_HIP(launch_head(stream, embed, norm, dims, bl));
+    CHECK_HIP(launch_head_argmax(stream, embed, dims, bl));
+    CHECK_HIP(hipMemcpyAsync(b.h, bl.h, (size_t)dims.hidden * 4, hipMemcpyDeviceToDevice, stream));
     return MOERT_OK;
   }
 
@@ -644,6 +678,57 @@ int moert_decode_step(moert_model* m, int token, float* logits, int* route_ids, 
   MTRY(m, model_sync(m));
   if (argmax) *argmax = am;
   m->host_pos = pos + 1;
+  return MOERT_OK;
+}
+
+int moert_step_batched(moert_model* m, const int* tokens, int n, float* logits, int* argmax) {
+  MODEL_OK(m);
+  CHECK_CFG(tokens && n >= 1 && n <= kPfMaxPos, "step_batched: %d positions outside [1, %d]", n, kPfMaxPos);
+  CHECK_CFG(!m->cached, "step_batched: the multi-position step runs on a resident model");
+  if (m->host_pos + n > m->max_len) {
+    set_err("KV cache full: %d + %d positions > %d", m->host_pos, n, m->max_len);
+    return MOERT_E_FULL;
+  }
+  for (int i = 0; i < n; i++)
+    if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab) {
+      set_err("token %d outside the vocabulary (%d)", tokens[i], m->cfg.vocab);
+      return MOERT_E_RANGE;
+    }
+  MTRY(m, m->ensure_pf());
+  const int pos0 = m->host_pos;
+  int st[2] = {pos0 + n - 1, pos0 + n};
+  MTRY(m, model_copy_in(m, m->pf.toks, tokens, (size_t)n * 4));
+  MTRY(m, model_copy_in(m, m->b.seq + pos0, tokens, (size_t)n * 4));
+  MTRY(m, model_copy_in(m, m->pf.pos0, &pos0, 4));
+  MTRY(m, model_copy_in(m, m->b.state, st, sizeof st));
+  MTRY(m, m->enqueue_batched(pos0, n));
+  if (logits) MTRY(m, model_copy_out(m, logits, m->b.logits, (size_t)m->cfg.vocab * 4));
+  int am = 0;
+  MTRY(m, model_copy_out(m, &am, m->b.argmax_hist + pos0 + n - 1, 4));
+  MTRY(m, model_sync(m));
+  if (argmax) *argmax = am;
+  m->host_pos = pos0 + n;
+  return MOERT_OK;
+}
+
+int moert_prefill(moert_model* m, const int* tokens, int n, float* logits, int* argmax) {
+  MODEL_OK(m);
+  // the checks of valida (rust/moe-rt/src/motor/leitura.rs:62-76), in its order, before any block runs
+  CHECK_CFG(tokens && n >= 1, "prefill: %d tokens", n);
+  for (int i = 0; i < n; i++)
+    if (tokens[i] < 0 || tokens[i] >= m->cfg.vocab) {
+      set_err("token %d (index %d) outside the vocabulary (%d)", tokens[i], i, m->cfg.vocab);
+      return MOERT_E_RANGE;
+    }
+  if (m->host_pos + n > m->max_len) {
+    set_err("KV cache full: %d + %d positions > %d", m->host_pos, n, m->max_len);
+    return MOERT_E_FULL;
+  }
+  for (int i = 0; i < n; i += kPfMaxPos) {
+    const int nb = std::min(kPfMaxPos, n - i), last = i + nb == n;
+    const int rc = moert_step_batched(m, tokens + i, nb, last ? logits : nullptr, last ? argmax : nullptr);
+    if (rc) return rc;
+  }
   return MOERT_OK;
 }
 

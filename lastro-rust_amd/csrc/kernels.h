@@ -50,6 +50,11 @@ hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const Ste
 hipError_t launch_qkv(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
 hipError_t launch_attn_split(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
 hipError_t launch_attn_combine(hipStream_t s, const Dims& d, const StepBufs& b);
+// Both attention kernels for ny consecutive positions of a multi-position step: position y has its query at
+// q + y * heads * 64, attends to *lenp + len_add + y cached positions and writes att + y * heads * 64 (part holds
+// ny * heads * splits * 66 floats).
+hipError_t launch_attn_batched(hipStream_t s, const LayerDev& L, const Dims& d, const int* lenp, int len_add, int ny,
+                               const float* q, float* part, float* att);
 hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
 // Router + gate/up of the routed experts (the router recomputed by every workgroup, workgroup 0 publishes it).
 // normalize: rmsnorm h with ln_moe first (decode step); otherwise h is the block input as is.

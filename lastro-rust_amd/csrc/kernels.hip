@@ -187,6 +187,12 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ q,
   __shared__ float Ps[G][64];
   const int g = blockIdx.x / splits, s = blockIdx.x % splits;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  {  // position blockIdx.y of a multi-position step: its own query, partials and length
+    const int nh = gridDim.x / splits * G;
+    q += (size_t)blockIdx.y * nh * 64;
+    part += (size_t)blockIdx.y * nh * splits * 66;
+    len_add += blockIdx.y;
+  }
   const int h = g * G + w;
   const float NEG_INF = __int_as_float(0xff800000);
   const uint16_t* K = kc + (size_t)g * max_len * 64;
@@ -344,6 +350,12 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
   __shared__ float Tm[G][T], Al[G][T], Ts[G][T];
   const int g = blockIdx.x / splits, s = blockIdx.x % splits;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  {  // position blockIdx.y of a multi-position step: its own query, partials and length
+    const int nh = gridDim.x / splits * G;
+    q += (size_t)blockIdx.y * nh * 64;
+    part += (size_t)blockIdx.y * nh * splits * 66;
+    len_add += blockIdx.y;
+  }
   const int wh = wid % G, wt = wid / G;
   const int h = g * G + wh;
   const float NEG_INF = __int_as_float(0xff800000);
@@ -463,6 +475,9 @@ __global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ p
   __shared__ float Cw[2][64];
   const int h = blockIdx.x, lane = threadIdx.x;
   const float NEG_INF = __int_as_float(0xff800000);
+  part += (size_t)blockIdx.y * gridDim.x * splits * 66;  // position blockIdx.y of a multi-position step
+  out += (size_t)blockIdx.y * gridDim.x * 64;
+  len_add += blockIdx.y;
   const float* base = part + (size_t)h * splits * 66;
   // every split's partial is requested before the length (and so the number of used splits) is known; indices
   // are clamped instead of guarded (SP >= splits), so the loads form one straight run
@@ -1056,10 +1071,10 @@ int attn_splits_for(int max_len, int tps) { return ((max_len + 63) / 64 + tps - 
 
 static hipError_t attn_split_dispatch(hipStream_t s, int G, int kvh, int tps, const float* q, const uint16_t* kc,
                                       const uint16_t* vc, const int* lenp, int len_add, int max_len, float scale,
-                                      float* part) {
+                                      float* part, int ny = 1) {
   const int splits = attn_splits_for(max_len, tps);
-  if (splits > 64 || max_len % 64) return hipErrorInvalidValue;
-  const int blocks = kvh * splits;
+  if (splits > 64 || max_len % 64 || ny < 1) return hipErrorInvalidValue;
+  const dim3 blocks(kvh * splits, ny);
 #define TILES_CASE(GG, TT)                                                                                   \
   if (G == GG && tps == TT) {                                                                                \
     klaunch(k_attn_tiles<GG, TT>, blocks, GG * TT * 64, 0, s, q, kc, vc, lenp, len_add, max_len, scale, splits, part); \
@@ -1081,18 +1096,27 @@ static hipError_t attn_split_dispatch(hipStream_t s, int G, int kvh, int tps, co
 }
 
 static hipError_t attn_combine_dispatch(hipStream_t s, int heads, int tps, int max_len, const int* lenp, int len_add,
-                                        const float* part, float* out) {
+                                        const float* part, float* out, int ny = 1) {
   const int splits = attn_splits_for(max_len, tps);
-  if (splits > 64 || max_len % 64) return hipErrorInvalidValue;
+  if (splits > 64 || max_len % 64 || ny < 1) return hipErrorInvalidValue;
+  const dim3 grid(heads, ny);
   if (splits <= 8)
-    klaunch(k_attn_combine<8>, heads, 64, 0, s, part, lenp, len_add, tps, splits, out);
+    klaunch(k_attn_combine<8>, grid, 64, 0, s, part, lenp, len_add, tps, splits, out);
   else if (splits <= 16)
-    klaunch(k_attn_combine<16>, heads, 64, 0, s, part, lenp, len_add, tps, splits, out);
+    klaunch(k_attn_combine<16>, grid, 64, 0, s, part, lenp, len_add, tps, splits, out);
   else if (splits <= 32)
-    klaunch(k_attn_combine<32>, heads, 64, 0, s, part, lenp, len_add, tps, splits, out);
+    klaunch(k_attn_combine<32>, grid, 64, 0, s, part, lenp, len_add, tps, splits, out);
   else
-    klaunch(k_attn_combine<64>, heads, 64, 0, s, part, lenp, len_add, tps, splits, out);
+    klaunch(k_attn_combine<64>, grid, 64, 0, s, part, lenp, len_add, tps, splits, out);
   return hipGetLastError();
+}
+
+hipError_t launch_attn_batched(hipStream_t s, const LayerDev& L, const Dims& d, const int* lenp, int len_add, int ny,
+                               const float* q, float* part, float* att) {
+  hipError_t e = attn_split_dispatch(s, d.heads / d.kv_heads, d.kv_heads, d.tps, q, L.k_cache, L.v_cache, lenp,
+                                     len_add, d.max_len, d.attn_mult, part, ny);
+  if (e != hipSuccess) return e;
+  return attn_combine_dispatch(s, d.heads, d.tps, d.max_len, lenp, len_add, part, att, ny);
 }
 
 hipError_t launch_attn_split(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b) {

@@ -1,0 +1,32 @@
+// Multi-position step of the whole model (prefill.hip): device buffers and launchers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kernels.h"
+
+namespace moert {
+
+constexpr int kPfMaxPos = 32;  // positions per step (the reference's block limit, cuda_backend.rs:272-274)
+
+// Device buffers of one multi-position step, sized for kPfMaxPos positions.
+struct PfBufs {
+  int* toks;     // [m] tokens of the positions
+  int* pos0;     // [1] first position of the step (the length every attention length is counted from)
+  float* h;      // [m, H] residual streams
+  float* q;      // [m, heads*d] queries
+  float* att;    // [m, heads*d] attention outputs
+  float* part;   // [m, heads, splits, 2 + d] split-KV partials
+  float* xn;     // [m, H] rmsnorm of h before the experts
+  int* ids;      // [m, k] routed experts, top-k order
+  float* w;      // [m, k] routing weights
+  float* act;    // [m, k, I] SwiGLU activations
+  float* o;      // [m, k, H] expert outputs
+};
+
+hipError_t launch_embed_b(hipStream_t s, const DMat& emb, const Dims& d, const PfBufs& p, int nv);
+// One layer for positions pos0 .. pos0 + nv - 1 (*lenp == pos0 on the device), rope: the [max_len, 64] table.
+hipError_t launch_layer_b(hipStream_t s, const LayerDev& L, const Dims& d, const PfBufs& p, const int* lenp, int pos0,
+                          int nv, const float* rope);
+
+}  // namespace moert

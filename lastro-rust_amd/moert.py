@@ -31,6 +31,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmoert.so")
 
 E_NAMES = {-1: "DEVICE", -2: "CONFIG", -3: "POISONED", -4: "FULL", -5: "RANGE"}
+E_DEVICE, E_CONFIG, E_POISONED, E_FULL, E_RANGE = -1, -2, -3, -4, -5
 
 
 class MoertError(RuntimeError):
@@ -87,6 +88,8 @@ def lib() -> ctypes.CDLL:
             "moert_cache_clear": (i, [vp]),
             "moert_decode_step": (i, [vp, i, vp, vp, vp, ip]),
             "moert_generate": (i, [vp, vp, i, i, vp, vp]),
+            "moert_step_batched": (i, [vp, vp, i, vp, ip]),
+            "moert_prefill": (i, [vp, vp, i, vp, ip]),
             "moert_reset_sequence": (i, [vp]),
             "moert_kv_prefill_fp16": (i, [vp, i, vp, vp, i]),
             "moert_set_position": (i, [vp, i]),
@@ -130,7 +133,8 @@ def lib() -> ctypes.CDLL:
 
 EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moert_model_destroy",
             "moert_model_create_cached", "moert_cache_stats", "moert_cache_clear",
-            "moert_decode_step", "moert_generate", "moert_reset_sequence", "moert_kv_prefill_fp16",
+            "moert_decode_step", "moert_generate", "moert_step_batched", "moert_prefill", "moert_reset_sequence",
+            "moert_kv_prefill_fp16",
             "moert_set_position", "moert_get_position", "moert_read_kv_fp16", "moert_read_hidden",
             "moert_time_steps", "moert_time_kernel", "moert_block_create", "moert_block_destroy",
             "moert_block_forward", "moert_block_time", "moert_block_forward_batched",
@@ -346,6 +350,23 @@ class GpuModel:
         am = ctypes.c_int(0)
         check(lib().moert_decode_step(self.h, int(token), ptr(lg), ptr(ids), ptr(w), ctypes.byref(am)))
         return lg, ids, w, am.value
+
+    def step_batched(self, tokens, want_logits: bool = True):
+        """Up to 32 tokens in one multi-position step: (logits of the last position, its argmax)
+        (begin_step_tokens + the model step over m positions)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        lg = np.empty(self.cfg.vocab, np.float32) if want_logits else None
+        am = ctypes.c_int(0)
+        check(lib().moert_step_batched(self.h, ptr(t), t.size, ptr(lg), ctypes.byref(am)))
+        return lg, am.value
+
+    def prefill(self, tokens, want_logits: bool = True):
+        """Any number of tokens in blocks of at most 32 positions (le_ids): (last logits, last argmax)."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        lg = np.empty(self.cfg.vocab, np.float32) if want_logits else None
+        am = ctypes.c_int(0)
+        check(lib().moert_prefill(self.h, ptr(t), t.size, ptr(lg), ctypes.byref(am)))
+        return lg, am.value
 
     def generate(self, prompt, n_new: int, gaps: bool = False):
         p = np.ascontiguousarray(prompt, np.int32)

@@ -1,0 +1,137 @@
+"""Multi-position steps of the whole model (moert_step_batched, moert_prefill) through the C ABI: a block of up to 32
+positions must leave exactly what the same tokens leave when decoded one at a time (the model-mode block step,
+cuda_backend.rs:499-516, 751-917, whose per-position loops make it equal to single steps): the KV rows of every
+position, the hidden state and logits of the last one, bit for bit, and the same greedy continuation. The
+single-position decode is itself pinned bit for bit against the oracle (test_gpu_model.py); the tiny case also
+checks the oracle directly."""
+import numpy as np
+import pytest
+
+import moert
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def decode_reference(g, toks, pos0, layers):
+    """Decodes toks one at a time from pos0: (last logits, last argmax, hidden, KV rows [pos0, pos0 + n) per layer)."""
+    g.set_position(pos0)
+    for t in toks:
+        lg, _, _, am = g.step(int(t))
+    n = pos0 + len(toks)
+    kv = [tuple(a[:, pos0:n] for a in g.read_kv(l, n)) for l in range(layers)]
+    return lg, am, g.hidden(), kv
+
+
+def check_block(g, toks, pos0, layers, ref, label):
+    lg, am, hid, kv = ref
+    g.set_position(pos0)
+    blg, bam = g.step_batched(toks) if len(toks) <= 32 else g.prefill(toks)
+    n = pos0 + len(toks)
+    assert g.position() == n, label
+    assert bits_equal(blg, lg), label
+    assert bam == am, label
+    assert bits_equal(g.hidden(), hid), label
+    for l in range(layers):
+        bk, bv = g.read_kv(l, n)
+        assert np.array_equal(bk[:, pos0:n], kv[l][0]) and np.array_equal(bv[:, pos0:n], kv[l][1]), (label, l)
+
+
+@pytest.mark.parametrize("wdtype,edtype", [(moert.Q8_0, moert.Q8_0), (moert.Q4_0, moert.F32), (moert.F32, moert.F32)])
+def test_tiny_batched_steps_equal_single_steps_and_the_oracle(gpu, wdtype, edtype):
+    cfg = moert.Config(**{**moert.TINY, "embedding_multiplier": 2.0, "residual_multiplier": 0.5,
+                          "attention_multiplier": 0.125, "logits_scaling": 4.0})
+    m = moert.SynthModel(cfg, seed=11, wdtype=wdtype, embed_dtype=edtype, std=0.1)
+    g = moert.GpuModel(m, 192, attn_splits=8)
+    toks = np.random.default_rng(12).integers(0, cfg.vocab, 150)
+    # blocks of 1, 5, 32, 17 and 32 positions, then the rest through prefill (blocks of 32 and a remainder)
+    pos = 0
+    for size in (1, 5, 32, 17, 32, 63):
+        block = toks[pos:pos + size]
+        say(f"tiny dtype={wdtype} block at {pos} of {size}")
+        ref = decode_reference(g, block, pos, cfg.layers)
+        check_block(g, block, pos, cfg.layers, ref, (wdtype, pos, size))
+        pos += size
+    # the oracle session over the same 150 tokens ends with the same logits and hidden state
+    s = oracle.CpuSession(m, 192, attn_splits=8, threads=4)
+    for t in toks:
+        olg, _, _, oh = s.step(int(t))
+    g.set_position(0)
+    blg, bam = g.prefill(toks)
+    assert bits_equal(blg, olg) and bits_equal(g.hidden(), oh) and bam == oracle.argmax(olg)
+    # the greedy continuation after a batched step equals the one after single steps
+    out_b = g.generate([bam], 8)
+    g.set_position(0)
+    for t in toks:
+        lg, _, _, am = g.step(int(t))
+    out_s = g.generate([am], 8)
+    assert np.array_equal(out_b, out_s)
+    g.close()
+
+
+def test_granite_1b_prefill_of_70_tokens_equals_decoding_them(gpu):
+    cfg = moert.Config(**moert.GRANITE_1B)
+    m = moert.SynthModel(cfg, seed=21)
+    g = moert.GpuModel(m, 256, attn_splits=32)
+    toks = np.random.default_rng(22).integers(0, cfg.vocab, 70)
+    say("1b decode 70 tokens")
+    ref = decode_reference(g, toks, 0, cfg.layers)
+    say("1b prefill 70 tokens (blocks 32, 32, 6)")
+    check_block(g, toks, 0, cfg.layers, ref, "1b prefill")
+    g.close()
+
+
+def test_granite_3b_batched_step_of_32_at_4096_cached_positions(gpu):
+    """The bench workload: 32 positions appended after 4096 cached ones (2-tile attention splits, G = 3)."""
+    cfg = moert.Config(**moert.GRANITE_3B)
+    m = moert.SynthModel(cfg, seed=31)
+    ctx = 4096
+    max_len = (ctx + 32 + 63) // 64 * 64
+    g = moert.GpuModel(m, max_len, attn_splits=32)
+    for l in range(cfg.layers):
+        k, v = moert.kv_prefill_data(cfg, 31, l, ctx)
+        g.kv_prefill(l, k, v)
+    toks = np.random.default_rng(32).integers(0, cfg.vocab, 32)
+    say("3b decode 32 tokens at 4096")
+    ref = decode_reference(g, toks, ctx, cfg.layers)
+    say("3b batched step of 32 at 4096")
+    check_block(g, toks, ctx, cfg.layers, ref, "3b block")
+    g.close()
+
+
+def test_batched_step_refuses_bad_blocks(gpu):
+    cfg = moert.Config(**moert.TINY)
+    m = moert.SynthModel(cfg, seed=3)
+    g = moert.GpuModel(m, 64, attn_splits=2)
+    for toks in ([], list(range(33))):
+        with pytest.raises(moert.MoertError):
+            g.step_batched(np.array(toks, np.int32) % cfg.vocab)
+    with pytest.raises(moert.MoertError) as e:
+        g.step_batched([1, cfg.vocab])
+    assert e.value.code == moert.E_RANGE
+    g.set_position(40)
+    with pytest.raises(moert.MoertError) as e:
+        g.prefill(np.zeros(25, np.int32))
+    assert e.value.code == moert.E_FULL
+    assert g.position() == 40  # nothing ran
+    with pytest.raises(moert.MoertError) as e:
+        g.prefill([0, cfg.vocab + 3])  # the vocabulary check comes first, as in valida
+    assert e.value.code == moert.E_RANGE
+    g.step_batched(np.arange(24) % cfg.vocab)  # exactly up to the end of the cache
+    assert g.position() == 64
+    g.close()
+    c = moert.GpuModel(m, 64, attn_splits=2, cache_slots=4)
+    with pytest.raises(moert.MoertError) as e:
+        c.step_batched([1, 2])
+    assert e.value.code == moert.E_CONFIG
+    c.close()
