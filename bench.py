@@ -198,6 +198,8 @@ def main():
                     help="KV splits requested for decode attention (tiles per split = ceil(tiles / splits))")
     ap.add_argument("--cache-steps", type=int, default=512,
                     help="greedy steps of the 3B Q4_0 model served from a 25%% expert cache (0 skips it)")
+    ap.add_argument("--prefill-reps", type=int, default=5,
+                    help="timed multi-position steps of 32 positions after the cached context (0: none)")
     ap.add_argument("--batched-iters", type=int, default=20,
                     help="rounds of the 16-position grouped MoE step over 4 rotating 3B blocks (0 skips it)")
     args = ap.parse_args()
@@ -255,7 +257,7 @@ def main():
     log("kernels: " + ", ".join(f"{k} {v['us']:.2f}us x{v['launches_per_step']} {v['gbs'] or 0:.0f}GB/s"
                                 for k, v in kernels.items()))
     moe = {k: kernels[k] for k in ("route_up", "expert_down")}
-    prefill = prefill_block(g, cfg, args.seed, CTX, tok_s)
+    prefill = prefill_block(g, cfg, args.seed, CTX, tok_s, reps=args.prefill_reps) if args.prefill_reps > 0 else None
     g.close()
     copy_bytes = 1 << 30
     copy_us = moert.copy_probe(copy_bytes, 10)
