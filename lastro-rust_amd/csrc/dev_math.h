@@ -38,6 +38,28 @@ __device__ __forceinline__ float dexp(float x) {
   return (p * 2.0f) * __int_as_float((ni - 1 + 127) << 23);
 }
 
+// dexp without branches, the same value for every x: the polynomial path runs on x clamped into [-87, 89] (which
+// leaves every x it serves unchanged) and the special cases are selected afterwards.
+__device__ __forceinline__ float dexp_sel(float x) {
+  const float xc = __builtin_fminf(__builtin_fmaxf(x, -87.0f), 89.0f);
+  float n = __builtin_rintf(xc * 1.44269504088896341f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, xc);
+  r = __builtin_fmaf(-n, 1.42860682030941723212e-6f, r);
+  float p = 1.98412698412698413e-4f;
+  p = __builtin_fmaf(p, r, 1.38888888888888889e-3f);
+  p = __builtin_fmaf(p, r, 8.33333333333333333e-3f);
+  p = __builtin_fmaf(p, r, 4.16666666666666667e-2f);
+  p = __builtin_fmaf(p, r, 1.66666666666666667e-1f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  float e = (p * 2.0f) * __int_as_float((ni - 1 + 127) << 23);
+  e = x < -86.5f ? 0.0f : e;
+  e = x > 89.0f ? __int_as_float(0x7f800000) : e;
+  return x != x ? x : e;
+}
+
 __device__ __forceinline__ float silu_mul(float g, float u) { return (g / (1.0f + dexp(-g))) * u; }
 
 // Cross-lane partner of stage S of a butterfly: a lane in the other half of its aligned 2S-lane group. DPP for

@@ -467,6 +467,215 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
   pp[2 + lane] = acc;
 }
 
+// Multi-position form of k_attn_tiles for the block step: one workgroup per (KV head g, split s, group of up to
+// kMqMaxPos consecutive positions of the block), one wave per tile of the split. The split's K and V tiles are read
+// once for the whole group and every (position, query head) unit of the group goes through the three steps of
+// k_attn_tiles: (1) scores (lane = position of the tile, the K row in registers) and tile maxima, (2) alpha, p and
+// the tile sum, then p.v (lane = dim, the V column in registers), (3) the in-order combine of the tiles into the
+// split's partial. The K row is needed only in (1) and the V column only from (2) on, so they share registers and
+// several units run side by side: two score chains, p of four units, four p.v chains. Queries, scores, p and p.v
+// go through LDS (a unit's score row becomes its p row, then its p.v row), and the V tile is moved into registers
+// through LDS in two halves; the small footprint keeps five workgroups on a compute unit. Position y of the block
+// sees the first len + y cache positions, so its valid rows differ per tile: rows at and past its tile length get
+// score -inf (p = 0) and V element +0, which is what k_attn_tiles' zeroed rows give; the partials are the same bit
+// for bit.
+constexpr int kMqMaxPos = 6;
+template <int G, int T>
+__global__ __launch_bounds__(T * 64) void k_attn_mq(const float* __restrict__ q, const uint16_t* __restrict__ kc,
+                                                   const uint16_t* __restrict__ vc, const int* __restrict__ lenp,
+                                                   int len_add, int max_len, float scale, int splits, int ny, int npw,
+                                                   float* __restrict__ part) {
+  constexpr int NU = kMqMaxPos * G;  // units of a group: unit u = position u / G, query head g * G + u % G
+  __shared__ __align__(16) float Vt[T][32 * 32];  // wave wt: half of its fp16 V tile, [32][64]
+  __shared__ __align__(16) float Sp[T][NU][64];    // wave wt: its scores, then p, then p.v, row = unit
+  __shared__ __align__(16) float Qs[NU][64];
+  __shared__ float Tm[NU][T], Al[NU][T], Ts[NU][T];
+  const int g = blockIdx.x / splits, s = blockIdx.x % splits;
+  const int lane = threadIdx.x & 63, wt = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: SGPRs
+  const int nh = gridDim.x / splits * G;
+  const int y0 = blockIdx.y * npw, yn = min(ny, y0 + npw) - y0;  // positions y0 .. y0 + yn - 1 of the block
+  const int units = yn * G;
+  const float NEG_INF = __int_as_float(0xff800000);
+  const uint16_t* K = kc + (size_t)g * max_len * 64;
+  const uint16_t* V = vc + (size_t)g * max_len * 64;
+  const int t0 = s * T, t = t0 + wt;
+  const int tl = min(t, max_len / 64 - 1);  // a tile past the end of the cache is never used by any position
+  // the group's queries and the first length, then the K row of this lane and the V tile in 8 pieces of 8 rows
+  for (int u = wt; u < units; u += T) Qs[u][lane] = q[((size_t)(y0 + u / G) * nh + g * G + u % G) * 64 + lane];
+  const int len0 = *lenp + len_add + y0;  // length seen by the group's first position; position y sees len0 + y
+  __builtin_amdgcn_sched_barrier(0);
+  Row8 kn;
+  kn.load(reinterpret_cast<const uint4*>(K + (size_t)(tl * 64 + lane) * 64));
+  Row8 vp;
+  {
+    const uint4* src = reinterpret_cast<const uint4*>(V + ((size_t)tl * 64 + (lane >> 3)) * 64 + (lane & 7) * 8);
+    vp.a = src[0 * 64]; vp.b = src[1 * 64]; vp.c = src[2 * 64]; vp.d = src[3 * 64];
+    vp.e = src[4 * 64]; vp.f = src[5 * 64]; vp.g = src[6 * 64]; vp.h = src[7 * 64];
+  }
+  if (t0 * 64 >= len0 + yn - 1) {  // no position of the group reaches this split
+    __builtin_amdgcn_s_waitcnt(0);
+    return;
+  }
+  uint4* const vt = reinterpret_cast<uint4*>(&Vt[wt][0]);  // row i = 8 uint4
+#pragma unroll
+  for (int e = 0; e < 4; e++) vt[(8 * e + (lane >> 3)) * 8 + (lane & 7)] = vp.at(e);  // rows 0..31
+  // valid rows of this wave's tile for unit u (0: the tile is past the position's length)
+  auto valid = [&](int u) { return max(0, min(64, len0 + u / G - t * 64)); };
+  float* const sp = &Sp[wt][0][0];
+  {
+    float kr[64];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const uint4 ke = kn.at(e);
+      const uint32_t wv[4] = {ke.x, ke.y, ke.z, ke.w};
+#pragma unroll
+      for (int j = 0; j < 8; j++) kr[8 * e + j] = h2f((uint16_t)(wv[j >> 1] >> (16 * (j & 1))));
+    }
+    __syncthreads();  // queries
+    // (1) scores: lane = position, chain over the 64 dims in order; the tile maximum. Two units at a time; the
+    // second of an odd count repeats the first and is not stored.
+    for (int k = 0; k < units; k += 2) {
+      const int kb = k + 1 < units ? k + 1 : k;
+      const int na = valid(k), nb = k + 1 < units ? valid(kb) : 0;
+      float sa = NEG_INF, sb = NEG_INF, ta = NEG_INF, tb = NEG_INF;
+      if (na > 0 || nb > 0) {
+        float da = 0.0f, db = 0.0f;
+#pragma unroll
+        for (int d4 = 0; d4 < 16; d4++) {
+          const float4 qa = *reinterpret_cast<const float4*>(&Qs[k][4 * d4]);
+          const float4 qb = *reinterpret_cast<const float4*>(&Qs[kb][4 * d4]);
+          da = __builtin_fmaf(qa.x, kr[4 * d4], da);
+          db = __builtin_fmaf(qb.x, kr[4 * d4], db);
+          da = __builtin_fmaf(qa.y, kr[4 * d4 + 1], da);
+          db = __builtin_fmaf(qb.y, kr[4 * d4 + 1], db);
+          da = __builtin_fmaf(qa.z, kr[4 * d4 + 2], da);
+          db = __builtin_fmaf(qb.z, kr[4 * d4 + 2], db);
+          da = __builtin_fmaf(qa.w, kr[4 * d4 + 3], da);
+          db = __builtin_fmaf(qb.w, kr[4 * d4 + 3], db);
+        }
+        sa = lane < na ? da * scale : NEG_INF;
+        sb = lane < nb ? db * scale : NEG_INF;
+        ta = group_max<64>(sa);
+        tb = group_max<64>(sb);
+      }
+      sp[k * 64 + lane] = sa;
+      if (k + 1 < units) sp[(k + 1) * 64 + lane] = sb;
+      if (lane == 0) {
+        Tm[k][wt] = ta;
+        if (k + 1 < units) Tm[k + 1][wt] = tb;
+      }
+    }
+  }
+  float vr[64];  // the V column of this lane, f32
+  {
+    const uint16_t* col = reinterpret_cast<const uint16_t*>(vt) + lane;
+#pragma unroll
+    for (int i = 0; i < 32; i++) vr[i] = h2f(col[i * 64]);
+    wave_lds_sync();  // the first half is read
+#pragma unroll
+    for (int e = 4; e < 8; e++) vt[(8 * (e - 4) + (lane >> 3)) * 8 + (lane & 7)] = vp.at(e);  // rows 32..63
+    wave_lds_sync();
+#pragma unroll
+    for (int i = 32; i < 64; i++) vr[i] = h2f(col[(i - 32) * 64]);
+  }
+  __syncthreads();  // tile maxima
+  // (2) lane u < units: m_prev, m and alpha of unit u for this tile
+  float mu = NEG_INF;
+  if (lane < units) {
+    float mprev = NEG_INF;
+#pragma unroll
+    for (int v = 0; v < T; v++)
+      if (v < wt) mprev = mprev > Tm[lane][v] ? mprev : Tm[lane][v];
+    const float tmax = Tm[lane][wt];
+    mu = mprev > tmax ? mprev : tmax;
+    if (valid(lane) > 0) Al[lane][wt] = dexp_sel(mprev - mu);
+  }
+  // p = exp(s - m) over the score rows and the tile sums, four units at a time (a unit whose tile is past its
+  // length gets a p row and sum that nothing reads)
+  for (int k0 = 0; k0 < units; k0 += 4) {
+    float pj[4], tj[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int k = min(k0 + j, units - 1);
+      const float m = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mu), k));
+      pj[j] = dexp_sel(sp[k * 64 + lane] - m);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) tj[j] = group_sum<64>(pj[j]);
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      if (k0 + j < units) {
+        sp[(k0 + j) * 64 + lane] = pj[j];
+        if (lane == 0) Ts[k0 + j][wt] = tj[j];
+      }
+    }
+  }
+  wave_lds_sync();  // this wave's p rows
+  // p.v: lane = dim, chain over the positions in order, the V elements of rows past the position's length as +0;
+  // four units at a time (past the last unit, the last unit's row again, not stored). Each result replaces its
+  // unit's p row (all of the row's reads come first: the result depends on them).
+  for (int k0 = 0; k0 < units; k0 += 4) {
+    int nv[4], row[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      row[j] = min(k0 + j, units - 1);
+      nv[j] = valid(row[j]);
+    }
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (nv[0] == 64 && nv[1] == 64 && nv[2] == 64 && nv[3] == 64) {
+#pragma unroll
+      for (int i0 = 0; i0 < 64; i0 += 4) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float4 p4 = *reinterpret_cast<const float4*>(&sp[row[j] * 64 + i0]);
+          acc[j] = __builtin_fmaf(p4.x, vr[i0], acc[j]);
+          acc[j] = __builtin_fmaf(p4.y, vr[i0 + 1], acc[j]);
+          acc[j] = __builtin_fmaf(p4.z, vr[i0 + 2], acc[j]);
+          acc[j] = __builtin_fmaf(p4.w, vr[i0 + 3], acc[j]);
+        }
+      }
+    } else {  // a tile the positions see in part (the last of the group's lengths)
+#pragma unroll
+      for (int i0 = 0; i0 < 64; i0 += 4) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          const float4 p4 = *reinterpret_cast<const float4*>(&sp[row[j] * 64 + i0]);
+          acc[j] = __builtin_fmaf(p4.x, i0 < nv[j] ? vr[i0] : 0.0f, acc[j]);
+          acc[j] = __builtin_fmaf(p4.y, i0 + 1 < nv[j] ? vr[i0 + 1] : 0.0f, acc[j]);
+          acc[j] = __builtin_fmaf(p4.z, i0 + 2 < nv[j] ? vr[i0 + 2] : 0.0f, acc[j]);
+          acc[j] = __builtin_fmaf(p4.w, i0 + 3 < nv[j] ? vr[i0 + 3] : 0.0f, acc[j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      if (k0 + j < units && nv[j] > 0) sp[(k0 + j) * 64 + lane] = acc[j];
+  }
+  __syncthreads();  // p.v, alpha and sums of every tile
+  // (3) the split's partial of each unit: l and acc over the used tiles in order
+  for (int k = wt; k < units; k += T) {
+    const int y = k / G, hh = k % G;
+    const int used = min(T, (len0 + y + 63) / 64 - t0);
+    if (used <= 0) continue;
+    float m = NEG_INF, l = 0.0f, acc = 0.0f;
+#pragma unroll
+    for (int v = 0; v < T; v++) {
+      if (v < used) {
+        const float a = Al[k][v];
+        l = __builtin_fmaf(l, a, Ts[k][v]);
+        acc = __builtin_fmaf(acc, a, Sp[v][k][lane]);
+        m = m > Tm[k][v] ? m : Tm[k][v];
+      }
+    }
+    float* pp = part + (((size_t)(y0 + y) * nh + g * G + hh) * splits + s) * 66;
+    if (lane == 0) {
+      pp[0] = m;
+      pp[1] = l;
+    }
+    pp[2 + lane] = acc;
+  }
+}
+
 // One wave per query head: M = max m_s; w_s = exp(m_s - M); den = fma chain of w_s * l_s; num_c = fma chain of
 // w_s * acc_sc, both over s = 0..used-1 in order; out_c = num_c / den. used <= splits <= 64.
 template <int SP>
@@ -1111,10 +1320,43 @@ static hipError_t attn_combine_dispatch(hipStream_t s, int heads, int tps, int m
   return hipGetLastError();
 }
 
+// Positions per workgroup of k_attn_mq: at most kMqMaxPos, and fewer when that brings the grid to about five
+// workgroups per compute unit (the LDS and register footprint allows five: 15 waves).
+static int mq_positions(int ny, int wgs) {
+  const int groups = std::min(ny, std::max(cdiv(ny, kMqMaxPos), cdiv(1280, wgs)));
+  return cdiv(ny, groups);
+}
+
+static bool attn_mq_dispatch(hipStream_t s, int G, int kvh, int tps, const float* q, const uint16_t* kc,
+                             const uint16_t* vc, const int* lenp, int len_add, int max_len, float scale, int ny,
+                             float* part) {
+  const int splits = attn_splits_for(max_len, tps);
+  if (G > 4 || tps > 4 || ny < 1 || splits > 64 || max_len % 64) return false;
+  const int npw = mq_positions(ny, kvh * splits);
+  const dim3 blocks(kvh * splits, cdiv(ny, npw));
+#define MQ_CASE(GG, TT)                                                                                           \
+  if (G == GG && tps == TT) {                                                                                     \
+    klaunch(k_attn_mq<GG, TT>, blocks, TT * 64, 0, s, q, kc, vc, lenp, len_add, max_len, scale, splits, ny,      \
+            npw, part);                                                                                           \
+    return true;                                                                                                  \
+  }
+  MQ_CASE(1, 1) MQ_CASE(2, 1) MQ_CASE(3, 1) MQ_CASE(4, 1)
+  MQ_CASE(1, 2) MQ_CASE(2, 2) MQ_CASE(3, 2) MQ_CASE(4, 2)
+  MQ_CASE(1, 3) MQ_CASE(2, 3) MQ_CASE(3, 3) MQ_CASE(4, 3)
+  MQ_CASE(1, 4) MQ_CASE(2, 4) MQ_CASE(3, 4) MQ_CASE(4, 4)
+#undef MQ_CASE
+  return false;
+}
+
 hipError_t launch_attn_batched(hipStream_t s, const LayerDev& L, const Dims& d, const int* lenp, int len_add, int ny,
                                const float* q, float* part, float* att) {
-  hipError_t e = attn_split_dispatch(s, d.heads / d.kv_heads, d.kv_heads, d.tps, q, L.k_cache, L.v_cache, lenp,
-                                     len_add, d.max_len, d.attn_mult, part, ny);
+  hipError_t e = hipSuccess;
+  if (attn_mq_dispatch(s, d.heads / d.kv_heads, d.kv_heads, d.tps, q, L.k_cache, L.v_cache, lenp, len_add,
+                       d.max_len, d.attn_mult, ny, part))
+    e = hipGetLastError();
+  else
+    e = attn_split_dispatch(s, d.heads / d.kv_heads, d.kv_heads, d.tps, q, L.k_cache, L.v_cache, lenp, len_add,
+                            d.max_len, d.attn_mult, part, ny);
   if (e != hipSuccess) return e;
   return attn_combine_dispatch(s, d.heads, d.tps, d.max_len, lenp, len_add, part, att, ny);
 }
