@@ -65,20 +65,59 @@ __device__ __forceinline__ void deq_fma(const DeqRows<DT, K, P>& w, const bool (
   }
 }
 
-// Canonical rmsnorm scale of the K floats at x (LDS): the sum of squares over 16-element chunks, chunk j in lane
-// j % 64, then the lane tree; r = 1 / sqrt(ss / K + eps). One wave.
-template <int K>
+// LDS layout of a staged activation row. Lane `sub` of a row reads whole weight chunks of x (16 floats for Q8_0,
+// 32 for Q4_0), so in a plain layout the lanes' 16-byte reads are 64 or 128 bytes apart and fall in the same banks.
+// The float4 slots of chunk j are therefore stored with their index xor-ed by sw(j) (slot q of chunk j at
+// NQ j + (q ^ sw(j))), which spreads the 8 or 16 lanes one LDS pass serves over distinct bank groups (32 or 64
+// banks). The values and the order they are used in do not change.
+template <int DT>
+__device__ __forceinline__ int xslot(int s) {
+  constexpr int NQ = Fmt<DT>::kElems / 4;  // float4 slots per chunk
+  if constexpr (NQ == 1) {
+    return s;
+  } else {
+    const int j = s / NQ, q = s % NQ;
+    const int sw = NQ == 4 ? ((j >> 1) ^ (j >> 3)) & 3 : (j ^ (j >> 3)) & 7;
+    return NQ * j + (q ^ sw);
+  }
+}
+
+// load_x over a row staged with xslot.
+template <int DT, int K>
+__device__ __forceinline__ void load_xs(XReg<DT, K>& xr, const float* x, int sub) {
+  using G = Geo<DT, K>;
+  constexpr int NQ = G::CE / 4;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
+#pragma unroll
+  for (int jj = 0; jj < G::NJ; jj++) {
+    const int j = sub + G::LPR * jj;
+    if (j < G::NCH) {
+#pragma unroll
+      for (int e = 0; e < NQ; e++) {
+        const float4 t = x4[xslot<DT>(NQ * j + e)];
+        xr.v[jj][4 * e] = t.x;
+        xr.v[jj][4 * e + 1] = t.y;
+        xr.v[jj][4 * e + 2] = t.z;
+        xr.v[jj][4 * e + 3] = t.w;
+      }
+    }
+  }
+}
+
+// Canonical rmsnorm scale of the K floats at x (LDS, staged with xslot): the sum of squares over 16-element chunks,
+// chunk j in lane j % 64, then the lane tree; r = 1 / sqrt(ss / K + eps). One wave.
+template <int DT, int K>
 __device__ __forceinline__ float wave_rms(const float* x, float eps, int lane) {
   constexpr int NCH = K / 16;
+  const float4* x4 = reinterpret_cast<const float4*>(x);
   float acc = 0.0f;
 #pragma unroll
   for (int jj = 0; jj < (NCH + 63) / 64; jj++) {
     const int j = lane + 64 * jj;
     if (j < NCH) {
-      const float4* p = reinterpret_cast<const float4*>(x + 16 * j);
 #pragma unroll
       for (int e = 0; e < 4; e++) {
-        const float4 t = p[e];
+        const float4 t = x4[xslot<DT>(4 * j + e)];
         acc = __builtin_fmaf(t.x, t.x, acc);
         acc = __builtin_fmaf(t.y, t.y, acc);
         acc = __builtin_fmaf(t.z, t.z, acc);
@@ -90,24 +129,35 @@ __device__ __forceinline__ float wave_rms(const float* x, float eps, int lane) {
   return 1.0f / sqrtf(ss / (float)K + eps);
 }
 
-// Stages positions [v0, v0 + n) of x ([*, K] rows, global) into xs ([kPfGroup][K], LDS); with lnw, each is then
-// normalised in place: xs = lnw * (x * r) (wave w normalises position w of the group). Ends with a barrier.
-template <int K>
+// Stages positions [v0, v0 + n) of x ([*, K] rows, global) into xs ([kPfGroup][K], LDS, layout xslot); with lnw,
+// each is then normalised in place: xs = lnw * (x * r) (wave w normalises position w of the group). Ends with a
+// barrier.
+template <int DT, int K>
 __device__ __forceinline__ void stage_group(const float* __restrict__ x, int v0, int n, const float* __restrict__ lnw,
                                             float eps, float (*xs)[K], float* rsv) {
+  constexpr int K4 = K / 4;
   const float4* src = reinterpret_cast<const float4*>(x + (size_t)v0 * K);
-  for (int i = threadIdx.x; i < n * K / 4; i += kPfNT) reinterpret_cast<float4*>(&xs[0][0])[i] = src[i];
+  for (int i = threadIdx.x; i < n * K4; i += kPfNT)
+    reinterpret_cast<float4*>(&xs[i / K4][0])[xslot<DT>(i % K4)] = src[i];
   __syncthreads();
   if (!lnw) return;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (wave < n) {
-    const float r = wave_rms<K>(&xs[wave][0], eps, lane);
+    const float r = wave_rms<DT, K>(&xs[wave][0], eps, lane);
     if (lane == 0) rsv[wave] = r;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < n * K; i += kPfNT) {
-    const int v = i / K, e = i % K;
-    xs[v][e] = lnw[e] * (xs[v][e] * rsv[v]);
+  for (int i = threadIdx.x; i < n * K4; i += kPfNT) {
+    const int v = i / K4, s = i % K4;
+    float4* p = reinterpret_cast<float4*>(&xs[v][0]) + xslot<DT>(s);
+    const float4 w = reinterpret_cast<const float4*>(lnw)[s];
+    const float r = rsv[v];
+    float4 t = *p;
+    t.x = w.x * (t.x * r);
+    t.y = w.y * (t.y * r);
+    t.z = w.z * (t.z * r);
+    t.w = w.w * (t.w * r);
+    *p = t;
   }
   __syncthreads();
 }
@@ -150,10 +200,10 @@ __global__ __launch_bounds__(kPfNT) void k_qkv_b(DMat m, const float* __restrict
     const int n = min(kPfGroup, nv - v0);
     __syncthreads();  // the previous group's activations are no longer read
     for (int i = threadIdx.x; i < n * 64; i += kPfNT) csv[i / 64][i % 64] = rope[(size_t)(pos0 + v0 + i / 64) * 64 + i % 64];
-    stage_group<K>(h, v0, n, lnw, eps, xs, rsv);
+    stage_group<DT, K>(h, v0, n, lnw, eps, xs, rsv);
     for (int v = 0; v < n; v++) {
       XReg<DT, K> xr;
-      load_x<DT, K>(xr, &xs[v][0], sub);
+      load_xs<DT, K>(xr, &xs[v][0], sub);
       float out[P];
       deq_fma<DT, K, P>(dw, ok, xr, sub, out);
       if (sub != 0) continue;
@@ -207,10 +257,10 @@ __global__ __launch_bounds__(kPfNT) void k_oproj_b(DMat m, const float* __restri
   for (int v0 = 0; v0 < nv; v0 += kPfGroup) {
     const int n = min(kPfGroup, nv - v0);
     __syncthreads();
-    stage_group<K>(att, v0, n, nullptr, 0.0f, xs, nullptr);
+    stage_group<DT, K>(att, v0, n, nullptr, 0.0f, xs, nullptr);
     for (int v = 0; v < n; v++) {
       XReg<DT, K> xr;
-      load_x<DT, K>(xr, &xs[v][0], sub);
+      load_xs<DT, K>(xr, &xs[v][0], sub);
       float out[P];
       deq_fma<DT, K, P>(dw, ok, xr, sub, out);
       if (sub != 0) continue;
@@ -353,12 +403,12 @@ __global__ __launch_bounds__(kPfNT) void k_moe_up_b(DMat gu, const float* __rest
     for (int i = threadIdx.x; i < n * K / 4; i += kPfNT) {
       const int c = i / (K / 4), w4 = i % (K / 4);
       const int vpos = nth_bit64(members, c0 + c);
-      reinterpret_cast<float4*>(&xs[c][0])[w4] = reinterpret_cast<const float4*>(xn + (size_t)vpos * K)[w4];
+      reinterpret_cast<float4*>(&xs[c][0])[xslot<DT>(w4)] = reinterpret_cast<const float4*>(xn + (size_t)vpos * K)[w4];
     }
     __syncthreads();
     for (int c = 0; c < n; c++) {
       XReg<DT, K> xr;
-      load_x<DT, K>(xr, &xs[c][0], sub);
+      load_xs<DT, K>(xr, &xs[c][0], sub);
       float out[P];
       deq_fma<DT, K, P>(dw, ok, xr, sub, out);
       if (sub != 0) continue;
@@ -404,13 +454,13 @@ __global__ __launch_bounds__(kPfNT) void k_moe_down_b(DMat dn, const float* __re
   for (int i = threadIdx.x; i < ne * K / 4; i += kPfNT) {
     const int c = i / (K / 4), w4 = i % (K / 4);
     const int vpos = nth_bit64(members, c);
-    reinterpret_cast<float4*>(&xs[c][0])[w4] =
+    reinterpret_cast<float4*>(&xs[c][0])[xslot<DT>(w4)] =
         reinterpret_cast<const float4*>(act + ((size_t)vpos * k + pl.rank[e][vpos]) * K)[w4];
   }
   __syncthreads();
   for (int c = 0; c < ne; c++) {
     XReg<DT, K> xr;
-    load_x<DT, K>(xr, &xs[c][0], sub);
+    load_xs<DT, K>(xr, &xs[c][0], sub);
     float out[P];
     deq_fma<DT, K, P>(dw, ok, xr, sub, out);
     if (sub != 0) continue;
