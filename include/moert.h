@@ -112,6 +112,16 @@ int moert_model_create_cached(const moert_config* cfg, const moert_model_weights
 int moert_cache_stats(moert_model* m, unsigned long long* hits, unsigned long long* copies);
 /* Empties the pool and zeroes the counters (ExpertCache::clear, rust/moe-rt/src/cache.rs:216-220). */
 int moert_cache_clear(moert_model* m);
+/* Copies into the free slots of the pool every expert not yet in it, in key order (key = layer * experts + expert),
+ * evicting nothing; stops when no slot is free. *copied = experts copied. Returns synchronised
+ * (ExpertCache::fill, rust/moe-rt/src/cache.rs:212-227). The hit/copy counters are not changed. */
+int moert_cache_fill(moert_model* m, int* copied);
+/* Brings experts[0..n) of `layer` into the pool ahead of a step (the expert-cache prefetch of the proposed
+ * moert_pool_prefetch; copy_expert on the copy stream, rust/moe-rt/src/motor/line.rs:423-439): one tick of the
+ * step's LRU rule (rust/moe-rt/tests/model.rs:380-412) over these keys, the records copied from the pinned store
+ * with hipMemcpyAsync on a side stream that the model stream waits for. Experts distinct, 1 <= n <= min(slots,
+ * experts). *copied = experts that were not in the pool. Returns synchronised; counters not changed. */
+int moert_cache_prefetch(moert_model* m, int layer, const int* experts, int n, int* copied);
 
 /* One token at the current position: logits of the next position (vocab floats, divided by logits_scaling),
  * the router decision of every layer (layers*top_k ids and weights, top-k order) and the greedy argmax.

@@ -302,7 +302,90 @@ struct moert_model {
     return MOERT_OK;
   }
 
+  // Expert records into pool slots decided on the host, between steps (ExpertCache::fill, rust/moe-rt/src/
+  // cache.rs:212-227, and a per-layer prefetch). The model stream is synchronised and the current copy of the slot
+  // tables read back; then for `keys` in order:
+  //  - prefetch (tick): one clock tick as a layer step's LRU decision makes it (lru_decide): keys already in the
+  //    pool are touched first (pinned for the tick); each other key takes the first free slot, else the least
+  //    recently used slot not touched at this tick (lowest index on ties);
+  //  - fill (!tick): a key not in the pool takes the first free slot, with last use 0; nothing is evicted and the
+  //    fill stops when no slot is free.
+  // The records are copied with hipMemcpyAsync from the pinned store on a side stream, the model stream waits for
+  // them, the tables and the clock are written back, and the call returns synchronised. The hit and copy counters
+  // count the requests of decode steps only and are left alone.
+  int cache_load(const int* keys, int n, bool tick, int* copied) {
+    const int S = cache.slots;
+    CHECK_HIP(hipStreamSynchronize(stream));
+    int cur = 0, clock = 0;
+    std::vector<int> skey(S), slast(S);
+    CHECK_HIP(hipMemcpy(&cur, cache.cur, 4, hipMemcpyDeviceToHost));
+    CHECK_HIP(hipMemcpy(&clock, cache.clock + cur, 4, hipMemcpyDeviceToHost));
+    CHECK_HIP(hipMemcpy(skey.data(), cache.slot_key + (size_t)cur * S, (size_t)S * 4, hipMemcpyDeviceToHost));
+    CHECK_HIP(hipMemcpy(slast.data(), cache.slot_last + (size_t)cur * S, (size_t)S * 4, hipMemcpyDeviceToHost));
+    std::vector<std::pair<int, int>> loads;  // (slot, key)
+    auto where = [&](int key) {
+      for (int i = 0; i < S; i++)
+        if (skey[i] == key) return i;
+      return -1;
+    };
+    if (tick) {
+      clock++;
+      for (int j = 0; j < n; j++) {
+        const int i = where(keys[j]);
+        if (i >= 0) slast[i] = clock;
+      }
+    }
+    for (int j = 0; j < n; j++) {
+      if (where(keys[j]) >= 0) continue;
+      int v = -1;
+      for (int i = 0; i < S && v < 0; i++)
+        if (skey[i] < 0) v = i;
+      if (v < 0 && tick)
+        for (int i = 0; i < S; i++)
+          if (slast[i] < clock && (v < 0 || slast[i] < slast[v])) v = i;
+      if (v < 0) {
+        if (!tick) break;  // fill: the pool is full
+        continue;          // (cannot happen: n <= slots)
+      }
+      skey[v] = keys[j];
+      slast[v] = tick ? clock : 0;
+      loads.push_back({v, keys[j]});
+    }
+    if (!loads.empty()) {
+      if (!side) CHECK_HIP(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
+      if (!side_done) CHECK_HIP(hipEventCreateWithFlags(&side_done, hipEventDisableTiming));
+      const size_t dn_d = cache.record_bytes - cache.gu_q - cache.gu_d - cache.dn_q;
+      for (const auto& ld : loads) {
+        const uint8_t* r = (const uint8_t*)host_store + (size_t)ld.second * cache.record_bytes;
+        const size_t v = (size_t)ld.first;
+        CHECK_HIP(hipMemcpyAsync((void*)(cache.pool_gu.q + v * cache.gu_q), r, cache.gu_q, hipMemcpyHostToDevice, side));
+        if (cache.gu_d)
+          CHECK_HIP(hipMemcpyAsync((void*)((const uint8_t*)cache.pool_gu.d + v * cache.gu_d), r + cache.gu_q, cache.gu_d,
+                                   hipMemcpyHostToDevice, side));
+        r += cache.gu_q + cache.gu_d;
+        CHECK_HIP(hipMemcpyAsync((void*)(cache.pool_dn.q + v * cache.dn_q), r, cache.dn_q, hipMemcpyHostToDevice, side));
+        if (dn_d)
+          CHECK_HIP(hipMemcpyAsync((void*)((const uint8_t*)cache.pool_dn.d + v * dn_d), r + cache.dn_q, dn_d,
+                                   hipMemcpyHostToDevice, side));
+      }
+      CHECK_HIP(hipEventRecord(side_done, side));
+      CHECK_HIP(hipStreamWaitEvent(stream, side_done, 0));
+    }
+    CHECK_HIP(hipMemcpyAsync(cache.slot_key + (size_t)cur * S, skey.data(), (size_t)S * 4, hipMemcpyHostToDevice, stream));
+    CHECK_HIP(hipMemcpyAsync(cache.slot_last + (size_t)cur * S, slast.data(), (size_t)S * 4, hipMemcpyHostToDevice,
+                             stream));
+    CHECK_HIP(hipMemcpyAsync(cache.clock + cur, &clock, 4, hipMemcpyHostToDevice, stream));
+    CHECK_HIP(hipStreamSynchronize(stream));
+    if (copied) *copied = (int)loads.size();
+    return MOERT_OK;
+  }
+  hipStream_t side = nullptr;  // copy stream of cache_load
+  hipEvent_t side_done = nullptr;
+
   ~moert_model() {
+    if (side) (void)hipStreamSynchronize(side);
+    if (side_done) (void)hipEventDestroy(side_done);
+    if (side) (void)hipStreamDestroy(side);
     if (stream) (void)hipStreamSynchronize(stream);
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
@@ -922,6 +1005,32 @@ int moert_cache_clear(moert_model* m) {
   MODEL_OK(m);
   CHECK_CFG(m->cached, "model has no expert cache");
   MTRY(m, m->cache_clear());
+  return MOERT_OK;
+}
+
+int moert_cache_fill(moert_model* m, int* copied) {
+  MODEL_OK(m);
+  CHECK_CFG(m->cached, "model has no expert cache");
+  std::vector<int> keys((size_t)m->cfg.layers * m->cfg.experts);
+  for (size_t i = 0; i < keys.size(); i++) keys[i] = (int)i;
+  MTRY(m, m->cache_load(keys.data(), (int)keys.size(), false, copied));
+  return MOERT_OK;
+}
+
+int moert_cache_prefetch(moert_model* m, int layer, const int* experts, int n, int* copied) {
+  MODEL_OK(m);
+  CHECK_CFG(m->cached, "model has no expert cache");
+  CHECK_CFG(layer >= 0 && layer < m->cfg.layers, "layer %d outside [0, %d)", layer, m->cfg.layers);
+  CHECK_CFG(experts && n >= 1 && n <= m->cache.slots && n <= m->cfg.experts,
+            "prefetch of %d experts: between 1 and min(slots %d, experts %d)", n, m->cache.slots, m->cfg.experts);
+  std::vector<int> keys(n);
+  for (int j = 0; j < n; j++) {
+    CHECK_CFG(experts[j] >= 0 && experts[j] < m->cfg.experts, "expert %d outside [0, %d)", experts[j],
+              m->cfg.experts);
+    for (int i = 0; i < j; i++) CHECK_CFG(experts[i] != experts[j], "expert %d requested twice", experts[j]);
+    keys[j] = layer * m->cfg.experts + experts[j];
+  }
+  MTRY(m, m->cache_load(keys.data(), n, true, copied));
   return MOERT_OK;
 }
 

@@ -86,6 +86,8 @@ def lib() -> ctypes.CDLL:
                                               i, i, ctypes.POINTER(vp)]),
             "moert_cache_stats": (i, [vp, ctypes.POINTER(ctypes.c_ulonglong), ctypes.POINTER(ctypes.c_ulonglong)]),
             "moert_cache_clear": (i, [vp]),
+            "moert_cache_fill": (i, [vp, ctypes.POINTER(ctypes.c_int)]),
+            "moert_cache_prefetch": (i, [vp, i, vp, i, ctypes.POINTER(ctypes.c_int)]),
             "moert_decode_step": (i, [vp, i, vp, vp, vp, ip]),
             "moert_generate": (i, [vp, vp, i, i, vp, vp]),
             "moert_step_batched": (i, [vp, vp, i, vp, ip]),
@@ -132,7 +134,8 @@ def lib() -> ctypes.CDLL:
 
 
 EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moert_model_destroy",
-            "moert_model_create_cached", "moert_cache_stats", "moert_cache_clear",
+            "moert_model_create_cached", "moert_cache_stats", "moert_cache_clear", "moert_cache_fill",
+            "moert_cache_prefetch",
             "moert_decode_step", "moert_generate", "moert_step_batched", "moert_prefill", "moert_reset_sequence",
             "moert_kv_prefill_fp16",
             "moert_set_position", "moert_get_position", "moert_read_kv_fp16", "moert_read_hidden",
@@ -329,6 +332,21 @@ class GpuModel:
 
     def cache_clear(self):
         check(lib().moert_cache_clear(self.h))
+
+    def cache_fill(self):
+        """Copies every expert not yet in the pool into its free slots, in key order, evicting nothing
+        (ExpertCache::fill); returns the number copied."""
+        n = ctypes.c_int(0)
+        check(lib().moert_cache_fill(self.h, ctypes.byref(n)))
+        return n.value
+
+    def cache_prefetch(self, layer, experts):
+        """Brings `experts` of `layer` into the pool ahead of a step (one tick of the LRU rule); returns the
+        number that were not in the pool."""
+        e = np.ascontiguousarray(experts, np.int32)
+        n = ctypes.c_int(0)
+        check(lib().moert_cache_prefetch(self.h, int(layer), ptr(e), len(e), ctypes.byref(n)))
+        return n.value
 
     def close(self):
         if self.h:

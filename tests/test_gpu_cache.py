@@ -120,3 +120,71 @@ def test_granite_3b_q4_0_quarter_pool_greedy_decode_equals_the_resident_model(gp
     assert cac.cache_stats() == (hits, copies)
     assert hits > 0 and copies > 0
     cac.close()
+
+
+@pytest.mark.parametrize("wdtype,slots", [(moert.Q4_0, 6), (moert.Q8_0, 8)])
+def test_prefetch_of_a_steps_routes_makes_that_step_all_hits(gpu, wdtype, slots):
+    """Before each step, every layer's routed experts (taken from the resident model) are prefetched: the step then
+    copies nothing and hits k per layer, and its outputs stay those of the resident model. A prefetch counts no
+    requests, so the counters grow by the steps' hits only."""
+    cfg = moert.Config(**TINY8)
+    m = moert.SynthModel(cfg, seed=16, wdtype=wdtype, embed_dtype=moert.F32, std=0.1, zipf_s=1.1)
+    res = moert.GpuModel(m, 64, attn_splits=4)
+    cac = moert.GpuModel(m, 64, attn_splits=4, cache_slots=slots)
+    toks = np.random.default_rng(31).integers(0, cfg.vocab, 20)
+    copied_total = 0
+    for t, tok in enumerate(toks):
+        say(f"prefetch dtype={wdtype} slots={slots} pos={t}")
+        lg, ids, w, am = res.step(int(tok))
+        for l in range(cfg.layers):
+            copied_total += cac.cache_prefetch(l, ids[l])
+        before = cac.cache_stats()
+        clg, cids, cw, cam = cac.step(int(tok))
+        after = cac.cache_stats()
+        assert after[1] == before[1], t
+        assert after[0] - before[0] == cfg.layers * cfg.top_k, t
+        assert bits_equal(lg, clg) and np.array_equal(ids, cids) and bits_equal(w, cw) and am == cam, t
+    assert copied_total > 0
+    hits, copies = cac.cache_stats()
+    assert (hits, copies) == (len(toks) * cfg.layers * cfg.top_k, 0)
+    # refusals: a repeated expert, more experts than slots, a layer out of range, a model without a cache
+    with pytest.raises(moert.MoertError):
+        cac.cache_prefetch(0, [1, 1])
+    with pytest.raises(moert.MoertError):
+        cac.cache_prefetch(0, list(range(slots + 1)))
+    with pytest.raises(moert.MoertError):
+        cac.cache_prefetch(cfg.layers, [0])
+    with pytest.raises(moert.MoertError):
+        res.cache_prefetch(0, [0])
+    res.close()
+    cac.close()
+
+
+@pytest.mark.parametrize("slots", [24, 5])
+def test_fill_puts_missing_experts_into_free_slots_in_key_order(gpu, slots):
+    """ExpertCache::fill (cache.rs:212-227): with room for every key (24 = 3 layers x 8 experts) the fill copies all
+    of them and later steps copy nothing; with 5 slots it copies keys 0..4 and stops. A second fill copies nothing.
+    Outputs stay the resident model's either way."""
+    cfg = moert.Config(**TINY8)
+    m = moert.SynthModel(cfg, seed=17, wdtype=moert.Q4_0, embed_dtype=moert.F32, std=0.1, zipf_s=1.1)
+    res = moert.GpuModel(m, 64, attn_splits=4)
+    cac = moert.GpuModel(m, 64, attn_splits=4, cache_slots=slots)
+    say(f"fill slots={slots}")
+    assert cac.cache_fill() == min(slots, cfg.layers * cfg.experts)
+    assert cac.cache_fill() == 0
+    assert cac.cache_stats() == (0, 0)
+    toks = np.random.default_rng(32).integers(0, cfg.vocab, 16)
+    for t, tok in enumerate(toks):
+        lg, ids, w, am = res.step(int(tok))
+        clg, cids, cw, cam = cac.step(int(tok))
+        assert bits_equal(lg, clg) and np.array_equal(ids, cids) and bits_equal(w, cw) and am == cam, t
+    hits, copies = cac.cache_stats()
+    assert hits + copies == len(toks) * cfg.layers * cfg.top_k
+    if slots == 24:
+        assert copies == 0
+    cac.cache_clear()
+    assert cac.cache_fill() == min(slots, cfg.layers * cfg.experts)
+    with pytest.raises(moert.MoertError):
+        res.cache_fill()
+    res.close()
+    cac.close()
