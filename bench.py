@@ -160,6 +160,12 @@ def expert_cache(cfg, seed, steps, frac=0.25):
     g.generate(forced, 1)
     fwall = time.perf_counter() - t0
     fhits, fcopies = g.cache_stats()
+    # the empty pool filled from the host between steps (moert_cache_fill: each slot's record copied with
+    # hipMemcpyAsync on a side stream, host-timed including the table read-back and write-back)
+    g.cache_clear()
+    t0 = time.perf_counter()
+    filled = g.cache_fill()
+    fill_s = time.perf_counter() - t0
     g.close()
     probe_bytes = 256 << 20
     pk, pm = moert.h2d_probe(probe_bytes, 4)
@@ -178,10 +184,12 @@ def expert_cache(cfg, seed, steps, frac=0.25):
                              "pcie_gbs_end_to_end": round(fcopies * record / fwall / 1e9, 2)},
            "h2d_probe": {"bytes": probe_bytes, "kernel_copy_gbs": round(probe_bytes / (pk * 1e-6) / 1e9, 2),
                          "hipmemcpy_gbs": round(probe_bytes / (pm * 1e-6) / 1e9, 2)},
+           "fill": {"experts": filled, "bytes": filled * record, "ms": round(fill_s * 1e3, 2),
+                    "gbs": round(filled * record / fill_s / 1e9, 2)},
            "resident_tok_s": round(1e3 / res_ms, 2)}
     log(f"expert cache {slots}/{cfg.layers * cfg.experts} slots: {tok_s:.1f} tok/s, hit rate {out['hit_rate']:.3f}, "
         f"{out['copied_bytes_per_token'] / 1e6:.1f} MB copied per token; resident {out['resident_tok_s']} tok/s; "
-        f"forced tokens {out['forced_tokens']}")
+        f"forced tokens {out['forced_tokens']}; fill {out['fill']}")
     return out
 
 

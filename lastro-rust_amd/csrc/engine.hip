@@ -355,18 +355,24 @@ struct moert_model {
       if (!side) CHECK_HIP(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
       if (!side_done) CHECK_HIP(hipEventCreateWithFlags(&side_done, hipEventDisableTiming));
       const size_t dn_d = cache.record_bytes - cache.gu_q - cache.gu_d - cache.dn_q;
-      for (const auto& ld : loads) {
-        const uint8_t* r = (const uint8_t*)host_store + (size_t)ld.second * cache.record_bytes;
-        const size_t v = (size_t)ld.first;
-        CHECK_HIP(hipMemcpyAsync((void*)(cache.pool_gu.q + v * cache.gu_q), r, cache.gu_q, hipMemcpyHostToDevice, side));
-        if (cache.gu_d)
-          CHECK_HIP(hipMemcpyAsync((void*)((const uint8_t*)cache.pool_gu.d + v * cache.gu_d), r + cache.gu_q, cache.gu_d,
-                                   hipMemcpyHostToDevice, side));
+      // a run of loads with consecutive slots and consecutive keys is one strided copy per piece: the records sit
+      // record_bytes apart in the store, and each piece's slots are contiguous in its pool plane
+      for (size_t a = 0; a < loads.size();) {
+        size_t b = a + 1;
+        while (b < loads.size() && loads[b].first == loads[b - 1].first + 1 &&
+               loads[b].second == loads[b - 1].second + 1)
+          b++;
+        const uint8_t* r = (const uint8_t*)host_store + (size_t)loads[a].second * cache.record_bytes;
+        const size_t v = (size_t)loads[a].first, rows = b - a, rb = cache.record_bytes;
+        auto piece = [&](const uint8_t* dst, const uint8_t* src, size_t bytes) -> hipError_t {
+          return hipMemcpy2DAsync((void*)dst, bytes, src, rb, bytes, rows, hipMemcpyHostToDevice, side);
+        };
+        CHECK_HIP(piece(cache.pool_gu.q + v * cache.gu_q, r, cache.gu_q));
+        if (cache.gu_d) CHECK_HIP(piece((const uint8_t*)cache.pool_gu.d + v * cache.gu_d, r + cache.gu_q, cache.gu_d));
         r += cache.gu_q + cache.gu_d;
-        CHECK_HIP(hipMemcpyAsync((void*)(cache.pool_dn.q + v * cache.dn_q), r, cache.dn_q, hipMemcpyHostToDevice, side));
-        if (dn_d)
-          CHECK_HIP(hipMemcpyAsync((void*)((const uint8_t*)cache.pool_dn.d + v * dn_d), r + cache.dn_q, dn_d,
-                                   hipMemcpyHostToDevice, side));
+        CHECK_HIP(piece(cache.pool_dn.q + v * cache.dn_q, r, cache.dn_q));
+        if (dn_d) CHECK_HIP(piece((const uint8_t*)cache.pool_dn.d + v * dn_d, r + cache.dn_q, dn_d));
+        a = b;
       }
       CHECK_HIP(hipEventRecord(side_done, side));
       CHECK_HIP(hipStreamWaitEvent(stream, side_done, 0));
