@@ -167,6 +167,11 @@ int moert_read_kv_fp16(moert_model* m, int layer, uint16_t* k, uint16_t* v, int 
 /* Hidden state after the last step (hidden floats, before the final norm). */
 int moert_read_hidden(moert_model* m, float* h);
 
+/* Logits of the last step (vocab floats, divided by logits_scaling), e.g. after moert_generate. Replaces
+ * Dense::read_logits / CudaBackend::read_logits (rust/moe-rt/src/cuda_dense.rs:446-459,
+ * rust/moe-rt/src/cuda_backend.rs:629-633). */
+int moert_read_logits(moert_model* m, float* logits);
+
 /* Times `iters` graph replays of the decode step (after `warmup`) with HIP events on the model's stream.
  * ms_per_step receives the mean. The position advances by warmup + iters. */
 int moert_time_steps(moert_model* m, int warmup, int iters, double* ms_per_step);

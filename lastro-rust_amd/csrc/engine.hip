@@ -308,8 +308,9 @@ struct moert_model {
   //  - prefetch (tick): one clock tick as a layer step's LRU decision makes it (lru_decide): keys already in the
   //    pool are touched first (pinned for the tick); each other key takes the first free slot, else the least
   //    recently used slot not touched at this tick (lowest index on ties);
-  //  - fill (!tick): a key not in the pool takes the first free slot, with last use 0; nothing is evicted and the
-  //    fill stops when no slot is free.
+  //  - fill (!tick): a key not in the pool takes the first free slot, stamped with the current clock (not advanced),
+  //    as copy_on_compute stamps last_use: self.clock (rust/moe-rt/src/cache/core.rs:366-377); nothing is evicted
+  //    and the fill stops when no slot is free.
   // The records are copied with hipMemcpyAsync from the pinned store on a side stream, the model stream waits for
   // them, the tables and the clock are written back, and the call returns synchronised. The hit and copy counters
   // count the requests of decode steps only and are left alone.
@@ -348,7 +349,7 @@ struct moert_model {
         continue;          // (cannot happen: n <= slots)
       }
       skey[v] = keys[j];
-      slast[v] = tick ? clock : 0;
+      slast[v] = clock;
       loads.push_back({v, keys[j]});
     }
     if (!loads.empty()) {
@@ -924,6 +925,14 @@ int moert_read_kv_fp16(moert_model* m, int layer, uint16_t* k, uint16_t* v, int 
 int moert_read_hidden(moert_model* m, float* h) {
   MODEL_OK(m);
   MTRY(m, model_copy_out(m, h, m->b.h, (size_t)m->cfg.hidden * 4));
+  MTRY(m, model_sync(m));
+  return MOERT_OK;
+}
+
+int moert_read_logits(moert_model* m, float* logits) {
+  MODEL_OK(m);
+  CHECK_CFG(logits, "null output");
+  MTRY(m, model_copy_out(m, logits, m->b.logits, (size_t)m->cfg.vocab * 4));
   MTRY(m, model_sync(m));
   return MOERT_OK;
 }

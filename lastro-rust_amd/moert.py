@@ -98,6 +98,7 @@ def lib() -> ctypes.CDLL:
             "moert_get_position": (i, [vp, ip]),
             "moert_read_kv_fp16": (i, [vp, i, vp, vp, i]),
             "moert_read_hidden": (i, [vp, vp]),
+            "moert_read_logits": (i, [vp, vp]),
             "moert_time_steps": (i, [vp, i, i, ctypes.POINTER(ctypes.c_double)]),
             "moert_time_kernel": (i, [vp, i, i, ctypes.POINTER(ctypes.c_double), ip]),
             "moert_block_create": (i, [i, i, i, i, ctypes.POINTER(moert_tensor), vp, ctypes.POINTER(moert_tensor),
@@ -138,7 +139,7 @@ EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moer
             "moert_cache_prefetch",
             "moert_decode_step", "moert_generate", "moert_step_batched", "moert_prefill", "moert_reset_sequence",
             "moert_kv_prefill_fp16",
-            "moert_set_position", "moert_get_position", "moert_read_kv_fp16", "moert_read_hidden",
+            "moert_set_position", "moert_get_position", "moert_read_kv_fp16", "moert_read_hidden", "moert_read_logits",
             "moert_time_steps", "moert_time_kernel", "moert_block_create", "moert_block_destroy",
             "moert_block_forward", "moert_block_time", "moert_block_forward_batched",
             "moert_block_experts_in_step", "moert_block_time_batched", "moert_router_topk", "moert_argmax", "moert_gemv",
@@ -420,6 +421,12 @@ class GpuModel:
     def hidden(self) -> np.ndarray:
         out = np.empty(self.cfg.hidden, np.float32)
         check(lib().moert_read_hidden(self.h, ptr(out)))
+        return out
+
+    def read_logits(self) -> np.ndarray:
+        """Logits of the last step (Dense::read_logits)."""
+        out = np.empty(self.cfg.vocab, np.float32)
+        check(lib().moert_read_logits(self.h, ptr(out)))
         return out
 
     def time_steps(self, warmup: int, iters: int) -> float:

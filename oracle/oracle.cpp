@@ -775,46 +775,109 @@ void orc_moe_block_batched(int hidden, int inter, int experts, int k, const moer
 // is resident is touched first (pinned for the tick); then, in top-k order, a resident key is a hit, and a missing
 // key takes the first free slot, else the slot with the oldest last use among those not used in this tick (lowest
 // index on ties), else goes to the CPU. out = {hits, copies, cpu}.
+struct orc_lru {
+  int layers, experts, slots;
+  std::vector<int> skey;                // key held by each slot, -1 when free
+  std::vector<unsigned long long> last; // clock of each slot's last use
+  std::vector<int> where;               // slot of each key, -1 when not in the pool
+  unsigned long long clock = 0, hits = 0, copies = 0, cpu = 0;
+
+  // One tick over the keys of one layer step (or one prefetch): requested keys already in the pool are touched
+  // first; then each missing key takes the first free slot, else the least recently used slot not touched at this
+  // tick (lowest index on ties), else it is left out (served by the CPU). Counted in hits / copies / cpu only when
+  // `counted` (a decode step's request, not a prefetch).
+  void tick(int layer, const int* ids, int n, bool counted, int* copied) {
+    clock++;
+    for (int j = 0; j < n; j++) {
+      const int sl = where[(size_t)layer * experts + ids[j]];
+      if (sl >= 0) last[sl] = clock;
+    }
+    int nc = 0;
+    for (int j = 0; j < n; j++) {
+      const int key = layer * experts + ids[j];
+      if (where[key] >= 0) {
+        if (counted) hits++;
+        continue;
+      }
+      int v = -1;
+      for (int i = 0; i < slots && v < 0; i++)
+        if (skey[i] < 0) v = i;
+      if (v < 0)
+        for (int i = 0; i < slots; i++)
+          if (last[i] < clock && (v < 0 || last[i] < last[v])) v = i;
+      if (v < 0) {
+        if (counted) cpu++;
+        continue;
+      }
+      if (skey[v] >= 0) where[skey[v]] = -1;
+      skey[v] = key;
+      last[v] = clock;
+      where[key] = v;
+      nc++;
+      if (counted) copies++;
+    }
+    if (copied) *copied = nc;
+  }
+};
+
+orc_lru* orc_lru_create(int layers, int experts, int slots) {
+  if (layers < 1 || experts < 1 || slots < 1) return nullptr;
+  orc_lru* c = new orc_lru;
+  c->layers = layers;
+  c->experts = experts;
+  c->slots = slots;
+  c->skey.assign(slots, -1);
+  c->last.assign(slots, 0);
+  c->where.assign((size_t)layers * experts, -1);
+  return c;
+}
+
+void orc_lru_destroy(orc_lru* c) { delete c; }
+
+void orc_lru_step_layer(orc_lru* c, int layer, const int* ids, int k) { c->tick(layer, ids, k, true, nullptr); }
+
+int orc_lru_prefetch(orc_lru* c, int layer, const int* ids, int n) {
+  int copied = 0;
+  c->tick(layer, ids, n, false, &copied);
+  return copied;
+}
+
+// ExpertCache::fill (rust/moe-rt/src/cache.rs:212-227): in key order, every key not in the pool takes the first free
+// slot, stamped with the current clock (copy_on_compute, rust/moe-rt/src/cache/core.rs:366-377); stops when no slot
+// is free. The clock does not advance and nothing is counted.
+int orc_lru_fill(orc_lru* c) {
+  int copied = 0;
+  for (int key = 0; key < c->layers * c->experts; key++) {
+    if (c->where[key] >= 0) continue;
+    int v = -1;
+    for (int i = 0; i < c->slots && v < 0; i++)
+      if (c->skey[i] < 0) v = i;
+    if (v < 0) break;
+    c->skey[v] = key;
+    c->last[v] = c->clock;
+    c->where[key] = v;
+    copied++;
+  }
+  return copied;
+}
+
+void orc_lru_stats(const orc_lru* c, unsigned long long* out) {
+  out[0] = c->hits;
+  out[1] = c->copies;
+  out[2] = c->cpu;
+}
+
+void orc_lru_slots(const orc_lru* c, int* keys) {
+  for (int i = 0; i < c->slots; i++) keys[i] = c->skey[i];
+}
+
 void orc_lru_replay(const int* routes, int steps, int layers, int k, int experts, int slots,
                     unsigned long long* out) {
-  std::vector<int> skey(slots, -1);
-  std::vector<unsigned long long> last(slots, 0);
-  std::vector<int> where((size_t)layers * experts, -1);
-  unsigned long long clock = 0, hits = 0, copies = 0, cpu = 0;
+  orc_lru* c = orc_lru_create(layers, experts, slots);
   for (int st = 0; st < steps; st++)
-    for (int l = 0; l < layers; l++) {
-      clock++;
-      const int* r = routes + ((size_t)st * layers + l) * k;
-      for (int j = 0; j < k; j++) {
-        int sl = where[(size_t)l * experts + r[j]];
-        if (sl >= 0) last[sl] = clock;
-      }
-      for (int j = 0; j < k; j++) {
-        const int key = l * experts + r[j];
-        if (where[key] >= 0) {
-          hits++;
-          continue;
-        }
-        int v = -1;
-        for (int i = 0; i < slots && v < 0; i++)
-          if (skey[i] < 0) v = i;
-        if (v < 0)
-          for (int i = 0; i < slots; i++)
-            if (last[i] < clock && (v < 0 || last[i] < last[v])) v = i;
-        if (v < 0) {
-          cpu++;
-          continue;
-        }
-        if (skey[v] >= 0) where[skey[v]] = -1;
-        skey[v] = key;
-        last[v] = clock;
-        where[key] = v;
-        copies++;
-      }
-    }
-  out[0] = hits;
-  out[1] = copies;
-  out[2] = cpu;
+    for (int l = 0; l < layers; l++) orc_lru_step_layer(c, l, routes + ((size_t)st * layers + l) * k, k);
+  orc_lru_stats(c, out);
+  orc_lru_destroy(c);
 }
 
 struct orc_session {

@@ -82,6 +82,19 @@ void orc_moe_block_batched(int hidden, int inter, int experts, int k, const moer
 void orc_lru_replay(const int* routes, int steps, int layers, int k, int experts, int slots,
                     unsigned long long* out);
 
+/* The same cache as a state machine, for traces that mix decode steps with fills and prefetches:
+ * step_layer = one counted tick over a layer's routed ids; prefetch = one uncounted tick over `ids` (returns the
+ * number copied); fill = ExpertCache::fill (free slots in key order, stamped with the current clock, no tick;
+ * returns the number copied); slots = the key held by each slot (-1 free). */
+typedef struct orc_lru orc_lru;
+orc_lru* orc_lru_create(int layers, int experts, int slots);
+void orc_lru_destroy(orc_lru* c);
+void orc_lru_step_layer(orc_lru* c, int layer, const int* ids, int k);
+int orc_lru_prefetch(orc_lru* c, int layer, const int* ids, int n);
+int orc_lru_fill(orc_lru* c);
+void orc_lru_stats(const orc_lru* c, unsigned long long* out);
+void orc_lru_slots(const orc_lru* c, int* keys);
+
 /* CpuSession. */
 int orc_session_create(const moert_config* cfg, const moert_model_weights* w, int max_len, int attn_splits,
                        int threads, orc_session** out);

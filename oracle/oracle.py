@@ -51,6 +51,13 @@ def lib() -> ctypes.CDLL:
             "orc_experts_grouped": (None, [i, i, i, i, vp, vp, vp, vp, vp, vp, i]),
             "orc_moe_block_batched": (None, [i, i, i, i, vp, vp, vp, vp, i, vp, vp, vp, vp, i]),
             "orc_lru_replay": (None, [vp, i, i, i, i, i, vp]),
+            "orc_lru_create": (vp, [i, i, i]),
+            "orc_lru_destroy": (None, [vp]),
+            "orc_lru_step_layer": (None, [vp, i, vp, i]),
+            "orc_lru_prefetch": (i, [vp, i, vp, i]),
+            "orc_lru_fill": (i, [vp]),
+            "orc_lru_stats": (None, [vp, vp]),
+            "orc_lru_slots": (None, [vp, vp]),
             "orc_session_create": (i, [vp, vp, i, i, i, ctypes.POINTER(vp)]),
             "orc_session_destroy": (None, [vp]),
             "orc_session_step": (i, [vp, i, vp, vp, vp, vp]),
@@ -275,6 +282,83 @@ def lru_reference(routes, experts, cap):
     return hits, copies, cpu
 
 
+class Lru:
+    """The LRU expert cache as a state machine (orc_lru): decode-step layers (counted), prefetch ticks and fills
+    (uncounted), for traces that mix them."""
+
+    def __init__(self, layers, experts, slots):
+        self.layers, self.experts, self.slots = layers, experts, slots
+        self.h = lib().orc_lru_create(layers, experts, slots)
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().orc_lru_destroy(self.h)
+            self.h = None
+
+    def step(self, routes):
+        """One decode step: routes [layers, k]."""
+        r = np.ascontiguousarray(routes, np.int32)
+        for l in range(r.shape[0]):
+            lib().orc_lru_step_layer(self.h, l, _p(r[l]), r.shape[1])
+
+    def prefetch(self, layer, ids):
+        a = np.ascontiguousarray(ids, np.int32)
+        return int(lib().orc_lru_prefetch(self.h, layer, _p(a), a.size))
+
+    def fill(self):
+        return int(lib().orc_lru_fill(self.h))
+
+    def stats(self):
+        out = np.zeros(3, np.uint64)
+        lib().orc_lru_stats(self.h, _p(out))
+        return tuple(int(v) for v in out)
+
+    def slot_keys(self):
+        out = np.empty(self.slots, np.int32)
+        lib().orc_lru_slots(self.h, _p(out))
+        return out
+
+
+def lru_reference_ops(ops, experts, cap, fill_stamp_clock=True):
+    """lru_reference over a trace of operations, for traces with fills and prefetches: ("step", layer, ids) is a
+    counted tick, ("prefetch", layer, ids) an uncounted one, ("fill", n_keys) puts every absent key in key order into
+    the first free slot with the current clock (ExpertCache::fill -> copy_on_compute, cache.rs:212-227,
+    cache/core.rs:366-377). fill_stamp_clock=False stamps 0 instead (a mutant the tests must tell apart)."""
+    slots = [None] * cap
+    clock = hits = copies = cpu = 0
+    for op in ops:
+        if op[0] == "fill":
+            for key in range(op[1]):
+                if any(s is not None and s[0] == key for s in slots):
+                    continue
+                free = next((i for i, s in enumerate(slots) if s is None), None)
+                if free is None:
+                    break
+                slots[free] = (key, clock if fill_stamp_clock else 0)
+            continue
+        kind, l, chosen = op
+        counted = kind == "step"
+        clock += 1
+        keys = [l * experts + int(e) for e in chosen]
+        for i, s in enumerate(slots):
+            if s is not None and s[0] in keys:
+                slots[i] = (s[0], clock)
+        for key in keys:
+            if any(s is not None and s[0] == key for s in slots):
+                hits += counted
+                continue
+            victim = next((i for i, s in enumerate(slots) if s is None), None)
+            if victim is None:
+                old = [(s[1], i) for i, s in enumerate(slots) if s[1] < clock]
+                victim = min(old)[1] if old else None
+            if victim is None:
+                cpu += counted
+            else:
+                slots[victim] = (key, clock)
+                copies += counted
+    return hits, copies, cpu
+
+
 class CpuSession:
     """CpuSession (rust/moe-rt/src/model.rs:160-243) over a moert.SynthModel, fp16 KV cache of max_len."""
 
@@ -338,4 +422,5 @@ class CpuSession:
             out.append(nxt)
             if i + 1 < n_new:
                 lg, _, _, self.last_hidden = self.step(nxt)
+        self.last_logits = lg  # the logits the last token was chosen from
         return np.array(out, np.int32), np.array(gaps, np.float32)

@@ -95,34 +95,125 @@ def test_cached_model_refuses_fewer_slots_than_top_k(gpu):
         moert.GpuModel(m, 64, attn_splits=4, cache_slots=1)
 
 
-def test_granite_3b_q4_0_quarter_pool_greedy_decode_equals_the_resident_model(gpu):
-    """The expert-cache workload at a reduced length: 3B shape, Q4_0, Zipf(1.1) router bias, a pool of 25% of the
-    1280 experts (320 slots); 96 greedy tokens identical to the resident model, counters equal to the oracle."""
-    cfg = moert.Config(**moert.GRANITE_3B)
-    m = moert.SynthModel(cfg, seed=4242, wdtype=moert.Q4_0, embed_dtype=moert.Q4_0, zipf_s=1.1)
-    prompt = np.random.default_rng(5).integers(0, cfg.vocab, 8)
-    say("3b q4_0 resident")
-    res = moert.GpuModel(m, 128, attn_splits=64)
-    want = res.generate(prompt, 96)
-    res.close()
-    say("3b q4_0 cached")
-    cac = moert.GpuModel(m, 128, attn_splits=64, cache_slots=320)
+def _forced_pair(res, cac, toks, label, every=1):
+    """Steps the resident and the cached model through the same forced tokens: logits (every `every` steps), ids,
+    weights and argmax bit for bit. Returns the routes [steps, layers, k]."""
     routes = []
-    toks = list(prompt) + list(want[:-1])
-    got = []
     for t, tok in enumerate(toks):
-        lg, ids, w, am = cac.step(int(tok))
+        if t % 64 == 0:
+            say(f"{label} step {t}")
+        want = t % every == 0
+        lg, ids, w, am = res.step(int(tok), want_logits=want)
+        clg, cids, cw, cam = cac.step(int(tok), want_logits=want)
+        assert np.array_equal(ids, cids) and bits_equal(w, cw) and am == cam, t
+        if want:
+            assert bits_equal(lg, clg), t
         routes.append(ids)
-        if t >= len(prompt) - 1:
-            got.append(am)
-    assert got == list(want)
-    hits, copies, cpu = oracle.lru_replay(np.array(routes), cfg.experts, 320)
+    return np.array(routes)
+
+
+@pytest.fixture(scope="module")
+def granite_3b_q4():
+    cfg = moert.Config(**moert.GRANITE_3B)
+    say("3b q4_0 build")
+    m = moert.SynthModel(cfg, seed=4242, wdtype=moert.Q4_0, embed_dtype=moert.Q4_0, zipf_s=1.1)
+    return cfg, m
+
+
+def test_granite_3b_q4_0_quarter_pool_forced_512_steps_equals_the_resident_model(gpu, granite_3b_q4):
+    """The expert-cache workload: 3B shape, Q4_0, Zipf(1.1) router bias, a pool of 25% of the 1280 experts (320
+    slots), 512 steps from an empty pool with a forced random token stream (so the pool keeps evicting): every
+    step's logits, ids, weights and argmax equal the resident model's bit for bit, and the hit / copy counters
+    equal the LRU oracle replayed over the routes."""
+    cfg, m = granite_3b_q4
+    toks = np.random.default_rng(512).integers(0, cfg.vocab, 512)
+    res = moert.GpuModel(m, 576, attn_splits=64)
+    cac = moert.GpuModel(m, 576, attn_splits=64, cache_slots=320)
+    routes = _forced_pair(res, cac, toks, "3b q4_0 forced")
+    hits, copies, cpu = oracle.lru_replay(routes, cfg.experts, 320)
+    say(f"3b q4_0 forced: {hits} hits, {copies} copies")
+    assert cpu == 0 and copies > 20000
     assert cac.cache_stats() == (hits, copies)
-    assert hits > 0 and copies > 0
+    res.close()
     cac.close()
 
 
-@pytest.mark.parametrize("wdtype,slots", [(moert.Q4_0, 6), (moert.Q8_0, 8)])
+def test_granite_3b_q4_0_filled_pool_copies_nothing_for_the_filled_layers(gpu, granite_3b_q4):
+    """A 320-slot pool filled from the host right after create holds keys 0..319 (layers 0-7): the first step then
+    copies only the experts of layers 8-31 (24 x 8), its outputs equal the resident model's, and 64 forced steps
+    keep equal outputs and counters equal to the LRU oracle started from the same fill (checks the strided fill
+    copies at the 3B Q4_0 record size)."""
+    cfg, m = granite_3b_q4
+    toks = np.random.default_rng(64).integers(0, cfg.vocab, 64)
+    res = moert.GpuModel(m, 128, attn_splits=64)
+    cac = moert.GpuModel(m, 128, attn_splits=64, cache_slots=320)
+    assert cac.cache_fill() == 320
+    routes = _forced_pair(res, cac, toks[:1], "3b q4_0 filled")
+    assert cac.cache_stats() == (8 * 8, 24 * 8)
+    routes = np.concatenate([routes, _forced_pair(res, cac, toks[1:], "3b q4_0 filled")])
+    lru = oracle.Lru(cfg.layers, cfg.experts, 320)
+    assert lru.fill() == 320
+    for r in routes:
+        lru.step(r)
+    hits, copies, _ = lru.stats()
+    assert cac.cache_stats() == (hits, copies)
+    res.close()
+    cac.close()
+
+
+def test_fill_after_decode_steps_stamps_the_current_clock(gpu):
+    """ExpertCache::fill on a partly filled pool after decode steps (no clear): the filled experts take the current
+    clock as their last use (copy_on_compute, cache/core.rs:366-377), so later steps evict them as recently used.
+    Counters equal the LRU oracle over the same trace (steps, fill, steps); the trace is one where stamping the fill
+    with 0 would give other counters."""
+    cfg = moert.Config(**TINY8)
+    m = moert.SynthModel(cfg, seed=13, wdtype=moert.Q4_0, embed_dtype=moert.F32, std=0.1, zipf_s=1.1)
+    res = moert.GpuModel(m, 64, attn_splits=4)
+    cac = moert.GpuModel(m, 64, attn_splits=4, cache_slots=22)
+    toks = np.random.default_rng(321).integers(0, cfg.vocab, 40)
+    say("fill after decode")
+    first = _forced_pair(res, cac, toks[:4], "fill after decode")
+    filled = cac.cache_fill()
+    second = _forced_pair(res, cac, toks[4:], "fill after decode")
+    ops = [("step", l, r[l].tolist()) for r in first for l in range(cfg.layers)] + [("fill", cfg.layers * cfg.experts)]
+    ops += [("step", l, r[l].tolist()) for r in second for l in range(cfg.layers)]
+    want = oracle.lru_reference_ops(ops, cfg.experts, 22)
+    assert want != oracle.lru_reference_ops(ops, cfg.experts, 22, fill_stamp_clock=False)
+    lru = oracle.Lru(cfg.layers, cfg.experts, 22)
+    for r in first:
+        lru.step(r)
+    assert lru.fill() == filled
+    for r in second:
+        lru.step(r)
+    assert lru.stats() == want
+    assert cac.cache_stats() == want[:2]
+    res.close()
+    cac.close()
+
+
+def test_prefetch_ticks_evict_like_the_lru_oracle(gpu):
+    """Per-layer prefetches (one uncounted tick of the LRU rule each) interleaved with decode steps on a 5-slot pool:
+    the outputs stay the resident model's, and the step counters equal the oracle's state machine over the same
+    trace, so each prefetch evicted the slots the rule chooses."""
+    cfg = moert.Config(**TINY8)
+    m = moert.SynthModel(cfg, seed=17, wdtype=moert.Q8_0, embed_dtype=moert.F32, std=0.1, zipf_s=1.1)
+    res = moert.GpuModel(m, 64, attn_splits=4)
+    cac = moert.GpuModel(m, 64, attn_splits=4, cache_slots=5)
+    lru = oracle.Lru(cfg.layers, cfg.experts, 5)
+    rng = np.random.default_rng(8)
+    toks = rng.integers(0, cfg.vocab, 24)
+    for t, tok in enumerate(toks):
+        say(f"prefetch trace step {t}")
+        if t % 3 == 1:
+            layer = int(rng.integers(0, cfg.layers))
+            ex = rng.choice(cfg.experts, size=int(rng.integers(1, 4)), replace=False)
+            assert cac.cache_prefetch(layer, ex) == lru.prefetch(layer, ex)
+        r = _forced_pair(res, cac, [tok], "prefetch trace")
+        lru.step(r[0])
+        assert cac.cache_stats() == lru.stats()[:2], t
+    res.close()
+    cac.close()
+
 def test_prefetch_of_a_steps_routes_makes_that_step_all_hits(gpu, wdtype, slots):
     """Before each step, every layer's routed experts (taken from the resident model) are prefetched: the step then
     copies nothing and hits k per layer, and its outputs stay those of the resident model. A prefetch counts no

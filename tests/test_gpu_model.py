@@ -90,46 +90,150 @@ def test_generate_on_the_device_equals_step_by_step_decoding(gpu):
     g.close()
 
 
-def test_granite_1b_greedy_128_prompt_256_tokens_identical(gpu):
-    """Granite-1B-A400M shape, Q8_0 weights, fp32 embedding/head; 128-token uniform prompt, 256 greedy tokens."""
+def _kv_rows_equal(g, s, cfg, lo, hi):
+    """KV rows [lo, hi) of every layer, bit for bit."""
+    for l in range(cfg.layers):
+        gk, gv = g.read_kv(l, hi)
+        ok, ov = s.read_kv(l, hi)
+        assert np.array_equal(gk[:, lo:hi], ok[:, lo:hi]) and np.array_equal(gv[:, lo:hi], ov[:, lo:hi]), l
+
+
+def _greedy_identity(g, s, prompt, n_new, label, min_distinct=1):
+    """Greedy generation on the device against the oracle: identical tokens, the last step's logits and hidden
+    state bit for bit. Prints the number of distinct tokens and the smallest top1 - top2 logit gap (the reference
+    logs the gap against TIE_GAP, bin/m1b-gulosa.rs:20) and asserts at least min_distinct distinct tokens."""
+    say(f"{label} gpu generate")
+    out = g.generate(prompt, n_new)
+    say(f"{label} oracle greedy")
+    want, gaps = s.generate(prompt, n_new)
+    distinct = len(set(want.tolist()))
+    say(f"{label}: {distinct} distinct tokens of {n_new}, smallest top1-top2 gap {float(gaps.min()):.3g}")
+    assert out.tolist() == want.tolist()
+    assert bits_equal(g.read_logits(), s.last_logits)
+    assert bits_equal(g.hidden(), s.last_hidden)
+    assert distinct >= min_distinct, distinct
+    return want
+
+
+def _forced_identity(g, s, toks, label, every=1):
+    """A forced token stream (the model is never at a fixed point): logits, routes and weights of every step bit
+    for bit (tests/model.rs:253-281 compares the GPU model with CpuSession at every position)."""
+    for t, tok in enumerate(toks):
+        if t % 32 == 0:
+            say(f"{label} forced step {t}")
+        want_logits = t % every == 0 or t == len(toks) - 1
+        lg, ids, w, am = g.step(int(tok), want_logits=want_logits)
+        olg, oids, ow, oh = s.step(int(tok), want_logits=want_logits)
+        assert np.array_equal(ids, oids) and bits_equal(w, ow), t
+        if want_logits:
+            assert bits_equal(lg, olg), t
+            assert am == oracle.argmax(olg), t
+    assert bits_equal(g.hidden(), oh)
+
+
+@pytest.fixture(scope="module")
+def granite_1b():
     cfg = moert.Config(**moert.GRANITE_1B)
     say("1B build")
-    m = moert.SynthModel(cfg, seed=2024, wdtype=moert.Q8_0, embed_dtype=moert.F32)
+    return cfg, moert.SynthModel(cfg, seed=2024, wdtype=moert.Q8_0, embed_dtype=moert.F32)
+
+
+def test_granite_1b_greedy_128_prompt_256_tokens_identical(gpu, granite_1b):
+    """Granite-1B-A400M shape, Q8_0 weights, fp32 embedding/head; 128-token uniform prompt, 256 greedy tokens:
+    identical tokens, last logits and hidden state bit for bit, every KV row the run appended. (With N(0, 0.02)
+    weights and a tied head the greedy run settles on one token; the forced and wider-init tests below cover
+    trajectories that move.)"""
+    cfg, m = granite_1b
     prompt = np.random.default_rng(2024).integers(0, cfg.vocab, 128)
     g = moert.GpuModel(m, 448, attn_splits=64)
-    say("1B gpu generate")
-    out = g.generate(prompt, 256)
-    say("1B oracle generate")
     s = oracle.CpuSession(m, 448, attn_splits=64, threads=THREADS)
-    want, gaps = s.generate(prompt, 256)
-    assert out.tolist() == want.tolist()
-    assert bits_equal(g.hidden(), s.last_hidden)  # residual stream after the last step
+    _greedy_identity(g, s, prompt, 256, "1B")
+    _kv_rows_equal(g, s, cfg, 0, 128 + 255)
     g.close()
 
 
-def test_granite_3b_long_context_256_steps_identical(gpu):
-    """Granite-3B-A800M shape, Q8_0 weights and head; KV cache pre-filled to 4096 positions with fp16 N(0,1);
-    256 decode steps. Logits of the first and last steps bit-identical, greedy tokens identical."""
+def test_granite_1b_forced_tokens_every_step_bit_identical(gpu, granite_1b):
+    """The 1B workload with a forced random token stream over its 384 positions (128 prompt + 256): logits, routes
+    and weights of every step, the final hidden state and every KV row, bit for bit."""
+    cfg, m = granite_1b
+    toks = np.random.default_rng(99).integers(0, cfg.vocab, 384)
+    g = moert.GpuModel(m, 448, attn_splits=64)
+    s = oracle.CpuSession(m, 448, attn_splits=64, threads=THREADS)
+    _forced_identity(g, s, toks, "1B")
+    _kv_rows_equal(g, s, cfg, 0, 384)
+    g.close()
+
+
+def test_granite_1b_wider_init_greedy_moves_and_stays_identical(gpu):
+    """The 1B shape with N(0, 0.1) weights, whose greedy trajectory does not settle: 128-token prompt, 256 greedy
+    tokens identical to the oracle (at least 100 distinct), last logits and hidden state bit for bit."""
+    cfg = moert.Config(**moert.GRANITE_1B)
+    say("1B wide build")
+    m = moert.SynthModel(cfg, seed=2024, wdtype=moert.Q8_0, embed_dtype=moert.F32, std=0.1)
+    prompt = np.random.default_rng(2025).integers(0, cfg.vocab, 128)
+    g = moert.GpuModel(m, 448, attn_splits=64)
+    s = oracle.CpuSession(m, 448, attn_splits=64, threads=THREADS)
+    _greedy_identity(g, s, prompt, 256, "1B wide", min_distinct=100)
+    g.close()
+
+
+def _granite_3b(std):
     cfg = moert.Config(**moert.GRANITE_3B)
-    say("3B build")
-    m = moert.SynthModel(cfg, seed=3003, wdtype=moert.Q8_0, embed_dtype=moert.Q8_0)
-    ctx, steps, max_len = 4096, 256, 4352
+    say(f"3B build std={std}")
+    m = moert.SynthModel(cfg, seed=3003, wdtype=moert.Q8_0, embed_dtype=moert.Q8_0, std=std)
+    return cfg, m, [moert.kv_prefill_data(cfg, 3003, l, 4096) for l in range(cfg.layers)]
+
+
+def _prefilled_pair(cfg, m, kv, max_len=4352, ctx=4096):
     g = moert.GpuModel(m, max_len, attn_splits=64)
     s = oracle.CpuSession(m, max_len, attn_splits=64, threads=THREADS)
-    for l in range(cfg.layers):
-        k, v = moert.kv_prefill_data(cfg, 3003, l, ctx)
+    for l, (k, v) in enumerate(kv):
         g.kv_prefill(l, k, v)
         s.kv_prefill(l, k, v)
     g.set_position(ctx)
     s.set_position(ctx)
+    return g, s
+
+
+@pytest.fixture(scope="module")
+def granite_3b():
+    return _granite_3b(0.02)
+
+
+def test_granite_3b_long_context_256_steps_identical(gpu, granite_3b):
+    """Granite-3B-A800M shape, Q8_0 weights and head; KV cache pre-filled to 4096 positions with fp16 N(0,1);
+    256 decode steps: the first step's logits and routes, the greedy tokens, the last step's logits and hidden state,
+    and the 256 KV rows of every layer, bit for bit."""
+    cfg, m, kv = granite_3b
+    g, s = _prefilled_pair(cfg, m, kv)
     tok = int(np.random.default_rng(3003).integers(0, cfg.vocab))
     say("3B first step")
     lg, ids, w, am = g.step(tok)
     olg, oids, ow, _ = s.step(tok)
     assert bits_equal(lg, olg) and np.array_equal(ids, oids) and bits_equal(w, ow)
-    say("3B gpu generate")
-    out = g.generate([am], steps - 1)
-    say("3B oracle greedy")
-    want, _ = s.generate([oracle.argmax(olg)], steps - 1)
-    assert out.tolist() == want.tolist()
+    assert am == oracle.argmax(olg)
+    _greedy_identity(g, s, [am], 255, "3B")
+    _kv_rows_equal(g, s, cfg, 4096, 4352)
+    g.close()
+
+
+def test_granite_3b_forced_tokens_at_4096_every_step_bit_identical(gpu, granite_3b):
+    """The 3B workload with a forced random token stream: 256 steps after the 4096 cached positions, logits, routes
+    and weights of every step, the final hidden state and the appended KV rows, bit for bit."""
+    cfg, m, kv = granite_3b
+    g, s = _prefilled_pair(cfg, m, kv)
+    toks = np.random.default_rng(31).integers(0, cfg.vocab, 256)
+    _forced_identity(g, s, toks, "3B")
+    _kv_rows_equal(g, s, cfg, 4096, 4352)
+    g.close()
+
+
+def test_granite_3b_wider_init_greedy_moves_and_stays_identical(gpu):
+    """The 3B long-context workload with N(0, 0.1) weights, whose greedy trajectory does not settle: 256 greedy steps
+    after 4096 cached positions, identical tokens (at least 100 distinct), last logits and hidden state bit for
+    bit."""
+    cfg, m, kv = _granite_3b(0.1)
+    g, s = _prefilled_pair(cfg, m, kv)
+    tok = int(np.random.default_rng(7).integers(0, cfg.vocab))
+    _greedy_identity(g, s, [tok], 256, "3B wide", min_distinct=100)
     g.close()
