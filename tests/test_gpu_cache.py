@@ -214,6 +214,8 @@ def test_prefetch_ticks_evict_like_the_lru_oracle(gpu):
     res.close()
     cac.close()
 
+
+@pytest.mark.parametrize("wdtype,slots", [(moert.Q4_0, 6), (moert.Q8_0, 8)])
 def test_prefetch_of_a_steps_routes_makes_that_step_all_hits(gpu, wdtype, slots):
     """Before each step, every layer's routed experts (taken from the resident model) are prefetched: the step then
     copies nothing and hits k per layer, and its outputs stay those of the resident model. A prefetch counts no
