@@ -194,6 +194,15 @@ typedef enum {
 } moert_kernel_kind;
 int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch, int* launches);
 
+/* Phase timeline of one decode step (measurement build libmoert_tl.so only; MOERT_E_CONFIG otherwise): one graph
+ * replay in which every workgroup of every launch stamps the 100 MHz real-time clock at its phase boundaries.
+ * out receives [launches][1024][8] u64 records: word 0 = ~(earliest wave start), word 1 = latest wave start,
+ * words 2..6 = phase ends seen by wave 0 (0 = no such phase), word 7 = latest wave end; kinds / layers receive each
+ * launch's moert_kernel_kind and layer (-1 outside the layers). The position advances by one. No reference
+ * counterpart (the reference's phase instrument is perfil_bloco.rs, host-side); used for the latency analysis. */
+int moert_timeline_step(moert_model* m, unsigned long long* out, int* kinds, int* layers, int max_launches,
+                        int* n_launches);
+
 /* ---------------------------------------------------------------------------------------------------------
  * One MoE block with every expert resident. Replaces GpuLayer::{upload, add_into_routed, run}
  * (rust/moe-rt/src/gpu.rs:430-541) and HostLayer::forward_cpu (rust/moe-rt/src/block.rs:56-62).

@@ -39,8 +39,9 @@ struct CacheDev {
 // The MoE half of a layer step of a cached model: rmsnorm + router + top-k + LRU decision + gate/up + SwiGLU of the
 // routed experts (k_route_up, cached mode), then down + combine + residual (k_expert_down, cached mode).
 hipError_t launch_route_up_cached(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
-                                  const CacheDev& c);
-hipError_t launch_expert_down_cached(hipStream_t s, const Dims& d, const StepBufs& b, int layer, const CacheDev& c);
+                                  const CacheDev& c, Tl tl = {});
+hipError_t launch_expert_down_cached(hipStream_t s, const Dims& d, const StepBufs& b, int layer, const CacheDev& c,
+                                     Tl tl = {});
 
 // Kernel copy of `bytes` (multiple of 16) from device-mapped pinned host memory to device memory (the PCIe rate
 // the cached kernels' host reads are bounded by).

@@ -188,46 +188,48 @@ struct moert_model {
   void* host_store = nullptr;
 
   // Launches one decode step. With `timed` >= 0, every launch of that kernel class records its dispatch start and
-  // end into the next event pair of `ev`.
+  // end into the next event pair of `ev`. With a timeline buffer (measurement build), launch i of the step records
+  // its workgroups' phase stamps into record i, and tl_kind / tl_layer say which launch that was.
   int enqueue(int timed, std::vector<hipEvent_t>* ev) {
     ev_i = 0;
-    auto arm = [&](int kind) {
+    tl_kind.clear();
+    tl_layer.clear();
+    auto arm = [&](int kind, int layer) -> Tl {
       if (kind == timed) {
         arm_launch_events((*ev)[ev_i], (*ev)[ev_i + 1]);
         ev_i += 2;
       }
+      Tl t{tl_buf ? tl_buf + tl_kind.size() * kTlRecord : nullptr};
+      tl_kind.push_back(kind);
+      tl_layer.push_back(layer);
+      return t;
     };
-    arm(MOERT_K_EMBED);
-    CHECK_HIP(launch_embed(stream, embed, dims, b));
+    CHECK_HIP(launch_embed(stream, embed, dims, b, arm(MOERT_K_EMBED, -1)));
     for (size_t l = 0; l < layers.size(); l++) {
       const LayerDev& L = layers[l];
-      arm(MOERT_K_QKV);
-      CHECK_HIP(launch_qkv(stream, L, dims, b));
-      arm(MOERT_K_ATTN_SPLIT);
-      CHECK_HIP(launch_attn_split(stream, L, dims, b));
-      arm(MOERT_K_ATTN_COMBINE);
-      CHECK_HIP(launch_attn_combine(stream, dims, b));
-      arm(MOERT_K_OPROJ);
-      CHECK_HIP(launch_oproj(stream, L, dims, b));
+      const int li = (int)l;
+      CHECK_HIP(launch_qkv(stream, L, dims, b, arm(MOERT_K_QKV, li)));
+      CHECK_HIP(launch_attn_split(stream, L, dims, b, arm(MOERT_K_ATTN_SPLIT, li)));
+      CHECK_HIP(launch_attn_combine(stream, dims, b, arm(MOERT_K_ATTN_COMBINE, li)));
+      CHECK_HIP(launch_oproj(stream, L, dims, b, arm(MOERT_K_OPROJ, li)));
       if (cached) {
-        arm(MOERT_K_ROUTE_UP);
-        CHECK_HIP(launch_route_up_cached(stream, L, dims, b, (int)l, cache));
-        arm(MOERT_K_EXPERT_DOWN);
-        CHECK_HIP(launch_expert_down_cached(stream, dims, b, (int)l, cache));
+        CHECK_HIP(launch_route_up_cached(stream, L, dims, b, li, cache, arm(MOERT_K_ROUTE_UP, li)));
+        CHECK_HIP(launch_expert_down_cached(stream, dims, b, li, cache, arm(MOERT_K_EXPERT_DOWN, li)));
       } else {
-        arm(MOERT_K_ROUTE_UP);
-        CHECK_HIP(launch_route_up(stream, L, dims, b, (int)l, true));
-        arm(MOERT_K_EXPERT_DOWN);
-        CHECK_HIP(launch_expert_down(stream, L, dims, b, (int)l, true));
+        CHECK_HIP(launch_route_up(stream, L, dims, b, li, true, arm(MOERT_K_ROUTE_UP, li)));
+        CHECK_HIP(launch_expert_down(stream, L, dims, b, li, true, arm(MOERT_K_EXPERT_DOWN, li)));
       }
     }
-    arm(MOERT_K_HEAD);
-    CHECK_HIP(launch_head(stream, embed, norm, dims, b));
-    arm(MOERT_K_HEAD_ARGMAX);
-    CHECK_HIP(launch_head_argmax(stream, embed, dims, b));
+    CHECK_HIP(launch_head(stream, embed, norm, dims, b, arm(MOERT_K_HEAD, -1)));
+    CHECK_HIP(launch_head_argmax(stream, embed, dims, b, arm(MOERT_K_HEAD_ARGMAX, -1)));
     return MOERT_OK;
   }
   int ev_i = 0;
+  // timeline records (measurement build): kTlRecord words per launch of a step
+  static constexpr size_t kTlRecord = (size_t)kTlMaxBlocks * kTlPhases;
+  unsigned long long* tl_buf = nullptr;
+  size_t tl_launches = 0;
+  std::vector<int> tl_kind, tl_layer;
 
   int fail(int rc) {
     if (rc == MOERT_E_DEVICE) {
@@ -396,6 +398,7 @@ struct moert_model {
     if (stream) (void)hipStreamSynchronize(stream);
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
+    if (tl_buf) (void)hipFree(tl_buf);
     arena.release();
     if (host_store) (void)hipHostFree(host_store);
     if (stream) (void)hipStreamDestroy(stream);
@@ -935,6 +938,50 @@ int moert_read_logits(moert_model* m, float* logits) {
   MTRY(m, model_copy_out(m, logits, m->b.logits, (size_t)m->cfg.vocab * 4));
   MTRY(m, model_sync(m));
   return MOERT_OK;
+}
+
+// One graph replay of the decode step with every workgroup of every launch stamping its phases (timeline build).
+// out: [launches][1024][8] u64 records (see timeline.h); kinds / layers: [launches]. The first call rebuilds the step
+// graph with the records attached.
+int moert_timeline_step(moert_model* m, unsigned long long* out, int* kinds, int* layers, int max_launches,
+                        int* n_launches) {
+  MODEL_OK(m);
+#ifndef MOERT_TIMELINE
+  (void)out; (void)kinds; (void)layers; (void)max_launches; (void)n_launches;
+  set_err("timeline: this library was built without MOERT_TIMELINE (use libmoert_tl.so)");
+  return MOERT_E_CONFIG;
+#else
+  CHECK_CFG(out && kinds && layers && n_launches, "null argument");
+  if (m->host_pos >= m->max_len) {
+    set_err("KV cache full (%d positions)", m->max_len);
+    return MOERT_E_FULL;
+  }
+  if (!m->tl_buf) {
+    const size_t launches = 3 + 6 * m->layers.size();
+    CHECK_HIP(hipMalloc(&m->tl_buf, launches * moert_model::kTlRecord * 8));
+    m->tl_launches = launches;
+    if (m->exec) CHECK_HIP(hipGraphExecDestroy(m->exec));
+    if (m->graph) CHECK_HIP(hipGraphDestroy(m->graph));
+    m->exec = nullptr;
+    m->graph = nullptr;
+    MTRY(m, m->build_graph());
+  }
+  const size_t n = m->tl_kind.size();
+  CHECK_CFG((int)n <= max_launches, "timeline: %zu launches, room for %d", n, max_launches);
+  int st[2] = {m->host_pos, 0};
+  MTRY(m, model_copy_in(m, m->b.state, st, sizeof st));
+  CHECK_HIP(hipMemsetAsync(m->tl_buf, 0, n * moert_model::kTlRecord * 8, m->stream));
+  MTRY(m, model_launch(m));
+  MTRY(m, model_copy_out(m, out, m->tl_buf, n * moert_model::kTlRecord * 8));
+  MTRY(m, model_sync(m));
+  for (size_t i = 0; i < n; i++) {
+    kinds[i] = m->tl_kind[i];
+    layers[i] = m->tl_layer[i];
+  }
+  *n_launches = (int)n;
+  m->host_pos++;
+  return MOERT_OK;
+#endif
 }
 
 static int time_steps_impl(moert_model* m, int warmup, int iters, double* ms) {

@@ -4,6 +4,7 @@
 #include <stdint.h>
 
 #include "dev_math.h"
+#include "timeline.h"
 
 namespace moert {
 
@@ -46,25 +47,27 @@ struct StepBufs {
   const float* rope; // [max_len, d]: cos of the d/2 frequencies, then sin
 };
 
-hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const StepBufs& b);
-hipError_t launch_qkv(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
-hipError_t launch_attn_split(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
-hipError_t launch_attn_combine(hipStream_t s, const Dims& d, const StepBufs& b);
+// tl: the launch's timeline record (measurement build; null otherwise).
+hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const StepBufs& b, Tl tl = {});
+hipError_t launch_qkv(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl = {});
+hipError_t launch_attn_split(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl = {});
+hipError_t launch_attn_combine(hipStream_t s, const Dims& d, const StepBufs& b, Tl tl = {});
 // Both attention kernels for ny consecutive positions of a multi-position step: position y has its query at
 // q + y * heads * 64, attends to *lenp + len_add + y cached positions and writes att + y * heads * 64 (part holds
 // ny * heads * splits * 66 floats).
 hipError_t launch_attn_batched(hipStream_t s, const LayerDev& L, const Dims& d, const int* lenp, int len_add, int ny,
                                const float* q, float* part, float* att);
-hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b);
+hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl = {});
 // Router + gate/up of the routed experts (the router recomputed by every workgroup, workgroup 0 publishes it).
 // normalize: rmsnorm h with ln_moe first (decode step); otherwise h is the block input as is.
 hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
-                           bool normalize);
+                           bool normalize, Tl tl = {});
 // accumulate: h += res * y (decode step); otherwise y is written to b.logits (standalone MoE block output).
 hipError_t launch_expert_down(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
-                              bool accumulate);
-hipError_t launch_head(hipStream_t s, const DMat& head, const float* norm, const Dims& d, const StepBufs& b);
-hipError_t launch_head_argmax(hipStream_t s, const DMat& head, const Dims& d, const StepBufs& b);
+                              bool accumulate, Tl tl = {});
+hipError_t launch_head(hipStream_t s, const DMat& head, const float* norm, const Dims& d, const StepBufs& b,
+                       Tl tl = {});
+hipError_t launch_head_argmax(hipStream_t s, const DMat& head, const Dims& d, const StepBufs& b, Tl tl = {});
 int head_blocks(const DMat& head);
 
 // The next kernel launched on this thread records its dispatch start/end into these events (hipExtLaunchKernelGGL).

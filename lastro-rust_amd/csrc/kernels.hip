@@ -8,6 +8,7 @@
 #include "dev_rows.h"
 #include "kernels.h"
 #include "launch.h"
+#include "timeline.h"
 
 namespace moert {
 
@@ -60,7 +61,8 @@ __global__ __launch_bounds__(kBlock) void k_gemv(DMat m, const float* __restrict
 // Embedding row times embedding_multiplier (model.rs:134-138); the token is seq[pos] on the device.
 template <int DT>
 __global__ __launch_bounds__(kBlock) void k_embed(DMat e, const int* __restrict__ seq, const int* __restrict__ st,
-                                                  float mult, float* __restrict__ h) {
+                                                  float mult, float* __restrict__ h, Tl tl) {
+  TL_START(tl);
   int tok = seq[st[ST_POS]];
   int H = e.cols;
   for (int i = threadIdx.x; i < H; i += kBlock) {
@@ -76,6 +78,7 @@ __global__ __launch_bounds__(kBlock) void k_embed(DMat e, const int* __restrict_
     }
     h[i] = v * mult;
   }
+  TL_END(tl);
 }
 
 constexpr int kQkvWaves = 8;  // waves per workgroup of k_qkv
@@ -89,7 +92,8 @@ template <int DT, int K, int NP>
 __global__ __launch_bounds__(kQkvWaves * 64) void k_qkv(DMat m, const float* __restrict__ h, const float* __restrict__ lnw,
                                                 float eps, const int* __restrict__ st, const float* __restrict__ rope,
                                                 int heads, int kvh, int max_len, float* __restrict__ q,
-                                                uint16_t* __restrict__ kc, uint16_t* __restrict__ vc) {
+                                                uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, Tl tl) {
+  TL_START(tl);
   using G = Geo<DT, K>;
   constexpr int P = 2 * NP;
   __shared__ float xs[K];
@@ -128,10 +132,12 @@ __global__ __launch_bounds__(kQkvWaves * 64) void k_qkv(DMat m, const float* __r
   Rows<DT, K, P> rr;
   rows_load<DT, K, P>(rr, m, row, ok, sub);
   norm_finish<K, (kQkvWaves * 64)>(hin, eps, xs, &rs);
+  TL_PHASE(tl, 2);
   XReg<DT, K> xr;
   load_x<DT, K>(xr, xs, sub);
   float out[P];
   rows_fma<DT, K, P>(rr, ok, xr, sub, out);
+  TL_PHASE(tl, 3);
   if (sub != 0) return;
 #pragma unroll
   for (int a = 0; a < NP; a++) {
@@ -152,6 +158,7 @@ __global__ __launch_bounds__(kQkvWaves * 64) void k_qkv(DMat m, const float* __r
       vp[jp + 32] = f2h(x2);
     }
   }
+  TL_END(tl);
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -339,7 +346,8 @@ template <int G, int T>
 __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restrict__ q, const uint16_t* __restrict__ kc,
                                                           const uint16_t* __restrict__ vc, const int* __restrict__ lenp,
                                                           int len_add, int max_len, float scale, int splits,
-                                                          float* __restrict__ part) {
+                                                          float* __restrict__ part, Tl tl) {
+  TL_START(tl);
   constexpr int TR = 8 % G == 0 ? 64 : 72;  // tile rows (64..71: padding for VShare when G does not divide 8)
   constexpr int KS = 68;                     // K row stride in floats: 16-byte rows, conflict-free row reads
   __shared__ __align__(16) float Vs[T][TR][64];  // V tiles in f32, row i = position
@@ -364,17 +372,17 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
   const int t0 = s * T, t = t0 + wt;
   // the tile's rows are requested before the length is known; a tile past the end of the cache (last split, when
   // T does not divide the tile count) reads the cache's last tile instead and is never used
-  const int tl = min(t, max_len / 64 - 1);
+  const int tc = min(t, max_len / 64 - 1);
   // q and the length first (loads complete in issue order), then this wave's shares of the tile's K and V (the G
   // waves of a tile move it together, each element is loaded and converted once)
   const float qv = q[h * 64 + lane];
   const int len = *lenp + len_add;
   __builtin_amdgcn_sched_barrier(0);
   VShare<G> ksh;
-  ksh.load(K, tl, lane, wh);
+  ksh.load(K, tc, lane, wh);
   __builtin_amdgcn_sched_barrier(0);  // K (needed first) ahead of V
   VShare<G> vsh;
-  vsh.load(V, tl, lane, wh);
+  vsh.load(V, tc, lane, wh);
   Qs[wh][lane] = qv;  // every wave of head wh stores the same q (an unconditional store keeps the q load first)
   const int nb = (len + 63) / 64;
   const int used = min(T, nb - t0);  // tiles of this split inside the length (>= 1 when the split is used)
@@ -382,6 +390,7 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
   const int nv = active ? min(64, len - t * 64) : 0;
   ksh.template store<KS>(&Ks[wt][0][0], lane, wh, nv);
   __syncthreads();  // Qs, K tiles
+  TL_PHASE(tl, 2);
   // scores: lane = position, chain over the 64 dims in order (an inactive tile's scores are discarded)
   float sc;
   {
@@ -401,6 +410,7 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
   const float tmax = group_max<64>(sc);
   if (lane == 0) Tm[wh][wt] = tmax;
   __syncthreads();  // tile maxima
+  TL_PHASE(tl, 3);
   float pv = 0.0f;
   if (active) {
     float mprev = NEG_INF;
@@ -417,6 +427,7 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
   }
   vsh.template store<64>(&Vs[wt][0][0], lane, wh, nv);
   __syncthreads();  // every share of every V tile stored; P written
+  TL_PHASE(tl, 4);
   if (active) {
     // p.v: lane = dim, chain over the positions in order, without branches so that every LDS read can be issued
     // ahead of the chain. A position past the length has p = exp(-inf) = 0 and its V element is stored as 0, so
@@ -451,7 +462,11 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
     if (wt > 0) Pv[wh][wt][lane] = pv;
   }
   __syncthreads();  // p.v of every tile
-  if (wt != 0 || used <= 0) return;
+  TL_PHASE(tl, 5);
+  if (wt != 0 || used <= 0) {
+    TL_END(tl);
+    return;
+  }
   float m = NEG_INF, l = 0.0f, acc = 0.0f;
   for (int u = 0; u < used; u++) {
     const float a = Al[wh][u];
@@ -465,6 +480,7 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_tiles(const float* __restri
     pp[1] = l;
   }
   pp[2 + lane] = acc;
+  TL_END(tl);
 }
 
 // Multi-position form of k_attn_tiles for the block step: one workgroup per (KV head g, split s, group of up to
@@ -680,7 +696,8 @@ __global__ __launch_bounds__(T * 64) void k_attn_mq(const float* __restrict__ q,
 // w_s * acc_sc, both over s = 0..used-1 in order; out_c = num_c / den. used <= splits <= 64.
 template <int SP>
 __global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ part, const int* __restrict__ lenp,
-                                                    int len_add, int tps, int splits, float* __restrict__ out) {
+                                                    int len_add, int tps, int splits, float* __restrict__ out, Tl tl) {
+  TL_START(tl);
   __shared__ float Cw[2][64];
   const int h = blockIdx.x, lane = threadIdx.x;
   const float NEG_INF = __int_as_float(0xff800000);
@@ -703,6 +720,7 @@ __global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ p
     ls = 0.0f;
   }
   const float M = group_max<64>(ms);
+  TL_PHASE(tl, 2);
   Cw[0][lane] = lane < used ? dexp(ms - M) : 0.0f;
   Cw[1][lane] = ls;
   wave_lds_sync();
@@ -716,6 +734,7 @@ __global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ p
     }
   }
   out[h * 64 + lane] = num / den;
+  TL_END(tl);
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -723,7 +742,8 @@ __global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ p
 // gpu_model.rs:386-394; model.rs:224-227).
 template <int DT, int K, int P>
 __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restrict__ att, float res,
-                                                  float* __restrict__ h) {
+                                                  float* __restrict__ h, Tl tl) {
+  TL_START(tl);
   using G = Geo<DT, K>;
   __shared__ float xs[K];
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -744,13 +764,16 @@ __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restric
   Rows<DT, K, P> rr;
   rows_load<DT, K, P>(rr, m, row, ok, sub);
   copy_finish<K, kBlock>(ain, xs);
+  TL_PHASE(tl, 2);
   XReg<DT, K> xr;
   load_x<DT, K>(xr, xs, sub);
   float out[P];
   rows_fma<DT, K, P>(rr, ok, xr, sub, out);
+  TL_PHASE(tl, 3);
 #pragma unroll
   for (int p = 0; p < P; p++)
     if (ok[p] && sub == 0) h[row[p]] = hold[p] + res * out[p];
+  TL_END(tl);
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -776,7 +799,8 @@ __global__ __launch_bounds__(route_waves(DT) * 64) void k_route_up(DMat router, 
                                                                const float* __restrict__ lnw, float eps, int k,
                                                                int inter, int layer, int* __restrict__ ids_out,
                                                                float* __restrict__ w_out, float* __restrict__ act,
-                                                               CacheDev c) {
+                                                               CacheDev c, Tl tl) {
+  TL_START(tl);
   using G = Geo<DT, K>;
   constexpr int NW = route_waves(DT);
   constexpr int NT = NW * 64;
@@ -824,6 +848,7 @@ __global__ __launch_bounds__(route_waves(DT) * 64) void k_route_up(DMat router, 
       norm_finish<K, NT>(hin, eps, xs, &rs);
     else
       copy_finish<K, NT>(cin, xs);
+    TL_PHASE(tl, 2);
     load_x<DT, K>(xr, xs, sub);
     float out[RP];
     rows_fma<DT, K, RP>(rr, ok, xr, sub, out);
@@ -832,11 +857,13 @@ __global__ __launch_bounds__(route_waves(DT) * 64) void k_route_up(DMat router, 
       if (ok[p] && sub == 0) lg[row[p]] = bias ? out[p] + bv[p] : out[p];
   }
   __syncthreads();
+  TL_PHASE(tl, 3);
   // routed ids as wave-uniform values, ranked by all waves
   int eid[8];
   const int rank = wg_rank<NW>(lg, E, lane, wave, part);
   const bool sel = lane < E && rank < k;
   ids_by_rank(sel, rank, k, eid);
+  TL_PHASE(tl, 4);
   if (blockIdx.x == 0 && wave == 0) route_weights(lg, sel, rank, k, lane, eid, ids_out, w_out);
   // expert-cache path: slots of the routed experts (eid becomes slot ids) and the keys of the misses
   int mk[8];
@@ -913,11 +940,13 @@ __global__ __launch_bounds__(route_waves(DT) * 64) void k_route_up(DMat router, 
     rows_load<DT, K, P>(rr, gu, row, ok, sub);
   float out[P];
   rows_fma<DT, K, P>(rr, ok, xr, sub, out);
+  TL_PHASE(tl, 5);
   if (CACHED) rows_store<DT, K, P>(rr, c.pool_gu, prow, put, sub);  // a missed expert's rows into its slot
   if (sub != 0) return;
 #pragma unroll
   for (int a = 0; a < NP; a++)
     if (ok[2 * a]) act[gp[a]] = silu_mul(out[2 * a], out[2 * a + 1]);
+  TL_END(tl);
 }
 
 // Down rows of the k routed experts, combined in top-k order, residual in the epilogue:
@@ -929,7 +958,8 @@ template <int DT, int K, bool CACHED>
 __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __restrict__ act,
                                                         const int* __restrict__ ids, const float* __restrict__ wts,
                                                         int k, int hidden, float res, bool accumulate,
-                                                        float* __restrict__ h, CacheDev c) {
+                                                        float* __restrict__ h, CacheDev c, Tl tl) {
+  TL_START(tl);
   using G = Geo<DT, K>;
   constexpr int KMAX = 8;
   constexpr int KP = (KMAX + G::RPW - 1) / G::RPW;
@@ -978,11 +1008,15 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __r
     reinterpret_cast<float4*>(xs)[i < k * K / 4 ? i : 0] = av[q];
   }
   __syncthreads();
+  TL_PHASE(tl, 2);
   if (CACHED) {
     if (blockIdx.x == 0 && threadIdx.x == 0) *c.cur ^= 1;
     rows_store<DT, K, KP>(rows, c.pool_dn, prow, put, sub);  // a missed expert's rows into its slot
   }
-  if (!rok) return;
+  if (!rok) {
+    TL_END(tl);
+    return;
+  }
   float dsum[KP];
 #pragma unroll
   for (int p = 0; p < KP; p++) {
@@ -999,6 +1033,7 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __r
     }
     dsum[p] = group_sum<G::LPR>(acc);
   }
+  TL_PHASE(tl, 3);
   float y = 0.0f;
 #pragma unroll
   for (int p = 0; p < KP; p++) {
@@ -1010,6 +1045,7 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __r
     }
   }
   if (lane == 0) h[r] = accumulate ? hold + res * y : y;
+  TL_END(tl);
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -1040,7 +1076,8 @@ __device__ __forceinline__ void wave_argmax(int& bk, int& bi) {
 template <int DT, int K, int P, int NB>
 __global__ __launch_bounds__(kBlock) void k_head(DMat m, const float* __restrict__ h, const float* __restrict__ lnw,
                                                  float eps, float ls, float* __restrict__ logits,
-                                                 int2* __restrict__ best) {
+                                                 int2* __restrict__ best, Tl tl) {
+  TL_START(tl);
   using G = Geo<DT, K>;
   __shared__ float xs[K];
   __shared__ float rs;
@@ -1063,6 +1100,7 @@ __global__ __launch_bounds__(kBlock) void k_head(DMat m, const float* __restrict
   Rows<DT, K, P> cur, nxt;
   rows_load<DT, K, P>(cur, m, row[0], ok[0], sub);
   norm_finish<K, kBlock>(hin, eps, xs, &rs);
+  TL_PHASE(tl, 2);
   XReg<DT, K> xr;
   load_x<DT, K>(xr, xs, sub);
   int bk = INT_MIN, bi = -1;
@@ -1099,13 +1137,15 @@ __global__ __launch_bounds__(kBlock) void k_head(DMat m, const float* __restrict
       }
     best[blockIdx.x] = make_int2(bk, bi);
   }
+  TL_END(tl);
 }
 
 // Greedy token from the per-block maxima of k_head (one block); records it, feeds it to the next position unless
 // that position holds a forced prompt token, and advances the position.
 __global__ __launch_bounds__(kBlock) void k_head_argmax(const int2* __restrict__ best, int nblocks,
                                                         int* __restrict__ st, int* __restrict__ seq,
-                                                        int* __restrict__ hist, int max_len) {
+                                                        int* __restrict__ hist, int max_len, Tl tl) {
+  TL_START(tl);
   __shared__ int sk[kWavesPerBlock], si[kWavesPerBlock];
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int bk = INT_MIN, bi = -1;
@@ -1134,6 +1174,7 @@ __global__ __launch_bounds__(kBlock) void k_head_argmax(const int2* __restrict__
     if (pos + 1 < max_len && pos + 1 >= st[ST_FIXED]) seq[pos + 1] = bi;
     st[ST_POS] = pos + 1;
   }
+  TL_END(tl);
 }
 
 // ------------------------------------------------------------------------------------------------------------
@@ -1253,23 +1294,23 @@ hipError_t launch_gemv(hipStream_t s, const DMat& w, const float* x, float* y) {
   return hipGetLastError();
 }
 
-hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const StepBufs& b) {
+hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const StepBufs& b, Tl tl) {
   switch (emb.dtype) {
-    case DT_Q8_0: klaunch(k_embed<DT_Q8_0>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h); break;
-    case DT_Q4_0: klaunch(k_embed<DT_Q4_0>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h); break;
-    case DT_F32: klaunch(k_embed<DT_F32>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h); break;
+    case DT_Q8_0: klaunch(k_embed<DT_Q8_0>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h, tl); break;
+    case DT_Q4_0: klaunch(k_embed<DT_Q4_0>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h, tl); break;
+    case DT_F32: klaunch(k_embed<DT_F32>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h, tl); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
-hipError_t launch_qkv(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b) {
+hipError_t launch_qkv(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl) {
 #define BODY(KK)                                                                                            \
   case KK: {                                                                                                \
     constexpr int PB = kQkvWaves * kQkvNP * Geo<DTC, KK>::RPW; /* pairs per block */                   \
     klaunch(k_qkv<DTC, KK, kQkvNP>, cdiv(L.qkv.rows / 2, PB), kQkvWaves * 64, 0, s,                                      \
         L.qkv, b.h, L.ln_attn, d.eps, b.state, b.rope, d.heads, d.kv_heads, d.max_len, b.q, L.k_cache,      \
-        L.v_cache);                                                                                         \
+        L.v_cache, tl);                                                                                     \
   } break;
   MOERT_DISPATCH(L.qkv.dtype, L.qkv.cols, BODY)
 #undef BODY
@@ -1280,13 +1321,13 @@ int attn_splits_for(int max_len, int tps) { return ((max_len + 63) / 64 + tps - 
 
 static hipError_t attn_split_dispatch(hipStream_t s, int G, int kvh, int tps, const float* q, const uint16_t* kc,
                                       const uint16_t* vc, const int* lenp, int len_add, int max_len, float scale,
-                                      float* part, int ny = 1) {
+                                      float* part, int ny = 1, Tl tl = {}) {
   const int splits = attn_splits_for(max_len, tps);
   if (splits > 64 || max_len % 64 || ny < 1) return hipErrorInvalidValue;
   const dim3 blocks(kvh * splits, ny);
 #define TILES_CASE(GG, TT)                                                                                   \
   if (G == GG && tps == TT) {                                                                                \
-    klaunch(k_attn_tiles<GG, TT>, blocks, GG * TT * 64, 0, s, q, kc, vc, lenp, len_add, max_len, scale, splits, part); \
+    klaunch(k_attn_tiles<GG, TT>, blocks, GG * TT * 64, 0, s, q, kc, vc, lenp, len_add, max_len, scale, splits, part, tl); \
     return hipGetLastError();                                                                                \
   }
   TILES_CASE(1, 1) TILES_CASE(2, 1) TILES_CASE(3, 1) TILES_CASE(4, 1)
@@ -1305,18 +1346,18 @@ static hipError_t attn_split_dispatch(hipStream_t s, int G, int kvh, int tps, co
 }
 
 static hipError_t attn_combine_dispatch(hipStream_t s, int heads, int tps, int max_len, const int* lenp, int len_add,
-                                        const float* part, float* out, int ny = 1) {
+                                        const float* part, float* out, int ny = 1, Tl tl = {}) {
   const int splits = attn_splits_for(max_len, tps);
   if (splits > 64 || max_len % 64 || ny < 1) return hipErrorInvalidValue;
   const dim3 grid(heads, ny);
   if (splits <= 8)
-    klaunch(k_attn_combine<8>, grid, 64, 0, s, part, lenp, len_add, tps, splits, out);
+    klaunch(k_attn_combine<8>, grid, 64, 0, s, part, lenp, len_add, tps, splits, out, tl);
   else if (splits <= 16)
-    klaunch(k_attn_combine<16>, grid, 64, 0, s, part, lenp, len_add, tps, splits, out);
+    klaunch(k_attn_combine<16>, grid, 64, 0, s, part, lenp, len_add, tps, splits, out, tl);
   else if (splits <= 32)
-    klaunch(k_attn_combine<32>, grid, 64, 0, s, part, lenp, len_add, tps, splits, out);
+    klaunch(k_attn_combine<32>, grid, 64, 0, s, part, lenp, len_add, tps, splits, out, tl);
   else
-    klaunch(k_attn_combine<64>, grid, 64, 0, s, part, lenp, len_add, tps, splits, out);
+    klaunch(k_attn_combine<64>, grid, 64, 0, s, part, lenp, len_add, tps, splits, out, tl);
   return hipGetLastError();
 }
 
@@ -1361,13 +1402,13 @@ hipError_t launch_attn_batched(hipStream_t s, const LayerDev& L, const Dims& d, 
   return attn_combine_dispatch(s, d.heads, d.tps, d.max_len, lenp, len_add, part, att, ny);
 }
 
-hipError_t launch_attn_split(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b) {
+hipError_t launch_attn_split(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl) {
   return attn_split_dispatch(s, d.heads / d.kv_heads, d.kv_heads, d.tps, b.q, L.k_cache, L.v_cache, b.state + ST_POS,
-                             1, d.max_len, d.attn_mult, b.part);
+                             1, d.max_len, d.attn_mult, b.part, 1, tl);
 }
 
-hipError_t launch_attn_combine(hipStream_t s, const Dims& d, const StepBufs& b) {
-  return attn_combine_dispatch(s, d.heads, d.tps, d.max_len, b.state + ST_POS, 1, b.part, b.att);
+hipError_t launch_attn_combine(hipStream_t s, const Dims& d, const StepBufs& b, Tl tl) {
+  return attn_combine_dispatch(s, d.heads, d.tps, d.max_len, b.state + ST_POS, 1, b.part, b.att, 1, tl);
 }
 
 hipError_t launch_attn_unit(hipStream_t s, const float* q, const uint16_t* kc, const uint16_t* vc, int heads,
@@ -1378,11 +1419,11 @@ hipError_t launch_attn_unit(hipStream_t s, const float* q, const uint16_t* kc, c
   return attn_combine_dispatch(s, heads, tps, max_len, len_dev, 0, part, out);
 }
 
-hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b) {
+hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl) {
 #define BODY(KK)                                                                            \
   case KK: {                                                                                \
     constexpr int RB = rows_per_block<DTC, KK, kOprojP>();                                  \
-    klaunch(k_oproj<DTC, KK, kOprojP>, cdiv(L.o.rows, RB), kBlock, 0, s, L.o, b.att, d.res_mult, b.h); \
+    klaunch(k_oproj<DTC, KK, kOprojP>, cdiv(L.o.rows, RB), kBlock, 0, s, L.o, b.att, d.res_mult, b.h, tl); \
   } break;
   MOERT_DISPATCH(L.o.dtype, L.o.cols, BODY)
 #undef BODY
@@ -1391,7 +1432,7 @@ hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const S
 
 
 hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
-                           bool normalize) {
+                           bool normalize, Tl tl) {
   if (L.router.dtype != L.gate_up.dtype || L.router.cols != L.gate_up.cols) return hipErrorInvalidValue;
   const CacheDev none{};
 #define BODY(KK)                                                                                           \
@@ -1401,11 +1442,11 @@ hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, cons
     if (normalize)                                                                                         \
       klaunch(k_route_up<DTC, KK, NP, true, false>, blocks, NW * 64, 0, s,                                      \
           L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter, layer,               \
-          b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, none);                        \
+          b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, none, tl);                    \
     else                                                                                                   \
       klaunch(k_route_up<DTC, KK, NP, false, false>, blocks, NW * 64, 0, s,                                     \
           L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter, layer,               \
-          b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, none);                        \
+          b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, none, tl);                    \
   } break;
   MOERT_DISPATCH(L.router.dtype, L.router.cols, BODY)
 #undef BODY
@@ -1413,7 +1454,7 @@ hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, cons
 }
 
 hipError_t launch_route_up_cached(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
-                                  const CacheDev& c) {
+                                  const CacheDev& c, Tl tl) {
   if (L.router.dtype != c.pool_gu.dtype || L.router.cols != c.pool_gu.cols || c.slots < d.top_k ||
       c.slots > kCacheMaxSlots || L.router.rows > 64 || d.top_k > 8)
     return hipErrorInvalidValue;
@@ -1423,7 +1464,7 @@ hipError_t launch_route_up_cached(hipStream_t s, const LayerDev& L, const Dims& 
     const int blocks = cdiv((long)d.top_k * d.inter, PB);                                                  \
     klaunch(k_route_up<DTC, KK, NP, true, true>, blocks, NW * 64, 0, s, L.router,                          \
             L.router_bias, c.pool_gu, b.h, L.ln_moe, d.eps, d.top_k, d.inter, layer,                       \
-            b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, c);                         \
+            b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, c, tl);                     \
   } break;
   MOERT_DISPATCH(L.router.dtype, L.router.cols, BODY)
 #undef BODY
@@ -1438,11 +1479,12 @@ hipError_t launch_route_up_cached(hipStream_t s, const LayerDev& L, const Dims& 
     default: return hipErrorInvalidValue;                                                                 \
   }
 
-hipError_t launch_expert_down_cached(hipStream_t s, const Dims& d, const StepBufs& b, int layer, const CacheDev& c) {
+hipError_t launch_expert_down_cached(hipStream_t s, const Dims& d, const StepBufs& b, int layer, const CacheDev& c,
+                                     Tl tl) {
 #define BODY(KK)                                                                                          \
   case KK:                                                                                                \
     klaunch(k_expert_down<DTC, KK, true>, cdiv(d.hidden, kWavesPerBlock), kBlock, 0, s, c.pool_dn, b.act,  \
-            (const int*)nullptr, b.route_w + layer * d.top_k, d.top_k, d.hidden, d.res_mult, true, b.h, c); \
+            (const int*)nullptr, b.route_w + layer * d.top_k, d.top_k, d.hidden, d.res_mult, true, b.h, c, tl); \
     break;
   DOWN_DISPATCH(c.pool_dn.dtype, c.pool_dn.cols, BODY)
 #undef BODY
@@ -1450,13 +1492,13 @@ hipError_t launch_expert_down_cached(hipStream_t s, const Dims& d, const StepBuf
 }
 
 hipError_t launch_expert_down(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
-                              bool accumulate) {
+                              bool accumulate, Tl tl) {
   const CacheDev none{};
 #define BODY(KK)                                                                                          \
   case KK:                                                                                                \
     klaunch(k_expert_down<DTC, KK, false>, cdiv(d.hidden, kWavesPerBlock), kBlock, 0, s,                      \
         L.down, b.act, b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, d.top_k, d.hidden,     \
-        d.res_mult, accumulate, accumulate ? b.h : b.logits, none);                                       \
+        d.res_mult, accumulate, accumulate ? b.h : b.logits, none, tl);                                   \
     break;
   DOWN_DISPATCH(L.down.dtype, L.down.cols, BODY)
 #undef BODY
@@ -1472,20 +1514,20 @@ int head_blocks(const DMat& head) {
   return cdiv(head.rows, kWavesPerBlock * kHeadNB * kHeadP * rpw);
 }
 
-hipError_t launch_head(hipStream_t s, const DMat& head, const float* norm, const Dims& d, const StepBufs& b) {
+hipError_t launch_head(hipStream_t s, const DMat& head, const float* norm, const Dims& d, const StepBufs& b, Tl tl) {
 #define BODY(KK)                                                                                        \
   case KK: {                                                                                            \
     constexpr int RB = rows_per_block<DTC, KK, kHeadP>() * kHeadNB;                                     \
     klaunch(k_head<DTC, KK, kHeadP, kHeadNB>, cdiv(head.rows, RB), kBlock, 0, s, head, b.h, norm, d.eps,     \
-                                                                   d.logits_scaling, b.logits, b.best); \
+                                                                   d.logits_scaling, b.logits, b.best, tl); \
   } break;
   MOERT_DISPATCH(head.dtype, head.cols, BODY)
 #undef BODY
   return hipGetLastError();
 }
 
-hipError_t launch_head_argmax(hipStream_t s, const DMat& head, const Dims& d, const StepBufs& b) {
-  klaunch(k_head_argmax, 1, kBlock, 0, s, b.best, head_blocks(head), b.state, b.seq, b.argmax_hist, d.max_len);
+hipError_t launch_head_argmax(hipStream_t s, const DMat& head, const Dims& d, const StepBufs& b, Tl tl) {
+  klaunch(k_head_argmax, 1, kBlock, 0, s, b.best, head_blocks(head), b.state, b.seq, b.argmax_hist, d.max_len, tl);
   return hipGetLastError();
 }
 

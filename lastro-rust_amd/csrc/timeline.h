@@ -14,6 +14,7 @@
 namespace moert {
 
 constexpr int kTlPhases = 8;
+constexpr int kTlMaxBlocks = 1024;  // workgroups per launch with a record (later ones are not stamped)
 
 struct Tl {
   unsigned long long* p;  // this launch's record, or null
@@ -21,28 +22,33 @@ struct Tl {
 
 #ifdef MOERT_TIMELINE
 __device__ __forceinline__ unsigned long long tl_now() { return __builtin_amdgcn_s_memrealtime(); }
+// The workgroup's record, or null (no record, or a workgroup past kTlMaxBlocks).
 __device__ __forceinline__ unsigned long long* tl_rec(const Tl& tl) {
-  return tl.p + (size_t)(blockIdx.y * gridDim.x + blockIdx.x) * kTlPhases;
+  const unsigned wg = blockIdx.y * gridDim.x + blockIdx.x;
+  return tl.p && wg < (unsigned)kTlMaxBlocks ? tl.p + (size_t)wg * kTlPhases : nullptr;
 }
 // Start of every wave (slot 0 keeps the earliest, slot 1 the latest).
 #define TL_START(tl)                                                                                      \
   do {                                                                                                    \
-    if ((tl).p && (threadIdx.x & 63) == 0) {                                                              \
+    unsigned long long* r_ = tl_rec(tl);                                                                  \
+    if (r_ && (threadIdx.x & 63) == 0) {                                                                  \
       const unsigned long long t_ = tl_now();                                                             \
-      __hip_atomic_fetch_max(tl_rec(tl), ~t_, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);                \
-      __hip_atomic_fetch_max(tl_rec(tl) + 1, t_, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);             \
+      __hip_atomic_fetch_max(r_, ~t_, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);                        \
+      __hip_atomic_fetch_max(r_ + 1, t_, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);                     \
     }                                                                                                     \
   } while (0)
 // End of phase `ph` (2 .. kTlPhases - 2) as wave 0 sees it.
 #define TL_PHASE(tl, ph)                                                                                  \
   do {                                                                                                    \
-    if ((tl).p && threadIdx.x == 0) tl_rec(tl)[ph] = tl_now();                                            \
+    unsigned long long* r_ = tl_rec(tl);                                                                  \
+    if (r_ && threadIdx.x == 0) r_[ph] = tl_now();                                                        \
   } while (0)
 // End of every wave (the latest is kept).
 #define TL_END(tl)                                                                                        \
   do {                                                                                                    \
-    if ((tl).p && (threadIdx.x & 63) == 0)                                                                \
-      __hip_atomic_fetch_max(tl_rec(tl) + kTlPhases - 1, tl_now(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); \
+    unsigned long long* r_ = tl_rec(tl);                                                                  \
+    if (r_ && (threadIdx.x & 63) == 0)                                                                    \
+      __hip_atomic_fetch_max(r_ + kTlPhases - 1, tl_now(), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   \
   } while (0)
 #else
 #define TL_START(tl) \

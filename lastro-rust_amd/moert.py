@@ -29,6 +29,7 @@ KERNEL_NAMES = ["embed", "qkv", "attn_split", "attn_combine", "oproj", "route_up
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmoert.so")
+TIMELINE_LIB_PATH = os.path.join(_HERE, "libmoert_tl.so")  # measurement build (phase timeline), see timeline.py
 
 E_NAMES = {-1: "DEVICE", -2: "CONFIG", -3: "POISONED", -4: "FULL", -5: "RANGE"}
 E_DEVICE, E_CONFIG, E_POISONED, E_FULL, E_RANGE = -1, -2, -3, -4, -5
@@ -101,6 +102,7 @@ def lib() -> ctypes.CDLL:
             "moert_read_logits": (i, [vp, vp]),
             "moert_time_steps": (i, [vp, i, i, ctypes.POINTER(ctypes.c_double)]),
             "moert_time_kernel": (i, [vp, i, i, ctypes.POINTER(ctypes.c_double), ip]),
+            "moert_timeline_step": (i, [vp, vp, vp, vp, i, ip]),
             "moert_block_create": (i, [i, i, i, i, ctypes.POINTER(moert_tensor), vp, ctypes.POINTER(moert_tensor),
                                        ctypes.POINTER(moert_tensor), ctypes.POINTER(vp)]),
             "moert_block_destroy": (i, [vp]),
@@ -140,7 +142,7 @@ EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moer
             "moert_decode_step", "moert_generate", "moert_step_batched", "moert_prefill", "moert_reset_sequence",
             "moert_kv_prefill_fp16",
             "moert_set_position", "moert_get_position", "moert_read_kv_fp16", "moert_read_hidden", "moert_read_logits",
-            "moert_time_steps", "moert_time_kernel", "moert_block_create", "moert_block_destroy",
+            "moert_time_steps", "moert_time_kernel", "moert_timeline_step", "moert_block_create", "moert_block_destroy",
             "moert_block_forward", "moert_block_time", "moert_block_forward_batched",
             "moert_block_experts_in_step", "moert_block_time_batched", "moert_router_topk", "moert_argmax", "moert_gemv",
             "moert_dequant", "moert_rmsnorm", "moert_rope", "moert_attn_decode", "moert_exp_device",
@@ -433,6 +435,17 @@ class GpuModel:
         ms = ctypes.c_double(0)
         check(lib().moert_time_steps(self.h, warmup, iters, ctypes.byref(ms)))
         return ms.value
+
+    def timeline_step(self):
+        """One step with per-workgroup phase stamps (libmoert_tl.so only): (records [launches, 1024, 8] u64,
+        kinds [launches], layers [launches])."""
+        n_max = 3 + 6 * self.cfg.layers
+        out = np.zeros((n_max, 1024, 8), np.uint64)
+        kinds = np.zeros(n_max, np.int32)
+        layers = np.zeros(n_max, np.int32)
+        n = ctypes.c_int(0)
+        check(lib().moert_timeline_step(self.h, ptr(out), ptr(kinds), ptr(layers), n_max, ctypes.byref(n)))
+        return out[:n.value], kinds[:n.value], layers[:n.value]
 
     def time_kernel(self, kind: int, iters: int):
         us, n = ctypes.c_double(0), ctypes.c_int(0)
