@@ -960,6 +960,7 @@ int moert_timeline_step(moert_model* m, unsigned long long* out, int* kinds, int
     const size_t launches = 3 + 6 * m->layers.size();
     CHECK_HIP(hipMalloc(&m->tl_buf, launches * moert_model::kTlRecord * 8));
     m->tl_launches = launches;
+    CHECK_HIP(hipStreamSynchronize(m->stream));
     if (m->exec) CHECK_HIP(hipGraphExecDestroy(m->exec));
     if (m->graph) CHECK_HIP(hipGraphDestroy(m->graph));
     m->exec = nullptr;
