@@ -21,6 +21,7 @@
 #include "cache.h"
 #include "grouped.h"
 #include "kernels.h"
+#include "moe_norm.h"
 #include "prefill.h"
 
 using namespace moert;
@@ -261,6 +262,7 @@ struct moert_model {
     if ((rc = zeros(arena, stream, (size_t)M, &pf.toks)) || (rc = zeros(arena, stream, (size_t)1, &pf.pos0)) ||
         (rc = zeros(arena, stream, (size_t)M * H, &pf.h)) || (rc = zeros(arena, stream, (size_t)M * qd, &pf.q)) ||
         (rc = zeros(arena, stream, (size_t)M * qd, &pf.att)) || (rc = zeros(arena, stream, parts, &pf.part)) ||
+        (rc = zeros(arena, stream, (size_t)M * kNormItems, &pf.zpart)) ||
         (rc = zeros(arena, stream, (size_t)M * H, &pf.xn)) || (rc = zeros(arena, stream, (size_t)M * K8, &pf.ids)) ||
         (rc = zeros(arena, stream, (size_t)M * K8, &pf.w)) ||
         (rc = zeros(arena, stream, (size_t)M * K8 * I, &pf.act)) ||
@@ -553,6 +555,7 @@ static int model_create(const moert_config* c, const moert_model_weights* w, int
   m->n_head_blocks = head_blocks(m->embed);
   if ((rc = zeros(a, s, H, &b.h)) || (rc = zeros(a, s, qd, &b.q)) || (rc = zeros(a, s, qd, &b.att)) ||
       (rc = zeros(a, s, (size_t)c->heads * attn_splits_for(max_len, tps) * 66, &b.part)) ||
+      (rc = zeros(a, s, (size_t)kNormItems, &b.zpart)) ||
       (rc = zeros(a, s, (size_t)c->top_k * I, &b.act)) ||
       (rc = zeros(a, s, (size_t)c->layers * c->top_k, &b.route_ids)) ||
       (rc = zeros(a, s, (size_t)c->layers * c->top_k, &b.route_w)) || (rc = zeros(a, s, c->vocab, &b.logits)) ||

@@ -36,6 +36,7 @@ struct StepBufs {
   float* q;          // [heads*d]
   float* att;        // [heads*d]
   float* part;       // [heads, splits, 2 + d] split-KV partials
+  float* zpart;      // [65, 256] MoE-norm partials of the current layer (moe_norm.h)
   float* act;        // [k, I] SwiGLU activations
   int* route_ids;    // [layers, k]
   float* route_w;    // [layers, k]
@@ -57,11 +58,13 @@ hipError_t launch_attn_combine(hipStream_t s, const Dims& d, const StepBufs& b, 
 // ny * heads * splits * 66 floats).
 hipError_t launch_attn_batched(hipStream_t s, const LayerDev& L, const Dims& d, const int* lenp, int len_add, int ny,
                                const float* q, float* part, float* att);
+// Output projection + residual; the epilogue writes the MoE-norm partials of the new h into b.zpart.
 hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl = {});
-// Router + gate/up of the routed experts (the router recomputed by every workgroup, workgroup 0 publishes it).
-// normalize: rmsnorm h with ln_moe first (decode step); otherwise h is the block input as is.
+// Router + gate/up of the routed experts (every workgroup ranks the experts, workgroup 0 publishes the routing).
+// partials: the rmsnorm of h and the router logits from the MoE-norm partials that launch_oproj wrote (decode
+// step); otherwise h is the normalised block input and the router's dots are computed in full.
 hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
-                           bool normalize, Tl tl = {});
+                           bool partials, Tl tl = {});
 // accumulate: h += res * y (decode step); otherwise y is written to b.logits (standalone MoE block output).
 hipError_t launch_expert_down(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
                               bool accumulate, Tl tl = {});

@@ -8,6 +8,7 @@
 #include "dev_rows.h"
 #include "kernels.h"
 #include "launch.h"
+#include "moe_norm.h"
 #include "timeline.h"
 
 namespace moert {
@@ -739,15 +740,21 @@ __global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ p
 
 // ------------------------------------------------------------------------------------------------------------
 // Output projection with the residual in the epilogue: h[r] = h[r] + res * (Wo att)[r] (gemv o + axpby,
-// gpu_model.rs:386-394; model.rs:224-227).
+// gpu_model.rs:386-394; model.rs:224-227). The epilogue also writes the MoE-norm partials of the workgroup's rows
+// (moe_norm.h: the router dots and the sum of squares of its 8-row blocks of the new h) for the router kernel.
 template <int DT, int K, int P>
 __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restrict__ att, float res,
-                                                  float* __restrict__ h, Tl tl) {
+                                                  float* __restrict__ h, DMat router, const float* __restrict__ lnw,
+                                                  float* __restrict__ zp, Tl tl) {
   TL_START(tl);
   using G = Geo<DT, K>;
+  constexpr int RB = kWavesPerBlock * P * G::RPW;  // rows of the workgroup: [r0, r0 + RB)
+  static_assert(RB % kNormBlk == 0, "the workgroup's rows must be whole partial blocks");
   __shared__ float xs[K];
+  __shared__ float hn[RB];
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int sub = lane % G::LPR, rw = lane / G::LPR;
+  const int r0 = blockIdx.x * RB;
   size_t base = ((size_t)blockIdx.x * kWavesPerBlock + wave) * (P * G::RPW);
   size_t row[P];
   bool ok[P];
@@ -756,6 +763,8 @@ __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restric
     row[p] = base + (size_t)p * G::RPW + rw;
     ok[p] = row[p] < (size_t)m.rows;
   }
+  NormPart<RB, kBlock> np;
+  norm_part_fetch<RB, kBlock>(router, lnw, r0, m.rows, np);
   CopyIn<K, kBlock> ain;
   copy_fetch<K, kBlock>(att, ain);
   float hold[P];
@@ -772,7 +781,13 @@ __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restric
   TL_PHASE(tl, 3);
 #pragma unroll
   for (int p = 0; p < P; p++)
-    if (ok[p] && sub == 0) h[row[p]] = hold[p] + res * out[p];
+    if (ok[p] && sub == 0) {
+      const float hv = hold[p] + res * out[p];
+      h[row[p]] = hv;
+      hn[row[p] - r0] = hv;
+    }
+  __syncthreads();
+  norm_part_finish<RB, kBlock>(np, hn, router.dtype, router.rows, r0, m.rows, zp);
   TL_END(tl);
 }
 
@@ -793,18 +808,19 @@ __host__ __device__ constexpr int route_np(int dt) { return 16 / route_waves(dt)
 // writes the updated tables into the other copy, the counters and the routed slots for the down kernel. Rows of a
 // routed expert come from its pool slot, or, when it missed, from its record in the host store; those rows are also
 // written into the slot.
-template <int DT, int K, int NP, bool NORM, bool CACHED>
+template <int DT, int K, int NP, bool PART, bool CACHED>
 __global__ __launch_bounds__(route_waves(DT) * 64) void k_route_up(DMat router, const float* __restrict__ bias, DMat gu,
                                                                const float* __restrict__ h,
-                                                               const float* __restrict__ lnw, float eps, int k,
-                                                               int inter, int layer, int* __restrict__ ids_out,
+                                                               const float* __restrict__ lnw, float eps,
+                                                               const float* __restrict__ zp, int k, int inter,
+                                                               int layer, int* __restrict__ ids_out,
                                                                float* __restrict__ w_out, float* __restrict__ act,
                                                                CacheDev c, Tl tl) {
   TL_START(tl);
   using G = Geo<DT, K>;
   constexpr int NW = route_waves(DT);
   constexpr int NT = NW * 64;
-  constexpr int RP = (64 + NW * G::RPW - 1) / (NW * G::RPW);  // router passes for 64 rows
+  constexpr int RP = PART ? 1 : (64 + NW * G::RPW - 1) / (NW * G::RPW);  // router passes for 64 rows
   constexpr int P = 2 * NP;
   constexpr int SMAX = CACHED ? kCacheMaxSlots : 1;
   __shared__ float xs[K];
@@ -813,18 +829,60 @@ __global__ __launch_bounds__(route_waves(DT) * 64) void k_route_up(DMat router, 
   __shared__ int skey[SMAX];
   __shared__ int slast[SMAX];
   __shared__ int lslot[8], lmiss[8], lfound[8];
-  __shared__ float rs;
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int sub = lane % G::LPR, rw = lane / G::LPR;
   const int E = router.rows;
   XReg<DT, K> xr;
-  NormIn<K, NT> hin;
-  CopyIn<K, NT> cin;
-  if (NORM)
-    norm_fetch<K, NT>(h, lnw, hin);
-  else
+  if (PART) {
+    // Model step: the rmsnorm and the router from the MoE-norm partials of the output projection (moe_norm.h).
+    // Loads first: the sum-of-squares partials (every wave forms r itself), this wave's router items and their
+    // bias, this thread's elements of h and of the norm weights, the slot tables.
+    constexpr int IPW = (64 + NW - 1) / NW;  // router items per wave
+    constexpr int XP = (K + NT - 1) / NT;    // elements of h per thread
+    const int nb = K / kNormBlk;
+    NormItem ssi, it[IPW];
+    float bv[IPW], hv[XP], wv[XP];
+    norm_item_fetch(zp, E, lane, ssi);
+#pragma unroll
+    for (int i = 0; i < IPW; i++) {
+      const int e = wave + i * NW, ec = e < E ? e : 0;
+      norm_item_fetch(zp, ec, lane, it[i]);
+      bv[i] = bias ? bias[ec] : 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < XP; e++) {
+      const int i = threadIdx.x + e * NT, ic = i < K ? i : 0;
+      hv[e] = h[ic];
+      wv[e] = lnw[ic];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (CACHED) {
+      const int cur = *c.cur, S = c.slots;
+      for (int i = threadIdx.x; i < S; i += NT) {
+        skey[i] = c.slot_key[cur * S + i];
+        slast[i] = c.slot_last[cur * S + i];
+      }
+    }
+    const float ss = norm_item_sum(ssi, nb, lane);
+    const float r = 1.0f / sqrtf(ss / (float)K + eps);
+    TL_PHASE(tl, 2);
+#pragma unroll
+    for (int i = 0; i < IPW; i++) {
+      const int e = wave + i * NW;
+      if (e < E) {
+        const float z = norm_item_sum(it[i], nb, lane);
+        if (lane == 0) lg[e] = bias ? z * r + bv[i] : z * r;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < XP; e++) {
+      const int i = threadIdx.x + e * NT;
+      if (i < K) xs[i] = wv[e] * (hv[e] * r);
+    }
+  } else {
+    // Standalone block: x is the already normalised input; the router's dots in the canonical order.
+    CopyIn<K, NT> cin;
     copy_fetch<K, NT>(h, cin);
-  {
     size_t row[RP];
     bool ok[RP];
 #pragma unroll
@@ -837,17 +895,7 @@ __global__ __launch_bounds__(route_waves(DT) * 64) void k_route_up(DMat router, 
     float bv[RP];
 #pragma unroll
     for (int p = 0; p < RP; p++) bv[p] = bias ? bias[ok[p] ? row[p] : 0] : 0.0f;  // clamped, not guarded: one run of loads
-    if (CACHED) {
-      const int cur = *c.cur, S = c.slots;
-      for (int i = threadIdx.x; i < S; i += NT) {
-        skey[i] = c.slot_key[cur * S + i];
-        slast[i] = c.slot_last[cur * S + i];
-      }
-    }
-    if (NORM)
-      norm_finish<K, NT>(hin, eps, xs, &rs);
-    else
-      copy_finish<K, NT>(cin, xs);
+    copy_finish<K, NT>(cin, xs);
     TL_PHASE(tl, 2);
     load_x<DT, K>(xr, xs, sub);
     float out[RP];
@@ -938,6 +986,7 @@ __global__ __launch_bounds__(route_waves(DT) * 64) void k_route_up(DMat router, 
     rows_load_from<DT, K, P>(rr, src, row, ok, sub);
   else
     rows_load<DT, K, P>(rr, gu, row, ok, sub);
+  if (PART) load_x<DT, K>(xr, xs, sub);  // the normalised input, staged before the rank's barrier
   float out[P];
   rows_fma<DT, K, P>(rr, ok, xr, sub, out);
   TL_PHASE(tl, 5);
@@ -1423,7 +1472,8 @@ hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const S
 #define BODY(KK)                                                                            \
   case KK: {                                                                                \
     constexpr int RB = rows_per_block<DTC, KK, kOprojP>();                                  \
-    klaunch(k_oproj<DTC, KK, kOprojP>, cdiv(L.o.rows, RB), kBlock, 0, s, L.o, b.att, d.res_mult, b.h, tl); \
+    klaunch(k_oproj<DTC, KK, kOprojP>, cdiv(L.o.rows, RB), kBlock, 0, s, L.o, b.att, d.res_mult, b.h, L.router, \
+            L.ln_moe, b.zpart, tl);                                                                 \
   } break;
   MOERT_DISPATCH(L.o.dtype, L.o.cols, BODY)
 #undef BODY
@@ -1432,21 +1482,21 @@ hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const S
 
 
 hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
-                           bool normalize, Tl tl) {
+                           bool partials, Tl tl) {
   if (L.router.dtype != L.gate_up.dtype || L.router.cols != L.gate_up.cols) return hipErrorInvalidValue;
   const CacheDev none{};
 #define BODY(KK)                                                                                           \
   case KK: {                                                                                               \
     constexpr int NW = route_waves(DTC), NP = route_np(DTC), PB = NW * NP * Geo<DTC, KK>::RPW;             \
     const int blocks = cdiv((long)d.top_k * d.inter, PB);                                                  \
-    if (normalize)                                                                                         \
-      klaunch(k_route_up<DTC, KK, NP, true, false>, blocks, NW * 64, 0, s,                                      \
-          L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter, layer,               \
+    if (partials)                                                                                          \
+      klaunch(k_route_up<DTC, KK, NP, true, false>, blocks, NW * 64, 0, s,                                 \
+          L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, b.zpart, d.top_k, d.inter, layer,      \
           b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, none, tl);                    \
     else                                                                                                   \
-      klaunch(k_route_up<DTC, KK, NP, false, false>, blocks, NW * 64, 0, s,                                     \
-          L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, d.top_k, d.inter, layer,               \
-          b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, none, tl);                    \
+      klaunch(k_route_up<DTC, KK, NP, false, false>, blocks, NW * 64, 0, s,                                \
+          L.router, L.router_bias, L.gate_up, b.h, L.ln_moe, d.eps, (const float*)nullptr, d.top_k, d.inter, \
+          layer, b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, none, tl);             \
   } break;
   MOERT_DISPATCH(L.router.dtype, L.router.cols, BODY)
 #undef BODY
@@ -1463,7 +1513,7 @@ hipError_t launch_route_up_cached(hipStream_t s, const LayerDev& L, const Dims& 
     constexpr int NW = route_waves(DTC), NP = route_np(DTC), PB = NW * NP * Geo<DTC, KK>::RPW;             \
     const int blocks = cdiv((long)d.top_k * d.inter, PB);                                                  \
     klaunch(k_route_up<DTC, KK, NP, true, true>, blocks, NW * 64, 0, s, L.router,                          \
-            L.router_bias, c.pool_gu, b.h, L.ln_moe, d.eps, d.top_k, d.inter, layer,                       \
+            L.router_bias, c.pool_gu, b.h, L.ln_moe, d.eps, b.zpart, d.top_k, d.inter, layer,              \
             b.route_ids + layer * d.top_k, b.route_w + layer * d.top_k, b.act, c, tl);                     \
   } break;
   MOERT_DISPATCH(L.router.dtype, L.router.cols, BODY)

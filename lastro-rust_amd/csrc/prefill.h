@@ -17,6 +17,7 @@ struct PfBufs {
   float* q;      // [m, heads*d] queries
   float* att;    // [m, heads*d] attention outputs
   float* part;   // [m, heads, splits, 2 + d] split-KV partials
+  float* zpart;  // [m, kNormItems] MoE-norm partials of each position (moe_norm.h)
   float* xn;     // [m, H] rmsnorm of h before the experts
   int* ids;      // [m, k] routed experts, top-k order
   float* w;      // [m, k] routing weights

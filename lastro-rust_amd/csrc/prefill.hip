@@ -9,8 +9,10 @@
 //   k_qkv_b        rmsnorm of each position, [q; k; v] rows of the layer once for all positions, RoPE at each
 //                  position, q to qb[v], k and v to row pos0 + v of the KV cache
 //   attention      the decode attention kernels over a grid of positions, position v attending to pos0 + v + 1
-//   k_oproj_b      output projection once for all positions, h[v] += res * (Wo att[v])
-//   k_route_b      per position: rmsnorm, router, top-k and weights (the decode router in full); xn[v] kept
+//   k_oproj_b      output projection once for all positions, h[v] += res * (Wo att[v]); MoE-norm partials of each
+//                  position's new rows (moe_norm.h)
+//   k_route_b      per position: rmsnorm scale, router logits from the partials, top-k and weights (the decode
+//                  router); xn[v] kept
 //   k_moe_up_b     per routed expert: its gate/up rows once, applied to the positions routed to it; SwiGLU into
 //                  act[v][j] (j = the expert's top-k rank at position v)
 //   k_moe_down_b   per routed expert: its down rows once for its positions, o[v][j] = down . act[v][j]
@@ -19,6 +21,7 @@
 
 #include "dev_rows.h"
 #include "launch.h"
+#include "moe_norm.h"
 #include "prefill.h"
 
 namespace moert {
@@ -233,14 +236,20 @@ __global__ __launch_bounds__(kPfNT) void k_qkv_b(DMat m, const float* __restrict
 }
 
 // ------------------------------------------------------------------------------------------------------------
-// h[v][r] = h[v][r] + res * (Wo att[v])[r] for every position v (k_oproj's arithmetic per position).
+// h[v][r] = h[v][r] + res * (Wo att[v])[r] for every position v (k_oproj's arithmetic per position), then the
+// MoE-norm partials of each position's new rows into zp + v * kNormItems (k_oproj's epilogue per position).
 template <int DT, int K, int P>
 __global__ __launch_bounds__(kPfNT) void k_oproj_b(DMat m, const float* __restrict__ att, int nv, float res,
-                                                   float* __restrict__ h) {
+                                                   float* __restrict__ h, DMat router, const float* __restrict__ lnw,
+                                                   float* __restrict__ zp) {
   using G = Geo<DT, K>;
+  constexpr int RB = kPfWaves * P * G::RPW;  // rows of the workgroup: [r0, r0 + RB)
+  static_assert(RB % kNormBlk == 0, "the workgroup's rows must be whole partial blocks");
   __shared__ __align__(16) float xs[kPfGroup][K];
+  __shared__ float hn[kPfGroup][RB];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int sub = lane % G::LPR, rw = lane / G::LPR;
+  const int r0 = blockIdx.x * RB;
   const size_t base = ((size_t)blockIdx.x * kPfWaves + wave) * (P * G::RPW);
   size_t row[P];
   bool ok[P];
@@ -249,6 +258,8 @@ __global__ __launch_bounds__(kPfNT) void k_oproj_b(DMat m, const float* __restri
     row[p] = base + (size_t)p * G::RPW + rw;
     ok[p] = row[p] < (size_t)m.rows;
   }
+  NormPart<RB, kPfNT> np;
+  norm_part_fetch<RB, kPfNT>(router, lnw, r0, m.rows, np);
   Rows<DT, K, P> rr;
   rows_load<DT, K, P>(rr, m, row, ok, sub);
   DeqRows<DT, K, P> dw;
@@ -269,9 +280,14 @@ __global__ __launch_bounds__(kPfNT) void k_oproj_b(DMat m, const float* __restri
       for (int p = 0; p < P; p++)
         if (ok[p]) {
           const float hold = hv[row[p]];
-          hv[row[p]] = hold + res * out[p];
+          const float hnew = hold + res * out[p];
+          hv[row[p]] = hnew;
+          hn[v][row[p] - r0] = hnew;
         }
     }
+    __syncthreads();
+    for (int v = 0; v < n; v++)
+      norm_part_finish<RB, kPfNT>(np, &hn[v][0], router.dtype, router.rows, r0, H, zp + (size_t)(v0 + v) * kNormItems);
   }
 }
 
@@ -284,44 +300,49 @@ __host__ __device__ constexpr int route_b_waves(int dt) { return dt == DT_F32 ? 
 template <int DT, int K>
 __global__ __launch_bounds__(route_b_waves(DT) * 64) void k_route_b(DMat router, const float* __restrict__ bias,
                                                                const float* __restrict__ h,
-                                                               const float* __restrict__ lnw, float eps, int k,
+                                                               const float* __restrict__ lnw, float eps,
+                                                               const float* __restrict__ zp, int k,
                                                                float* __restrict__ xn, int* __restrict__ ids,
                                                                float* __restrict__ wts) {
-  using G = Geo<DT, K>;
   constexpr int NW = route_b_waves(DT), NT = NW * 64;
-  constexpr int RP = (64 + NW * G::RPW - 1) / (NW * G::RPW);
-  __shared__ __align__(16) float xs[K];
+  constexpr int IPW = (64 + NW - 1) / NW;  // router items per wave
+  constexpr int XP = (K + NT - 1) / NT;    // elements of h per thread
   __shared__ __align__(16) float lg[64];
   __shared__ int part[64][NW];
-  __shared__ float rs;
   const int v = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int sub = lane % G::LPR, rw = lane / G::LPR;
-  const int E = router.rows;
-  NormIn<K, NT> hin;
-  norm_fetch<K, NT>(h + (size_t)v * K, lnw, hin);
-  size_t row[RP];
-  bool ok[RP];
+  const int E = router.rows, nb = K / kNormBlk;
+  zp += (size_t)v * kNormItems;
+  NormItem ssi, it[IPW];
+  float bv[IPW], hv[XP], wv[XP];
+  norm_item_fetch(zp, E, lane, ssi);
 #pragma unroll
-  for (int p = 0; p < RP; p++) {
-    row[p] = (size_t)(p * NW + wave) * G::RPW + rw;
-    ok[p] = row[p] < (size_t)E;
+  for (int i = 0; i < IPW; i++) {
+    const int e = wave + i * NW, ec = e < E ? e : 0;
+    norm_item_fetch(zp, ec, lane, it[i]);
+    bv[i] = bias ? bias[ec] : 0.0f;
   }
-  Rows<DT, K, RP> rr;
-  rows_load<DT, K, RP>(rr, router, row, ok, sub);
-  float bv[RP];
 #pragma unroll
-  for (int p = 0; p < RP; p++) bv[p] = bias ? bias[ok[p] ? row[p] : 0] : 0.0f;
-  norm_finish<K, NT>(hin, eps, xs, &rs);
-  for (int i = threadIdx.x; i < K / 4; i += NT)
-    reinterpret_cast<float4*>(xn + (size_t)v * K)[i] = reinterpret_cast<const float4*>(xs)[i];
-  XReg<DT, K> xr;
-  load_x<DT, K>(xr, xs, sub);
-  float out[RP];
-  rows_fma<DT, K, RP>(rr, ok, xr, sub, out);
+  for (int e = 0; e < XP; e++) {
+    const int i = threadIdx.x + e * NT, ic = i < K ? i : 0;
+    hv[e] = h[(size_t)v * K + ic];
+    wv[e] = lnw[ic];
+  }
+  const float ss = norm_item_sum(ssi, nb, lane);
+  const float r = 1.0f / sqrtf(ss / (float)K + eps);
 #pragma unroll
-  for (int p = 0; p < RP; p++)
-    if (ok[p] && sub == 0) lg[row[p]] = bias ? out[p] + bv[p] : out[p];
+  for (int i = 0; i < IPW; i++) {
+    const int e = wave + i * NW;
+    if (e < E) {
+      const float z = norm_item_sum(it[i], nb, lane);
+      if (lane == 0) lg[e] = bias ? z * r + bv[i] : z * r;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < XP; e++) {
+    const int i = threadIdx.x + e * NT;
+    if (i < K) xn[(size_t)v * K + i] = wv[e] * (hv[e] * r);
+  }
   __syncthreads();
   int eid[8];
   const int rank = wg_rank<NW>(lg, E, lane, wave, part);
@@ -543,7 +564,8 @@ hipError_t launch_layer_b(hipStream_t s, const LayerDev& L, const Dims& d, const
 #define BODY(KK)                                                                                         \
   case KK: {                                                                                             \
     constexpr int RB = kPfWaves * kPfOprojP * Geo<DTC, KK>::RPW;                                         \
-    klaunch(k_oproj_b<DTC, KK, kPfOprojP>, cdiv(L.o.rows, RB), kPfNT, 0, s, L.o, p.att, nv, d.res_mult, p.h); \
+    klaunch(k_oproj_b<DTC, KK, kPfOprojP>, cdiv(L.o.rows, RB), kPfNT, 0, s, L.o, p.att, nv, d.res_mult, p.h, \
+            L.router, L.ln_moe, p.zpart);                                                                \
   } break;
   MOERT_DISPATCH(L.o.dtype, L.o.cols, BODY)
 #undef BODY
@@ -552,7 +574,7 @@ hipError_t launch_layer_b(hipStream_t s, const LayerDev& L, const Dims& d, const
 #define BODY(KK)                                                                                         \
   case KK: {                                                                                             \
     klaunch(k_route_b<DTC, KK>, nv, route_b_waves(DTC) * 64, 0, s, L.router, L.router_bias, p.h, L.ln_moe, d.eps, \
-            d.top_k, p.xn, p.ids, p.w);                                                                  \
+            p.zpart, d.top_k, p.xn, p.ids, p.w);                                                         \
   } break;
   MOERT_DISPATCH(L.router.dtype, L.router.cols, BODY)
 #undef BODY

@@ -506,6 +506,42 @@ void orc_route(const float* logits, const float* bias, int n, int k, int* ids, f
   }
 }
 
+// The MoE half's rmsnorm and router from partial sums over blocks of 8 rows (the engine's producer/consumer split,
+// lastro-rust_amd/csrc/moe_norm.h), rmsnorm model.rs:141-145 + router block.rs:56-62 with r factored out of the dots:
+//   per block b: z[e][b] = fmaf chain over t of W[e][8b+t] * (lnw[8b+t] * h[8b+t]); ss[b] = fmaf chain of h^2;
+//   per item: block b in lane b % 64, lanes add their blocks in increasing b from +0, then the 64-lane pairwise tree;
+//   r = 1/sqrtf(ss/H + eps); xn = lnw * (h * r); logits[e] = z[e] * r (+ bias[e]).
+void orc_moe_norm_route(const float* h, const float* lnw, const moert_tensor* router, const float* bias, int H, int E,
+                        float eps, float* xn, float* logits) {
+  const int nb = H / 8;
+  std::vector<float> w((size_t)E * H);
+  for (int e = 0; e < E; e++) dequant_row(router->data, router->dtype, H, (size_t)e, &w[(size_t)e * H]);
+  auto reduce = [&](const std::function<float(int)>& part) {
+    float acc[kLanes];
+    for (int l = 0; l < kLanes; l++) acc[l] = 0.0f;
+    for (int b = 0; b < nb; b++) acc[b % kLanes] = acc[b % kLanes] + part(b);
+    for (int st = 1; st < kLanes; st *= 2)
+      for (int l = 0; l < kLanes; l += 2 * st) acc[l] = acc[l] + acc[l + st];
+    return acc[0];
+  };
+  const float ss = reduce([&](int b) {
+    float a = 0.0f;
+    for (int t = 0; t < 8; t++) a = std::fmaf(h[8 * b + t], h[8 * b + t], a);
+    return a;
+  });
+  const float r = 1.0f / std::sqrt(ss / (float)H + eps);
+  for (int i = 0; i < H; i++) xn[i] = lnw[i] * (h[i] * r);
+  for (int e = 0; e < E; e++) {
+    const float* we = &w[(size_t)e * H];
+    const float z = reduce([&](int b) {
+      float a = 0.0f;
+      for (int t = 0; t < 8; t++) a = std::fmaf(we[8 * b + t], lnw[8 * b + t] * h[8 * b + t], a);
+      return a;
+    });
+    logits[e] = bias ? z * r + bias[e] : z * r;
+  }
+}
+
 void orc_swiglu(const float* h, int inter, float* a) {
   for (int j = 0; j < inter; j++) a[j] = silu_mul(h[j], h[inter + j]);
 }
@@ -974,9 +1010,8 @@ int orc_session_step(orc_session* s, int token, float* logits, int* route_ids, f
               c.attention_multiplier, s->tps, att.data());
     gemv(pool, L.o.data, L.o.dtype, H, qd, att.data(), o.data());
     for (int i = 0; i < H; i++) x[i] = x[i] + c.residual_multiplier * o[i];
-    orc_rmsnorm(x.data(), L.ln_moe, H, c.eps, xn.data());
-    gemv(pool, L.router.data, L.router.dtype, c.experts, H, xn.data(), rl.data());
-    orc_route(rl.data(), L.router_bias, c.experts, k, ids.data(), wts.data());
+    orc_moe_norm_route(x.data(), L.ln_moe, &L.router, L.router_bias, H, c.experts, c.eps, xn.data(), rl.data());
+    orc_route(rl.data(), nullptr, c.experts, k, ids.data(), wts.data());
     experts(pool, H, I, &L.gate_up, &L.down, xn.data(), ids.data(), wts.data(), k, y.data());
     for (int i = 0; i < H; i++) x[i] = x[i] + c.residual_multiplier * y[i];
     if (route_ids)

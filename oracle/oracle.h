@@ -45,6 +45,11 @@ void orc_rope(float* x, int n, int head_dim, const float* cs);
 /* Routing::from_logits with an optional bias added first. */
 void orc_route(const float* logits, const float* bias, int n, int k, int* ids, float* weights);
 void orc_swiglu(const float* h, int inter, float* a);
+/* The MoE half's rmsnorm + router logits (bias included) in the engine's partial-block order: per 8-row block b,
+ * z[e][b] and ss[b] as fmaf chains, reduced over b in the 64-lane order; r = 1/sqrtf(ss/H + eps),
+ * xn = lnw * (h * r), logits[e] = z[e] * r (+ bias[e]). */
+void orc_moe_norm_route(const float* h, const float* lnw, const moert_tensor* router, const float* bias, int H, int E,
+                        float eps, float* xn, float* logits);
 int orc_argmax(const float* v, int n);
 
 /* HostLayer::forward_cpu on a normalised x. */

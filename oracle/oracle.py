@@ -41,6 +41,7 @@ def lib() -> ctypes.CDLL:
             "orc_rope": (None, [vp, i, i, vp]),
             "orc_route": (None, [vp, vp, i, i, vp, vp]),
             "orc_swiglu": (None, [vp, i, vp]),
+            "orc_moe_norm_route": (None, [vp, vp, vp, vp, i, i, f, vp, vp]),
             "orc_argmax": (i, [vp, i]),
             "orc_moe_block": (None, [i, i, i, i, vp, vp, vp, vp, vp, vp, vp, vp, i]),
             "orc_attention": (None, [vp, vp, vp, i, i, i, i, i, f, i, vp]),
@@ -144,6 +145,18 @@ def route(logits, k, bias=None):
     w = np.empty(k, np.float32)
     lib().orc_route(_p(l), _p(None if bias is None else _f32(bias)), l.size, k, _p(ids), _p(w))
     return ids, w
+
+
+def moe_norm_route(h, lnw, router, dtype, experts, eps, bias=None):
+    """The MoE half's rmsnorm and router logits in the engine's partial-block order: (xn, logits)."""
+    mt = _moert()
+    h, lnw = _f32(h), _f32(lnw)
+    r = mt.moert_tensor(router.ctypes.data, dtype)
+    xn = np.empty_like(h)
+    lg = np.empty(experts, np.float32)
+    lib().orc_moe_norm_route(_p(h), _p(lnw), ctypes.byref(r), _p(None if bias is None else _f32(bias)), h.size,
+                             experts, eps, _p(xn), _p(lg))
+    return xn, lg
 
 
 def swiglu(h):

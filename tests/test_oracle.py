@@ -413,6 +413,77 @@ def test_batched_block_routes_every_position_like_the_single_position_block():
             assert np.array_equal(w[p].view(np.uint32), w1.view(np.uint32))
 
 
+# ---- MoE-half norm + router from 8-row partials ----------------------------------------------------------------------
+def test_moe_norm_route_known_answer():
+    """h = [3, 4, 0, ...] (H = 16), norm weights 1, eps 0: ss = 25, r = 1/sqrt(25/16) = 0.8, xn = [2.4, 3.2, 0...];
+    router rows all ones and alternating +1/-1 give z = [7, -1] and logits [5.6, -0.8]; a bias is added after."""
+    h = np.zeros(16, np.float32)
+    h[:2] = [3, 4]
+    w = np.ones((2, 16), np.float32)
+    w[1, 1::2] = -1
+    xn, lg = oracle.moe_norm_route(h, np.ones(16, np.float32), w.ravel(), moert.F32, 2, 0.0)
+    assert np.allclose(xn[:2], [2.4, 3.2], rtol=1e-6) and not xn[2:].any()
+    assert np.allclose(lg, [5.6, -0.8], rtol=1e-6)
+    _, lb = oracle.moe_norm_route(h, np.ones(16, np.float32), w.ravel(), moert.F32, 2, 0.0, bias=np.array([1, 2], np.float32))
+    assert np.allclose(lb, [6.6, 1.2], rtol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", [moert.Q8_0, moert.Q4_0, moert.F32])
+@pytest.mark.parametrize("H,E", [(1536, 40), (1024, 32), (256, 4), (512, 64)])
+def test_moe_norm_route_matches_float64_and_its_own_block_order(dtype, H, E):
+    """Against float64 rmsnorm + router over the dequantised weights (xn within 1e-6, logits within 1e-5 of the
+    largest); against a direct numpy restatement of the block order (per 8-row block fma chains, blocks summed per
+    lane b % 64, pairwise lane tree) bit for bit; and not the unblocked order (canonical rmsnorm, then dot): the two
+    must differ on some logit, so the block order is what is pinned."""
+    rng = np.random.default_rng(H + E + dtype)
+    h = rng.normal(size=H).astype(np.float32) * 3
+    lnw = (1 + 0.1 * rng.normal(size=H)).astype(np.float32)
+    w = moert.quantize(rng.normal(size=E * H).astype(np.float32) * 0.02, dtype) if dtype != moert.F32 else \
+        (rng.normal(size=E * H).astype(np.float32) * 0.02)
+    bias = rng.normal(size=E).astype(np.float32)
+    xn, lg = oracle.moe_norm_route(h, lnw, w, dtype, E, 1e-6, bias=bias)
+    wd = oracle.dequant(w, dtype, E * H).reshape(E, H).astype(np.float64)
+    h64 = h.astype(np.float64)
+    xn64 = lnw * h64 / np.sqrt((h64 * h64).mean() + 1e-6)
+    assert np.abs(xn - xn64).max() <= 1e-6 * np.abs(xn64).max()
+    lg64 = wd @ xn64 + bias
+    assert np.abs(lg - lg64).max() <= 1e-5 * np.abs(lg64).max()
+    # numpy restatement with float32 rounding at every step (np.float32 arithmetic; fma emulated in float64, exact
+    # for one product + one addend then rounded once)
+    def fma(a, b, c):
+        return np.float32(np.float64(a) * np.float64(b) + np.float64(c))
+    def reduce(parts):
+        acc = [np.float32(0)] * 64
+        for b, v in enumerate(parts):
+            acc[b % 64] = np.float32(acc[b % 64] + v)
+        s = 1
+        while s < 64:
+            for l in range(0, 64, 2 * s):
+                acc[l] = np.float32(acc[l] + acc[l + s])
+            s *= 2
+        return acc[0]
+    nb = H // 8
+    ssp = []
+    for b in range(nb):
+        a = np.float32(0)
+        for t in range(8):
+            a = fma(h[8 * b + t], h[8 * b + t], a)
+        ssp.append(a)
+    r = np.float32(1) / np.sqrt(np.float32(reduce(ssp) / np.float32(H) + np.float32(1e-6)), dtype=np.float32)
+    wf = wd.astype(np.float32)
+    for e in range(0, E, max(1, E // 4)):
+        zp = []
+        for b in range(nb):
+            a = np.float32(0)
+            for t in range(8):
+                a = fma(wf[e, 8 * b + t], np.float32(lnw[8 * b + t] * h[8 * b + t]), a)
+            zp.append(a)
+        want = np.float32(np.float32(reduce(zp) * r) + bias[e])
+        assert np.float32(lg[e]).view(np.uint32) == want.view(np.uint32), e
+    old = oracle.gemv(w, dtype, E, H, oracle.rmsnorm(h, lnw, 1e-6)) + bias
+    assert not np.array_equal(old.view(np.uint32), lg.view(np.uint32))
+
+
 # ---- expert cache (LRU) -----------------------------------------------------------------------------------------------
 def test_lru_known_answers():
     """Hand-worked traces of the LruSync rule (tests/model.rs:380-412): a 2-slot cache over 4 tokens; the pin rule
