@@ -763,8 +763,6 @@ __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restric
     row[p] = base + (size_t)p * G::RPW + rw;
     ok[p] = row[p] < (size_t)m.rows;
   }
-  NormPart<RB, kBlock> np;
-  norm_part_fetch<RB, kBlock>(router, lnw, r0, m.rows, np);
   CopyIn<K, kBlock> ain;
   copy_fetch<K, kBlock>(att, ain);
   float hold[P];
@@ -772,6 +770,11 @@ __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restric
   for (int p = 0; p < P; p++) hold[p] = (ok[p] && sub == 0) ? h[row[p]] : 0.0f;
   Rows<DT, K, P> rr;
   rows_load<DT, K, P>(rr, m, row, ok, sub);
+  // the router columns and norm weights of the epilogue last: loads complete in issue order, so they must not sit
+  // in front of the activation or the weight rows
+  __builtin_amdgcn_sched_barrier(0);
+  NormPart<RB, kBlock> np;
+  norm_part_fetch<RB, kBlock>(router, lnw, r0, m.rows, np);
   copy_finish<K, kBlock>(ain, xs);
   TL_PHASE(tl, 2);
   XReg<DT, K> xr;
@@ -1122,9 +1125,13 @@ __device__ __forceinline__ void wave_argmax(int& bk, int& bi) {
   argmax_stage<32>(bk, bi);
 }
 
+// Row group g (NB batches of P rows per wave, 4 waves) = rows [g * RG, g * RG + RG). The grid holds at most as many
+// workgroups as are resident at once, and a workgroup takes groups blockIdx.x, blockIdx.x + gridDim.x, ...: with
+// one group past a whole number of resident waves (49155 rows = 768 groups of 64 + 3 rows) the last small group
+// runs as a second group of an early workgroup instead of waiting for a free slot.
 template <int DT, int K, int P, int NB>
 __global__ __launch_bounds__(kBlock) void k_head(DMat m, const float* __restrict__ h, const float* __restrict__ lnw,
-                                                 float eps, float ls, float* __restrict__ logits,
+                                                 float eps, float ls, int groups, float* __restrict__ logits,
                                                  int2* __restrict__ best, Tl tl) {
   TL_START(tl);
   using G = Geo<DT, K>;
@@ -1134,16 +1141,19 @@ __global__ __launch_bounds__(kBlock) void k_head(DMat m, const float* __restrict
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int sub = lane % G::LPR, rw = lane / G::LPR;
   // NB batches of P rows per wave; the next batch's loads are issued before the current batch's arithmetic
-  const size_t wbase = ((size_t)blockIdx.x * kWavesPerBlock + wave) * (NB * P * G::RPW);
   size_t row[NB][P];
   bool ok[NB][P];
+  auto group_rows = [&](int g) {
+    const size_t wbase = ((size_t)g * kWavesPerBlock + wave) * (NB * P * G::RPW);
 #pragma unroll
-  for (int bt = 0; bt < NB; bt++)
+    for (int bt = 0; bt < NB; bt++)
 #pragma unroll
-    for (int p = 0; p < P; p++) {
-      row[bt][p] = wbase + (size_t)(bt * P + p) * G::RPW + rw;
-      ok[bt][p] = row[bt][p] < (size_t)m.rows;
-    }
+      for (int p = 0; p < P; p++) {
+        row[bt][p] = wbase + (size_t)(bt * P + p) * G::RPW + rw;
+        ok[bt][p] = row[bt][p] < (size_t)m.rows;
+      }
+  };
+  group_rows(blockIdx.x);
   NormIn<K, kBlock> hin;
   norm_fetch<K, kBlock>(h, lnw, hin);
   Rows<DT, K, P> cur, nxt;
@@ -1153,24 +1163,30 @@ __global__ __launch_bounds__(kBlock) void k_head(DMat m, const float* __restrict
   XReg<DT, K> xr;
   load_x<DT, K>(xr, xs, sub);
   int bk = INT_MIN, bi = -1;
+  for (int g = blockIdx.x;;) {
 #pragma unroll
-  for (int bt = 0; bt < NB; bt++) {
-    if (bt + 1 < NB) rows_load<DT, K, P>(nxt, m, row[bt + 1], ok[bt + 1], sub);
-    float out[P];
-    rows_fma<DT, K, P>(cur, ok[bt], xr, sub, out);
+    for (int bt = 0; bt < NB; bt++) {
+      if (bt + 1 < NB) rows_load<DT, K, P>(nxt, m, row[bt + 1], ok[bt + 1], sub);
+      float out[P];
+      rows_fma<DT, K, P>(cur, ok[bt], xr, sub, out);
 #pragma unroll
-    for (int p = 0; p < P; p++) {
-      if (ok[bt][p]) {
-        float v = out[p] / ls;
-        if (sub == 0) logits[row[bt][p]] = v;
-        int kk = total_key(v);
-        if (later_better(kk, (int)row[bt][p], bk, bi)) {
-          bk = kk;
-          bi = (int)row[bt][p];
+      for (int p = 0; p < P; p++) {
+        if (ok[bt][p]) {
+          float v = out[p] / ls;
+          if (sub == 0) logits[row[bt][p]] = v;
+          int kk = total_key(v);
+          if (later_better(kk, (int)row[bt][p], bk, bi)) {
+            bk = kk;
+            bi = (int)row[bt][p];
+          }
         }
       }
+      if (bt + 1 < NB) cur = nxt;
     }
-    if (bt + 1 < NB) cur = nxt;
+    g += gridDim.x;
+    if (g >= groups) break;
+    group_rows(g);
+    rows_load<DT, K, P>(cur, m, row[0], ok[0], sub);
   }
   wave_argmax(bk, bi);
   if (lane == 0) {
@@ -1558,19 +1574,47 @@ hipError_t launch_expert_down(hipStream_t s, const LayerDev& L, const Dims& d, c
 
 constexpr int kHeadNB = 4;
 
-int head_blocks(const DMat& head) {
+// Row groups of the head (rows per workgroup pass: 4 waves x kHeadNB batches x kHeadP rows x rows per wave).
+static int head_groups(const DMat& head) {
   int ce = head.dtype == DT_Q8_0 ? 16 : head.dtype == DT_Q4_0 ? 32 : 4;
   int rpw = kWave / lanes_per_row(head.cols / ce);
   return cdiv(head.rows, kWavesPerBlock * kHeadNB * kHeadP * rpw);
 }
 
+// Workgroups of k_head<DT, K> resident on the device at once (occupancy x compute units).
+template <int DT, int K>
+static int head_resident() {
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_head<DT, K, kHeadP, kHeadNB>, kBlock, 0) != hipSuccess ||
+      cus < 1 || per_cu < 1)
+    return 1 << 30;  // unknown: one workgroup per group
+  return cus * per_cu;
+}
+
+int head_blocks(const DMat& head) {
+  int resident = 1 << 30;
+#define HB(DTC, KK) \
+  case KK:          \
+    resident = head_resident<DTC, KK>(); \
+    break;
+  switch (head.dtype) {
+    case DT_Q8_0: switch (head.cols) { HB(DT_Q8_0, 128) HB(DT_Q8_0, 256) HB(DT_Q8_0, 512) HB(DT_Q8_0, 1024) HB(DT_Q8_0, 1536) } break;
+    case DT_Q4_0: switch (head.cols) { HB(DT_Q4_0, 128) HB(DT_Q4_0, 256) HB(DT_Q4_0, 512) HB(DT_Q4_0, 1024) HB(DT_Q4_0, 1536) } break;
+    case DT_F32: switch (head.cols) { HB(DT_F32, 128) HB(DT_F32, 256) HB(DT_F32, 512) HB(DT_F32, 1024) HB(DT_F32, 1536) } break;
+  }
+#undef HB
+  return std::min(head_groups(head), resident);
+}
+
 hipError_t launch_head(hipStream_t s, const DMat& head, const float* norm, const Dims& d, const StepBufs& b, Tl tl) {
+  const int groups = head_groups(head), grid = head_blocks(head);
 #define BODY(KK)                                                                                        \
-  case KK: {                                                                                            \
-    constexpr int RB = rows_per_block<DTC, KK, kHeadP>() * kHeadNB;                                     \
-    klaunch(k_head<DTC, KK, kHeadP, kHeadNB>, cdiv(head.rows, RB), kBlock, 0, s, head, b.h, norm, d.eps,     \
-                                                                   d.logits_scaling, b.logits, b.best, tl); \
-  } break;
+  case KK:                                                                                              \
+    klaunch(k_head<DTC, KK, kHeadP, kHeadNB>, grid, kBlock, 0, s, head, b.h, norm, d.eps,                 \
+            d.logits_scaling, groups, b.logits, b.best, tl);                                            \
+    break;
   MOERT_DISPATCH(head.dtype, head.cols, BODY)
 #undef BODY
   return hipGetLastError();

@@ -258,10 +258,11 @@ __global__ __launch_bounds__(kPfNT) void k_oproj_b(DMat m, const float* __restri
     row[p] = base + (size_t)p * G::RPW + rw;
     ok[p] = row[p] < (size_t)m.rows;
   }
-  NormPart<RB, kPfNT> np;
-  norm_part_fetch<RB, kPfNT>(router, lnw, r0, m.rows, np);
   Rows<DT, K, P> rr;
   rows_load<DT, K, P>(rr, m, row, ok, sub);
+  __builtin_amdgcn_sched_barrier(0);
+  NormPart<RB, kPfNT> np;
+  norm_part_fetch<RB, kPfNT>(router, lnw, r0, m.rows, np);
   DeqRows<DT, K, P> dw;
   deq_rows<DT, K, P>(rr, dw);
   const int H = m.rows;
