@@ -491,7 +491,8 @@ static int model_create(const moert_config* c, const moert_model_weights* w, int
   for (int l = 0; l < c->layers; l++) {
     const moert_layer_weights& L = w->layers[l];
     CHECK_CFG(L.q.dtype == L.k.dtype && L.q.dtype == L.v.dtype, "layer %d: q, k, v must share a dtype", l);
-    CHECK_CFG(L.router.dtype == L.gate_up.dtype, "layer %d: router and gate_up must share a dtype", l);
+    CHECK_CFG(L.router.dtype == L.gate_up.dtype && L.o.dtype == L.router.dtype,
+              "layer %d: o, router and gate_up must share a dtype", l);
     CHECK_CFG(L.ln_attn && L.ln_moe, "layer %d: missing norm weights", l);
   }
   moert_model* m = new moert_model;

@@ -741,7 +741,8 @@ __global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ p
 // ------------------------------------------------------------------------------------------------------------
 // Output projection with the residual in the epilogue: h[r] = h[r] + res * (Wo att)[r] (gemv o + axpby,
 // gpu_model.rs:386-394; model.rs:224-227). The epilogue also writes the MoE-norm partials of the workgroup's rows
-// (moe_norm.h: the router dots and the sum of squares of its 8-row blocks of the new h) for the router kernel.
+// (moe_norm.h: the router dots and the sum of squares of its 8-row blocks of the new h) for the router kernel; the
+// router has the output projection's dtype DT.
 template <int DT, int K, int P>
 __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restrict__ att, float res,
                                                   float* __restrict__ h, DMat router, const float* __restrict__ lnw,
@@ -767,15 +768,14 @@ __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restric
   copy_fetch<K, kBlock>(att, ain);
   float hold[P];
 #pragma unroll
-  for (int p = 0; p < P; p++) hold[p] = (ok[p] && sub == 0) ? h[row[p]] : 0.0f;
+  for (int p = 0; p < P; p++) hold[p] = h[ok[p] ? row[p] : 0];  // clamped, not guarded: no branch in the load run
   Rows<DT, K, P> rr;
   rows_load<DT, K, P>(rr, m, row, ok, sub);
-  // the router columns and norm weights of the epilogue last: loads complete in issue order, so they must not sit
-  // in front of the activation or the weight rows
-  __builtin_amdgcn_sched_barrier(0);
-  NormPart<RB, kBlock> np;
-  norm_part_fetch<RB, kBlock>(router, lnw, r0, m.rows, np);
   copy_finish<K, kBlock>(ain, xs);
+  // the router columns and norm weights of the epilogue after the activation has arrived: loads complete in issue
+  // order, so they must not sit in front of it (they arrive with the weight rows, before the epilogue)
+  NormPart<RB, kBlock> np;
+  norm_part_fetch<DT, RB, kBlock>(router, lnw, r0, m.rows, np);
   TL_PHASE(tl, 2);
   XReg<DT, K> xr;
   load_x<DT, K>(xr, xs, sub);
@@ -790,7 +790,7 @@ __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restric
       hn[row[p] - r0] = hv;
     }
   __syncthreads();
-  norm_part_finish<RB, kBlock>(np, hn, router.dtype, router.rows, r0, m.rows, zp);
+  norm_part_finish<DT, RB, kBlock>(np, hn, router.rows, r0, m.rows, zp);
   TL_END(tl);
 }
 
@@ -1125,13 +1125,14 @@ __device__ __forceinline__ void wave_argmax(int& bk, int& bi) {
   argmax_stage<32>(bk, bi);
 }
 
-// Row group g (NB batches of P rows per wave, 4 waves) = rows [g * RG, g * RG + RG). The grid holds at most as many
-// workgroups as are resident at once, and a workgroup takes groups blockIdx.x, blockIdx.x + gridDim.x, ...: with
-// one group past a whole number of resident waves (49155 rows = 768 groups of 64 + 3 rows) the last small group
-// runs as a second group of an early workgroup instead of waiting for a free slot.
-template <int DT, int K, int P, int NB>
+// The rows are cut into slots of RPW rows (one pass of a wave) and the slots are dealt out to the grid's waves in
+// contiguous runs, as evenly as possible (the first S % W waves take one more): with at most as many workgroups as
+// are resident at once, 49155 rows on 3072 waves is 16 slots each and 17 for three waves, instead of a 769th
+// workgroup waiting for a free slot. A wave streams its run in batches of P slots, the next batch's loads issued
+// before the current batch's arithmetic.
+template <int DT, int K, int P>
 __global__ __launch_bounds__(kBlock) void k_head(DMat m, const float* __restrict__ h, const float* __restrict__ lnw,
-                                                 float eps, float ls, int groups, float* __restrict__ logits,
+                                                 float eps, float ls, float* __restrict__ logits,
                                                  int2* __restrict__ best, Tl tl) {
   TL_START(tl);
   using G = Geo<DT, K>;
@@ -1140,53 +1141,57 @@ __global__ __launch_bounds__(kBlock) void k_head(DMat m, const float* __restrict
   __shared__ int sk[kWavesPerBlock], si[kWavesPerBlock];
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int sub = lane % G::LPR, rw = lane / G::LPR;
-  // NB batches of P rows per wave; the next batch's loads are issued before the current batch's arithmetic
-  size_t row[NB][P];
-  bool ok[NB][P];
-  auto group_rows = [&](int g) {
-    const size_t wbase = ((size_t)g * kWavesPerBlock + wave) * (NB * P * G::RPW);
+  const int slots = (m.rows + G::RPW - 1) / G::RPW, waves = gridDim.x * kWavesPerBlock;
+  const int wv = blockIdx.x * kWavesPerBlock + wave;
+  const int base = slots / waves, extra = slots % waves;
+  const int s0 = wv * base + min(wv, extra), ns = base + (wv < extra ? 1 : 0);
+  const int nbat = (ns + P - 1) / P;
+  size_t row[P];
+  bool ok[P];
+  auto batch_rows = [&](int bt) {
 #pragma unroll
-    for (int bt = 0; bt < NB; bt++)
-#pragma unroll
-      for (int p = 0; p < P; p++) {
-        row[bt][p] = wbase + (size_t)(bt * P + p) * G::RPW + rw;
-        ok[bt][p] = row[bt][p] < (size_t)m.rows;
-      }
+    for (int p = 0; p < P; p++) {
+      row[p] = (size_t)(s0 + bt * P + p) * G::RPW + rw;
+      ok[p] = bt * P + p < ns && row[p] < (size_t)m.rows;
+    }
   };
-  group_rows(blockIdx.x);
+  batch_rows(0);
   NormIn<K, kBlock> hin;
   norm_fetch<K, kBlock>(h, lnw, hin);
   Rows<DT, K, P> cur, nxt;
-  rows_load<DT, K, P>(cur, m, row[0], ok[0], sub);
+  rows_load<DT, K, P>(cur, m, row, ok, sub);
   norm_finish<K, kBlock>(hin, eps, xs, &rs);
   TL_PHASE(tl, 2);
   XReg<DT, K> xr;
   load_x<DT, K>(xr, xs, sub);
   int bk = INT_MIN, bi = -1;
-  for (int g = blockIdx.x;;) {
+  for (int bt = 0; bt < nbat; bt++) {
+    size_t rcur[P];
+    bool ocur[P];
 #pragma unroll
-    for (int bt = 0; bt < NB; bt++) {
-      if (bt + 1 < NB) rows_load<DT, K, P>(nxt, m, row[bt + 1], ok[bt + 1], sub);
-      float out[P];
-      rows_fma<DT, K, P>(cur, ok[bt], xr, sub, out);
+    for (int p = 0; p < P; p++) {
+      rcur[p] = row[p];
+      ocur[p] = ok[p];
+    }
+    if (bt + 1 < nbat) {
+      batch_rows(bt + 1);
+      rows_load<DT, K, P>(nxt, m, row, ok, sub);
+    }
+    float out[P];
+    rows_fma<DT, K, P>(cur, ocur, xr, sub, out);
 #pragma unroll
-      for (int p = 0; p < P; p++) {
-        if (ok[bt][p]) {
-          float v = out[p] / ls;
-          if (sub == 0) logits[row[bt][p]] = v;
-          int kk = total_key(v);
-          if (later_better(kk, (int)row[bt][p], bk, bi)) {
-            bk = kk;
-            bi = (int)row[bt][p];
-          }
+    for (int p = 0; p < P; p++) {
+      if (ocur[p]) {
+        float v = out[p] / ls;
+        if (sub == 0) logits[rcur[p]] = v;
+        int kk = total_key(v);
+        if (later_better(kk, (int)rcur[p], bk, bi)) {
+          bk = kk;
+          bi = (int)rcur[p];
         }
       }
-      if (bt + 1 < NB) cur = nxt;
     }
-    g += gridDim.x;
-    if (g >= groups) break;
-    group_rows(g);
-    rows_load<DT, K, P>(cur, m, row[0], ok[0], sub);
+    cur = nxt;
   }
   wave_argmax(bk, bi);
   if (lane == 0) {
@@ -1574,7 +1579,8 @@ hipError_t launch_expert_down(hipStream_t s, const LayerDev& L, const Dims& d, c
 
 constexpr int kHeadNB = 4;
 
-// Row groups of the head (rows per workgroup pass: 4 waves x kHeadNB batches x kHeadP rows x rows per wave).
+// Rows of the head per workgroup at kHeadNB batches per wave (the grid's upper bound: the rows are then dealt out
+// to the resident waves).
 static int head_groups(const DMat& head) {
   int ce = head.dtype == DT_Q8_0 ? 16 : head.dtype == DT_Q4_0 ? 32 : 4;
   int rpw = kWave / lanes_per_row(head.cols / ce);
@@ -1587,9 +1593,9 @@ static int head_resident() {
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_head<DT, K, kHeadP, kHeadNB>, kBlock, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_head<DT, K, kHeadP>, kBlock, 0) != hipSuccess ||
       cus < 1 || per_cu < 1)
-    return 1 << 30;  // unknown: one workgroup per group
+    return 1 << 30;  // unknown: the group count alone
   return cus * per_cu;
 }
 
@@ -1609,11 +1615,11 @@ int head_blocks(const DMat& head) {
 }
 
 hipError_t launch_head(hipStream_t s, const DMat& head, const float* norm, const Dims& d, const StepBufs& b, Tl tl) {
-  const int groups = head_groups(head), grid = head_blocks(head);
+  const int grid = head_blocks(head);
 #define BODY(KK)                                                                                        \
   case KK:                                                                                              \
-    klaunch(k_head<DTC, KK, kHeadP, kHeadNB>, grid, kBlock, 0, s, head, b.h, norm, d.eps,                 \
-            d.logits_scaling, groups, b.logits, b.best, tl);                                            \
+    klaunch(k_head<DTC, KK, kHeadP>, grid, kBlock, 0, s, head, b.h, norm, d.eps, d.logits_scaling, b.logits, \
+            b.best, tl);                                                                                \
     break;
   MOERT_DISPATCH(head.dtype, head.cols, BODY)
 #undef BODY

@@ -20,18 +20,19 @@ constexpr int kNormBlk = 8;       // rows per partial block
 constexpr int kNormMaxBlk = 256;  // blocks per item in the partial buffer (hidden <= 2048)
 constexpr int kNormItems = 65 * kNormMaxBlk;  // floats of one position's partials: [E + 1 <= 65][kNormMaxBlk]
 
-// Raw weights of 8 consecutive columns [c0, c0 + 8) of row e of a router matrix (c0 a multiple of 8): Q8_0 / Q4_0
-// 8 payload bytes (w[0..1]) and the block's scale bits, f32 the 8 values. The dtype is a run-time value (uniform
-// over the workgroup).
+// Raw weights of 8 consecutive columns [c0, c0 + 8) of row e of a router matrix (c0 a multiple of 8) of dtype DT:
+// Q8_0 / Q4_0 8 payload bytes (w[0..1]) and the block's scale bits, f32 the 8 values. The dtype is a template
+// parameter: a run-time branch around these loads would split the producer kernel's load run and make it wait.
 struct Col8 {
   uint32_t w[8];
   uint32_t d;
 };
 
+template <int DT>
 __device__ __forceinline__ Col8 load_col8(const DMat& m, int e, int c0) {
   Col8 c;
   const size_t row = (size_t)e;
-  if (m.dtype == DT_F32) {
+  if (DT == DT_F32) {
     const uint4* p = reinterpret_cast<const uint4*>(m.q + (row * m.cols + c0) * 4);
     const uint4 a = p[0], b = p[1];
     c.w[0] = a.x; c.w[1] = a.y; c.w[2] = a.z; c.w[3] = a.w;
@@ -39,7 +40,7 @@ __device__ __forceinline__ Col8 load_col8(const DMat& m, int e, int c0) {
     c.d = 0x3c00u;
   } else {
     const size_t off =
-        m.dtype == DT_Q8_0 ? row * m.cols + c0 : row * (m.cols / 2) + (size_t)(c0 / 32) * 16 + (c0 & 15);
+        DT == DT_Q8_0 ? row * m.cols + c0 : row * (m.cols / 2) + (size_t)(c0 / 32) * 16 + (c0 & 15);
     const uint2 v = *reinterpret_cast<const uint2*>(m.q + off);
     c.w[0] = v.x;
     c.w[1] = v.y;
@@ -49,17 +50,19 @@ __device__ __forceinline__ Col8 load_col8(const DMat& m, int e, int c0) {
   return c;
 }
 
-// Element t of a Col8 of dtype dt (c0 says which nibble of a Q4_0 byte holds the columns): q * d, exact.
-__device__ __forceinline__ float col8_elem(const Col8& c, int dt, int t, int c0) {
-  if (dt == DT_F32) return __uint_as_float(c.w[t]);
+// Element t of a Col8 (c0 says which nibble of a Q4_0 byte holds the columns): q * d, exact.
+template <int DT>
+__device__ __forceinline__ float col8_elem(const Col8& c, int t, int c0) {
+  if (DT == DT_F32) return __uint_as_float(c.w[t]);
   const uint32_t byte = (c.w[t >> 2] >> (8 * (t & 3))) & 0xffu;
   const float d = h2f((uint16_t)c.d);
-  if (dt == DT_Q8_0) return (float)(int8_t)byte * d;
+  if (DT == DT_Q8_0) return (float)(int8_t)byte * d;
   const int nib = (c0 & 31) >= 16 ? (int)(byte >> 4) : (int)(byte & 15u);
   return (float)(nib - 8) * d;
 }
 
-// Producer side, for a workgroup of NT threads that owns rows [r0, r0 + RB) of h (RB a multiple of 8): its
+// Producer side, for a workgroup of NT threads that owns rows [r0, r0 + RB) of h (RB a multiple of 8) and a router
+// of dtype DT: its
 // RB / 8 blocks x (E + 1) items, IPT per thread. norm_part_fetch issues the router and norm-weight loads (place it
 // before the kernel's own weight loads); norm_part_finish runs once the new rows sit in LDS hn[RB] (after a
 // workgroup barrier) and writes the partials of blocks r0/8 ... into zp ([E + 1][kNormMaxBlk]).
@@ -71,7 +74,7 @@ struct NormPart {
   float4 l0[IPT], l1[IPT];
 };
 
-template <int RB, int NT>
+template <int DT, int RB, int NT>
 __device__ __forceinline__ void norm_part_fetch(const DMat& router, const float* __restrict__ lnw, int r0, int H,
                                                 NormPart<RB, NT>& np) {
   using NP = NormPart<RB, NT>;
@@ -83,15 +86,15 @@ __device__ __forceinline__ void norm_part_fetch(const DMat& router, const float*
     const int blk = it / (E + 1), e = it % (E + 1);
     int c0 = r0 + kNormBlk * blk;
     c0 = c0 < H ? c0 : 0;
-    np.w[i] = load_col8(router, e < E ? e : 0, c0);
+    np.w[i] = load_col8<DT>(router, e < E ? e : 0, c0);
     np.l0[i] = *reinterpret_cast<const float4*>(lnw + c0);
     np.l1[i] = *reinterpret_cast<const float4*>(lnw + c0 + 4);
   }
 }
 
-template <int RB, int NT>
-__device__ __forceinline__ void norm_part_finish(const NormPart<RB, NT>& np, const float* hn, int dt, int E, int r0,
-                                                 int H, float* __restrict__ zp) {
+template <int DT, int RB, int NT>
+__device__ __forceinline__ void norm_part_finish(const NormPart<RB, NT>& np, const float* hn, int E, int r0, int H,
+                                                 float* __restrict__ zp) {
   using NP = NormPart<RB, NT>;
   const int items = NP::NBLK * (E + 1);
 #pragma unroll
@@ -107,7 +110,7 @@ __device__ __forceinline__ void norm_part_finish(const NormPart<RB, NT>& np, con
     float acc = 0.0f;
     if (e < E) {
 #pragma unroll
-      for (int t = 0; t < kNormBlk; t++) acc = __builtin_fmaf(col8_elem(np.w[i], dt, t, c0), lw[t] * hb[t], acc);
+      for (int t = 0; t < kNormBlk; t++) acc = __builtin_fmaf(col8_elem<DT>(np.w[i], t, c0), lw[t] * hb[t], acc);
     } else {
 #pragma unroll
       for (int t = 0; t < kNormBlk; t++) acc = __builtin_fmaf(hb[t], hb[t], acc);

@@ -262,7 +262,7 @@ __global__ __launch_bounds__(kPfNT) void k_oproj_b(DMat m, const float* __restri
   rows_load<DT, K, P>(rr, m, row, ok, sub);
   __builtin_amdgcn_sched_barrier(0);
   NormPart<RB, kPfNT> np;
-  norm_part_fetch<RB, kPfNT>(router, lnw, r0, m.rows, np);
+  norm_part_fetch<DT, RB, kPfNT>(router, lnw, r0, m.rows, np);
   DeqRows<DT, K, P> dw;
   deq_rows<DT, K, P>(rr, dw);
   const int H = m.rows;
@@ -288,7 +288,7 @@ __global__ __launch_bounds__(kPfNT) void k_oproj_b(DMat m, const float* __restri
     }
     __syncthreads();
     for (int v = 0; v < n; v++)
-      norm_part_finish<RB, kPfNT>(np, &hn[v][0], router.dtype, router.rows, r0, H, zp + (size_t)(v0 + v) * kNormItems);
+      norm_part_finish<DT, RB, kPfNT>(np, &hn[v][0], router.rows, r0, H, zp + (size_t)(v0 + v) * kNormItems);
   }
 }
 
