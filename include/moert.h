@@ -261,6 +261,17 @@ int moert_rope(float* x, int heads, int head_dim, float theta, int pos);
 int moert_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache, int heads, int kv_heads,
                       int head_dim, int max_len, int len, float scale, int tiles_per_split, float* out);
 
+/* moert_attn_decode for callers that cannot allocate device memory (code under graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc); it has no counterpart in the reference. q_dev, k_cache_dev, v_cache_dev and
+ * out_dev are the caller's device buffers (layouts as moert_attn_decode); the work is enqueued on `stream` (a
+ * hipStream_t, NULL for the default stream) and the call returns without synchronising. The split partials and the
+ * length word live in a fixed device scratch of 1,081,600 bytes per GPU, held until the process ends: heads x splits
+ * must not exceed 64 x 64 (MOERT_E_CONFIG otherwise). No hipMalloc, hipFree or memset is made. Calls that overlap
+ * on one GPU (several streams or threads) share that GPU's scratch and race. */
+int moert_attn_decode_noalloc(const float* q_dev, const uint16_t* k_cache_dev, const uint16_t* v_cache_dev, int heads,
+                              int kv_heads, int head_dim, int max_len, int len, float scale, int tiles_per_split,
+                              float* out_dev, void* stream);
+
 /* Achievable HBM bandwidth reference: mean microseconds of one device-to-device streaming copy of `bytes`
  * (multiple of 16) over `iters` launches, each timed by its own dispatch events. No reference counterpart (the
  * reference measures PCIe and HBM rates with separate CUDA tools); used to calibrate the roofline. */

@@ -22,6 +22,7 @@
 #include "grouped.h"
 #include "kernels.h"
 #include "moe_norm.h"
+#include "noalloc.h"
 #include "prefill.h"
 
 using namespace moert;
@@ -1366,6 +1367,31 @@ int moert_attn_decode(const float* q, const uint16_t* k_cache, const uint16_t* v
   TRY(sc.dev(&dout, (size_t)heads * 64));
   CHECK_HIP(launch_attn_unit(sc.s, dq, dk, dv, heads, kv_heads, max_len, dlen, scale, tiles_per_split, part, dout));
   TRY(sc.get(out, dout, (size_t)heads * 64 * 4));
+  return MOERT_OK;
+}
+
+int moert_attn_decode_noalloc(const float* q_dev, const uint16_t* k_cache_dev, const uint16_t* v_cache_dev, int heads,
+                              int kv_heads, int head_dim, int max_len, int len, float scale, int tiles_per_split,
+                              float* out_dev, void* stream) {
+  CHECK_CFG(q_dev && k_cache_dev && v_cache_dev && out_dev, "attn_noalloc: null argument");
+  CHECK_CFG(head_dim == 64 && heads >= 1 && kv_heads >= 1 && heads % kv_heads == 0 && heads / kv_heads <= 4 &&
+                max_len >= 64 && max_len % 64 == 0 && len >= 1 && len <= max_len && tiles_per_split >= 1 &&
+                attn_splits_for(max_len, tiles_per_split) <= 64,
+            "attn_noalloc: heads %d, kv %d, d %d, max_len %d, len %d, tiles_per_split %d", heads, kv_heads, head_dim,
+            max_len, len, tiles_per_split);
+  const size_t need = kNoallocHeader + (size_t)heads * attn_splits_for(max_len, tiles_per_split) * 66 * 4;
+  CHECK_CFG(need <= kNoallocScratchBytes,
+            "attn_noalloc: %d heads x %d splits need %zu bytes of partials; the fixed scratch holds %zu", heads,
+            attn_splits_for(max_len, tiles_per_split), need - kNoallocHeader, kNoallocScratchBytes - kNoallocHeader);
+  hipError_t e;
+  uint8_t* base = (uint8_t*)noalloc_scratch(&e);
+  CHECK_HIP(e);
+  hipStream_t s = (hipStream_t)stream;
+  int* lenp = (int*)base;
+  float* part = (float*)(base + kNoallocHeader);
+  CHECK_HIP(launch_set_int(s, lenp, len));
+  CHECK_HIP(launch_attn_unit(s, q_dev, k_cache_dev, v_cache_dev, heads, kv_heads, max_len, lenp, scale,
+                             tiles_per_split, part, out_dev));
   return MOERT_OK;
 }
 

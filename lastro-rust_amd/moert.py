@@ -118,6 +118,7 @@ def lib() -> ctypes.CDLL:
             "moert_rmsnorm": (i, [vp, vp, i, f, vp]),
             "moert_rope": (i, [vp, i, i, f, i]),
             "moert_attn_decode": (i, [vp, vp, vp, i, i, i, i, i, f, i, vp]),
+            "moert_attn_decode_noalloc": (i, [vp, vp, vp, i, i, i, i, i, f, i, vp, vp]),
             "moert_exp_device": (i, [vp, vp, i]),
             "moert_copy_probe": (i, [sz, i, ctypes.POINTER(ctypes.c_double)]),
             "moert_read_probe": (i, [sz, i, ctypes.POINTER(ctypes.c_double)]),
@@ -145,7 +146,8 @@ EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moer
             "moert_time_steps", "moert_time_kernel", "moert_timeline_step", "moert_block_create", "moert_block_destroy",
             "moert_block_forward", "moert_block_time", "moert_block_forward_batched",
             "moert_block_experts_in_step", "moert_block_time_batched", "moert_router_topk", "moert_argmax", "moert_gemv",
-            "moert_dequant", "moert_rmsnorm", "moert_rope", "moert_attn_decode", "moert_exp_device",
+            "moert_dequant", "moert_rmsnorm", "moert_rope", "moert_attn_decode", "moert_attn_decode_noalloc",
+            "moert_exp_device",
             "moert_copy_probe", "moert_read_probe", "moert_h2d_probe", "moert_quantize", "moert_dtype_bytes", "moert_synth_normal", "moert_synth_quantized",
             "moert_synth_fp16"]
 
@@ -580,6 +582,15 @@ def attn_decode(q, k_cache, v_cache, heads, kv_heads, max_len, length, scale, ti
     check(lib().moert_attn_decode(ptr(q), ptr(k_cache), ptr(v_cache), heads, kv_heads, 64, max_len, length, scale,
                                   tiles_per_split, ptr(out)))
     return out
+
+
+def attn_decode_noalloc(q_dev: int, k_dev: int, v_dev: int, heads, kv_heads, max_len, length, scale,
+                        tiles_per_split, out_dev: int, stream: int = 0) -> None:
+    """moert_attn_decode on the caller's device buffers (raw device addresses), enqueued on `stream` (a hipStream_t
+    address, 0 = default stream), with the split partials in the library's fixed scratch: no allocation."""
+    check(lib().moert_attn_decode_noalloc(ctypes.c_void_p(q_dev), ctypes.c_void_p(k_dev), ctypes.c_void_p(v_dev),
+                                          heads, kv_heads, 64, max_len, length, scale, tiles_per_split,
+                                          ctypes.c_void_p(out_dev), ctypes.c_void_p(stream)))
 
 
 def exp_device(x: np.ndarray) -> np.ndarray:
