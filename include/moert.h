@@ -292,6 +292,40 @@ int moert_h2d_probe(size_t bytes, int iters, double* kernel_us, double* memcpy_u
 int moert_exp_device(const float* x, float* y, int n);
 
 /* ---------------------------------------------------------------------------------------------------------
+ * Checkpoint loading (host only, no device needed). Replaces Checkpoint::{open, bf16}
+ * (rust/moe-rt/src/weights.rs:52-122), Config::from_json (rust/moe-rt/src/model.rs:34-61) and HostModel::load
+ * (rust/moe-rt/src/model.rs:100-132, HostLayer::load rust/moe-rt/src/block.rs:31-53), with the BF16 matrices
+ * quantised on load to the engine's formats.
+ * ------------------------------------------------------------------------------------------------------- */
+typedef struct moert_checkpoint moert_checkpoint;
+typedef struct moert_host_model moert_host_model;
+
+/* Granite config.json (len bytes of JSON): refuses model_type other than granitemoe, rope_scaling, attention_bias
+ * and untied embeddings; head_dim defaults to hidden / heads. */
+int moert_config_from_json(const char* json, size_t len, moert_config* out);
+/* Index of every *.safetensors file of `dir` (sorted by name): 8-byte little-endian header length (at most
+ * 100 MiB), JSON header {name: {dtype, shape, data_offsets}}, data. Malformed headers, offsets outside a file and
+ * a directory without safetensors files are refused with MOERT_E_CONFIG; tensors are read on demand. */
+int moert_checkpoint_open(const char* dir, moert_checkpoint** out);
+int moert_checkpoint_close(moert_checkpoint* ck);
+/* dtype string, shape (up to max_dims) and rank of a tensor; MOERT_E_RANGE when it is missing. */
+int moert_checkpoint_tensor(const moert_checkpoint* ck, const char* name, char* dtype, int dtype_len,
+                            uint64_t* shape, int max_dims, int* ndim);
+/* The n BF16 values (bits) of a tensor; refuses another dtype, a size that does not match the shape and n that
+ * differs from the element count. */
+int moert_checkpoint_read_bf16(const moert_checkpoint* ck, const char* name, uint16_t* out, size_t n);
+/* The Granite-MoE weights of `cfg` (transformers names: model.embed_tokens / model.norm / model.layers.{l}.
+ * input_layernorm, post_attention_layernorm, self_attn.{q,k,v,o}_proj, block_sparse_moe.router.layer,
+ * block_sparse_moe.input_linear [E, 2I, H], block_sparse_moe.output_linear [E, H, I]), each BF16 matrix widened to
+ * f32 and quantised to wdtype (embedding / tied head: embed_dtype), norm weights f32. Shapes are checked. */
+int moert_checkpoint_load(const moert_checkpoint* ck, const moert_config* cfg, int wdtype, int embed_dtype,
+                          moert_host_model** out);
+/* The loaded weights as moert_model_create takes them (valid while the host model lives). */
+const moert_model_weights* moert_host_model_weights(const moert_host_model* hm);
+int moert_host_model_config(const moert_host_model* hm, moert_config* cfg);
+int moert_host_model_destroy(moert_host_model* hm);
+
+/* ---------------------------------------------------------------------------------------------------------
  * Host utilities (no device needed).
  * ------------------------------------------------------------------------------------------------------- */
 

@@ -59,6 +59,23 @@ void set_err(const char* fmt, ...) {
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
+}  // namespace
+
+namespace moert {
+// The thread-local error message, for the other host files of the library; returns `code`.
+int set_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+}  // namespace moert
+
+namespace {
+
 // Device allocations owned by one handle, freed only after its stream is idle
 // (Release after both streams synced, rust/moe-rt/src/motor/mem.rs:1-13).
 struct Arena {

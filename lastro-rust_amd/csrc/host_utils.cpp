@@ -130,7 +130,7 @@ static void normal_range(uint64_t seed, uint64_t stream, size_t i0, size_t i1, f
   }
 }
 
-static void parallel_for(size_t n, size_t grain, const std::function<void(size_t, size_t)>& f) {
+void parallel_for(size_t n, size_t grain, const std::function<void(size_t, size_t)>& f) {
   unsigned hw = std::thread::hardware_concurrency();
   size_t nt = std::min<size_t>(hw ? hw : 1, 16);
   size_t chunks = (n + grain - 1) / grain;

@@ -15,5 +15,7 @@ int quantize(const float* x, size_t n, int dtype, void* out);
 int synth_normal(uint64_t seed, uint64_t stream, size_t n, float scale, float offset, float* out);
 int synth_quantized(uint64_t seed, uint64_t stream, size_t n, float scale, int dtype, void* out);
 int synth_fp16(uint64_t seed, uint64_t stream, size_t n, float scale, uint16_t* out);
+// f(begin, end) over [0, n) in chunks of `grain`, on up to 16 threads.
+void parallel_for(size_t n, size_t grain, const std::function<void(size_t, size_t)>& f);
 
 }  // namespace moert

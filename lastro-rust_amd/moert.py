@@ -128,6 +128,15 @@ def lib() -> ctypes.CDLL:
             "moert_synth_normal": (i, [u64, u64, sz, f, f, vp]),
             "moert_synth_quantized": (i, [u64, u64, sz, f, i, vp]),
             "moert_synth_fp16": (i, [u64, u64, sz, f, vp]),
+            "moert_config_from_json": (i, [ctypes.c_char_p, sz, ctypes.POINTER(moert_config)]),
+            "moert_checkpoint_open": (i, [ctypes.c_char_p, ctypes.POINTER(vp)]),
+            "moert_checkpoint_close": (i, [vp]),
+            "moert_checkpoint_tensor": (i, [vp, ctypes.c_char_p, ctypes.c_char_p, i, vp, i, ip]),
+            "moert_checkpoint_read_bf16": (i, [vp, ctypes.c_char_p, vp, sz]),
+            "moert_checkpoint_load": (i, [vp, ctypes.POINTER(moert_config), i, i, ctypes.POINTER(vp)]),
+            "moert_host_model_weights": (ctypes.POINTER(moert_model_weights), [vp]),
+            "moert_host_model_config": (i, [vp, ctypes.POINTER(moert_config)]),
+            "moert_host_model_destroy": (i, [vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -149,7 +158,9 @@ EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moer
             "moert_dequant", "moert_rmsnorm", "moert_rope", "moert_attn_decode", "moert_attn_decode_noalloc",
             "moert_exp_device",
             "moert_copy_probe", "moert_read_probe", "moert_h2d_probe", "moert_quantize", "moert_dtype_bytes", "moert_synth_normal", "moert_synth_quantized",
-            "moert_synth_fp16"]
+            "moert_synth_fp16", "moert_config_from_json", "moert_checkpoint_open", "moert_checkpoint_close",
+            "moert_checkpoint_tensor", "moert_checkpoint_read_bf16", "moert_checkpoint_load", "moert_host_model_weights",
+            "moert_host_model_config", "moert_host_model_destroy"]
 
 
 def check(rc: int) -> None:
@@ -453,6 +464,96 @@ class GpuModel:
         us, n = ctypes.c_double(0), ctypes.c_int(0)
         check(lib().moert_time_kernel(self.h, kind, iters, ctypes.byref(us), ctypes.byref(n)))
         return us.value, n.value
+
+
+# ---- checkpoints ------------------------------------------------------------------------------------------------
+def config_from_json_native(text: str) -> Config:
+    """Config::from_json (model.rs:34-61) through the library's parser."""
+    b = text.encode()
+    c = moert_config()
+    check(lib().moert_config_from_json(b, len(b), ctypes.byref(c)))
+    return Config(**{n: getattr(c, n) for n, _ in moert_config._fields_})
+
+
+class Checkpoint:
+    """Index of the *.safetensors files of a directory (Checkpoint::open, weights.rs:52-106); tensors read on
+    demand (Checkpoint::bf16, weights.rs:109-122)."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        check(lib().moert_checkpoint_open(str(path).encode(), ctypes.byref(h)))
+        self.h = h
+
+    def tensor(self, name: str):
+        """(dtype, shape) of a tensor."""
+        dt = ctypes.create_string_buffer(32)
+        shape = np.zeros(8, np.uint64)
+        nd = ctypes.c_int(0)
+        check(lib().moert_checkpoint_tensor(self.h, name.encode(), dt, 32, ptr(shape), 8, ctypes.byref(nd)))
+        return dt.value.decode(), tuple(int(d) for d in shape[:nd.value])
+
+    def bf16(self, name: str) -> np.ndarray:
+        """The BF16 bits of a tensor, shaped."""
+        _, shape = self.tensor(name)
+        out = np.empty(int(np.prod(shape, dtype=np.uint64)) if shape else 1, np.uint16)
+        check(lib().moert_checkpoint_read_bf16(self.h, name.encode(), ptr(out), out.size))
+        return out.reshape(shape)
+
+    def close(self):
+        if self.h:
+            lib().moert_checkpoint_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class LoadedModel:
+    """HostModel::load (model.rs:100-132) from a checkpoint, each BF16 matrix quantised on load to wdtype (the tied
+    embedding / head to embed_dtype); usable wherever a SynthModel is (GpuModel, the oracle's CpuSession)."""
+
+    def __init__(self, ck: Checkpoint, cfg: Config, wdtype: int = Q8_0, embed_dtype: int = Q8_0):
+        h = ctypes.c_void_p()
+        check(lib().moert_checkpoint_load(ck.h, ctypes.byref(cfg.c()), wdtype, embed_dtype, ctypes.byref(h)))
+        self.h, self.cfg, self.wdtype, self.embed_dtype = h, cfg, wdtype, embed_dtype
+
+    def weights(self) -> moert_model_weights:
+        return lib().moert_host_model_weights(self.h).contents
+
+    def close(self):
+        if self.h:
+            lib().moert_host_model_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def write_safetensors(path: str, tensors):
+    """A safetensors file from (name, dtype string, shape, raw bytes) entries (the reference's test writer,
+    tests/common/mod.rs:103-118, restated)."""
+    import json
+    head, data = {}, bytearray()
+    for name, dt, shape, raw in tensors:
+        start = len(data)
+        data += raw
+        head[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [start, len(data)]}
+    h = json.dumps(head).encode()
+    with open(path, "wb") as f:
+        f.write(len(h).to_bytes(8, "little") + h + bytes(data))
+
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """f32 -> BF16 bits, round to nearest even (bf16::from_f32)."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return r.astype(np.uint16)
 
 
 def kv_prefill_data(cfg: Config, seed: int, layer: int, n: int):

@@ -237,3 +237,24 @@ def test_granite_3b_wider_init_greedy_moves_and_stays_identical(gpu):
     tok = int(np.random.default_rng(7).integers(0, cfg.vocab))
     _greedy_identity(g, s, [tok], 256, "3B wide", min_distinct=100)
     g.close()
+
+
+def test_model_loaded_from_a_bf16_checkpoint_decodes_like_the_oracle(gpu, tmp_path):
+    """A synthetic Granite-MoE checkpoint in BF16 (two safetensors files) loaded with quantize-on-load to Q8_0, then
+    decoded on the device: 24 steps bit for bit against the oracle's session over the same loaded weights."""
+    from test_checkpoint import granite_checkpoint
+    cfg = moert.Config(**moert.TINY)
+    granite_checkpoint(str(tmp_path), cfg)
+    ck = moert.Checkpoint(tmp_path)
+    m = moert.LoadedModel(ck, cfg, moert.Q8_0, moert.Q8_0)
+    g = moert.GpuModel(m, 64, attn_splits=4)
+    s = oracle.CpuSession(m, 64, attn_splits=4, threads=2)
+    for t, tok in enumerate(np.random.default_rng(24).integers(0, cfg.vocab, 24)):
+        say(f"loaded checkpoint pos={t}")
+        lg, ids, w, am = g.step(int(tok))
+        olg, oids, ow, _ = s.step(int(tok))
+        assert bits_equal(lg, olg) and np.array_equal(ids, oids) and bits_equal(w, ow), t
+    g.close()
+    del s
+    m.close()
+    ck.close()
