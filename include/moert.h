@@ -122,6 +122,32 @@ int moert_cache_fill(moert_model* m, int* copied);
  * with hipMemcpyAsync on a side stream that the model stream waits for. Experts distinct, 1 <= n <= min(slots,
  * experts). *copied = experts that were not in the pool. Returns synchronised; counters not changed. */
 int moert_cache_prefetch(moert_model* m, int layer, const int* experts, int n, int* copied);
+/* Prefetch inside the step (north_star item 6: transfer overlapping attention): with on = 1, each layer step of the
+ * cached model also runs, on a side stream of the step graph, a prediction of the layer's experts (the layer's router
+ * applied to rmsnorm of the layer's input, top-k) and one uncounted tick of the LRU rule over the predicted keys (as
+ * moert_cache_prefetch), then copies the predicted misses from the pinned store into their slots while the layer's
+ * attention runs; the router + gate/up kernel waits for the copies. Outputs are unchanged (a misprediction is read
+ * from the host as before); the counters count the step's requests as before and the prefetched copies apart.
+ * on = 0 restores the plain cached step. No reference counterpart beyond copy_in_background (rust/moe-rt/src/cache/
+ * core.rs:380), whose copies start only after the miss. */
+int moert_cache_prefetch_mode(moert_model* m, int on);
+/* The experts predicted for positions [pos0, pos0 + n): [n][layers][8] ids in top-k order (-1 past top_k, and for
+ * positions not decoded with prefetch since the last clear). */
+int moert_cache_predictions(moert_model* m, int pos0, int n, int* ids);
+/* Per position and layer of [pos0, pos0 + n): [n][layers][4] = requests served from the pool, copies inside the step,
+ * experts copied ahead by the prefetch branch, 0 (the reference's per-token counters, CacheStats,
+ * rust/moe-rt/src/cache.rs:111-124, per token). */
+int moert_cache_token_counts(moert_model* m, int pos0, int n, int* counts);
+/* Cumulative counters since creation or the last clear; mirrors CacheStats (rust/moe-rt/src/cache.rs:111-124) and
+ * the engine's Stats (rust/moe-rt/src/motor/mod.rs:96-109): needed = requests, hits, copies (sync_copies: inside the
+ * step), prefetched (copies ahead of the layer), cpu / dropped / deferred (experts served on the host, admissions
+ * refused, copies deferred past the victim's layer: 0 for the in-kernel cache), bytes moved host -> HBM by copies,
+ * pool slots. */
+typedef struct {
+  unsigned long long needed, hits, copies, prefetched, cpu, dropped, deferred, bytes_copied;
+  int slots;
+} moert_cache_counters;
+int moert_cache_counters_get(moert_model* m, moert_cache_counters* out);
 
 /* One token at the current position: logits of the next position (vocab floats, divided by logits_scaling),
  * the router decision of every layer (layers*top_k ids and weights, top-k order) and the greedy argmax.

@@ -13,8 +13,9 @@ namespace moert {
 
 constexpr int kCacheMaxSlots = 4096;
 
-// Statistics words (unsigned long long): requests that hit, copies from the host store.
-enum { CS_HITS = 0, CS_COPIES = 1, CS_WORDS = 4 };
+// Statistics words (unsigned long long): requests that hit, copies from the host store inside steps, experts copied
+// ahead of their layer by the prefetch branch.
+enum { CS_HITS = 0, CS_COPIES = 1, CS_PREFETCH = 2, CS_WORDS = 4 };
 
 struct CacheDev {
   DMat pool_gu;           // [slots * 2I, H]: slot s holds rows [s*2I, s*2I + 2I) (gate rows, then up rows)
@@ -34,6 +35,12 @@ struct CacheDev {
   unsigned long long* stats;  // [CS_WORDS]
   int* route;             // [16] the current layer step: slot of each routed expert in top-k order, then its host
                           // key when it missed (read from the host store by the down kernel), -1 when it hit
+  // prefetch branch (moert_cache_prefetch_mode)
+  int* pf;                // [1 + 2 * 8] experts to copy ahead of the current layer: count, then (slot, key) pairs
+  int* pred_hist;         // [max_len][layers][8] predicted experts of each position and layer (-1: none)
+  int* tok_hist;          // [max_len][layers][4] per position and layer: hits, copies, prefetched, 0
+  const int* state;       // the step state (ST_POS: the position being decoded)
+  int layers;
 };
 
 // The MoE half of a layer step of a cached model: rmsnorm + router + top-k + LRU decision + gate/up + SwiGLU of the
@@ -42,6 +49,15 @@ hipError_t launch_route_up_cached(hipStream_t s, const LayerDev& L, const Dims& 
                                   const CacheDev& c, Tl tl = {});
 hipError_t launch_expert_down_cached(hipStream_t s, const Dims& d, const StepBufs& b, int layer, const CacheDev& c,
                                      Tl tl = {});
+
+// Prefetch branch of a cached step, for layer `layer` (run on a side stream while the layer's attention runs):
+// launch_prefetch_decide predicts the layer's experts from its input h (the layer's router on rmsnorm(h, ln_moe),
+// top-k), records them in c.pred_hist, applies one uncounted tick of the LRU rule to the current slot tables in place
+// and lists the (slot, key) pairs to copy in c.pf; launch_prefetch_copy copies those records from the host store into
+// their pool slots.
+hipError_t launch_prefetch_decide(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
+                                  const CacheDev& c);
+hipError_t launch_prefetch_copy(hipStream_t s, const CacheDev& c);
 
 // Kernel copy of `bytes` (multiple of 16) from device-mapped pinned host memory to device memory (the PCIe rate
 // the cached kernels' host reads are bounded by).

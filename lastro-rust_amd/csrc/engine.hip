@@ -205,6 +205,10 @@ struct moert_model {
   bool cached = false;
   CacheDev cache{};
   void* host_store = nullptr;
+  // prefetch branch of the cached step (moert_cache_prefetch_mode): side stream and its fork / join events
+  bool prefetch = false;
+  hipStream_t pf_stream = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_pred = nullptr, ev_copy = nullptr;
 
   // Launches one decode step. With `timed` >= 0, every launch of that kernel class records its dispatch start and
   // end into the next event pair of `ev`. With a timeline buffer (measurement build), launch i of the step records
@@ -227,10 +231,24 @@ struct moert_model {
     for (size_t l = 0; l < layers.size(); l++) {
       const LayerDev& L = layers[l];
       const int li = (int)l;
+      const bool pf = cached && prefetch;
+      if (pf) {
+        // side branch: predict the layer's experts from its input and copy the predicted misses into the pool while
+        // the attention half runs; the output projection (which rewrites h) waits for the prediction, the router +
+        // gate/up kernel for the copies
+        CHECK_HIP(hipEventRecord(ev_fork, stream));
+        CHECK_HIP(hipStreamWaitEvent(pf_stream, ev_fork, 0));
+        CHECK_HIP(launch_prefetch_decide(pf_stream, L, dims, b, li, cache));
+        CHECK_HIP(hipEventRecord(ev_pred, pf_stream));
+        CHECK_HIP(launch_prefetch_copy(pf_stream, cache));
+        CHECK_HIP(hipEventRecord(ev_copy, pf_stream));
+      }
       CHECK_HIP(launch_qkv(stream, L, dims, b, arm(MOERT_K_QKV, li)));
       CHECK_HIP(launch_attn_split(stream, L, dims, b, arm(MOERT_K_ATTN_SPLIT, li)));
       CHECK_HIP(launch_attn_combine(stream, dims, b, arm(MOERT_K_ATTN_COMBINE, li)));
+      if (pf) CHECK_HIP(hipStreamWaitEvent(stream, ev_pred, 0));
       CHECK_HIP(launch_oproj(stream, L, dims, b, arm(MOERT_K_OPROJ, li)));
+      if (pf) CHECK_HIP(hipStreamWaitEvent(stream, ev_copy, 0));
       if (cached) {
         CHECK_HIP(launch_route_up_cached(stream, L, dims, b, li, cache, arm(MOERT_K_ROUTE_UP, li)));
         CHECK_HIP(launch_expert_down_cached(stream, dims, b, li, cache, arm(MOERT_K_EXPERT_DOWN, li)));
@@ -320,6 +338,9 @@ struct moert_model {
     CHECK_HIP(hipMemsetAsync(cache.clock, 0, 2 * 4, stream));
     CHECK_HIP(hipMemsetAsync(cache.cur, 0, 4, stream));
     CHECK_HIP(hipMemsetAsync(cache.stats, 0, CS_WORDS * 8, stream));
+    CHECK_HIP(hipMemsetAsync(cache.pf, 0, 17 * 4, stream));
+    CHECK_HIP(hipMemsetAsync(cache.pred_hist, 0xff, (size_t)max_len * cfg.layers * 8 * 4, stream));
+    CHECK_HIP(hipMemsetAsync(cache.tok_hist, 0, (size_t)max_len * cfg.layers * 4 * 4, stream));
     CHECK_HIP(hipStreamSynchronize(stream));
     return MOERT_OK;
   }
@@ -412,6 +433,7 @@ struct moert_model {
   hipEvent_t side_done = nullptr;
 
   ~moert_model() {
+    if (pf_stream) (void)hipStreamSynchronize(pf_stream);
     if (side) (void)hipStreamSynchronize(side);
     if (side_done) (void)hipEventDestroy(side_done);
     if (side) (void)hipStreamDestroy(side);
@@ -421,6 +443,9 @@ struct moert_model {
     if (tl_buf) (void)hipFree(tl_buf);
     arena.release();
     if (host_store) (void)hipHostFree(host_store);
+    for (hipEvent_t e : {ev_fork, ev_pred, ev_copy})
+      if (e) (void)hipEventDestroy(e);
+    if (pf_stream) (void)hipStreamDestroy(pf_stream);
     if (stream) (void)hipStreamDestroy(stream);
   }
 };
@@ -487,6 +512,14 @@ static int cache_create(moert_model* m, const moert_model_weights* w, int slots)
   cd.stats = (unsigned long long*)p;
   if ((rc = a.alloc(&p, 16 * 4))) return rc;
   cd.route = (int*)p;
+  if ((rc = a.alloc(&p, 17 * 4))) return rc;
+  cd.pf = (int*)p;
+  if ((rc = a.alloc(&p, (size_t)m->max_len * L * 8 * 4))) return rc;
+  cd.pred_hist = (int*)p;
+  if ((rc = a.alloc(&p, (size_t)m->max_len * L * 4 * 4))) return rc;
+  cd.tok_hist = (int*)p;
+  cd.state = m->b.state;
+  cd.layers = L;
   m->cached = true;
   return m->cache_clear();
 }
@@ -1090,6 +1123,65 @@ int moert_cache_clear(moert_model* m) {
   MODEL_OK(m);
   CHECK_CFG(m->cached, "model has no expert cache");
   MTRY(m, m->cache_clear());
+  return MOERT_OK;
+}
+
+int moert_cache_prefetch_mode(moert_model* m, int on) {
+  MODEL_OK(m);
+  CHECK_CFG(m->cached, "model has no expert cache");
+  CHECK_CFG(on == 0 || on == 1, "prefetch mode %d: 0 (off) or 1 (each layer's experts predicted from its input)", on);
+  if ((on != 0) == m->prefetch) return MOERT_OK;
+  if (!m->pf_stream) {
+    CHECK_HIP(hipStreamCreateWithFlags(&m->pf_stream, hipStreamNonBlocking));
+    for (hipEvent_t* e : {&m->ev_fork, &m->ev_pred, &m->ev_copy})
+      CHECK_HIP(hipEventCreateWithFlags(e, hipEventDisableTiming));
+  }
+  CHECK_HIP(hipStreamSynchronize(m->stream));
+  CHECK_HIP(hipStreamSynchronize(m->pf_stream));
+  if (m->exec) CHECK_HIP(hipGraphExecDestroy(m->exec));
+  if (m->graph) CHECK_HIP(hipGraphDestroy(m->graph));
+  m->exec = nullptr;
+  m->graph = nullptr;
+  m->prefetch = on != 0;
+  MTRY(m, m->build_graph());
+  return MOERT_OK;
+}
+
+int moert_cache_predictions(moert_model* m, int pos0, int n, int* ids) {
+  MODEL_OK(m);
+  CHECK_CFG(m->cached, "model has no expert cache");
+  CHECK_CFG(ids && pos0 >= 0 && n >= 0 && pos0 + n <= m->max_len, "predictions: positions [%d, %d)", pos0, pos0 + n);
+  const size_t row = (size_t)m->cfg.layers * 8;
+  MTRY(m, model_copy_out(m, ids, m->cache.pred_hist + (size_t)pos0 * row, (size_t)n * row * 4));
+  MTRY(m, model_sync(m));
+  return MOERT_OK;
+}
+
+int moert_cache_token_counts(moert_model* m, int pos0, int n, int* counts) {
+  MODEL_OK(m);
+  CHECK_CFG(m->cached, "model has no expert cache");
+  CHECK_CFG(counts && pos0 >= 0 && n >= 0 && pos0 + n <= m->max_len, "token counts: positions [%d, %d)", pos0,
+            pos0 + n);
+  const size_t row = (size_t)m->cfg.layers * 4;
+  MTRY(m, model_copy_out(m, counts, m->cache.tok_hist + (size_t)pos0 * row, (size_t)n * row * 4));
+  MTRY(m, model_sync(m));
+  return MOERT_OK;
+}
+
+int moert_cache_counters_get(moert_model* m, moert_cache_counters* out) {
+  MODEL_OK(m);
+  CHECK_CFG(m->cached && out, "model has no expert cache (or null output)");
+  unsigned long long st[CS_WORDS];
+  MTRY(m, model_copy_out(m, st, m->cache.stats, sizeof st));
+  MTRY(m, model_sync(m));
+  moert_cache_counters c{};
+  c.hits = st[CS_HITS];
+  c.copies = st[CS_COPIES];
+  c.prefetched = st[CS_PREFETCH];
+  c.needed = c.hits + c.copies;
+  c.bytes_copied = (c.copies + c.prefetched) * (unsigned long long)m->cache.record_bytes;
+  c.slots = m->cache.slots;
+  *out = c;
   return MOERT_OK;
 }
 

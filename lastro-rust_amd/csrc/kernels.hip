@@ -942,6 +942,9 @@ __global__ __launch_bounds__(route_waves(DT) * 64) void k_route_up(DMat router, 
           c.clock[cur ^ 1] = clock;
           c.stats[CS_HITS] += (unsigned long long)hits;
           c.stats[CS_COPIES] += (unsigned long long)misses;
+          int* th = c.tok_hist + ((size_t)c.state[ST_POS] * c.layers + layer) * 4;
+          th[0] = hits;
+          th[1] = misses;
         }
       }
     }

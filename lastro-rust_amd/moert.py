@@ -59,6 +59,12 @@ class moert_layer_weights(ctypes.Structure):
                 ("router_bias", ctypes.c_void_p), ("gate_up", moert_tensor), ("down", moert_tensor)]
 
 
+class moert_cache_counters(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_ulonglong) for n in
+                ("needed", "hits", "copies", "prefetched", "cpu", "dropped", "deferred", "bytes_copied")] + \
+               [("slots", ctypes.c_int)]
+
+
 class moert_model_weights(ctypes.Structure):
     _fields_ = [("embed", moert_tensor), ("norm", ctypes.c_void_p),
                 ("layers", ctypes.POINTER(moert_layer_weights))]
@@ -89,6 +95,10 @@ def lib() -> ctypes.CDLL:
             "moert_cache_clear": (i, [vp]),
             "moert_cache_fill": (i, [vp, ctypes.POINTER(ctypes.c_int)]),
             "moert_cache_prefetch": (i, [vp, i, vp, i, ctypes.POINTER(ctypes.c_int)]),
+            "moert_cache_prefetch_mode": (i, [vp, i]),
+            "moert_cache_predictions": (i, [vp, i, i, vp]),
+            "moert_cache_token_counts": (i, [vp, i, i, vp]),
+            "moert_cache_counters_get": (i, [vp, ctypes.POINTER(moert_cache_counters)]),
             "moert_decode_step": (i, [vp, i, vp, vp, vp, ip]),
             "moert_generate": (i, [vp, vp, i, i, vp, vp]),
             "moert_step_batched": (i, [vp, vp, i, vp, ip]),
@@ -148,7 +158,8 @@ def lib() -> ctypes.CDLL:
 
 EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moert_model_destroy",
             "moert_model_create_cached", "moert_cache_stats", "moert_cache_clear", "moert_cache_fill",
-            "moert_cache_prefetch",
+            "moert_cache_prefetch", "moert_cache_prefetch_mode", "moert_cache_predictions", "moert_cache_token_counts",
+            "moert_cache_counters_get",
             "moert_decode_step", "moert_generate", "moert_step_batched", "moert_prefill", "moert_reset_sequence",
             "moert_kv_prefill_fp16",
             "moert_set_position", "moert_get_position", "moert_read_kv_fp16", "moert_read_hidden", "moert_read_logits",
@@ -363,6 +374,28 @@ class GpuModel:
         n = ctypes.c_int(0)
         check(lib().moert_cache_prefetch(self.h, int(layer), ptr(e), len(e), ctypes.byref(n)))
         return n.value
+
+    def cache_prefetch_mode(self, on: bool):
+        """Prefetch branch inside the cached step (predicted experts copied while the attention half runs)."""
+        check(lib().moert_cache_prefetch_mode(self.h, 1 if on else 0))
+
+    def cache_predictions(self, pos0: int, n: int) -> np.ndarray:
+        """Experts predicted by the prefetch branch: [n, layers, top_k] (-1 where none was recorded)."""
+        c = self.cfg
+        out = np.empty((n, c.layers, 8), np.int32)
+        check(lib().moert_cache_predictions(self.h, pos0, n, ptr(out)))
+        return out[:, :, :c.top_k]
+
+    def cache_token_counts(self, pos0: int, n: int) -> np.ndarray:
+        """Per position and layer: [n, layers, 3] = hits, copies inside the step, prefetched copies."""
+        out = np.empty((n, self.cfg.layers, 4), np.int32)
+        check(lib().moert_cache_token_counts(self.h, pos0, n, ptr(out)))
+        return out[:, :, :3]
+
+    def cache_counters(self) -> dict:
+        c = moert_cache_counters()
+        check(lib().moert_cache_counters_get(self.h, ctypes.byref(c)))
+        return {n: getattr(c, n) for n, _ in moert_cache_counters._fields_}
 
     def close(self):
         if self.h:

@@ -161,6 +161,70 @@ def test_granite_3b_q4_0_filled_pool_copies_nothing_for_the_filled_layers(gpu, g
     cac.close()
 
 
+def _replay_with_predictions(cfg, slots, routes, preds):
+    """The LRU state machine over a prefetched run: per step and layer, the prefetch tick over the recorded
+    prediction, then the layer's counted step. Returns (stats, per-step-layer prefetched copies)."""
+    lru = oracle.Lru(cfg.layers, cfg.experts, slots)
+    pf = np.zeros(routes.shape[:2], np.int64)
+    for t in range(routes.shape[0]):
+        for l in range(cfg.layers):
+            assert (preds[t, l] >= 0).all(), (t, l)
+            pf[t, l] = lru.prefetch(l, preds[t, l])
+            lib = oracle.lib()
+            a = np.ascontiguousarray(routes[t, l], np.int32)
+            lib.orc_lru_step_layer(lru.h, l, a.ctypes.data_as(oracle.ctypes.c_void_p), a.size)
+    return lru.stats(), pf
+
+
+@pytest.mark.parametrize("slots", [3, 6, 12])
+def test_prefetch_branch_keeps_outputs_and_its_evictions_replay_on_the_lru_oracle(gpu, slots):
+    """The cached step with the prefetch branch (each layer's experts predicted from its input and copied on a side
+    stream during attention): outputs equal the resident model's bit for bit; the recorded predictions replayed on
+    the LRU state machine (prefetch tick, then the counted step, per layer) give the device's counters, per position
+    and layer and in total."""
+    cfg = moert.Config(**TINY8)
+    m = moert.SynthModel(cfg, seed=13, wdtype=moert.Q4_0, embed_dtype=moert.F32, std=0.1, zipf_s=1.1)
+    res = moert.GpuModel(m, 64, attn_splits=4)
+    cac = moert.GpuModel(m, 64, attn_splits=4, cache_slots=slots)
+    cac.cache_prefetch_mode(True)
+    toks = np.random.default_rng(321).integers(0, cfg.vocab, 40)
+    say(f"prefetch branch slots={slots}")
+    routes = _forced_pair(res, cac, toks, "prefetch branch")
+    preds = cac.cache_predictions(0, len(toks))
+    (hits, copies, cpu), pf = _replay_with_predictions(cfg, slots, routes, preds)
+    counts = cac.cache_token_counts(0, len(toks))
+    c = cac.cache_counters()
+    assert (c["hits"], c["copies"], c["prefetched"]) == (hits, copies, int(pf.sum()))
+    assert np.array_equal(counts[:, :, 2], pf)
+    assert counts[:, :, 0].sum() == hits and counts[:, :, 1].sum() == copies
+    assert cpu == 0 and c["needed"] == hits + copies
+    res.close()
+    cac.close()
+
+
+def test_granite_3b_q4_0_prefetch_branch_forced_512_steps(gpu, granite_3b_q4):
+    """The expert-cache workload with the prefetch branch: 512 forced steps from an empty 320-slot pool, outputs
+    equal to the resident model's bit for bit, counters equal to the replay with the recorded predictions, and most
+    predicted experts used (the prediction from the layer's input routes like the layer)."""
+    cfg, m = granite_3b_q4
+    toks = np.random.default_rng(512).integers(0, cfg.vocab, 512)
+    res = moert.GpuModel(m, 576, attn_splits=64)
+    cac = moert.GpuModel(m, 576, attn_splits=64, cache_slots=320)
+    cac.cache_prefetch_mode(True)
+    routes = _forced_pair(res, cac, toks, "3b q4_0 prefetch")
+    preds = cac.cache_predictions(0, len(toks))
+    (hits, copies, _), pf = _replay_with_predictions(cfg, 320, routes, preds)
+    c = cac.cache_counters()
+    say(f"3b prefetch: {hits} hits, {copies} copies in steps, {int(pf.sum())} prefetched")
+    assert (c["hits"], c["copies"], c["prefetched"]) == (hits, copies, int(pf.sum()))
+    agree = np.mean([len(set(preds[t, l]) & set(routes[t, l])) / cfg.top_k
+                     for t in range(len(toks)) for l in range(cfg.layers)])
+    say(f"3b prefetch: predicted experts routed {agree:.3f}")
+    assert agree > 0.5
+    res.close()
+    cac.close()
+
+
 def test_fill_after_decode_steps_stamps_the_current_clock(gpu):
     """ExpertCache::fill on a partly filled pool after decode steps (no clear): the filled experts take the current
     clock as their last use (copy_on_compute, cache/core.rs:366-377), so later steps evict them as recently used.
