@@ -160,6 +160,31 @@ def expert_cache(cfg, seed, steps, frac=0.25):
     g.generate(forced, 1)
     fwall = time.perf_counter() - t0
     fhits, fcopies = g.cache_stats()
+    # the same forced run with the prefetch branch: each layer's experts predicted from the layer's input (its norm and
+    # router applied to the residual before attention) and copied into the pool on a side stream while attention runs
+    log("expert cache: forced-token run with the prefetch branch")
+    g.cache_prefetch_mode(True)
+    g.cache_clear()
+    g.reset()
+    c0 = g.cache_counters()
+    t0 = time.perf_counter()
+    g.generate(forced, 1)
+    pwall = time.perf_counter() - t0
+    c1 = g.cache_counters()
+    # the cost of the branch itself: the greedy run (all hits after its first steps) with the branch on
+    g.reset()
+    g.step(tok, want_logits=False)
+    t0 = time.perf_counter()
+    g.time_steps(0, steps - 1)
+    pgreedy = (steps - 1) / (time.perf_counter() - t0)
+    g.cache_prefetch_mode(False)
+    pc = {k: c1[k] - c0[k] for k in ("hits", "copies", "prefetched")}
+    # miss bytes overlapped: the records copied ahead by the branch, of all records copied in the run
+    prefetch = {"tok_s": round((steps + 1) / pwall, 2), "hits": pc["hits"], "copies_in_step": pc["copies"],
+                "prefetched": pc["prefetched"],
+                "overlapped_miss_bytes_frac": round(pc["prefetched"] / max(1, pc["prefetched"] + pc["copies"]), 4),
+                "copied_bytes_per_token": round((pc["copies"] + pc["prefetched"]) * record / steps),
+                "greedy_tok_s": round(pgreedy, 2)}
     # the empty pool filled from the host between steps (moert_cache_fill: each slot's record copied with
     # hipMemcpyAsync on a side stream, host-timed including the table read-back and write-back)
     g.cache_clear()
@@ -182,6 +207,7 @@ def expert_cache(cfg, seed, steps, frac=0.25):
                              "hit_rate": round(fhits / max(1, fhits + fcopies), 4),
                              "copied_bytes_per_token": round(fcopies * record / steps),
                              "pcie_gbs_end_to_end": round(fcopies * record / fwall / 1e9, 2)},
+           "forced_tokens_prefetch": prefetch,
            "h2d_probe": {"bytes": probe_bytes, "kernel_copy_gbs": round(probe_bytes / (pk * 1e-6) / 1e9, 2),
                          "hipmemcpy_gbs": round(probe_bytes / (pm * 1e-6) / 1e9, 2)},
            "fill": {"experts": filled, "bytes": filled * record, "ms": round(fill_s * 1e3, 2),
@@ -189,7 +215,7 @@ def expert_cache(cfg, seed, steps, frac=0.25):
            "resident_tok_s": round(1e3 / res_ms, 2)}
     log(f"expert cache {slots}/{cfg.layers * cfg.experts} slots: {tok_s:.1f} tok/s, hit rate {out['hit_rate']:.3f}, "
         f"{out['copied_bytes_per_token'] / 1e6:.1f} MB copied per token; resident {out['resident_tok_s']} tok/s; "
-        f"forced tokens {out['forced_tokens']}; fill {out['fill']}")
+        f"forced tokens {out['forced_tokens']}; with prefetch {prefetch}; fill {out['fill']}")
     return out
 
 
