@@ -352,6 +352,64 @@ int moert_host_model_config(const moert_host_model* hm, moert_config* cfg);
 int moert_host_model_destroy(moert_host_model* hm);
 
 /* ---------------------------------------------------------------------------------------------------------
+ * Runtime metrics (host only). Replaces the runtime side of the monitor's transport,
+ * rust/moe-monitor/src/snapshot.rs: a JSON snapshot of schema 1 (Snapshot, snapshot.rs:18-40, with Model, State,
+ * Speed, Context, ExpertCache, Window, Request and Event as snapshot.rs:42-139 define them), rewritten atomically
+ * (temporary file in the same directory, data synced, then rename; Publisher::publish, snapshot.rs:172-185), by
+ * default at $XDG_RUNTIME_DIR/moe-rt/metrics.json or /tmp/moe-rt-<uid>/metrics.json (default_path,
+ * snapshot.rs:146-156). Fractions are over the last window between two publications; totals since the start.
+ * ------------------------------------------------------------------------------------------------------- */
+typedef struct moert_metrics moert_metrics;
+
+enum { MOERT_STATE_IDLE = 0, MOERT_STATE_READING = 1, MOERT_STATE_GENERATING = 2, MOERT_STATE_QUEUED = 3,
+       MOERT_STATE_ERROR = 4 };
+
+typedef struct { double decode_now, decode_last, prefill_now, prefill_request; } moert_metrics_speed;
+typedef struct {
+  uint32_t slots_total, slots_resident, slots_loading;
+  double hit_frac, copy_frac, cpu_frac;
+  uint32_t copies_inflight;
+  double h2d_gbs;
+  uint64_t total_hits, total_copies, total_cpu;
+} moert_metrics_cache;
+typedef struct { double exposure_frac, gpu_wait_frac, ms_per_token; } moert_metrics_window;
+typedef struct {
+  uint64_t started_ms, prompt_tokens, reused_tokens, output_tokens, duration_ms;
+  double prefill_tok_s, decode_tok_s;
+  const char* status; /* "ok", "erro", "em curso", "cancelada" */
+} moert_metrics_request;
+
+/* A publisher for `path` (NULL: the default path; its directory is created). started_ms and pid are set here. */
+int moert_metrics_create(const char* path, moert_metrics** out);
+int moert_metrics_destroy(moert_metrics* mx);
+/* The file the publisher writes (NUL-terminated, truncated to len). */
+int moert_metrics_path(const moert_metrics* mx, char* buf, int len);
+int moert_metrics_set_model(moert_metrics* mx, const char* name, int layers, int experts, int experts_per_tok);
+/* kind MOERT_STATE_*: READING (a = done, b = total), GENERATING (a = tokens, b = max_tokens), QUEUED (a = waiting),
+ * ERROR (message). */
+int moert_metrics_set_state(moert_metrics* mx, int kind, uint64_t a, uint64_t b, const char* message);
+int moert_metrics_set_speed(moert_metrics* mx, const moert_metrics_speed* s);
+int moert_metrics_set_context(moert_metrics* mx, uint64_t used, uint64_t max);
+int moert_metrics_set_cache(moert_metrics* mx, const moert_metrics_cache* c);
+int moert_metrics_set_window(moert_metrics* mx, const moert_metrics_window* w);
+/* Most recent first; the publisher keeps the last 32. */
+int moert_metrics_add_request(moert_metrics* mx, const moert_metrics_request* r);
+int moert_metrics_setting(moert_metrics* mx, const char* key, const char* value);
+/* level "info", "aviso" or "erro"; oldest first, the publisher keeps the last 64. */
+int moert_metrics_event(moert_metrics* mx, const char* level, const char* message);
+/* The snapshot as JSON with ts_ms = now (NUL-terminated into buf when it fits; *needed = its length + 1). */
+int moert_metrics_json(moert_metrics* mx, char* buf, size_t len, size_t* needed);
+/* Writes the snapshot (ts_ms = now) to a temporary file beside the path, syncs it and renames it over the path. */
+int moert_metrics_publish(moert_metrics* mx);
+
+/* Lets the model fill `mx` during moert_generate (NULL detaches; the publisher must outlive the attachment): model
+ * constants and settings on attach; state (reading the prompt, then generating), context, speed, expert-cache
+ * fractions and totals, copy rate and window from the device counters, read back asynchronously every
+ * min_interval_ms while the steps run (publications throttled to that interval); on return a request entry, an
+ * event and a forced publication. The engine's per-token counters are those of moert_cache_token_counts. */
+int moert_model_attach_metrics(moert_model* m, moert_metrics* mx, int min_interval_ms);
+
+/* ---------------------------------------------------------------------------------------------------------
  * Host utilities (no device needed).
  * ------------------------------------------------------------------------------------------------------- */
 

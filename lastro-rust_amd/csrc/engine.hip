@@ -8,6 +8,7 @@
 // same graph serves every position and greedy generation needs no host synchronisation between tokens.
 #include <hip/hip_runtime.h>
 
+#include <chrono>
 #include <cmath>
 #include <cstdlib>
 #include <cstdarg>
@@ -209,6 +210,19 @@ struct moert_model {
   bool prefetch = false;
   hipStream_t pf_stream = nullptr;
   hipEvent_t ev_fork = nullptr, ev_pred = nullptr, ev_copy = nullptr;
+  // runtime metrics (moert_model_attach_metrics): the publisher, the pinned read-back of the device counters and
+  // the step state, and the generate call's timing marks
+  using Clock = std::chrono::steady_clock;
+  moert_metrics* mx = nullptr;
+  int mx_interval_ms = 500;
+  unsigned char* mx_pin = nullptr;
+  hipEvent_t mx_ev = nullptr, mx_t[3] = {};
+  bool mx_pending = false;
+  Clock::time_point mx_last_read, mx_last_pub, mx_prev_t;
+  unsigned long long mx_prev[CS_WORDS] = {};
+  int mx_prev_pos = 0;
+  double mx_wait_s = 0;
+  double mx_speed_last[2] = {};  // decode and prefill tok/s of the last finished request
 
   // Launches one decode step. With `timed` >= 0, every launch of that kernel class records its dispatch start and
   // end into the next event pair of `ev`. With a timeline buffer (measurement build), launch i of the step records
@@ -443,8 +457,9 @@ struct moert_model {
     if (tl_buf) (void)hipFree(tl_buf);
     arena.release();
     if (host_store) (void)hipHostFree(host_store);
-    for (hipEvent_t e : {ev_fork, ev_pred, ev_copy})
+    for (hipEvent_t e : {ev_fork, ev_pred, ev_copy, mx_ev, mx_t[0], mx_t[1], mx_t[2]})
       if (e) (void)hipEventDestroy(e);
+    if (mx_pin) (void)hipHostFree(mx_pin);
     if (pf_stream) (void)hipStreamDestroy(pf_stream);
     if (stream) (void)hipStreamDestroy(stream);
   }
@@ -802,6 +817,114 @@ static int model_sync(moert_model* m) {
   return MOERT_OK;
 }
 
+// ---- runtime metrics during moert_generate ----
+// Read-back layout in the pinned buffer: the cache counters [CS_WORDS] (u64), the step state [ST_WORDS], the current
+// slot-table copy, then both copies of the slot keys [2][slots].
+static size_t mx_pin_bytes(const moert_model* m) {
+  return 8 * CS_WORDS + 4 * (ST_WORDS + 1 + 2 * (size_t)(m->cached ? m->cache.slots : 0));
+}
+
+// Queues the read-back behind the steps launched so far; its event completes when they have.
+static int mx_enqueue_read(moert_model* m) {
+  unsigned char* p = m->mx_pin;
+  if (m->cached) {
+    CHECK_HIP(hipMemcpyAsync(p, m->cache.stats, 8 * CS_WORDS, hipMemcpyDeviceToHost, m->stream));
+    CHECK_HIP(hipMemcpyAsync(p + 8 * CS_WORDS + 4 * ST_WORDS, m->cache.cur, 4, hipMemcpyDeviceToHost, m->stream));
+    CHECK_HIP(hipMemcpyAsync(p + 8 * CS_WORDS + 4 * (ST_WORDS + 1), m->cache.slot_key, 8 * (size_t)m->cache.slots,
+                             hipMemcpyDeviceToHost, m->stream));
+  } else {
+    memset(p, 0, 8 * CS_WORDS);
+  }
+  CHECK_HIP(hipMemcpyAsync(p + 8 * CS_WORDS, m->b.state, 4 * ST_WORDS, hipMemcpyDeviceToHost, m->stream));
+  CHECK_HIP(hipEventRecord(m->mx_ev, m->stream));
+  return MOERT_OK;
+}
+
+struct MxCall {
+  int pos0, n_prompt, n_new;
+  uint64_t started_ms;
+  moert_model::Clock::time_point t0;
+};
+
+// Fills the publisher from a completed read-back: state, context, speed and the cache fractions over the window
+// since the previous read-back, totals since the counters were cleared.
+static void mx_consume(moert_model* m, const MxCall& c, moert_model::Clock::time_point now) {
+  const unsigned long long* st = (const unsigned long long*)m->mx_pin;
+  const int* state = (const int*)(m->mx_pin + 8 * CS_WORDS);
+  const int s = state[ST_POS] - c.pos0;  // steps completed
+  const double dt = std::chrono::duration<double>(now - m->mx_prev_t).count();
+  const int ds = s - m->mx_prev_pos;
+  moert_metrics* mx = m->mx;
+  const bool reading = s < c.n_prompt - 1;
+  if (reading)
+    (void)moert_metrics_set_state(mx, MOERT_STATE_READING, (uint64_t)s, (uint64_t)c.n_prompt, nullptr);
+  else
+    (void)moert_metrics_set_state(mx, MOERT_STATE_GENERATING, (uint64_t)(s - (c.n_prompt - 1)), (uint64_t)c.n_new,
+                                  nullptr);
+  (void)moert_metrics_set_context(mx, (uint64_t)state[ST_POS], (uint64_t)m->max_len);
+  if (dt > 0 && ds > 0) {
+    moert_metrics_speed sp{};
+    sp.decode_now = reading ? 0.0 : ds / dt;
+    sp.prefill_now = reading ? ds / dt : 0.0;
+    sp.decode_last = m->mx_speed_last[0];
+    sp.prefill_request = m->mx_speed_last[1];
+    (void)moert_metrics_set_speed(mx, &sp);
+    moert_metrics_window w{};
+    w.ms_per_token = dt * 1e3 / ds;
+    const double wall = std::chrono::duration<double>(now - c.t0).count();
+    w.gpu_wait_frac = wall > 0 ? m->mx_wait_s / wall : 0.0;
+    (void)moert_metrics_set_window(mx, &w);
+  }
+  moert_metrics_cache ca{};
+  if (m->cached) {
+    const int S = m->cache.slots, cur = state[ST_WORDS];
+    const int* keys = state + ST_WORDS + 1 + (size_t)(cur & 1) * S;
+    uint32_t res = 0;
+    for (int i = 0; i < S; i++) res += keys[i] >= 0;
+    const unsigned long long dh = st[CS_HITS] - m->mx_prev[CS_HITS], dc = st[CS_COPIES] - m->mx_prev[CS_COPIES],
+                             dp = st[CS_PREFETCH] - m->mx_prev[CS_PREFETCH];
+    const double need = (double)(dh + dc);
+    ca.slots_total = (uint32_t)S;
+    ca.slots_resident = res;
+    ca.hit_frac = need > 0 ? dh / need : 0.0;
+    ca.copy_frac = need > 0 ? dc / need : 0.0;
+    ca.h2d_gbs = dt > 0 ? (double)(dc + dp) * m->cache.record_bytes / dt / 1e9 : 0.0;
+    ca.total_hits = st[CS_HITS];
+    ca.total_copies = st[CS_COPIES] + st[CS_PREFETCH];
+    memcpy(m->mx_prev, st, sizeof m->mx_prev);
+  } else {
+    ca.slots_total = ca.slots_resident = (uint32_t)(m->cfg.layers * m->cfg.experts);
+    ca.hit_frac = 1.0;
+  }
+  (void)moert_metrics_set_cache(mx, &ca);
+  m->mx_prev_t = now;
+  m->mx_prev_pos = s;
+}
+
+static void mx_publish(moert_model* m, moert_model::Clock::time_point now, bool force) {
+  if (!force && now - m->mx_last_pub < std::chrono::milliseconds(m->mx_interval_ms)) return;
+  (void)moert_metrics_publish(m->mx);  // a failed publication leaves the previous file (as the reference ignores it)
+  m->mx_last_pub = now;
+}
+
+// Between step launches: consumes a completed read-back, or queues the next one once the interval has passed.
+static int mx_poll(moert_model* m, const MxCall& c) {
+  const auto now = moert_model::Clock::now();
+  if (m->mx_pending) {
+    const hipError_t q = hipEventQuery(m->mx_ev);
+    if (q == hipErrorNotReady) return MOERT_OK;
+    CHECK_HIP(q);
+    m->mx_pending = false;
+    mx_consume(m, c, now);
+    mx_publish(m, now, false);
+  } else if (now - m->mx_last_read >= std::chrono::milliseconds(m->mx_interval_ms)) {
+    MTRY(m, mx_enqueue_read(m));
+    m->mx_pending = true;
+    m->mx_last_read = now;
+  }
+  return MOERT_OK;
+}
+
 int moert_decode_step(moert_model* m, int token, float* logits, int* route_ids, float* route_weights, int* argmax) {
   MODEL_OK(m);
   if (m->host_pos >= m->max_len) {
@@ -880,8 +1003,8 @@ int moert_prefill(moert_model* m, const int* tokens, int n, float* logits, int* 
   return MOERT_OK;
 }
 
-int moert_generate(moert_model* m, const int* prompt, int n_prompt, int n_new, int* out_tokens, float* gaps) {
-  MODEL_OK(m);
+static int generate(moert_model* m, const int* prompt, int n_prompt, int n_new, int* out_tokens, float* gaps,
+                    MxCall* mc) {
   if (!prompt || n_prompt < 1 || n_new < 1 || !out_tokens) {
     set_err("generate needs a prompt of at least one token and n_new >= 1");
     return MOERT_E_CONFIG;
@@ -899,12 +1022,31 @@ int moert_generate(moert_model* m, const int* prompt, int n_prompt, int n_new, i
   int st[2] = {pos0, pos0 + n_prompt};
   MTRY(m, model_copy_in(m, m->b.seq + pos0, prompt, (size_t)n_prompt * 4));
   MTRY(m, model_copy_in(m, m->b.state, st, sizeof st));
+  if (mc) {
+    mc->pos0 = pos0;
+    mc->n_prompt = n_prompt;
+    mc->n_new = n_new;
+    m->mx_prev_pos = 0;
+    m->mx_wait_s = 0;
+    (void)moert_metrics_set_state(m->mx, n_prompt > 1 ? MOERT_STATE_READING : MOERT_STATE_GENERATING, 0,
+                                  (uint64_t)(n_prompt > 1 ? n_prompt : n_new), nullptr);
+    (void)moert_metrics_set_context(m->mx, (uint64_t)pos0, (uint64_t)m->max_len);
+    mx_publish(m, moert_model::Clock::now(), true);
+    CHECK_HIP(hipEventRecord(m->mx_t[0], m->stream));
+    if (n_prompt == 1) CHECK_HIP(hipEventRecord(m->mx_t[1], m->stream));
+  }
   std::vector<float> lg(gaps ? m->cfg.vocab : 0);
   for (int i = 0; i < steps; i++) {
     MTRY(m, model_launch(m));
+    if (mc) {
+      if (i == n_prompt - 2) CHECK_HIP(hipEventRecord(m->mx_t[1], m->stream));
+      MTRY(m, mx_poll(m, *mc));
+    }
     if (gaps && i >= n_prompt - 1) {
       MTRY(m, model_copy_out(m, lg.data(), m->b.logits, lg.size() * 4));
+      const auto w0 = moert_model::Clock::now();
       MTRY(m, model_sync(m));
+      m->mx_wait_s += std::chrono::duration<double>(moert_model::Clock::now() - w0).count();
       float t1 = -INFINITY, t2 = -INFINITY;
       for (float v : lg) {
         if (v > t1) {
@@ -919,9 +1061,112 @@ int moert_generate(moert_model* m, const int* prompt, int n_prompt, int n_new, i
   }
   // token i was chosen at position pos0 + n_prompt - 1 + i (the last one is never fed back)
   MTRY(m, model_copy_out(m, out_tokens, m->b.argmax_hist + pos0 + n_prompt - 1, (size_t)n_new * 4));
+  if (mc) CHECK_HIP(hipEventRecord(m->mx_t[2], m->stream));
+  const auto w0 = moert_model::Clock::now();
   MTRY(m, model_sync(m));
+  m->mx_wait_s += std::chrono::duration<double>(moert_model::Clock::now() - w0).count();
   m->host_pos = pos0 + steps;
   return MOERT_OK;
+}
+
+int moert_generate(moert_model* m, const int* prompt, int n_prompt, int n_new, int* out_tokens, float* gaps) {
+  MODEL_OK(m);
+  if (!m->mx) return generate(m, prompt, n_prompt, n_new, out_tokens, gaps, nullptr);
+  // with a metrics publisher: state and counters while the steps run, then the request entry (Request,
+  // rust/moe-monitor/src/snapshot.rs:121-135), an event and a forced publication
+  MxCall mc{0, n_prompt, n_new, 0, moert_model::Clock::now()};
+  mc.started_ms = (uint64_t)std::chrono::duration_cast<std::chrono::milliseconds>(
+                      std::chrono::system_clock::now().time_since_epoch())
+                      .count();
+  m->mx_prev_t = mc.t0;
+  const int rc = generate(m, prompt, n_prompt, n_new, out_tokens, gaps, &mc);
+  const auto now = moert_model::Clock::now();
+  const double wall = std::chrono::duration<double>(now - mc.t0).count();
+  moert_metrics_request r{};
+  r.started_ms = mc.started_ms;
+  r.prompt_tokens = (uint64_t)(n_prompt > 0 ? n_prompt : 0);
+  r.duration_ms = (uint64_t)(wall * 1e3);
+  char msg[320];
+  if (rc != MOERT_OK) {
+    // the message of the failure (the model may be poisoned: nothing more is read from the device)
+    snprintf(msg, sizeof msg, "generate: %s", moert_last_error());
+    (void)moert_metrics_set_state(m->mx, MOERT_STATE_ERROR, 0, 0, msg);
+    r.status = "erro";
+    (void)moert_metrics_add_request(m->mx, &r);
+    (void)moert_metrics_event(m->mx, "erro", msg);
+    m->mx_pending = false;
+    mx_publish(m, now, true);
+    return rc;
+  }
+  // the final read-back (after the stream has drained), and the phase times from the timing marks
+  int rc2 = mx_enqueue_read(m);
+  if (rc2 == MOERT_OK) rc2 = model_sync(m);
+  if (rc2 != MOERT_OK) return m->fail(rc2);
+  m->mx_pending = false;
+  mx_consume(m, mc, now);
+  float pre_ms = 0, dec_ms = 0;
+  CHECK_HIP(hipEventElapsedTime(&pre_ms, m->mx_t[0], m->mx_t[1]));
+  CHECK_HIP(hipEventElapsedTime(&dec_ms, m->mx_t[1], m->mx_t[2]));
+  r.output_tokens = (uint64_t)n_new;
+  r.prefill_tok_s = n_prompt > 1 && pre_ms > 0 ? (n_prompt - 1) / (pre_ms * 1e-3) : 0.0;
+  r.decode_tok_s = dec_ms > 0 ? n_new / (dec_ms * 1e-3) : 0.0;
+  r.status = "ok";
+  m->mx_speed_last[0] = r.decode_tok_s;
+  m->mx_speed_last[1] = r.prefill_tok_s;
+  moert_metrics_speed sp{};
+  sp.decode_last = r.decode_tok_s;
+  sp.prefill_request = r.prefill_tok_s;
+  (void)moert_metrics_set_speed(m->mx, &sp);
+  moert_metrics_window w{};
+  w.ms_per_token = n_new > 0 ? dec_ms / n_new : 0.0;
+  w.gpu_wait_frac = wall > 0 ? m->mx_wait_s / wall : 0.0;
+  (void)moert_metrics_set_window(m->mx, &w);
+  (void)moert_metrics_set_state(m->mx, MOERT_STATE_IDLE, 0, 0, nullptr);
+  (void)moert_metrics_add_request(m->mx, &r);
+  snprintf(msg, sizeof msg, "generate: %d prompt tokens, %d new tokens, %.1f tok/s decode, %.1f tok/s prompt",
+           n_prompt, n_new, r.decode_tok_s, r.prefill_tok_s);
+  (void)moert_metrics_event(m->mx, "info", msg);
+  mx_publish(m, now, true);
+  return MOERT_OK;
+}
+
+int moert_model_attach_metrics(moert_model* m, moert_metrics* mx, int min_interval_ms) {
+  MODEL_OK(m);
+  CHECK_CFG(min_interval_ms >= 0, "metrics interval %d ms", min_interval_ms);
+  CHECK_HIP(hipStreamSynchronize(m->stream));
+  m->mx = nullptr;
+  m->mx_pending = false;
+  if (!mx) return MOERT_OK;
+  if (!m->mx_pin) {
+    CHECK_HIP(hipHostMalloc((void**)&m->mx_pin, mx_pin_bytes(m), hipHostMallocDefault));
+    CHECK_HIP(hipEventCreateWithFlags(&m->mx_ev, hipEventDisableTiming));
+    for (hipEvent_t& e : m->mx_t) CHECK_HIP(hipEventCreate(&e));
+  }
+  m->mx = mx;
+  m->mx_interval_ms = min_interval_ms;
+  char buf[96];
+  (void)moert_metrics_set_model(mx, "granite-moe", m->cfg.layers, m->cfg.experts, m->cfg.top_k);
+  snprintf(buf, sizeof buf, "%d", m->max_len);
+  (void)moert_metrics_setting(mx, "positions", buf);
+  snprintf(buf, sizeof buf, "%d", m->splits);
+  (void)moert_metrics_setting(mx, "attention splits", buf);
+  if (m->cached)
+    snprintf(buf, sizeof buf, "%d of %d", m->cache.slots, m->cfg.layers * m->cfg.experts);
+  else
+    snprintf(buf, sizeof buf, "all %d resident", m->cfg.layers * m->cfg.experts);
+  (void)moert_metrics_setting(mx, "expert pool slots", buf);
+  // the counters as they stand now, as the base of the first window
+  MTRY(m, mx_enqueue_read(m));
+  MTRY(m, model_sync(m));
+  memcpy(m->mx_prev, m->mx_pin, sizeof m->mx_prev);
+  MxCall mc{m->host_pos, 1, 0, 0, moert_model::Clock::now()};
+  m->mx_prev_pos = 0;
+  m->mx_prev_t = mc.t0;
+  mx_consume(m, mc, mc.t0);
+  (void)moert_metrics_set_state(mx, MOERT_STATE_IDLE, 0, 0, nullptr);
+  m->mx_last_pub = mc.t0;
+  m->mx_last_read = mc.t0;
+  return moert_metrics_publish(mx);
 }
 
 int moert_reset_sequence(moert_model* m) {

@@ -12,8 +12,10 @@ The library is required: every entry point raises if libmoert.so is missing or a
 from __future__ import annotations
 
 import ctypes
+import json
 import math
 import os
+import time
 from dataclasses import dataclass, field
 from typing import List, Optional
 
@@ -63,6 +65,27 @@ class moert_cache_counters(ctypes.Structure):
     _fields_ = [(n, ctypes.c_ulonglong) for n in
                 ("needed", "hits", "copies", "prefetched", "cpu", "dropped", "deferred", "bytes_copied")] + \
                [("slots", ctypes.c_int)]
+
+
+class moert_metrics_speed(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_double) for n in ("decode_now", "decode_last", "prefill_now", "prefill_request")]
+
+
+class moert_metrics_cache(ctypes.Structure):
+    _fields_ = [("slots_total", ctypes.c_uint32), ("slots_resident", ctypes.c_uint32),
+                ("slots_loading", ctypes.c_uint32), ("hit_frac", ctypes.c_double), ("copy_frac", ctypes.c_double),
+                ("cpu_frac", ctypes.c_double), ("copies_inflight", ctypes.c_uint32), ("h2d_gbs", ctypes.c_double),
+                ("total_hits", ctypes.c_uint64), ("total_copies", ctypes.c_uint64), ("total_cpu", ctypes.c_uint64)]
+
+
+class moert_metrics_window(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_double) for n in ("exposure_frac", "gpu_wait_frac", "ms_per_token")]
+
+
+class moert_metrics_request(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint64) for n in
+                ("started_ms", "prompt_tokens", "reused_tokens", "output_tokens", "duration_ms")] + \
+               [("prefill_tok_s", ctypes.c_double), ("decode_tok_s", ctypes.c_double), ("status", ctypes.c_char_p)]
 
 
 class moert_model_weights(ctypes.Structure):
@@ -147,6 +170,21 @@ def lib() -> ctypes.CDLL:
             "moert_host_model_weights": (ctypes.POINTER(moert_model_weights), [vp]),
             "moert_host_model_config": (i, [vp, ctypes.POINTER(moert_config)]),
             "moert_host_model_destroy": (i, [vp]),
+            "moert_metrics_create": (i, [ctypes.c_char_p, ctypes.POINTER(vp)]),
+            "moert_metrics_destroy": (i, [vp]),
+            "moert_metrics_path": (i, [vp, ctypes.c_char_p, i]),
+            "moert_metrics_set_model": (i, [vp, ctypes.c_char_p, i, i, i]),
+            "moert_metrics_set_state": (i, [vp, i, u64, u64, ctypes.c_char_p]),
+            "moert_metrics_set_speed": (i, [vp, ctypes.POINTER(moert_metrics_speed)]),
+            "moert_metrics_set_context": (i, [vp, u64, u64]),
+            "moert_metrics_set_cache": (i, [vp, ctypes.POINTER(moert_metrics_cache)]),
+            "moert_metrics_set_window": (i, [vp, ctypes.POINTER(moert_metrics_window)]),
+            "moert_metrics_add_request": (i, [vp, ctypes.POINTER(moert_metrics_request)]),
+            "moert_metrics_setting": (i, [vp, ctypes.c_char_p, ctypes.c_char_p]),
+            "moert_metrics_event": (i, [vp, ctypes.c_char_p, ctypes.c_char_p]),
+            "moert_metrics_json": (i, [vp, ctypes.c_char_p, sz, ctypes.POINTER(sz)]),
+            "moert_metrics_publish": (i, [vp]),
+            "moert_model_attach_metrics": (i, [vp, vp, i]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -171,7 +209,11 @@ EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moer
             "moert_copy_probe", "moert_read_probe", "moert_h2d_probe", "moert_quantize", "moert_dtype_bytes", "moert_synth_normal", "moert_synth_quantized",
             "moert_synth_fp16", "moert_config_from_json", "moert_checkpoint_open", "moert_checkpoint_close",
             "moert_checkpoint_tensor", "moert_checkpoint_read_bf16", "moert_checkpoint_load", "moert_host_model_weights",
-            "moert_host_model_config", "moert_host_model_destroy"]
+            "moert_host_model_config", "moert_host_model_destroy", "moert_metrics_create", "moert_metrics_destroy",
+            "moert_metrics_path", "moert_metrics_set_model", "moert_metrics_set_state", "moert_metrics_set_speed",
+            "moert_metrics_set_context", "moert_metrics_set_cache", "moert_metrics_set_window",
+            "moert_metrics_add_request", "moert_metrics_setting", "moert_metrics_event", "moert_metrics_json",
+            "moert_metrics_publish", "moert_model_attach_metrics"]
 
 
 def check(rc: int) -> None:
@@ -391,6 +433,11 @@ class GpuModel:
         out = np.empty((n, self.cfg.layers, 4), np.int32)
         check(lib().moert_cache_token_counts(self.h, pos0, n, ptr(out)))
         return out[:, :, :3]
+
+    def attach_metrics(self, mx: Optional["Metrics"], interval_ms: int = 500):
+        """Lets generate() fill and publish `mx` (None detaches); the publisher must outlive the attachment."""
+        check(lib().moert_model_attach_metrics(self.h, mx.h if mx is not None else None, interval_ms))
+        self._mx = mx
 
     def cache_counters(self) -> dict:
         c = moert_cache_counters()
@@ -777,3 +824,100 @@ def step_bytes(cfg: Config, wdtype: int, embed_dtype: int, context: int) -> int:
     kv = cfg.layers * 2 * kvd * 2 * context
     head = dtype_bytes(embed_dtype, cfg.vocab * H)
     return cfg.layers * per_layer + kv + head
+
+
+# ---- runtime metrics (the reference's moe-monitor transport, rust/moe-monitor/src/snapshot.rs) ----
+METRICS_SCHEMA = 1  # SCHEMA (snapshot.rs:14)
+METRICS_STALE_MS = 3000  # STALE_MS (snapshot.rs:16)
+STATE_IDLE, STATE_READING, STATE_GENERATING, STATE_QUEUED, STATE_ERROR = range(5)
+
+
+class Metrics:
+    """The native snapshot publisher (moert_metrics_*), as Publisher + Snapshot (snapshot.rs:18-185): sections set
+    field by field, published atomically (temporary file + rename) to `path` (None: the default path)."""
+
+    def __init__(self, path=None):
+        h = ctypes.c_void_p()
+        check(lib().moert_metrics_create(None if path is None else os.fsencode(path), ctypes.byref(h)))
+        self.h = h.value
+
+    @property
+    def path(self) -> str:
+        buf = ctypes.create_string_buffer(4096)
+        check(lib().moert_metrics_path(self.h, buf, len(buf)))
+        return os.fsdecode(buf.value)
+
+    def set_model(self, name, layers, experts, experts_per_tok):
+        check(lib().moert_metrics_set_model(self.h, name.encode(), layers, experts, experts_per_tok))
+
+    def set_state(self, kind, a=0, b=0, message=None):
+        check(lib().moert_metrics_set_state(self.h, kind, a, b, None if message is None else message.encode()))
+
+    def set_speed(self, **kw):
+        check(lib().moert_metrics_set_speed(self.h, ctypes.byref(moert_metrics_speed(**kw))))
+
+    def set_context(self, used, max_):
+        check(lib().moert_metrics_set_context(self.h, used, max_))
+
+    def set_cache(self, **kw):
+        check(lib().moert_metrics_set_cache(self.h, ctypes.byref(moert_metrics_cache(**kw))))
+
+    def set_window(self, **kw):
+        check(lib().moert_metrics_set_window(self.h, ctypes.byref(moert_metrics_window(**kw))))
+
+    def add_request(self, status="ok", **kw):
+        r = moert_metrics_request(status=status.encode(), **kw)
+        check(lib().moert_metrics_add_request(self.h, ctypes.byref(r)))
+
+    def setting(self, key, value):
+        check(lib().moert_metrics_setting(self.h, key.encode(), value.encode()))
+
+    def event(self, level, message):
+        check(lib().moert_metrics_event(self.h, level.encode(), message.encode()))
+
+    def json(self) -> str:
+        need = ctypes.c_size_t()
+        check(lib().moert_metrics_json(self.h, None, 0, ctypes.byref(need)))
+        buf = ctypes.create_string_buffer(need.value + 4096)
+        check(lib().moert_metrics_json(self.h, buf, len(buf), ctypes.byref(need)))
+        return buf.value.decode()
+
+    def publish(self):
+        check(lib().moert_metrics_publish(self.h))
+
+    def close(self):
+        if self.h:
+            lib().moert_metrics_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def metrics_now_ms() -> int:
+    return int(time.time() * 1000)
+
+
+def read_metrics(path, now_ms=None):
+    """What a monitor knows of the runtime from one read of the file (snapshot::read, snapshot.rs:187-215):
+    ("absent", None) without a file, ("invalid", message) for unreadable JSON or another schema, ("stale", snap)
+    after METRICS_STALE_MS without a publication, else ("live", snap)."""
+    now_ms = metrics_now_ms() if now_ms is None else now_ms
+    try:
+        raw = open(path, "rb").read()
+    except FileNotFoundError:
+        return "absent", None
+    except OSError as e:
+        return "invalid", str(e)
+    try:
+        snap = json.loads(raw)
+    except ValueError as e:
+        return "invalid", f"invalid JSON: {e}"
+    if not isinstance(snap, dict) or snap.get("schema") != METRICS_SCHEMA:
+        return "invalid", f"schema {snap.get('schema') if isinstance(snap, dict) else None} " \
+                          f"(the monitor knows {METRICS_SCHEMA})"
+    age = max(0, now_ms - int(snap.get("ts_ms", 0)))
+    return ("stale" if age > METRICS_STALE_MS else "live"), snap
