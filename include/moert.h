@@ -410,6 +410,38 @@ int moert_metrics_publish(moert_metrics* mx);
 int moert_model_attach_metrics(moert_model* m, moert_metrics* mx, int min_interval_ms);
 
 /* ---------------------------------------------------------------------------------------------------------
+ * Expert placement of the host-CPU hybrid (host only). Replaces the service line of the D1 engine in its
+ * deterministic mode (rust/moe-rt/src/motor/line.rs: serve_layer 512-583, victim 605-648, copy_after_reader
+ * 653-674, end_token 678-716; AdmitMode::TokenBarrier, policy LfuCpu) and Freq (rust/moe-rt/src/cache.rs:60-87).
+ * A token reads the table published at its start: resident experts are computed on the GPU, all other requests on
+ * the host; after a layer's host work its missed keys without a slot are admitted when fewer than `backlog` copies
+ * are pending in the token and a slot is free or the weakest resident outside the layer's keys (lowest (score,
+ * version, key)) scores below the candidate; a copy into the slot of a victim whose layer has not run yet in the
+ * token is held until that layer has passed; at the token's end every copy has landed and the next table is
+ * published. The counters are those of moert_cache_counters (needed, hits, cpu, copies, dropped, deferred).
+ * ------------------------------------------------------------------------------------------------------- */
+typedef struct moert_placement moert_placement;
+typedef struct moert_freq moert_freq;
+
+/* slots may be 0 (every request on the host); slots <= layers * experts. */
+int moert_placement_create(int layers, int experts, int top_k, int slots, int backlog, moert_placement** out);
+int moert_placement_destroy(moert_placement* p);
+/* One step of m positions through every layer: ids [layers][m][top_k] (distinct ids within a position). Optional
+ * outputs: the requests served on the GPU, the copies queued. */
+int moert_placement_step(moert_placement* p, const int* ids, int m, int* gpu_requests, int* copies);
+int moert_placement_counters(const moert_placement* p, moert_cache_counters* out);
+/* The table of the next token: [layers * experts] slot of each key, -1 when not resident. */
+int moert_placement_table(const moert_placement* p, int* table);
+
+/* Freq alone (cache.rs:33-71): touch(key, step) with steps that do not go back per key; score = log2 of the decayed
+ * value + step / (128 * layers); -inf for a key never touched. */
+int moert_freq_create(int keys, int layers, moert_freq** out);
+int moert_freq_destroy(moert_freq* f);
+int moert_freq_touch(moert_freq* f, int key, uint64_t step);
+int moert_freq_score(const moert_freq* f, int key, double* score);
+int moert_freq_clear(moert_freq* f);
+
+/* ---------------------------------------------------------------------------------------------------------
  * Host utilities (no device needed).
  * ------------------------------------------------------------------------------------------------------- */
 

@@ -185,6 +185,16 @@ def lib() -> ctypes.CDLL:
             "moert_metrics_json": (i, [vp, ctypes.c_char_p, sz, ctypes.POINTER(sz)]),
             "moert_metrics_publish": (i, [vp]),
             "moert_model_attach_metrics": (i, [vp, vp, i]),
+            "moert_placement_create": (i, [i, i, i, i, i, ctypes.POINTER(vp)]),
+            "moert_placement_destroy": (i, [vp]),
+            "moert_placement_step": (i, [vp, vp, i, ip, ip]),
+            "moert_placement_counters": (i, [vp, ctypes.POINTER(moert_cache_counters)]),
+            "moert_placement_table": (i, [vp, vp]),
+            "moert_freq_create": (i, [i, i, ctypes.POINTER(vp)]),
+            "moert_freq_destroy": (i, [vp]),
+            "moert_freq_touch": (i, [vp, i, u64]),
+            "moert_freq_score": (i, [vp, i, ctypes.POINTER(ctypes.c_double)]),
+            "moert_freq_clear": (i, [vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -213,7 +223,9 @@ EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moer
             "moert_metrics_path", "moert_metrics_set_model", "moert_metrics_set_state", "moert_metrics_set_speed",
             "moert_metrics_set_context", "moert_metrics_set_cache", "moert_metrics_set_window",
             "moert_metrics_add_request", "moert_metrics_setting", "moert_metrics_event", "moert_metrics_json",
-            "moert_metrics_publish", "moert_model_attach_metrics"]
+            "moert_metrics_publish", "moert_model_attach_metrics", "moert_placement_create", "moert_placement_destroy",
+            "moert_placement_step", "moert_placement_counters", "moert_placement_table", "moert_freq_create",
+            "moert_freq_destroy", "moert_freq_touch", "moert_freq_score", "moert_freq_clear"]
 
 
 def check(rc: int) -> None:
@@ -921,3 +933,70 @@ def read_metrics(path, now_ms=None):
                           f"(the monitor knows {METRICS_SCHEMA})"
     age = max(0, now_ms - int(snap.get("ts_ms", 0)))
     return ("stale" if age > METRICS_STALE_MS else "live"), snap
+
+
+# ---- expert placement of the host-CPU hybrid (the D1 service line in its deterministic mode) ----
+PLACEMENT_FIELDS = ("needed", "hits", "cpu", "copies", "dropped", "deferred")
+
+
+class Placement:
+    """moert_placement_*: the table / LFU admission / held-copy state machine of the hybrid, stepped on routes."""
+
+    def __init__(self, layers, experts, top_k, slots, backlog):
+        h = ctypes.c_void_p()
+        check(lib().moert_placement_create(layers, experts, top_k, slots, backlog, ctypes.byref(h)))
+        self.h, self.L, self.E, self.k = h.value, layers, experts, top_k
+
+    def step(self, ids):
+        """ids [layers][m][top_k]; returns (requests served on the GPU, copies queued)."""
+        a = np.ascontiguousarray(ids, np.int32)
+        assert a.ndim == 3 and a.shape[0] == self.L and a.shape[2] == self.k, a.shape
+        g, c = ctypes.c_int(), ctypes.c_int()
+        check(lib().moert_placement_step(self.h, ptr(a), a.shape[1], ctypes.byref(g), ctypes.byref(c)))
+        return g.value, c.value
+
+    def counters(self) -> dict:
+        c = moert_cache_counters()
+        check(lib().moert_placement_counters(self.h, ctypes.byref(c)))
+        return {n: getattr(c, n) for n in PLACEMENT_FIELDS}
+
+    def table(self) -> np.ndarray:
+        t = np.empty(self.L * self.E, np.int32)
+        check(lib().moert_placement_table(self.h, ptr(t)))
+        return t
+
+    def close(self):
+        if self.h:
+            lib().moert_placement_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Freq:
+    """moert_freq_*: the decayed frequency of the LFU admission."""
+
+    def __init__(self, keys, layers):
+        h = ctypes.c_void_p()
+        check(lib().moert_freq_create(keys, layers, ctypes.byref(h)))
+        self.h = h.value
+
+    def touch(self, key, step):
+        check(lib().moert_freq_touch(self.h, key, step))
+
+    def score(self, key) -> float:
+        v = ctypes.c_double()
+        check(lib().moert_freq_score(self.h, key, ctypes.byref(v)))
+        return v.value
+
+    def clear(self):
+        check(lib().moert_freq_clear(self.h))
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().moert_freq_destroy(self.h)
+            self.h = None
