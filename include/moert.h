@@ -107,6 +107,20 @@ int moert_model_destroy(moert_model* m);
  * 197-200, rust/moe-rt/src/cache.rs:140-354, LRU rule of rust/moe-rt/tests/model.rs:380-412). */
 int moert_model_create_cached(const moert_config* cfg, const moert_model_weights* w, int max_len, int attn_splits,
                               int slots, moert_model** out);
+/* Host-CPU hybrid (the reference's D1 engine in its deterministic mode, AdmitMode::TokenBarrier with the LfuCpu
+ * policy: rust/moe-rt/src/motor/engine.rs, motor/line.rs run 802-840, serve_layer 512-583; HostExperts::compute for
+ * the misses, rust/moe-rt/src/cpu.rs:116-148; cuda_backend.rs:940-1014). Every expert lives in pinned host memory;
+ * a pool of `slots` (0 <= slots <= min(4096, layers*experts); fewer than top_k allowed) holds some of them. Each
+ * step is driven from the calling thread: the token's table (the experts resident when it starts) goes to the
+ * device; per layer the GPU computes attention, the routing and the experts in the table, the routing and the
+ * normalised input come back, the host computes every other routed expert (cpu_threads threads) and a kernel adds
+ * their weighted sum into the residual stream; then the placement (moert_placement_*) admits the misses with LFU
+ * and the backlog bound, and their records are copied into the pool behind the work already queued, or held until
+ * the victim's layer has passed. Outputs equal the resident model's up to the order of the expert sum (the host
+ * part is added after the GPU part). moert_cache_stats / _counters / _token_counts / _clear apply; the prefetch and
+ * fill entry points, moert_time_kernel, the timeline and the multi-position step refuse a hybrid model. */
+int moert_model_create_hybrid(const moert_config* cfg, const moert_model_weights* w, int max_len, int attn_splits,
+                              int slots, int backlog, int cpu_threads, moert_model** out);
 /* Cache counters since creation or the last clear: requests served from the pool, and copies from host memory
  * (CacheStats::{hits, sync_copies}, rust/moe-rt/src/cache.rs:112-124). */
 int moert_cache_stats(moert_model* m, unsigned long long* hits, unsigned long long* copies);
@@ -136,7 +150,8 @@ int moert_cache_prefetch_mode(moert_model* m, int on);
 int moert_cache_predictions(moert_model* m, int pos0, int n, int* ids);
 /* Per position and layer of [pos0, pos0 + n): [n][layers][4] = requests served from the pool, copies inside the step,
  * experts copied ahead by the prefetch branch, 0 (the reference's per-token counters, CacheStats,
- * rust/moe-rt/src/cache.rs:111-124, per token). */
+ * rust/moe-rt/src/cache.rs:111-124, per token). For a hybrid model: hits, admissions (copies), admissions refused
+ * (dropped), requests computed on the host. */
 int moert_cache_token_counts(moert_model* m, int pos0, int n, int* counts);
 /* Cumulative counters since creation or the last clear; mirrors CacheStats (rust/moe-rt/src/cache.rs:111-124) and
  * the engine's Stats (rust/moe-rt/src/motor/mod.rs:96-109): needed = requests, hits, copies (sync_copies: inside the

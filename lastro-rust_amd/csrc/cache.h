@@ -41,6 +41,11 @@ struct CacheDev {
   int* tok_hist;          // [max_len][layers][4] per position and layer: hits, copies, prefetched, 0
   const int* state;       // the step state (ST_POS: the position being decoded)
   int layers;
+  // host-CPU hybrid (moert_model_create_hybrid): the token's table, key -> pool slot or -1 (the host computes that
+  // expert), decided on the host; the cached kernels then read it instead of deciding, and the gate/up kernel
+  // publishes the layer's normalised input for the host
+  const int* table;
+  float* xn;              // [H]
 };
 
 // The MoE half of a layer step of a cached model: rmsnorm + router + top-k + LRU decision + gate/up + SwiGLU of the
@@ -49,6 +54,8 @@ hipError_t launch_route_up_cached(hipStream_t s, const LayerDev& L, const Dims& 
                                   const CacheDev& c, Tl tl = {});
 hipError_t launch_expert_down_cached(hipStream_t s, const Dims& d, const StepBufs& b, int layer, const CacheDev& c,
                                      Tl tl = {});
+// h[i] += res * y[i] for i < n (hybrid: the host-computed experts of a layer step)
+hipError_t launch_add_scaled(hipStream_t s, float* h, const float* y, float res, int n);
 
 // Prefetch branch of a cached step, for layer `layer` (run on a side stream while the layer's attention runs):
 // launch_prefetch_decide predicts the layer's experts from its input h (the layer's router on rmsnorm(h, ln_moe),

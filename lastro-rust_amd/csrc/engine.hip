@@ -10,6 +10,7 @@
 
 #include <chrono>
 #include <cmath>
+#include <memory>
 #include <cstdlib>
 #include <cstdarg>
 #include <cstdio>
@@ -19,6 +20,8 @@
 
 #include "../../include/moert.h"
 #include "host_utils.h"
+#include "host_experts.h"
+#include "placement.h"
 #include "cache.h"
 #include "grouped.h"
 #include "kernels.h"
@@ -223,6 +226,23 @@ struct moert_model {
   int mx_prev_pos = 0;
   double mx_wait_s = 0;
   double mx_speed_last[2] = {};  // decode and prefill tok/s of the last finished request
+  // host-CPU hybrid (moert_model_create_hybrid): the placement state machine, the token's table on the device, the
+  // pinned read-backs of each layer's routing and normalised input, the host experts' sum (mapped for the add
+  // kernel), and per position and layer: hits, copies, dropped, host-computed requests
+  bool hybrid = false;
+  std::unique_ptr<Placement> place;
+  int hy_threads = 1;
+  int* hy_table = nullptr;  // device
+  int* hy_table_pin = nullptr;
+  int* hy_ids_pin = nullptr;
+  float* hy_w_pin = nullptr;
+  float* hy_xn_pin = nullptr;
+  float* hy_y_pin = nullptr;
+  float* hy_y_dev = nullptr;
+  float* hy_xn_dev = nullptr;
+  hipEvent_t hy_ev = nullptr;
+  std::vector<float> hy_act, hy_y;
+  std::vector<int> hy_tok;  // [max_len][layers][4]
 
   // Launches one decode step. With `timed` >= 0, every launch of that kernel class records its dispatch start and
   // end into the next event pair of `ev`. With a timeline buffer (measurement build), launch i of the step records
@@ -281,6 +301,105 @@ struct moert_model {
   unsigned long long* tl_buf = nullptr;
   size_t tl_launches = 0;
   std::vector<int> tl_kind, tl_layer;
+
+  // A hybrid record copy (host store -> pool slot), queued on the model stream behind the work queued so far.
+  int hy_copy(int slot, int key) {
+    const uint8_t* r = (const uint8_t*)host_store + (size_t)key * cache.record_bytes;
+    const size_t v = (size_t)slot, dn_d = cache.record_bytes - cache.gu_q - cache.gu_d - cache.dn_q;
+    CHECK_HIP(hipMemcpyAsync((void*)(cache.pool_gu.q + v * cache.gu_q), r, cache.gu_q, hipMemcpyHostToDevice, stream));
+    if (cache.gu_d)
+      CHECK_HIP(hipMemcpyAsync((uint8_t*)cache.pool_gu.d + v * cache.gu_d, r + cache.gu_q, cache.gu_d,
+                               hipMemcpyHostToDevice, stream));
+    r += cache.gu_q + cache.gu_d;
+    CHECK_HIP(hipMemcpyAsync((void*)(cache.pool_dn.q + v * cache.dn_q), r, cache.dn_q, hipMemcpyHostToDevice, stream));
+    if (dn_d)
+      CHECK_HIP(hipMemcpyAsync((uint8_t*)cache.pool_dn.d + v * dn_d, r + cache.dn_q, dn_d, hipMemcpyHostToDevice,
+                               stream));
+    return MOERT_OK;
+  }
+
+  int hy_copies() {
+    for (const CopyOrder& o : place->take_copies()) {
+      int rc = hy_copy(o.slot, o.key);
+      if (rc) return rc;
+    }
+    return MOERT_OK;
+  }
+
+  // One hybrid decode step (the D1 protocol in its deterministic mode, driven from this thread): the token's table
+  // to the device; per layer the attention half and the gate/up kernel (experts in the table from their slots), the
+  // routing and the normalised input read back, the down kernel; then, on the host, the layer's requests served
+  // (placement), the experts outside the table computed and added into the residual stream by a small kernel, and
+  // the admissions' copies queued (or held until their victim's layer has passed); at the end of the token every
+  // copy queued precedes the next token's work in stream order (the barrier), and the next table is published.
+  int hybrid_step() {
+    Placement& P = *place;
+    const int L = cfg.layers, E = cfg.experts, K = cfg.top_k, H = cfg.hidden, I = cfg.inter;
+    // the previous token has ended (so its table copy has been read, and its position is final)
+    CHECK_HIP(hipStreamSynchronize(stream));
+    int pos = 0;
+    CHECK_HIP(hipMemcpy(&pos, b.state + ST_POS, 4, hipMemcpyDeviceToHost));
+    std::memcpy(hy_table_pin, P.table().data(), (size_t)L * E * 4);
+    CHECK_HIP(hipMemcpyAsync(hy_table, hy_table_pin, (size_t)L * E * 4, hipMemcpyHostToDevice, stream));
+    CHECK_HIP(launch_embed(stream, embed, dims, b));
+    std::vector<int> keys, n_e;
+    std::vector<char> gpu;
+    for (int l = 0; l < L; l++) {
+      const LayerDev& Ld = layers[l];
+      CHECK_HIP(launch_qkv(stream, Ld, dims, b));
+      CHECK_HIP(launch_attn_split(stream, Ld, dims, b));
+      CHECK_HIP(launch_attn_combine(stream, dims, b));
+      CHECK_HIP(launch_oproj(stream, Ld, dims, b));
+      CHECK_HIP(launch_route_up_cached(stream, Ld, dims, b, l, cache));
+      CHECK_HIP(hipMemcpyAsync(hy_ids_pin, b.route_ids + l * K, (size_t)K * 4, hipMemcpyDeviceToHost, stream));
+      CHECK_HIP(hipMemcpyAsync(hy_w_pin, b.route_w + l * K, (size_t)K * 4, hipMemcpyDeviceToHost, stream));
+      CHECK_HIP(hipMemcpyAsync(hy_xn_pin, hy_xn_dev, (size_t)H * 4, hipMemcpyDeviceToHost, stream));
+      CHECK_HIP(hipEventRecord(hy_ev, stream));
+      CHECK_HIP(launch_expert_down_cached(stream, dims, b, l, cache));
+      CHECK_HIP(hipEventSynchronize(hy_ev));
+      for (int j = 0; j < K; j++)
+        if (hy_ids_pin[j] < 0 || hy_ids_pin[j] >= E) {
+          set_err("hybrid step: routed expert %d outside [0, %d)", hy_ids_pin[j], E);
+          return MOERT_E_DEVICE;
+        }
+      const PlacementStats s0 = P.stats();
+      P.serve_layer(l, hy_ids_pin, 1, &keys, &n_e, &gpu);
+      // the host experts in top-k order (CPU-served requests, HostExperts::compute)
+      bool any = false;
+      std::fill(hy_y.begin(), hy_y.end(), 0.0f);
+      for (int j = 0; j < K; j++) {
+        const int key = l * E + hy_ids_pin[j];
+        if (P.table()[key] >= 0) continue;
+        host_expert_ffn((const uint8_t*)host_store + (size_t)key * cache.record_bytes, cache.pool_gu.dtype, H, I,
+                        cache.gu_q, cache.gu_d, cache.dn_q, hy_xn_pin, hy_w_pin[j], hy_act.data(), hy_y.data(),
+                        hy_threads);
+        any = true;
+      }
+      if (any) {
+        std::memcpy(hy_y_pin, hy_y.data(), (size_t)H * 4);
+        CHECK_HIP(launch_add_scaled(stream, b.h, hy_y_dev, dims.res_mult, H));
+      }
+      P.admit_layer();
+      const PlacementStats& s1 = P.stats();
+      if (pos >= 0 && pos < max_len) {
+        int* t = hy_tok.data() + ((size_t)pos * L + l) * 4;
+        t[0] = (int)(s1.hits - s0.hits);
+        t[1] = (int)(s1.copies - s0.copies);
+        t[2] = (int)(s1.dropped - s0.dropped);
+        t[3] = (int)(s1.cpu - s0.cpu);
+      }
+      // (the next layer's sum is written into the same pinned buffer only after its routing event, which follows
+      // this layer's add kernel in stream order)
+      int rc = hy_copies();
+      if (rc) return rc;
+    }
+    P.end_token();
+    int rc = hy_copies();
+    if (rc) return rc;
+    CHECK_HIP(launch_head(stream, embed, norm, dims, b));
+    CHECK_HIP(launch_head_argmax(stream, embed, dims, b));
+    return MOERT_OK;
+  }
 
   int fail(int rc) {
     if (rc == MOERT_E_DEVICE) {
@@ -460,6 +579,9 @@ struct moert_model {
     for (hipEvent_t e : {ev_fork, ev_pred, ev_copy, mx_ev, mx_t[0], mx_t[1], mx_t[2]})
       if (e) (void)hipEventDestroy(e);
     if (mx_pin) (void)hipHostFree(mx_pin);
+    if (hy_ev) (void)hipEventDestroy(hy_ev);
+    for (void* p : {(void*)hy_table_pin, (void*)hy_ids_pin, (void*)hy_w_pin, (void*)hy_xn_pin, (void*)hy_y_pin})
+      if (p) (void)hipHostFree(p);
     if (pf_stream) (void)hipStreamDestroy(pf_stream);
     if (stream) (void)hipStreamDestroy(stream);
   }
@@ -540,7 +662,7 @@ static int cache_create(moert_model* m, const moert_model_weights* w, int slots)
 }
 
 static int model_create(const moert_config* c, const moert_model_weights* w, int max_len, int splits,
-                        int cache_slots, moert_model** out) {
+                        int cache_slots, moert_model** out, bool graph = true) {
   CHECK_CFG(c && w && out, "null argument");
   *out = nullptr;
   CHECK_CFG(c->head_dim == 64, "head_dim %d: the attention kernels are built for 64", c->head_dim);
@@ -635,7 +757,7 @@ static int model_create(const moert_config* c, const moert_model_weights* w, int
     return bail(MOERT_E_DEVICE);
   }
   if (cache_slots > 0 && (rc = cache_create(m, w, cache_slots))) return bail(rc);
-  if ((rc = m->build_graph())) return bail(rc);
+  if (graph && (rc = m->build_graph())) return bail(rc);
   *out = m;
   return MOERT_OK;
 }
@@ -766,6 +888,50 @@ int moert_model_create_cached(const moert_config* cfg, const moert_model_weights
   return model_create(cfg, w, max_len, attn_splits, slots, out);
 }
 
+int moert_model_create_hybrid(const moert_config* cfg, const moert_model_weights* w, int max_len, int attn_splits,
+                              int slots, int backlog, int cpu_threads, moert_model** out) {
+  CHECK_CFG(cfg && out, "null argument");
+  CHECK_CFG(slots >= 0 && slots <= cfg->layers * cfg->experts && slots <= kCacheMaxSlots,
+            "hybrid: %d slots outside [0, min(layers * experts, %d)]", slots, kCacheMaxSlots);
+  CHECK_CFG(backlog >= 0 && cpu_threads >= 1 && cpu_threads <= 64, "hybrid: backlog %d, cpu_threads %d", backlog,
+            cpu_threads);
+  // the pool and the host store of the expert cache (at least top_k slots are allocated; the placement uses `slots`)
+  int rc = model_create(cfg, w, max_len, attn_splits, std::max(slots, cfg->top_k), out, false);
+  if (rc) return rc;
+  moert_model* m = *out;
+  auto bail = [&](int code) {
+    delete m;
+    *out = nullptr;
+    return code;
+  };
+  const int L = cfg->layers, E = cfg->experts, H = cfg->hidden;
+  m->hybrid = true;
+  m->hy_threads = cpu_threads;
+  m->place.reset(new Placement(L, E, cfg->top_k, slots, backlog));
+  m->place->start();
+  void* p = nullptr;
+  if ((rc = m->arena.alloc(&p, (size_t)L * E * 4))) return bail(rc);
+  m->hy_table = (int*)p;
+  if ((rc = m->arena.alloc(&p, (size_t)H * 4))) return bail(rc);
+  m->hy_xn_dev = (float*)p;
+  if (hipHostMalloc((void**)&m->hy_table_pin, (size_t)L * E * 4, hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void**)&m->hy_ids_pin, 8 * 4, hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void**)&m->hy_w_pin, 8 * 4, hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void**)&m->hy_xn_pin, (size_t)H * 4, hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void**)&m->hy_y_pin, (size_t)H * 4, hipHostMallocMapped) != hipSuccess ||
+      hipHostGetDevicePointer((void**)&m->hy_y_dev, m->hy_y_pin, 0) != hipSuccess ||
+      hipEventCreateWithFlags(&m->hy_ev, hipEventDisableTiming) != hipSuccess) {
+    set_err("hybrid: pinned host buffers or event");
+    return bail(MOERT_E_DEVICE);
+  }
+  m->cache.table = m->hy_table;
+  m->cache.xn = m->hy_xn_dev;
+  m->hy_act.assign((size_t)cfg->inter, 0.0f);
+  m->hy_y.assign((size_t)H, 0.0f);
+  m->hy_tok.assign((size_t)max_len * L * 4, 0);
+  return MOERT_OK;
+}
+
 int moert_model_destroy(moert_model* m) {
   delete m;
   return MOERT_OK;
@@ -808,6 +974,7 @@ static bool use_graph() {
 }
 
 static int model_launch(moert_model* m) {
+  if (m->hybrid) return m->hybrid_step();
   if (!use_graph()) return m->enqueue(-1, nullptr);
   CHECK_HIP(hipGraphLaunch(m->exec, m->stream));
   return MOERT_OK;
@@ -827,7 +994,16 @@ static size_t mx_pin_bytes(const moert_model* m) {
 // Queues the read-back behind the steps launched so far; its event completes when they have.
 static int mx_enqueue_read(moert_model* m) {
   unsigned char* p = m->mx_pin;
-  if (m->cached) {
+  if (m->hybrid) {
+    // the placement's counters (host side, current: the host serves every layer before the next is queued);
+    // word 3: the requests computed on the host
+    unsigned long long* st = (unsigned long long*)p;
+    const PlacementStats& s = m->place->stats();
+    st[CS_HITS] = s.hits;
+    st[CS_COPIES] = s.copies;
+    st[CS_PREFETCH] = 0;
+    st[3] = s.cpu;
+  } else if (m->cached) {
     CHECK_HIP(hipMemcpyAsync(p, m->cache.stats, 8 * CS_WORDS, hipMemcpyDeviceToHost, m->stream));
     CHECK_HIP(hipMemcpyAsync(p + 8 * CS_WORDS + 4 * ST_WORDS, m->cache.cur, 4, hipMemcpyDeviceToHost, m->stream));
     CHECK_HIP(hipMemcpyAsync(p + 8 * CS_WORDS + 4 * (ST_WORDS + 1), m->cache.slot_key, 8 * (size_t)m->cache.slots,
@@ -876,7 +1052,21 @@ static void mx_consume(moert_model* m, const MxCall& c, moert_model::Clock::time
     (void)moert_metrics_set_window(mx, &w);
   }
   moert_metrics_cache ca{};
-  if (m->cached) {
+  if (m->hybrid) {
+    // requests served from the pool or on the host; copies are background admissions
+    const unsigned long long dh = st[CS_HITS] - m->mx_prev[CS_HITS], dc = st[CS_COPIES] - m->mx_prev[CS_COPIES],
+                             du = st[3] - m->mx_prev[3];
+    const double need = (double)(dh + du);
+    ca.slots_total = (uint32_t)m->place->slots();
+    ca.slots_resident = (uint32_t)m->place->resident();
+    ca.hit_frac = need > 0 ? dh / need : 0.0;
+    ca.cpu_frac = need > 0 ? du / need : 0.0;
+    ca.h2d_gbs = dt > 0 ? (double)dc * m->cache.record_bytes / dt / 1e9 : 0.0;
+    ca.total_hits = st[CS_HITS];
+    ca.total_copies = st[CS_COPIES];
+    ca.total_cpu = st[3];
+    memcpy(m->mx_prev, st, sizeof m->mx_prev);
+  } else if (m->cached) {
     const int S = m->cache.slots, cur = state[ST_WORDS];
     const int* keys = state + ST_WORDS + 1 + (size_t)(cur & 1) * S;
     uint32_t res = 0;
@@ -1246,6 +1436,7 @@ int moert_read_logits(moert_model* m, float* logits) {
 int moert_timeline_step(moert_model* m, unsigned long long* out, int* kinds, int* layers, int max_launches,
                         int* n_launches) {
   MODEL_OK(m);
+  CHECK_CFG(!m->hybrid, "the hybrid model steps from the host, layer by layer: no per-kernel timing");
 #ifndef MOERT_TIMELINE
   (void)out; (void)kinds; (void)layers; (void)max_launches; (void)n_launches;
   set_err("timeline: this library was built without MOERT_TIMELINE (use libmoert_tl.so)");
@@ -1340,6 +1531,7 @@ static int time_kernel_impl(moert_model* m, int kind, int iters, double* us, int
 
 int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch, int* launches) {
   MODEL_OK(m);
+  CHECK_CFG(!m->hybrid, "the hybrid model steps from the host, layer by layer: no per-kernel timing");
   if (kind < 0 || kind >= MOERT_K_COUNT || iters < 1 || !us_per_launch) {
     set_err("time_kernel: kind %d, iters %d", kind, iters);
     return MOERT_E_CONFIG;
@@ -1357,8 +1549,14 @@ int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch
 int moert_cache_stats(moert_model* m, unsigned long long* hits, unsigned long long* copies) {
   MODEL_OK(m);
   CHECK_CFG(m->cached, "model has no expert cache");
+  if (m->hybrid) {
+    if (hits) *hits = m->place->stats().hits;
+    if (copies) *copies = m->place->stats().copies;
+    return MOERT_OK;
+  }
   unsigned long long st[CS_WORDS];
   MTRY(m, model_copy_out(m, st, m->cache.stats, sizeof st));
+  MTRY(m, model_sync(m));
   if (hits) *hits = st[CS_HITS];
   if (copies) *copies = st[CS_COPIES];
   return MOERT_OK;
@@ -1367,6 +1565,15 @@ int moert_cache_stats(moert_model* m, unsigned long long* hits, unsigned long lo
 int moert_cache_clear(moert_model* m) {
   MODEL_OK(m);
   CHECK_CFG(m->cached, "model has no expert cache");
+  if (m->hybrid) {
+    // an empty pool, a fresh frequency and zero counters (the pool's contents are never read without a table entry)
+    MTRY(m, model_sync(m));
+    const Placement& P = *m->place;
+    m->place.reset(new Placement(m->cfg.layers, m->cfg.experts, m->cfg.top_k, P.slots(), m->place->backlog()));
+    m->place->start();
+    std::fill(m->hy_tok.begin(), m->hy_tok.end(), 0);
+    return MOERT_OK;
+  }
   MTRY(m, m->cache_clear());
   return MOERT_OK;
 }
@@ -1374,6 +1581,7 @@ int moert_cache_clear(moert_model* m) {
 int moert_cache_prefetch_mode(moert_model* m, int on) {
   MODEL_OK(m);
   CHECK_CFG(m->cached, "model has no expert cache");
+  CHECK_CFG(!m->hybrid, "prefetch mode: the hybrid model's copies are decided by its placement");
   CHECK_CFG(on == 0 || on == 1, "prefetch mode %d: 0 (off) or 1 (each layer's experts predicted from its input)", on);
   if ((on != 0) == m->prefetch) return MOERT_OK;
   if (!m->pf_stream) {
@@ -1394,7 +1602,7 @@ int moert_cache_prefetch_mode(moert_model* m, int on) {
 
 int moert_cache_predictions(moert_model* m, int pos0, int n, int* ids) {
   MODEL_OK(m);
-  CHECK_CFG(m->cached, "model has no expert cache");
+  CHECK_CFG(m->cached && !m->hybrid, "model has no expert cache with a prefetch branch");
   CHECK_CFG(ids && pos0 >= 0 && n >= 0 && pos0 + n <= m->max_len, "predictions: positions [%d, %d)", pos0, pos0 + n);
   const size_t row = (size_t)m->cfg.layers * 8;
   MTRY(m, model_copy_out(m, ids, m->cache.pred_hist + (size_t)pos0 * row, (size_t)n * row * 4));
@@ -1408,6 +1616,11 @@ int moert_cache_token_counts(moert_model* m, int pos0, int n, int* counts) {
   CHECK_CFG(counts && pos0 >= 0 && n >= 0 && pos0 + n <= m->max_len, "token counts: positions [%d, %d)", pos0,
             pos0 + n);
   const size_t row = (size_t)m->cfg.layers * 4;
+  if (m->hybrid) {
+    MTRY(m, model_sync(m));
+    std::memcpy(counts, m->hy_tok.data() + (size_t)pos0 * row, (size_t)n * row * 4);
+    return MOERT_OK;
+  }
   MTRY(m, model_copy_out(m, counts, m->cache.tok_hist + (size_t)pos0 * row, (size_t)n * row * 4));
   MTRY(m, model_sync(m));
   return MOERT_OK;
@@ -1416,6 +1629,21 @@ int moert_cache_token_counts(moert_model* m, int pos0, int n, int* counts) {
 int moert_cache_counters_get(moert_model* m, moert_cache_counters* out) {
   MODEL_OK(m);
   CHECK_CFG(m->cached && out, "model has no expert cache (or null output)");
+  if (m->hybrid) {
+    MTRY(m, model_sync(m));
+    const PlacementStats& s = m->place->stats();
+    moert_cache_counters c{};
+    c.needed = s.needed;
+    c.hits = s.hits;
+    c.cpu = s.cpu;
+    c.copies = s.copies;
+    c.dropped = s.dropped;
+    c.deferred = s.deferred;
+    c.bytes_copied = s.copies * (unsigned long long)m->cache.record_bytes;
+    c.slots = m->place->slots();
+    *out = c;
+    return MOERT_OK;
+  }
   unsigned long long st[CS_WORDS];
   MTRY(m, model_copy_out(m, st, m->cache.stats, sizeof st));
   MTRY(m, model_sync(m));
@@ -1432,7 +1660,7 @@ int moert_cache_counters_get(moert_model* m, moert_cache_counters* out) {
 
 int moert_cache_fill(moert_model* m, int* copied) {
   MODEL_OK(m);
-  CHECK_CFG(m->cached, "model has no expert cache");
+  CHECK_CFG(m->cached && !m->hybrid, "model has no expert cache with device-side placement");
   std::vector<int> keys((size_t)m->cfg.layers * m->cfg.experts);
   for (size_t i = 0; i < keys.size(); i++) keys[i] = (int)i;
   MTRY(m, m->cache_load(keys.data(), (int)keys.size(), false, copied));
@@ -1441,7 +1669,7 @@ int moert_cache_fill(moert_model* m, int* copied) {
 
 int moert_cache_prefetch(moert_model* m, int layer, const int* experts, int n, int* copied) {
   MODEL_OK(m);
-  CHECK_CFG(m->cached, "model has no expert cache");
+  CHECK_CFG(m->cached && !m->hybrid, "model has no expert cache with device-side placement");
   CHECK_CFG(layer >= 0 && layer < m->cfg.layers, "layer %d outside [0, %d)", layer, m->cfg.layers);
   CHECK_CFG(experts && n >= 1 && n <= m->cache.slots && n <= m->cfg.experts,
             "prefetch of %d experts: between 1 and min(slots %d, experts %d)", n, m->cache.slots, m->cfg.experts);

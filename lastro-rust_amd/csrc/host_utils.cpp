@@ -132,7 +132,11 @@ static void normal_range(uint64_t seed, uint64_t stream, size_t i0, size_t i1, f
 
 void parallel_for(size_t n, size_t grain, const std::function<void(size_t, size_t)>& f) {
   unsigned hw = std::thread::hardware_concurrency();
-  size_t nt = std::min<size_t>(hw ? hw : 1, 16);
+  parallel_for_n(n, grain, (int)std::min<unsigned>(hw ? hw : 1, 16), f);
+}
+
+void parallel_for_n(size_t n, size_t grain, int threads, const std::function<void(size_t, size_t)>& f) {
+  size_t nt = threads > 1 ? (size_t)threads : 1;
   size_t chunks = (n + grain - 1) / grain;
   if (nt <= 1 || chunks <= 1) {
     f(0, n);

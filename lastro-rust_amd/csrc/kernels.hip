@@ -920,7 +920,22 @@ __global__ __launch_bounds__(route_waves(DT) * 64) void k_route_up(DMat router, 
   int mk[8];
 #pragma unroll
   for (int r = 0; r < 8; r++) mk[r] = -1;
-  if (CACHED) {
+  if (CACHED && c.table) {
+    // hybrid: the slot of each routed expert from the token's table; an expert without one is computed on the host
+    int e = 0;
+#pragma unroll
+    for (int r = 0; r < 8; r++) e = lane == r ? eid[r] : e;
+    if (wave == 0 && lane < k) lslot[lane] = c.table[layer * c.experts + e];
+    if (blockIdx.x == 0 && wave == 0 && lane < k) {
+      c.route[lane] = lslot[lane];
+      c.route[8 + lane] = -1;
+    }
+    if (blockIdx.x == 0)
+      for (int i = threadIdx.x; i < K; i += NT) c.xn[i] = xs[i];
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 8; r++) eid[r] = r < k ? lslot[r] : 0;
+  } else if (CACHED) {
     const int cur = *c.cur, S = c.slots;
     if (wave == 0) {
       int key = 0;
@@ -977,6 +992,7 @@ __global__ __launch_bounds__(route_waves(DT) * 64) void k_route_up(DMat router, 
       ej = j == q ? eid[q] : ej;
       mj = j == q ? mk[q] : mj;
     }
+    if (CACHED && ej < 0) v = false;  // hybrid: an expert the host computes
     size_t r0 = (size_t)ej * 2 * inter;
     src[2 * a] = src[2 * a + 1] = CACHED ? expert_source(c, 0, ej, mj, r0) : gu;
     row[2 * a] = r0 + r;
@@ -1047,10 +1063,11 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __r
   DMat src[KP];
 #pragma unroll
   for (int p = 0; p < KP; p++) {
-    size_t r0 = (size_t)idj[p] * hidden;
-    src[p] = CACHED ? expert_source(c, 1, idj[p], mkj[p], r0) : m;
+    const int sl = CACHED && idj[p] < 0 ? 0 : idj[p];  // hybrid: an expert the host computes (rows unused)
+    size_t r0 = (size_t)sl * hidden;
+    src[p] = CACHED ? expert_source(c, 1, sl, mkj[p], r0) : m;
     srow[p] = r0 + (rok ? r : 0);
-    prow[p] = (size_t)idj[p] * hidden + (rok ? r : 0);
+    prow[p] = (size_t)sl * hidden + (rok ? r : 0);
     all[p] = true;
     put[p] = CACHED && rok && mkj[p] >= 0 && p * G::RPW + rw < k;
   }
@@ -1077,7 +1094,7 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __r
   for (int p = 0; p < KP; p++) {
     int j = p * G::RPW + rw;
     float acc = 0.0f;
-    if (j < k) {
+    if (j < k && (!CACHED || idj[p] >= 0)) {
       XReg<DT, K> xr;
       load_x<DT, K>(xr, xs + (size_t)j * K, sub);
 #pragma unroll
@@ -1096,7 +1113,8 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(DMat m, const float* __r
     for (int g2 = 0; g2 < G::RPW; g2++) {
       int j = p * G::RPW + g2;
       float dj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(dsum[p]), g2 * G::LPR));
-      if (j < k) y = y + wts[j] * dj;
+      const bool live = !CACHED || __builtin_amdgcn_readlane(idj[p], g2 * G::LPR) >= 0;
+      if (j < k && live) y = y + wts[j] * dj;
     }
   }
   if (lane == 0) h[r] = accumulate ? hold + res * y : y;
@@ -1529,7 +1547,7 @@ hipError_t launch_route_up(hipStream_t s, const LayerDev& L, const Dims& d, cons
 
 hipError_t launch_route_up_cached(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
                                   const CacheDev& c, Tl tl) {
-  if (L.router.dtype != c.pool_gu.dtype || L.router.cols != c.pool_gu.cols || c.slots < d.top_k ||
+  if (L.router.dtype != c.pool_gu.dtype || L.router.cols != c.pool_gu.cols || (!c.table && c.slots < d.top_k) ||
       c.slots > kCacheMaxSlots || L.router.rows > 64 || d.top_k > 8)
     return hipErrorInvalidValue;
 #define BODY(KK)                                                                                           \
@@ -1562,6 +1580,18 @@ hipError_t launch_expert_down_cached(hipStream_t s, const Dims& d, const StepBuf
     break;
   DOWN_DISPATCH(c.pool_dn.dtype, c.pool_dn.cols, BODY)
 #undef BODY
+  return hipGetLastError();
+}
+
+// h[i] += res * y[i] (the host-computed experts of a hybrid layer step, y in mapped host memory)
+__global__ __launch_bounds__(256) void k_add_scaled(float* __restrict__ h, const float* __restrict__ y, float res,
+                                                    int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) h[i] = h[i] + res * y[i];
+}
+
+hipError_t launch_add_scaled(hipStream_t s, float* h, const float* y, float res, int n) {
+  klaunch(k_add_scaled, cdiv(n, 256), 256, 0, s, h, y, res, n);
   return hipGetLastError();
 }
 

@@ -63,6 +63,7 @@ class Placement {
   std::vector<CopyOrder> take_copies();                      // the copies queued since the last call
   const PlacementStats& stats() const { return stats_; }
   int slots() const { return (int)slot_.size(); }
+  int backlog() const { return backlog_; }
   int resident() const;
   double score(int key) const { return freq_.score(key); }
 

@@ -121,6 +121,8 @@ def lib() -> ctypes.CDLL:
             "moert_cache_prefetch_mode": (i, [vp, i]),
             "moert_cache_predictions": (i, [vp, i, i, vp]),
             "moert_cache_token_counts": (i, [vp, i, i, vp]),
+            "moert_model_create_hybrid": (i, [ctypes.POINTER(moert_config), ctypes.POINTER(moert_model_weights), i,
+                                              i, i, i, i, ctypes.POINTER(vp)]),
             "moert_cache_counters_get": (i, [vp, ctypes.POINTER(moert_cache_counters)]),
             "moert_decode_step": (i, [vp, i, vp, vp, vp, ip]),
             "moert_generate": (i, [vp, vp, i, i, vp, vp]),
@@ -207,7 +209,7 @@ def lib() -> ctypes.CDLL:
 EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moert_model_destroy",
             "moert_model_create_cached", "moert_cache_stats", "moert_cache_clear", "moert_cache_fill",
             "moert_cache_prefetch", "moert_cache_prefetch_mode", "moert_cache_predictions", "moert_cache_token_counts",
-            "moert_cache_counters_get",
+            "moert_cache_counters_get", "moert_model_create_hybrid",
             "moert_decode_step", "moert_generate", "moert_step_batched", "moert_prefill", "moert_reset_sequence",
             "moert_kv_prefill_fp16",
             "moert_set_position", "moert_get_position", "moert_read_kv_fp16", "moert_read_hidden", "moert_read_logits",
@@ -393,11 +395,18 @@ class GpuModel:
     cache_slots, the experts are served from an expert cache of that many HBM slots over a pinned host store
     (GpuModel::upload_cached, gpu_model.rs:197-200)."""
 
-    def __init__(self, model: SynthModel, max_len: int, attn_splits: int = 64, cache_slots: Optional[int] = None):
+    def __init__(self, model: SynthModel, max_len: int, attn_splits: int = 64, cache_slots: Optional[int] = None,
+                 hybrid: Optional[tuple] = None):
+        """hybrid = (slots, backlog, cpu_threads): the host-CPU hybrid (moert_model_create_hybrid) instead."""
         self.model, self.cfg, self.max_len = model, model.cfg, max_len
         self.cache_slots = cache_slots
         h = ctypes.c_void_p()
-        if cache_slots is None:
+        if hybrid is not None:
+            slots, backlog, threads = hybrid
+            check(lib().moert_model_create_hybrid(ctypes.byref(model.cfg.c()), ctypes.byref(model.weights()),
+                                                  max_len, attn_splits, int(slots), int(backlog), int(threads),
+                                                  ctypes.byref(h)))
+        elif cache_slots is None:
             check(lib().moert_model_create(ctypes.byref(model.cfg.c()), ctypes.byref(model.weights()), max_len,
                                            attn_splits, ctypes.byref(h)))
         else:
@@ -440,11 +449,12 @@ class GpuModel:
         check(lib().moert_cache_predictions(self.h, pos0, n, ptr(out)))
         return out[:, :, :c.top_k]
 
-    def cache_token_counts(self, pos0: int, n: int) -> np.ndarray:
-        """Per position and layer: [n, layers, 3] = hits, copies inside the step, prefetched copies."""
+    def cache_token_counts(self, pos0: int, n: int, words: int = 3) -> np.ndarray:
+        """Per position and layer: [n, layers, words] = hits, copies inside the step, prefetched copies (hybrid: hits,
+        admissions, admissions refused, requests computed on the host)."""
         out = np.empty((n, self.cfg.layers, 4), np.int32)
         check(lib().moert_cache_token_counts(self.h, pos0, n, ptr(out)))
-        return out[:, :, :3]
+        return out[:, :, :words]
 
     def attach_metrics(self, mx: Optional["Metrics"], interval_ms: int = 500):
         """Lets generate() fill and publish `mx` (None detaches); the publisher must outlive the attachment."""

@@ -32,3 +32,13 @@ def gpu():
         pytest.skip("no GPU visible")
     print(f"\n[gpu] {name}", flush=True)
     return name
+
+
+@pytest.fixture(scope="session")
+def granite_3b_q4():
+    """The expert-cache workload's model: 3B-A800M shape, Q4_0 weights and head, Zipf(1.1) router bias."""
+    import moert
+    cfg = moert.Config(**moert.GRANITE_3B)
+    print("[case] 3b q4_0 build", flush=True)
+    m = moert.SynthModel(cfg, seed=4242, wdtype=moert.Q4_0, embed_dtype=moert.Q4_0, zipf_s=1.1)
+    return cfg, m

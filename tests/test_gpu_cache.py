@@ -112,14 +112,6 @@ def _forced_pair(res, cac, toks, label, every=1):
     return np.array(routes)
 
 
-@pytest.fixture(scope="module")
-def granite_3b_q4():
-    cfg = moert.Config(**moert.GRANITE_3B)
-    say("3b q4_0 build")
-    m = moert.SynthModel(cfg, seed=4242, wdtype=moert.Q4_0, embed_dtype=moert.Q4_0, zipf_s=1.1)
-    return cfg, m
-
-
 def test_granite_3b_q4_0_quarter_pool_forced_512_steps_equals_the_resident_model(gpu, granite_3b_q4):
     """The expert-cache workload: 3B shape, Q4_0, Zipf(1.1) router bias, a pool of 25% of the 1280 experts (320
     slots), 512 steps from an empty pool with a forced random token stream (so the pool keeps evicting): every
