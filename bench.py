@@ -124,7 +124,7 @@ def batched_step(cfg, seed, iters, m=16, nblocks=4):
     return out
 
 
-def expert_cache(cfg, seed, steps, frac=0.25):
+def expert_cache(cfg, seed, steps, frac=0.25, hybrid_steps=128):
     """The 3B shape with Q4_0 weights and the Zipf(1.1) router bias, experts served from an HBM pool holding 25% of
     the 1280 experts (320 slots) over pinned host memory: `steps` greedy tokens from an empty pool, one graph per
     token (routing, LRU and the host->pool copies all on the device). Reports tok/s, the hit rate, the bytes copied
@@ -192,6 +192,21 @@ def expert_cache(cfg, seed, steps, frac=0.25):
     filled = g.cache_fill()
     fill_s = time.perf_counter() - t0
     g.close()
+    # the host-CPU hybrid on the same model and forced tokens: experts outside the token's table computed on the host
+    # (16 threads), LFU admission with the reference's backlog of 4 copies, copies queued behind the layer
+    hsteps = min(steps, hybrid_steps)
+    hybrid = None
+    if hsteps > 0:
+        log(f"expert cache: host-CPU hybrid, {hsteps} forced tokens")
+        hy = moert.GpuModel(m, max_len, attn_splits=64, hybrid=(slots, 4, 16))
+        t0 = time.perf_counter()
+        hy.generate(forced[:hsteps], 1)
+        hwall = time.perf_counter() - t0
+        hc = hy.cache_counters()
+        hy.close()
+        hybrid = {"tok_s": round((hsteps + 1) / hwall, 2), "steps": hsteps + 1, "cpu_threads": 16, "backlog": 4,
+                  **{k: hc[k] for k in ("needed", "hits", "cpu", "copies", "dropped", "deferred")},
+                  "hit_frac": round(hc["hits"] / max(1, hc["needed"]), 4)}
     probe_bytes = 256 << 20
     pk, pm = moert.h2d_probe(probe_bytes, 4)
     log("expert cache: resident comparison")
@@ -208,6 +223,7 @@ def expert_cache(cfg, seed, steps, frac=0.25):
                              "copied_bytes_per_token": round(fcopies * record / steps),
                              "pcie_gbs_end_to_end": round(fcopies * record / fwall / 1e9, 2)},
            "forced_tokens_prefetch": prefetch,
+           "forced_tokens_hybrid": hybrid,
            "h2d_probe": {"bytes": probe_bytes, "kernel_copy_gbs": round(probe_bytes / (pk * 1e-6) / 1e9, 2),
                          "hipmemcpy_gbs": round(probe_bytes / (pm * 1e-6) / 1e9, 2)},
            "fill": {"experts": filled, "bytes": filled * record, "ms": round(fill_s * 1e3, 2),
