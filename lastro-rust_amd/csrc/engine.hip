@@ -365,17 +365,20 @@ struct moert_model {
       const PlacementStats s0 = P.stats();
       P.serve_layer(l, hy_ids_pin, 1, &keys, &n_e, &gpu);
       // the host experts in top-k order (CPU-served requests, HostExperts::compute)
-      bool any = false;
-      std::fill(hy_y.begin(), hy_y.end(), 0.0f);
+      const uint8_t* recs[8];
+      float wts[8];
+      int n_host = 0;
       for (int j = 0; j < K; j++) {
         const int key = l * E + hy_ids_pin[j];
         if (P.table()[key] >= 0) continue;
-        host_expert_ffn((const uint8_t*)host_store + (size_t)key * cache.record_bytes, cache.pool_gu.dtype, H, I,
-                        cache.gu_q, cache.gu_d, cache.dn_q, hy_xn_pin, hy_w_pin[j], hy_act.data(), hy_y.data(),
-                        hy_threads);
-        any = true;
+        recs[n_host] = (const uint8_t*)host_store + (size_t)key * cache.record_bytes;
+        wts[n_host++] = hy_w_pin[j];
       }
+      const bool any = n_host > 0;
       if (any) {
+        std::fill(hy_y.begin(), hy_y.end(), 0.0f);
+        const HostRecordGeo geo{cache.pool_gu.dtype, H, I, cache.gu_q, cache.gu_d, cache.dn_q};
+        host_experts_layer(geo, recs, wts, n_host, hy_xn_pin, hy_act.data(), hy_y.data(), hy_threads);
         std::memcpy(hy_y_pin, hy_y.data(), (size_t)H * 4);
         CHECK_HIP(launch_add_scaled(stream, b.h, hy_y_dev, dims.res_mult, H));
       }
@@ -926,7 +929,7 @@ int moert_model_create_hybrid(const moert_config* cfg, const moert_model_weights
   }
   m->cache.table = m->hy_table;
   m->cache.xn = m->hy_xn_dev;
-  m->hy_act.assign((size_t)cfg->inter, 0.0f);
+  m->hy_act.assign((size_t)cfg->top_k * cfg->inter, 0.0f);
   m->hy_y.assign((size_t)H, 0.0f);
   m->hy_tok.assign((size_t)max_len * L * 4, 0);
   return MOERT_OK;

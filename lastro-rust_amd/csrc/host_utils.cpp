@@ -2,7 +2,10 @@
 // generator used to build random-init models (no device code).
 #include <algorithm>
 #include <cmath>
+#include <condition_variable>
 #include <cstring>
+#include <memory>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -135,20 +138,94 @@ void parallel_for(size_t n, size_t grain, const std::function<void(size_t, size_
   parallel_for_n(n, grain, (int)std::min<unsigned>(hw ? hw : 1, 16), f);
 }
 
+namespace {
+
+// Worker threads that live for the process, so that a parallel loop costs a wake-up, not thread creation. One loop
+// runs at a time; the caller works on it too. Each loop has its own chunk counters, so a worker that wakes late for
+// an earlier loop finds its chunks taken and never calls that loop's function.
+struct Job {
+  const std::function<void(size_t, size_t)>* f;
+  size_t n, grain, chunks;
+  int limit;  // workers with id + 1 < limit take part (the caller is the last participant)
+  std::atomic<size_t> next{0}, done{0};
+};
+
+class Workers {
+ public:
+  static Workers& get() {
+    static Workers* w = new Workers();  // never destroyed: the threads sleep until the process ends
+    return *w;
+  }
+  int size() const { return (int)threads_.size(); }
+
+  void run(size_t n, size_t grain, int threads, const std::function<void(size_t, size_t)>& f) {
+    std::lock_guard<std::mutex> one(run_mu_);
+    auto job = std::make_shared<Job>();
+    job->f = &f;
+    job->n = n;
+    job->grain = grain;
+    job->chunks = (n + grain - 1) / grain;
+    job->limit = threads;
+    {
+      std::lock_guard<std::mutex> l(mu_);
+      cur_ = job;
+      gen_++;
+    }
+    cv_.notify_all();
+    work(*job);
+    std::unique_lock<std::mutex> l(mu_);
+    done_cv_.wait(l, [&] { return job->done.load() == job->chunks; });
+  }
+
+ private:
+  Workers() {
+    const unsigned hw = std::thread::hardware_concurrency();
+    const int n = (int)std::min<unsigned>(hw ? hw : 1, 64) - 1;
+    for (int i = 0; i < n; i++) threads_.emplace_back([this, i] { loop(i); });
+    for (auto& t : threads_) t.detach();
+  }
+
+  void work(Job& j) {
+    for (size_t c; (c = j.next.fetch_add(1)) < j.chunks;) {
+      (*j.f)(c * j.grain, std::min(j.n, (c + 1) * j.grain));
+      if (j.done.fetch_add(1) + 1 == j.chunks) {
+        std::lock_guard<std::mutex> l(mu_);
+        done_cv_.notify_all();
+      }
+    }
+  }
+
+  void loop(int id) {
+    uint64_t seen = 0;
+    for (;;) {
+      std::shared_ptr<Job> job;
+      {
+        std::unique_lock<std::mutex> l(mu_);
+        cv_.wait(l, [&] { return gen_ != seen; });
+        seen = gen_;
+        job = cur_;
+      }
+      if (id + 1 < job->limit) work(*job);
+    }
+  }
+
+  std::mutex run_mu_, mu_;
+  std::condition_variable cv_, done_cv_;
+  std::shared_ptr<Job> cur_;
+  uint64_t gen_ = 0;
+  std::vector<std::thread> threads_;
+};
+
+}  // namespace
+
 void parallel_for_n(size_t n, size_t grain, int threads, const std::function<void(size_t, size_t)>& f) {
-  size_t nt = threads > 1 ? (size_t)threads : 1;
-  size_t chunks = (n + grain - 1) / grain;
-  if (nt <= 1 || chunks <= 1) {
+  const size_t chunks = (n + grain - 1) / grain;
+  if (threads <= 1 || chunks <= 1) {
     f(0, n);
     return;
   }
-  std::atomic<size_t> next{0};
-  std::vector<std::thread> ts;
-  for (size_t t = 0; t < nt; t++)
-    ts.emplace_back([&] {
-      for (size_t c; (c = next.fetch_add(1)) < chunks;) f(c * grain, std::min(n, (c + 1) * grain));
-    });
-  for (auto& t : ts) t.join();
+  Workers& w = Workers::get();
+  w.run(n, grain, std::min(threads, w.size() + 1), f);
 }
 
 int synth_normal(uint64_t seed, uint64_t stream, size_t n, float scale, float offset, float* out) {
