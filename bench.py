@@ -29,7 +29,9 @@ def log(msg):
 def kernel_bytes(kind, cfg, ctx, wd, ed, nsplit):
     """Algorithmic HBM bytes of one launch of a kernel class at `ctx` cached positions: the weights it must stream
     (only the k routed experts for the expert kernels), the KV it must read and the split partials the attention
-    kernels exchange; other activations are < 0.1% of a layer's bytes and left out."""
+    kernels exchange; other activations are < 0.1% of a layer's bytes and left out. The output projection also reads
+    the router's columns of its rows (for the MoE-norm partials of its epilogue) and the router kernel reads those
+    partials instead of the router."""
     import moert
     H, d, I = cfg.hidden, cfg.head_dim, cfg.inter
     qd, kvd = cfg.heads * d, cfg.kv_heads * d
@@ -39,8 +41,8 @@ def kernel_bytes(kind, cfg, ctx, wd, ed, nsplit):
         moert.K_QKV: b(wd, (qd + 2 * kvd) * H),
         moert.K_ATTN_SPLIT: 2 * kvd * 2 * ctx,
         moert.K_ATTN_COMBINE: cfg.heads * nsplit * 66 * 4,
-        moert.K_OPROJ: b(wd, H * qd),
-        moert.K_ROUTE_UP: b(wd, cfg.experts * H) + cfg.top_k * b(wd, 2 * I * H),
+        moert.K_OPROJ: b(wd, H * qd) + b(wd, cfg.experts * H),
+        moert.K_ROUTE_UP: 65 * 256 * 4 + cfg.top_k * b(wd, 2 * I * H),
         moert.K_EXPERT_DOWN: cfg.top_k * b(wd, H * I),
         moert.K_HEAD: b(ed, cfg.vocab * H),
         moert.K_HEAD_ARGMAX: 0,
