@@ -68,19 +68,32 @@ def prefill_block(g, cfg, seed, ctx, decode_tok_s, m=32, reps=5):
     own synchronisation."""
     import numpy as np
     toks = np.random.default_rng(seed + 7).integers(0, cfg.vocab, m)
-    g.set_position(ctx)
-    g.step_batched(toks, want_logits=False)
-    best = None
-    for _ in range(reps):
+
+    def timed():
         g.set_position(ctx)
-        t0 = time.perf_counter()
         g.step_batched(toks, want_logits=False)
-        t = time.perf_counter() - t0
-        best = t if best is None else min(best, t)
+        best = None
+        for _ in range(reps):
+            g.set_position(ctx)
+            t0 = time.perf_counter()
+            g.step_batched(toks, want_logits=False)
+            t = time.perf_counter() - t0
+            best = t if best is None else min(best, t)
+        return best
+
+    best = timed()
     log(f"multi-position step of {m} at {ctx}: {best * 1e3:.2f} ms, {m / best:.0f} tok/s "
         f"({m / best / decode_tok_s:.2f}x the decode loop)")
-    return {"positions": m, "context": ctx, "ms_per_block": round(best * 1e3, 3), "tok_s": round(m / best, 1),
-            "vs_decode": round(m / best / decode_tok_s, 2)}
+    out = {"positions": m, "context": ctx, "ms_per_block": round(best * 1e3, 3), "tok_s": round(m / best, 1),
+           "vs_decode": round(m / best / decode_tok_s, 2)}
+    # the same block with the experts through the grouped int8 MFMA kernels (moert_batched_mode 1)
+    g.batched_mode(1)
+    gbest = timed()
+    g.batched_mode(0)
+    log(f"multi-position step of {m} at {ctx}, grouped experts: {gbest * 1e3:.2f} ms, {m / gbest:.0f} tok/s")
+    out["grouped"] = {"ms_per_block": round(gbest * 1e3, 3), "tok_s": round(m / gbest, 1),
+                      "vs_decode": round(m / gbest / decode_tok_s, 2)}
+    return out
 
 
 def batched_step(cfg, seed, iters, m=16, nblocks=4):

@@ -170,6 +170,15 @@ int moert_cache_counters_get(moert_model* m, moert_cache_counters* out);
 int moert_decode_step(moert_model* m, int token, float* logits, int* route_ids, float* route_weights,
                       int* argmax);
 
+/* Mode of the multi-position step (moert_step_batched, moert_prefill): 0 (default) the per-row FMA kernels, bit for
+ * bit equal to decode steps; 1 the routed experts through the grouped int8 MFMA kernels of the block API
+ * (moert_block_forward_batched): the step's own routing, the normalised inputs as 15-bit hi/lo codes, every expert's
+ * rows read once for its member positions, exact int32 block products, the sum in first-appearance order, then the
+ * residual. Mode 1 needs Q8_0 experts, hidden 1024 or 1536 and inter 128/256/512 on a resident model, and keeps a
+ * tiled copy of every layer's experts (built on the first switch). The block prefill through the grouped GEMM
+ * (rust/moe-rt/src/cuda_dense.rs:236-288, motor/leitura.rs:79-85). */
+int moert_batched_mode(moert_model* m, int mode);
+
 /* Greedy generation with no host synchronisation between tokens: feeds the n_prompt tokens one position at a
  * time, then n_new tokens chosen by argmax (last index on ties). out_tokens receives the n_new generated ids;
  * gaps (optional, n_new floats) receives top1 - top2 of the logits each generated token was chosen from.

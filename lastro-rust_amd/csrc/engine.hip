@@ -444,12 +444,53 @@ struct moert_model {
     return MOERT_OK;
   }
 
+  // grouped mode of the multi-position step (moert_batched_mode): the grouped kernels' buffers and every layer's
+  // experts in their tiled layout, built on first use
+  int batched_mode = 0;
+  GroupBufs mg{};
+  std::vector<std::pair<TMat, TMat>> tiled;
+  int ensure_grouped() {
+    if (mg.xh) return MOERT_OK;
+    const int H = dims.hidden, I = dims.inter, M = kGrpMaxPos, S = kGrpMaxPos * 8;
+    int rc;
+    if ((rc = zeros(arena, stream, (size_t)M * H, &mg.xh)) || (rc = zeros(arena, stream, (size_t)M * H, &mg.xl)) ||
+        (rc = zeros(arena, stream, (size_t)M * (H / 32), &mg.xd)) ||
+        (rc = zeros(arena, stream, (size_t)GRP_WORDS, &mg.grp)) || (rc = zeros(arena, stream, (size_t)S * I, &mg.ah)) ||
+        (rc = zeros(arena, stream, (size_t)S * I, &mg.al)) || (rc = zeros(arena, stream, (size_t)S * (I / 32), &mg.ad)) ||
+        (rc = zeros(arena, stream, (size_t)S * H, &mg.o)))
+      return rc;
+    auto tile = [&](const DMat& src, TMat* dst) -> int {
+      uint8_t* q;
+      uint16_t* d;
+      const size_t n = (size_t)src.rows * src.cols;
+      int r;
+      if ((r = arena.alloc((void**)&q, n)) || (r = arena.alloc((void**)&d, n / 32 * 2))) return r;
+      CHECK_HIP(launch_tile_q8(stream, src, q, d));
+      *dst = TMat{q, d, src.rows, src.cols};
+      return MOERT_OK;
+    };
+    for (const LayerDev& L : layers) {
+      TMat gu{}, dn{};
+      if ((rc = tile(L.gate_up, &gu)) || (rc = tile(L.down, &dn))) return rc;
+      tiled.push_back({gu, dn});
+    }
+    CHECK_HIP(hipStreamSynchronize(stream));
+    return MOERT_OK;
+  }
+
   // Positions pos0 .. pos0 + nv - 1 through every layer, then the final norm, head and argmax of the last one (the
   // device state already holds pos = pos0 + nv - 1, fixed = pos0 + nv and *pf.pos0 = pos0); its hidden state is
   // left in b.h, as after a decode step.
   int enqueue_batched(int pos0, int nv) {
     CHECK_HIP(launch_embed_b(stream, embed, dims, pf, nv));
-    for (const LayerDev& L : layers) CHECK_HIP(launch_layer_b(stream, L, dims, pf, pf.pos0, pos0, nv, b.rope));
+    for (size_t l = 0; l < layers.size(); l++) {
+      GroupBufs g = mg;
+      if (batched_mode == 1) {
+        g.gu = tiled[l].first;
+        g.dn = tiled[l].second;
+      }
+      CHECK_HIP(launch_layer_b(stream, layers[l], dims, pf, pf.pos0, pos0, nv, b.rope, batched_mode == 1 ? &g : nullptr));
+    }
     StepBufs bl = b;
     bl.h = pf.h + (size_t)(nv - 1) * dims.hidden;
     CHECK_HIP(launch_head(stream, embed, norm, dims, bl));
@@ -1172,6 +1213,23 @@ int moert_step_batched(moert_model* m, const int* tokens, int n, float* logits, 
   MTRY(m, model_sync(m));
   if (argmax) *argmax = am;
   m->host_pos = pos0 + n;
+  return MOERT_OK;
+}
+
+int moert_batched_mode(moert_model* m, int mode) {
+  MODEL_OK(m);
+  CHECK_CFG(mode == 0 || mode == 1, "batched mode %d: 0 (per-row FMA) or 1 (grouped int8 MFMA experts)", mode);
+  if (mode == 1) {
+    CHECK_CFG(!m->cached, "batched mode: the multi-position step runs on a resident model");
+    const moert_config& c = m->cfg;
+    CHECK_CFG((c.hidden == 1024 || c.hidden == 1536) && (c.inter == 128 || c.inter == 256 || c.inter == 512) &&
+                  c.experts <= 64 && c.top_k <= 8,
+              "grouped mode: hidden %d (1024 or 1536), inter %d (128, 256 or 512)", c.hidden, c.inter);
+    for (const LayerDev& L : m->layers)
+      CHECK_CFG(L.gate_up.dtype == DT_Q8_0 && L.down.dtype == DT_Q8_0, "grouped mode: Q8_0 experts only");
+    MTRY(m, m->ensure_grouped());
+  }
+  m->batched_mode = mode;
   return MOERT_OK;
 }
 

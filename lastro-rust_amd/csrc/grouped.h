@@ -48,5 +48,10 @@ hipError_t launch_tile_q8(hipStream_t s, const DMat& src, uint8_t* q, uint16_t* 
 // (route, up, down, combine) record their dispatch start/end into ev[2i], ev[2i+1].
 hipError_t launch_grouped_block(hipStream_t s, const LayerDev& L, int m, int k, int inter, const float* x,
                                 GroupBufs g, float* y, const hipEvent_t* ev = nullptr);
+// The experts of a multi-position model step through the grouped kernels: g.ids / g.w already hold the step's
+// routing (top-k order), xn[m, H] the normalised inputs; their codes, then gate/up, down and y[m, H] = the
+// weighted sum of each position's experts in list order (no residual).
+hipError_t launch_grouped_experts(hipStream_t s, const LayerDev& L, int m, int k, int inter, const float* xn,
+                                  GroupBufs g, float* y);
 
 }  // namespace moert

@@ -28,6 +28,50 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int kRouteThreads = 1024;
 
+// The hi/lo codes of the 32-element block b of position p's input (8 lanes per block, 4 elements per lane, v[] the
+// lane's elements): d = amax / 32639, q = rint(x / d) = 256 hi + lo with hi, lo int8.
+template <int H>
+__device__ __forceinline__ void block_codes(const float (&v)[4], bool valid, int p, int b, int part, GroupBufs g) {
+  constexpr int NB = H / 32;
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float a = fabsf(v[i]);
+    amax = a > amax ? a : amax;
+  }
+  amax = group_max<8>(amax);
+  const float d = amax / 32639.0f;
+  uint32_t hw = 0, lw = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int q = d > 0.0f ? (int)__builtin_rintf(v[i] / d) : 0;
+    const int h = (q + 128) >> 8;
+    hw |= (uint32_t)(uint8_t)(int8_t)h << (8 * i);
+    lw |= (uint32_t)(uint8_t)(int8_t)(q - 256 * h) << (8 * i);
+  }
+  if (valid) {
+    reinterpret_cast<uint32_t*>(g.xh + (size_t)p * H)[8 * b + part] = hw;
+    reinterpret_cast<uint32_t*>(g.xl + (size_t)p * H)[8 * b + part] = lw;
+    if (part == 0) g.xd[(size_t)p * NB + b] = d;
+  }
+}
+
+// The codes of the m already-normalised inputs x[m, H] (the experts of a multi-position model step, routed by its
+// own router): workgroup p.
+template <int H>
+__global__ __launch_bounds__(256) void k_grp_codes(const float* __restrict__ x, GroupBufs g) {
+  constexpr int NB = H / 32;
+  const int p = blockIdx.x;
+  for (int base = 0; base < NB; base += 256 / 8) {
+    const int b = base + (threadIdx.x >> 3), part = threadIdx.x & 7;
+    const bool valid = b < NB;
+    float v[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) v[i] = valid ? x[(size_t)p * H + 32 * b + 4 * part + i] : 0.0f;
+    block_codes<H>(v, valid, p, b, part, g);
+  }
+}
+
 // ------------------------------------------------------------------------------------------------------------
 // Per-position router (canonical dot, optional bias), top-k, and the hi/lo codes of x_p: workgroup p.
 template <int DT, int H>
@@ -69,28 +113,9 @@ __global__ __launch_bounds__(kRouteThreads) void k_grp_route(DMat router, const 
     const int b = base + (threadIdx.x >> 3), part = threadIdx.x & 7;
     const bool valid = b < NB;
     float v[4];
-    float amax = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      v[i] = valid ? xs[32 * b + 4 * part + i] : 0.0f;
-      const float a = fabsf(v[i]);
-      amax = a > amax ? a : amax;
-    }
-    amax = group_max<8>(amax);
-    const float d = amax / 32639.0f;
-    uint32_t hw = 0, lw = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int q = d > 0.0f ? (int)__builtin_rintf(v[i] / d) : 0;
-      const int h = (q + 128) >> 8;
-      hw |= (uint32_t)(uint8_t)(int8_t)h << (8 * i);
-      lw |= (uint32_t)(uint8_t)(int8_t)(q - 256 * h) << (8 * i);
-    }
-    if (valid) {
-      reinterpret_cast<uint32_t*>(g.xh + (size_t)p * H)[8 * b + part] = hw;
-      reinterpret_cast<uint32_t*>(g.xl + (size_t)p * H)[8 * b + part] = lw;
-      if (part == 0) g.xd[(size_t)p * NB + b] = d;
-    }
+    for (int i = 0; i < 4; i++) v[i] = valid ? xs[32 * b + 4 * part + i] : 0.0f;
+    block_codes<H>(v, valid, p, b, part, g);
   }
   __syncthreads();
   if (wave == 0) wave_topk(lg, E, k, lane, tk, g.ids + (size_t)p * k, g.w + (size_t)p * k);
@@ -493,6 +518,9 @@ __global__ __launch_bounds__(256) void k_grp_combine(int k, int hidden, GroupBuf
 }
 
 // ------------------------------------------------------------------------------------------------------------
+static hipError_t launch_grouped_core(hipStream_t s, int H, int E, int m, int k, int inter, GroupBufs g, float* y,
+                                      const hipEvent_t* ev);
+
 hipError_t launch_grouped_block(hipStream_t s, const LayerDev& L, int m, int k, int inter, const float* x,
                                 GroupBufs g, float* y, const hipEvent_t* ev) {
   auto arm = [&](int i) {
@@ -504,8 +532,6 @@ hipError_t launch_grouped_block(hipStream_t s, const LayerDev& L, int m, int k, 
       !g.gu.q || !g.dn.q || g.gu.rows != L.gate_up.rows || g.gu.cols != H || g.dn.rows != L.down.rows ||
       g.dn.cols != inter)
     return hipErrorInvalidValue;
-  const int U = m * k < E ? m * k : E;
-  const bool wide = m > 16;
   arm(0);
   switch (H) {
     case 1024: klaunch(k_grp_route<DT_Q8_0, 1024>, m, kRouteThreads, 0, s, L.router, L.router_bias, x, k, g); break;
@@ -514,6 +540,35 @@ hipError_t launch_grouped_block(hipStream_t s, const LayerDev& L, int m, int k, 
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  return launch_grouped_core(s, H, E, m, k, inter, g, y, ev);
+}
+
+hipError_t launch_grouped_experts(hipStream_t s, const LayerDev& L, int m, int k, int inter, const float* xn,
+                                  GroupBufs g, float* y) {
+  const int H = L.gate_up.cols, E = L.router.rows;
+  if (m < 1 || m > kGrpMaxPos || k < 1 || k > 8 || E > 64 || L.gate_up.dtype != DT_Q8_0 ||
+      L.down.dtype != DT_Q8_0 || L.down.cols != inter || inter % 64 || H % 256 || !g.gu.q || !g.dn.q ||
+      g.gu.rows != L.gate_up.rows || g.gu.cols != H || g.dn.rows != L.down.rows || g.dn.cols != inter)
+    return hipErrorInvalidValue;
+  switch (H) {
+    case 1024: klaunch(k_grp_codes<1024>, m, 256, 0, s, xn, g); break;
+    case 1536: klaunch(k_grp_codes<1536>, m, 256, 0, s, xn, g); break;
+    default: return hipErrorInvalidValue;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  return launch_grouped_core(s, H, E, m, k, inter, g, y, nullptr);
+}
+
+// gate/up, down and combine of a grouped step whose ids, weights and input codes are in g
+static hipError_t launch_grouped_core(hipStream_t s, int H, int E, int m, int k, int inter, GroupBufs g, float* y,
+                                      const hipEvent_t* ev) {
+  auto arm = [&](int i) {
+    if (ev) arm_launch_events(ev[2 * i], ev[2 * i + 1]);
+  };
+  hipError_t e;
+  const int U = m * k < E ? m * k : E;
+  const bool wide = m > 16;
   // u is the slow grid index, so the workgroups of list indices past the step's expert count (which end at once)
   // are dispatched last
   constexpr int NT = kGrpUpThreads, RT = 16 * NT / 128;

@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "grouped.h"
 #include "kernels.h"
 
 namespace moert {
@@ -27,7 +28,9 @@ struct PfBufs {
 
 hipError_t launch_embed_b(hipStream_t s, const DMat& emb, const Dims& d, const PfBufs& p, int nv);
 // One layer for positions pos0 .. pos0 + nv - 1 (*lenp == pos0 on the device), rope: the [max_len, 64] table.
+// With grp (the layer's tiled experts and the grouped step's buffers), the experts go through the grouped int8 MFMA
+// kernels (launch_grouped_experts) instead of the per-row FMA kernels.
 hipError_t launch_layer_b(hipStream_t s, const LayerDev& L, const Dims& d, const PfBufs& p, const int* lenp, int pos0,
-                          int nv, const float* rope);
+                          int nv, const float* rope, const GroupBufs* grp = nullptr);
 
 }  // namespace moert

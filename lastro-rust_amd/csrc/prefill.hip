@@ -19,7 +19,9 @@
 //   k_moe_comb_b   h[v] += res * sum over j in top-k order of w[v][j] * o[v][j]
 #include <algorithm>
 
+#include "cache.h"
 #include "dev_rows.h"
+#include "grouped.h"
 #include "launch.h"
 #include "moe_norm.h"
 #include "prefill.h"
@@ -548,7 +550,7 @@ hipError_t launch_embed_b(hipStream_t s, const DMat& emb, const Dims& d, const P
 }
 
 hipError_t launch_layer_b(hipStream_t s, const LayerDev& L, const Dims& d, const PfBufs& p, const int* lenp, int pos0,
-                          int nv, const float* rope) {
+                          int nv, const float* rope, const GroupBufs* grp) {
   if (nv < 1 || nv > kPfMaxPos || d.top_k > 8 || d.experts > 64 || d.head_dim != 64) return hipErrorInvalidValue;
 #define BODY(KK)                                                                                         \
   case KK: {                                                                                             \
@@ -580,6 +582,15 @@ hipError_t launch_layer_b(hipStream_t s, const LayerDev& L, const Dims& d, const
   MOERT_DISPATCH(L.router.dtype, L.router.cols, BODY)
 #undef BODY
   if ((e = hipGetLastError()) != hipSuccess) return e;
+  if (grp) {
+    // grouped mode: the routed experts through the int8 MFMA kernels (codes of xn, gate/up, down, sum in list
+    // order into o[0 .. nv*H)), then the residual
+    GroupBufs g = *grp;
+    g.ids = p.ids;
+    g.w = p.w;
+    if ((e = launch_grouped_experts(s, L, nv, d.top_k, d.inter, p.xn, g, p.o)) != hipSuccess) return e;
+    return launch_add_scaled(s, p.h, p.o, d.res_mult, nv * d.hidden);
+  }
   const int U = std::min(nv * d.top_k, d.experts);
 #define BODY(KK)                                                                                         \
   case KK: {                                                                                             \

@@ -121,6 +121,7 @@ def lib() -> ctypes.CDLL:
             "moert_cache_prefetch_mode": (i, [vp, i]),
             "moert_cache_predictions": (i, [vp, i, i, vp]),
             "moert_cache_token_counts": (i, [vp, i, i, vp]),
+            "moert_batched_mode": (i, [vp, i]),
             "moert_model_create_hybrid": (i, [ctypes.POINTER(moert_config), ctypes.POINTER(moert_model_weights), i,
                                               i, i, i, i, ctypes.POINTER(vp)]),
             "moert_cache_counters_get": (i, [vp, ctypes.POINTER(moert_cache_counters)]),
@@ -209,7 +210,7 @@ def lib() -> ctypes.CDLL:
 EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moert_model_destroy",
             "moert_model_create_cached", "moert_cache_stats", "moert_cache_clear", "moert_cache_fill",
             "moert_cache_prefetch", "moert_cache_prefetch_mode", "moert_cache_predictions", "moert_cache_token_counts",
-            "moert_cache_counters_get", "moert_model_create_hybrid",
+            "moert_cache_counters_get", "moert_model_create_hybrid", "moert_batched_mode",
             "moert_decode_step", "moert_generate", "moert_step_batched", "moert_prefill", "moert_reset_sequence",
             "moert_kv_prefill_fp16",
             "moert_set_position", "moert_get_position", "moert_read_kv_fp16", "moert_read_hidden", "moert_read_logits",
@@ -486,6 +487,11 @@ class GpuModel:
         am = ctypes.c_int(0)
         check(lib().moert_decode_step(self.h, int(token), ptr(lg), ptr(ids), ptr(w), ctypes.byref(am)))
         return lg, ids, w, am.value
+
+    def batched_mode(self, mode: int):
+        """0: multi-position steps with the per-row FMA kernels (bit-identical to decode steps); 1: experts through the
+        grouped int8 MFMA kernels."""
+        check(lib().moert_batched_mode(self.h, int(mode)))
 
     def step_batched(self, tokens, want_logits: bool = True):
         """Up to 32 tokens in one multi-position step: (logits of the last position, its argmax)

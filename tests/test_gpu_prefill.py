@@ -135,3 +135,66 @@ def test_batched_step_refuses_bad_blocks(gpu):
         c.step_batched([1, 2])
     assert e.value.code == moert.E_CONFIG
     c.close()
+
+
+@pytest.mark.parametrize("shape,seed", [("1b", 41), ("3b", 43)])
+def test_grouped_mode_prefill_within_1e2_of_the_fma_path(gpu, shape, seed):
+    """moert_batched_mode(1): the block prefill's experts through the grouped int8 MFMA kernels (15-bit activation
+    codes, exact int32 block products, experts summed in first-appearance order). A 70-token prompt (blocks 32, 32,
+    6), then 8 forced decode steps: the last prompt position's logits and every decode step's logits within 1e-2 of
+    the default per-row FMA path (which equals decode steps and the oracle bit for bit), and the argmax equal wherever
+    that path's top1 - top2 gap exceeds 2e-2. Switching back to mode 0 gives the FMA path's logits bit for bit."""
+    cfg = moert.Config(**(moert.GRANITE_1B if shape == "1b" else moert.GRANITE_3B))
+    m = moert.SynthModel(cfg, seed=seed, zipf_s=1.1)
+    rng = np.random.default_rng(seed + 1)
+    toks = rng.integers(0, cfg.vocab, 70)
+    forced = rng.integers(0, cfg.vocab, 8)
+    fma = moert.GpuModel(m, 128, attn_splits=32)
+    grp = moert.GpuModel(m, 128, attn_splits=32)
+    say(f"{shape} grouped mode on")
+    grp.batched_mode(1)
+
+    def close(a, b, label):
+        d = float(np.abs(a - b).max())
+        s = np.sort(a)
+        if s[-1] - s[-2] > 2e-2:
+            assert int(np.argmax(a)) == int(np.argmax(b)), label
+        assert d <= 1e-2, (label, d)
+        return d
+
+    say(f"{shape} prefill 70 tokens, fma and grouped")
+    lf, af = fma.prefill(toks)
+    lg, ag = grp.prefill(toks)
+    diffs = [close(lf, lg, "prefill")]
+    for i, tok in enumerate(forced):
+        a = fma.step(int(tok))[0]
+        b = grp.step(int(tok))[0]
+        diffs.append(close(a, b, f"decode {i}"))
+    say(f"{shape} grouped mode: max logit difference {max(diffs):.2e}")
+    assert max(diffs) > 0.0  # the modes really differ (codes, sum order)
+    grp.batched_mode(0)
+    grp.reset()
+    fma.reset()
+    a = fma.prefill(toks)[0]
+    b = grp.prefill(toks)[0]
+    assert bits_equal(a, b)
+    fma.close()
+    grp.close()
+
+
+def test_grouped_mode_refusals(gpu):
+    """Mode 1 needs a resident model with Q8_0 experts at a row length the grouped kernels are built for."""
+    tiny = moert.SynthModel(moert.Config(**moert.TINY), seed=3)
+    g = moert.GpuModel(tiny, 64, attn_splits=2)
+    with pytest.raises(moert.MoertError, match="hidden"):
+        g.batched_mode(1)
+    with pytest.raises(moert.MoertError):
+        g.batched_mode(2)
+    g.batched_mode(0)
+    g.close()
+    cfg = moert.Config(**moert.GRANITE_1B)
+    m4 = moert.SynthModel(cfg, seed=5, wdtype=moert.Q4_0)
+    g4 = moert.GpuModel(m4, 64, attn_splits=2)
+    with pytest.raises(moert.MoertError, match="Q8_0"):
+        g4.batched_mode(1)
+    g4.close()
