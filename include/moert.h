@@ -466,6 +466,41 @@ int moert_freq_score(const moert_freq* f, int key, double* score);
 int moert_freq_clear(moert_freq* f);
 
 /* ---------------------------------------------------------------------------------------------------------
+ * Tokenizer (host only). Replaces rust/moe-rt/src/tokenizador.rs: the byte-level BPE of the Granite 3.1 tokenizer.json
+ * (no normalizer; ByteLevel pre-tokenizer with the GPT-2 pattern and no prefix space; BPE by merge rank without
+ * dropout, byte fallback or unknown token; ByteLevel decoder; added tokens found in the raw text by the longest match
+ * at the leftmost position). Other configurations are refused at load (MOERT_E_CONFIG), as are sparse ids. Bytes
+ * whose ByteLevel character is not in the vocabulary are dropped, as the library does without an unknown token.
+ * ------------------------------------------------------------------------------------------------------- */
+typedef struct moert_tokenizer moert_tokenizer;
+
+/* Tokenizador::carrega / de_bytes (tokenizador.rs:214-330). */
+int moert_tokenizer_load(const char* path, moert_tokenizer** out);
+int moert_tokenizer_from_json(const char* json, size_t len, moert_tokenizer** out);
+int moert_tokenizer_destroy(moert_tokenizer* t);
+/* Size of the id table (largest id + 1). */
+int moert_tokenizer_vocab_size(const moert_tokenizer* t, int* n);
+/* Text (valid UTF-8) to ids, as the library's encode without special-token post-processing (Tokenizador::codifica,
+ * tokenizador.rs:420-448). *n_ids = the count; ids may be NULL to ask for it, else max_ids must hold them (at most len
+ * ids). */
+int moert_tokenizer_encode(moert_tokenizer* t, const char* text, size_t len, uint32_t* ids, size_t max_ids,
+                           size_t* n_ids);
+/* Ids to bytes (Tokenizador::decodifica_bytes; added tokens as their literal text); with lossy_text, to UTF-8 with each
+ * maximal invalid subpart replaced by U+FFFD (Tokenizador::decodifica). MOERT_E_RANGE for an id outside the
+ * vocabulary. *n_bytes = the length; out may be NULL to ask for it. */
+int moert_tokenizer_decode(const moert_tokenizer* t, const uint32_t* ids, size_t n, int lossy_text, char* out,
+                           size_t max, size_t* n_bytes);
+/* The GPT-2 pattern's pieces of a text (pre_tokeniza, tokenizador.rs:118-179): byte offsets of their ends. */
+int moert_tokenizer_pretokenize(const char* text, size_t len, size_t* ends, size_t max, size_t* n);
+/* The fixed rendering of the Granite 3.1 chat template (renderiza_chat, tokenizador.rs:494-528): roles 0 system,
+ * 1 user, 2 assistant; a first system message replaces the default one, which carries `date`; with
+ * add_generation_prompt the assistant's opening follows the last message. *needed = the length. */
+int moert_chat_render(const int* roles, const char* const* contents, int n, int add_generation_prompt,
+                      const char* date, char* out, size_t max, size_t* needed);
+/* strftime('%B %d, %Y') in English, validated (formata_data, tokenizador.rs:531-548): NUL-terminated into out. */
+int moert_format_date(int year, int month, int day, char* out, size_t max);
+
+/* ---------------------------------------------------------------------------------------------------------
  * Host utilities (no device needed).
  * ------------------------------------------------------------------------------------------------------- */
 

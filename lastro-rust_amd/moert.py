@@ -198,6 +198,16 @@ def lib() -> ctypes.CDLL:
             "moert_freq_touch": (i, [vp, i, u64]),
             "moert_freq_score": (i, [vp, i, ctypes.POINTER(ctypes.c_double)]),
             "moert_freq_clear": (i, [vp]),
+            "moert_tokenizer_load": (i, [ctypes.c_char_p, ctypes.POINTER(vp)]),
+            "moert_tokenizer_from_json": (i, [ctypes.c_char_p, sz, ctypes.POINTER(vp)]),
+            "moert_tokenizer_destroy": (i, [vp]),
+            "moert_tokenizer_vocab_size": (i, [vp, ip]),
+            "moert_tokenizer_encode": (i, [vp, ctypes.c_char_p, sz, vp, sz, ctypes.POINTER(sz)]),
+            "moert_tokenizer_decode": (i, [vp, vp, sz, i, ctypes.c_char_p, sz, ctypes.POINTER(sz)]),
+            "moert_tokenizer_pretokenize": (i, [ctypes.c_char_p, sz, vp, sz, ctypes.POINTER(sz)]),
+            "moert_chat_render": (i, [ip, ctypes.POINTER(ctypes.c_char_p), i, i, ctypes.c_char_p, ctypes.c_char_p, sz,
+                                      ctypes.POINTER(sz)]),
+            "moert_format_date": (i, [i, i, i, ctypes.c_char_p, sz]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -228,7 +238,10 @@ EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moer
             "moert_metrics_add_request", "moert_metrics_setting", "moert_metrics_event", "moert_metrics_json",
             "moert_metrics_publish", "moert_model_attach_metrics", "moert_placement_create", "moert_placement_destroy",
             "moert_placement_step", "moert_placement_counters", "moert_placement_table", "moert_freq_create",
-            "moert_freq_destroy", "moert_freq_touch", "moert_freq_score", "moert_freq_clear"]
+            "moert_freq_destroy", "moert_freq_touch", "moert_freq_score", "moert_freq_clear", "moert_tokenizer_load",
+            "moert_tokenizer_from_json", "moert_tokenizer_destroy", "moert_tokenizer_vocab_size",
+            "moert_tokenizer_encode", "moert_tokenizer_decode", "moert_tokenizer_pretokenize", "moert_chat_render",
+            "moert_format_date"]
 
 
 def check(rc: int) -> None:
@@ -1016,3 +1029,93 @@ class Freq:
         if getattr(self, "h", None):
             lib().moert_freq_destroy(self.h)
             self.h = None
+
+
+# ---- tokenizer (tokenizador.rs) ----
+ROLE_SYSTEM, ROLE_USER, ROLE_ASSISTANT = 0, 1, 2
+
+
+class Tokenizer:
+    """moert_tokenizer_*: the byte-level BPE of a Granite tokenizer.json (Tokenizador)."""
+
+    def __init__(self, path=None, json_text=None):
+        h = ctypes.c_void_p()
+        if json_text is not None:
+            raw = json_text.encode() if isinstance(json_text, str) else bytes(json_text)
+            check(lib().moert_tokenizer_from_json(raw, len(raw), ctypes.byref(h)))
+        else:
+            check(lib().moert_tokenizer_load(os.fsencode(path), ctypes.byref(h)))
+        self.h = h.value
+
+    def vocab_size(self) -> int:
+        n = ctypes.c_int()
+        check(lib().moert_tokenizer_vocab_size(self.h, ctypes.byref(n)))
+        return n.value
+
+    def encode(self, text: str) -> List[int]:
+        raw = text.encode()
+        out = np.empty(max(1, len(raw)), np.uint32)
+        n = ctypes.c_size_t()
+        check(lib().moert_tokenizer_encode(self.h, raw, len(raw), ptr(out), out.size, ctypes.byref(n)))
+        return [int(v) for v in out[:n.value]]
+
+    def decode_bytes(self, ids) -> bytes:
+        a = np.ascontiguousarray(ids, np.uint32)
+        n = ctypes.c_size_t()
+        check(lib().moert_tokenizer_decode(self.h, ptr(a), a.size, 0, None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(n.value + 1)
+        check(lib().moert_tokenizer_decode(self.h, ptr(a), a.size, 0, buf, len(buf), ctypes.byref(n)))
+        return buf.raw[:n.value]
+
+    def decode(self, ids) -> str:
+        a = np.ascontiguousarray(ids, np.uint32)
+        n = ctypes.c_size_t()
+        check(lib().moert_tokenizer_decode(self.h, ptr(a), a.size, 1, None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(n.value + 1)
+        check(lib().moert_tokenizer_decode(self.h, ptr(a), a.size, 1, buf, len(buf), ctypes.byref(n)))
+        return buf.raw[:n.value].decode()
+
+    def close(self):
+        if self.h:
+            lib().moert_tokenizer_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def pretokenize(text: str) -> List[str]:
+    """The GPT-2 pattern's pieces of `text` (pre_tokeniza)."""
+    raw = text.encode()
+    n = ctypes.c_size_t()
+    check(lib().moert_tokenizer_pretokenize(raw, len(raw), None, 0, ctypes.byref(n)))
+    ends = np.empty(max(1, n.value), np.uint64)
+    check(lib().moert_tokenizer_pretokenize(raw, len(raw), ptr(ends), ends.size, ctypes.byref(n)))
+    out, s = [], 0
+    for e in ends[:n.value]:
+        out.append(raw[s:int(e)].decode())
+        s = int(e)
+    return out
+
+
+def chat_render(messages, add_generation_prompt=True, date="") -> str:
+    """messages: [(role, content)] with roles ROLE_*; the fixed Granite 3.1 chat template (renderiza_chat)."""
+    n = len(messages)
+    roles = (ctypes.c_int * max(1, n))(*[r for r, _ in messages])
+    contents = (ctypes.c_char_p * max(1, n))(*[c.encode() for _, c in messages])
+    need = ctypes.c_size_t()
+    check(lib().moert_chat_render(roles, contents, n, int(add_generation_prompt), date.encode(), None, 0,
+                                  ctypes.byref(need)))
+    buf = ctypes.create_string_buffer(need.value + 1)
+    check(lib().moert_chat_render(roles, contents, n, int(add_generation_prompt), date.encode(), buf, len(buf),
+                                  ctypes.byref(need)))
+    return buf.raw[:need.value].decode()
+
+
+def format_date(year, month, day) -> str:
+    buf = ctypes.create_string_buffer(64)
+    check(lib().moert_format_date(year, month, day, buf, len(buf)))
+    return buf.value.decode()
