@@ -448,13 +448,17 @@ struct moert_model {
   // experts in their tiled layout, built on first use
   int batched_mode = 0;
   GroupBufs mg{};
-  std::vector<std::pair<TMat, TMat>> tiled;
+  struct TiledLayer {
+    TMat gu, dn, qkv, o;
+  };
+  std::vector<TiledLayer> tiled;
   int ensure_grouped() {
     if (mg.xh) return MOERT_OK;
     const int H = dims.hidden, I = dims.inter, M = kGrpMaxPos, S = kGrpMaxPos * 8;
+    const int X = std::max(H, dims.heads * dims.head_dim);  // code rows: block inputs and attention outputs
     int rc;
-    if ((rc = zeros(arena, stream, (size_t)M * H, &mg.xh)) || (rc = zeros(arena, stream, (size_t)M * H, &mg.xl)) ||
-        (rc = zeros(arena, stream, (size_t)M * (H / 32), &mg.xd)) ||
+    if ((rc = zeros(arena, stream, (size_t)M * X, &mg.xh)) || (rc = zeros(arena, stream, (size_t)M * X, &mg.xl)) ||
+        (rc = zeros(arena, stream, (size_t)M * (X / 32), &mg.xd)) ||
         (rc = zeros(arena, stream, (size_t)GRP_WORDS, &mg.grp)) || (rc = zeros(arena, stream, (size_t)S * I, &mg.ah)) ||
         (rc = zeros(arena, stream, (size_t)S * I, &mg.al)) || (rc = zeros(arena, stream, (size_t)S * (I / 32), &mg.ad)) ||
         (rc = zeros(arena, stream, (size_t)S * H, &mg.o)))
@@ -470,9 +474,11 @@ struct moert_model {
       return MOERT_OK;
     };
     for (const LayerDev& L : layers) {
-      TMat gu{}, dn{};
-      if ((rc = tile(L.gate_up, &gu)) || (rc = tile(L.down, &dn))) return rc;
-      tiled.push_back({gu, dn});
+      TiledLayer t{};
+      if ((rc = tile(L.gate_up, &t.gu)) || (rc = tile(L.down, &t.dn)) || (rc = tile(L.qkv, &t.qkv)) ||
+          (rc = tile(L.o, &t.o)))
+        return rc;
+      tiled.push_back(t);
     }
     CHECK_HIP(hipStreamSynchronize(stream));
     return MOERT_OK;
@@ -483,13 +489,19 @@ struct moert_model {
   // left in b.h, as after a decode step.
   int enqueue_batched(int pos0, int nv) {
     CHECK_HIP(launch_embed_b(stream, embed, dims, pf, nv));
+    if (batched_mode == 1) CHECK_HIP(launch_norm_codes(stream, dims.hidden, nv, pf.h, layers[0].ln_attn, dims.eps, mg));
     for (size_t l = 0; l < layers.size(); l++) {
-      GroupBufs g = mg;
       if (batched_mode == 1) {
-        g.gu = tiled[l].first;
-        g.dn = tiled[l].second;
+        GroupBufs g = mg;
+        g.gu = tiled[l].gu;
+        g.dn = tiled[l].dn;
+        g.qkv = tiled[l].qkv;
+        g.oproj = tiled[l].o;
+        const float* next = l + 1 < layers.size() ? layers[l + 1].ln_attn : nullptr;
+        CHECK_HIP(launch_layer_grouped(stream, layers[l], dims, pf, pf.pos0, pos0, nv, b.rope, g, next));
+      } else {
+        CHECK_HIP(launch_layer_b(stream, layers[l], dims, pf, pf.pos0, pos0, nv, b.rope));
       }
-      CHECK_HIP(launch_layer_b(stream, layers[l], dims, pf, pf.pos0, pos0, nv, b.rope, batched_mode == 1 ? &g : nullptr));
     }
     StepBufs bl = b;
     bl.h = pf.h + (size_t)(nv - 1) * dims.hidden;
@@ -1222,11 +1234,15 @@ int moert_batched_mode(moert_model* m, int mode) {
   if (mode == 1) {
     CHECK_CFG(!m->cached, "batched mode: the multi-position step runs on a resident model");
     const moert_config& c = m->cfg;
-    CHECK_CFG((c.hidden == 1024 || c.hidden == 1536) && (c.inter == 128 || c.inter == 256 || c.inter == 512) &&
-                  c.experts <= 64 && c.top_k <= 8,
-              "grouped mode: hidden %d (1024 or 1536), inter %d (128, 256 or 512)", c.hidden, c.inter);
+    const int qd = c.heads * c.head_dim;
+    CHECK_CFG((c.hidden == 1024 || c.hidden == 1536) && (qd == 1024 || qd == 1536) && c.head_dim == 64 &&
+                  (c.inter == 128 || c.inter == 256 || c.inter == 512) && c.experts <= 64 && c.top_k <= 8,
+              "grouped mode: hidden %d and heads x head_dim %d (1024 or 1536, head_dim 64), inter %d (128, 256 or 512)",
+              c.hidden, qd, c.inter);
     for (const LayerDev& L : m->layers)
-      CHECK_CFG(L.gate_up.dtype == DT_Q8_0 && L.down.dtype == DT_Q8_0, "grouped mode: Q8_0 experts only");
+      CHECK_CFG(L.gate_up.dtype == DT_Q8_0 && L.down.dtype == DT_Q8_0 && L.qkv.dtype == DT_Q8_0 &&
+                    L.o.dtype == DT_Q8_0 && L.router.dtype == DT_Q8_0,
+                "grouped mode: Q8_0 weights only (q/k/v, output, router and experts)");
     MTRY(m, m->ensure_grouped());
   }
   m->batched_mode = mode;

@@ -38,6 +38,7 @@ struct GroupBufs {
   float* ad;     // [m*k, I/32]
   float* o;      // [m*k, H] down outputs by member slot
   TMat gu, dn;   // gate_up [E*2I, H] and down [E*H, I] of the block in the tiled layout
+  TMat qkv, oproj;  // the layer's q/k/v [(heads + 2 kv_heads) * 64, H] and output [H, heads * 64] projections, tiled
 };
 
 // Tiled copy (TMat layout) of the Q8_0 matrix src into q [rows*cols] and d [rows*cols/32].
@@ -48,10 +49,29 @@ hipError_t launch_tile_q8(hipStream_t s, const DMat& src, uint8_t* q, uint16_t* 
 // (route, up, down, combine) record their dispatch start/end into ev[2i], ev[2i+1].
 hipError_t launch_grouped_block(hipStream_t s, const LayerDev& L, int m, int k, int inter, const float* x,
                                 GroupBufs g, float* y, const hipEvent_t* ev = nullptr);
-// The experts of a multi-position model step through the grouped kernels: g.ids / g.w already hold the step's
-// routing (top-k order), xn[m, H] the normalised inputs; their codes, then gate/up, down and y[m, H] = the
-// weighted sum of each position's experts in list order (no residual).
-hipError_t launch_grouped_experts(hipStream_t s, const LayerDev& L, int m, int k, int inter, const float* xn,
-                                  GroupBufs g, float* y);
+// Pieces of a layer of the multi-position step in grouped mode (every projection an int8 MFMA GEMM), on m <= 32
+// positions; the activation codes live in g.xh / g.xl / g.xd between kernels.
+//   launch_norm_codes     codes of rmsnorm(h[p], lnw) (H 1024 or 1536)
+//   launch_gd_qkv         q/k/v of the coded rows through g.qkv, RoPE at positions pos0 + p, q [m, heads*64] in f32,
+//                         K and V into the fp16 cache rows pos0 + p
+//   launch_grp_codes      codes of x[m, K] (the attention outputs)
+//   launch_gd_oproj       h += res * (g.oproj times the coded rows)
+//   launch_grp_route_norm router of rmsnorm(h[p], lnw) (+ bias), top-k into g.ids / g.w, codes of the normalised row
+//   launch_grp_experts    gate/up and down of the routed experts (tiled g.gu / g.dn) into g.o by member slot; with
+//                         `ev` (8 events), record the dispatches of the two kernels into ev[2], ev[3] and ev[4], ev[5]
+//   launch_gd_combine     h[p] += res * (sum over p's experts in list order of w * o), then with lnw the codes of
+//                         rmsnorm(h[p], lnw)
+hipError_t launch_norm_codes(hipStream_t s, int H, int m, const float* h, const float* lnw, float eps,
+                             const GroupBufs& g);
+hipError_t launch_gd_qkv(hipStream_t s, const Dims& d, int m, int pos0, const float* rope, float* q, uint16_t* kc,
+                         uint16_t* vc, const GroupBufs& g);
+hipError_t launch_grp_codes(hipStream_t s, int K, int m, const float* x, const GroupBufs& g);
+hipError_t launch_gd_oproj(hipStream_t s, int m, float res, float* h, const GroupBufs& g);
+hipError_t launch_grp_route_norm(hipStream_t s, const LayerDev& L, int m, int k, const float* h, const float* lnw,
+                                 float eps, const GroupBufs& g);
+hipError_t launch_grp_experts(hipStream_t s, int H, int E, int m, int k, int inter, const GroupBufs& g,
+                              const hipEvent_t* ev = nullptr);
+hipError_t launch_gd_combine(hipStream_t s, int H, int m, int k, float res, float* h, const float* lnw, float eps,
+                             const GroupBufs& g);
 
 }  // namespace moert

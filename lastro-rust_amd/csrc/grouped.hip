@@ -21,40 +21,11 @@
 #include "dev_rows.h"
 #include "grouped.h"
 #include "launch.h"
+#include "mfma_q8.h"
 
 namespace moert {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-
 constexpr int kRouteThreads = 1024;
-
-// The hi/lo codes of the 32-element block b of position p's input (8 lanes per block, 4 elements per lane, v[] the
-// lane's elements): d = amax / 32639, q = rint(x / d) = 256 hi + lo with hi, lo int8.
-template <int H>
-__device__ __forceinline__ void block_codes(const float (&v)[4], bool valid, int p, int b, int part, GroupBufs g) {
-  constexpr int NB = H / 32;
-  float amax = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const float a = fabsf(v[i]);
-    amax = a > amax ? a : amax;
-  }
-  amax = group_max<8>(amax);
-  const float d = amax / 32639.0f;
-  uint32_t hw = 0, lw = 0;
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int q = d > 0.0f ? (int)__builtin_rintf(v[i] / d) : 0;
-    const int h = (q + 128) >> 8;
-    hw |= (uint32_t)(uint8_t)(int8_t)h << (8 * i);
-    lw |= (uint32_t)(uint8_t)(int8_t)(q - 256 * h) << (8 * i);
-  }
-  if (valid) {
-    reinterpret_cast<uint32_t*>(g.xh + (size_t)p * H)[8 * b + part] = hw;
-    reinterpret_cast<uint32_t*>(g.xl + (size_t)p * H)[8 * b + part] = lw;
-    if (part == 0) g.xd[(size_t)p * NB + b] = d;
-  }
-}
 
 // The codes of the m already-normalised inputs x[m, H] (the experts of a multi-position model step, routed by its
 // own router): workgroup p.
@@ -68,15 +39,17 @@ __global__ __launch_bounds__(256) void k_grp_codes(const float* __restrict__ x, 
     float v[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) v[i] = valid ? x[(size_t)p * H + 32 * b + 4 * part + i] : 0.0f;
-    block_codes<H>(v, valid, p, b, part, g);
+    block_codes<H>(v, valid, p, b, part, g.xh, g.xl, g.xd);
   }
 }
 
 // ------------------------------------------------------------------------------------------------------------
 // Per-position router (canonical dot, optional bias), top-k, and the hi/lo codes of x_p: workgroup p.
-template <int DT, int H>
+template <int DT, int H, bool NORM>
 __global__ __launch_bounds__(kRouteThreads) void k_grp_route(DMat router, const float* __restrict__ bias,
-                                                             const float* __restrict__ x, int k, GroupBufs g) {
+                                                             const float* __restrict__ x,
+                                                             const float* __restrict__ lnw, float eps, int k,
+                                                             GroupBufs g) {
   using G = Geo<DT, H>;
   constexpr int NW = kRouteThreads / 64;
   constexpr int RP = (64 + NW * G::RPW - 1) / (NW * G::RPW);
@@ -101,6 +74,21 @@ __global__ __launch_bounds__(kRouteThreads) void k_grp_route(DMat router, const 
 #pragma unroll
   for (int q = 0; q < RP; q++) bv[q] = bias ? bias[ok[q] ? row[q] : 0] : 0.0f;  // clamped, not guarded: one run of loads
   wg_copy<H, kRouteThreads>(x + (size_t)p * H, xs);
+  if (NORM) {
+    // x is the residual stream: xs = lnw * (x * r), r = 1 / sqrt(mean(x^2) + eps)
+    __shared__ float wsum[NW];
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < H; i += kRouteThreads) ss = __builtin_fmaf(xs[i], xs[i], ss);
+    ss = group_sum<64>(ss);
+    if (lane == 0) wsum[wave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) tot = tot + wsum[w];
+    const float r = 1.0f / sqrtf(tot / (float)H + eps);
+    for (int i = threadIdx.x; i < H; i += kRouteThreads) xs[i] = lnw[i] * (xs[i] * r);
+    __syncthreads();
+  }
   XReg<DT, H> xr;
   load_x<DT, H>(xr, xs, sub);
   float out[RP];
@@ -115,7 +103,7 @@ __global__ __launch_bounds__(kRouteThreads) void k_grp_route(DMat router, const 
     float v[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) v[i] = valid ? xs[32 * b + 4 * part + i] : 0.0f;
-    block_codes<H>(v, valid, p, b, part, g);
+    block_codes<H>(v, valid, p, b, part, g.xh, g.xl, g.xd);
   }
   __syncthreads();
   if (wave == 0) wave_topk(lg, E, k, lane, tk, g.ids + (size_t)p * k, g.w + (size_t)p * k);
@@ -237,142 +225,6 @@ hipError_t launch_tile_q8(hipStream_t s, const DMat& src, uint8_t* q, uint16_t* 
 }
 
 // ------------------------------------------------------------------------------------------------------------
-// MFMA tile of one wave: 16 weight rows x NM member columns over NB 32-element blocks.
-//   a[p]  : this lane's weight codes of blocks 2p and 2p+1 (row lane%16, elements 8*(lane/16) .. +8 of each)
-//   bh/bl : LDS [NM][stride] hi / lo codes of the members
-//   sdt   : LDS [NB][16] fp16 scales of the 16 rows
-//   dx    : LDS [NM][NB] activation scales
-// acc[ct][i] = output (row 4*(lane/16) + i, column 16*ct + lane%16).
-template <int NB, int NM>
-__device__ __forceinline__ void mfma_tile(const uint4 (&a)[NB / 2], const int8_t* bh, const int8_t* bl, int stride,
-                                          const uint16_t* sdt, const float* dx, float (&acc)[NM / 16][4]) {
-  const int lane = threadIdx.x & 63, col = lane & 15, grp = lane >> 4;
-#pragma unroll
-  for (int ct = 0; ct < NM / 16; ct++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) acc[ct][i] = 0.0f;
-#pragma unroll
-  for (int b = 0; b < NB; b++) {
-    const uint4& ap = a[b / 2];
-    const long av = (b & 1) ? (long)(((unsigned long long)ap.w << 32) | ap.z)
-                            : (long)(((unsigned long long)ap.y << 32) | ap.x);
-    const uint2 s4 = *reinterpret_cast<const uint2*>(sdt + b * 16 + 4 * grp);
-    const float dw[4] = {h2f((uint16_t)(s4.x & 0xffff)), h2f((uint16_t)(s4.x >> 16)), h2f((uint16_t)(s4.y & 0xffff)),
-                         h2f((uint16_t)(s4.y >> 16))};
-#pragma unroll
-    for (int ct = 0; ct < NM / 16; ct++) {
-      const int c = 16 * ct + col;
-      const uint2 h2 = *reinterpret_cast<const uint2*>(bh + (size_t)c * stride + 32 * b + 8 * grp);
-      const uint2 l2 = *reinterpret_cast<const uint2*>(bl + (size_t)c * stride + 32 * b + 8 * grp);
-      const long hv = (long)(((unsigned long long)h2.y << 32) | h2.x);
-      const long lv = (long)(((unsigned long long)l2.y << 32) | l2.x);
-      const v4i z = {0, 0, 0, 0};
-      const v4i sh = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, hv, z, 0, 0, 0);
-      const v4i sl = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, lv, z, 0, 0, 0);
-      const float dxc = dx[c * NB + b];
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int S = 256 * sh[i] + sl[i];
-        acc[ct][i] = __builtin_fmaf((float)S, dw[i] * dxc, acc[ct][i]);
-      }
-    }
-  }
-}
-
-// Operands of one wave's 16-row weight tile and of the member activations, fetched in the order scales,
-// activations, weights, so that writing the first two into LDS waits only for them while the weight stream is
-// still in flight.
-template <int NB>
-struct TileScales {
-  static constexpr int N = (4 * NB + 63) / 64;  // 8-byte pieces (4 scales) per lane
-  uint2 v[N];
-};
-
-// The [NB][16] scales of tile t16, 8 bytes a lane.
-template <int NB>
-__device__ __forceinline__ void fetch_scales(const TMat& m, size_t t16, TileScales<NB>& sc) {
-  const int lane = threadIdx.x & 63;
-  const uint2* p = reinterpret_cast<const uint2*>(m.d + t16 * NB * 16);
-#pragma unroll
-  for (int q = 0; q < TileScales<NB>::N; q++)
-    if (4 * NB % 64 == 0 || lane + 64 * q < 4 * NB) sc.v[q] = p[lane + 64 * q];
-}
-template <int NB>
-__device__ __forceinline__ void store_scales(const TileScales<NB>& sc, uint16_t* sdt) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int q = 0; q < TileScales<NB>::N; q++)
-    if (4 * NB % 64 == 0 || lane + 64 * q < 4 * NB) reinterpret_cast<uint2*>(sdt)[lane + 64 * q] = sc.v[q];
-}
-
-// This lane's A operands of tile t16: one 16-byte load per pair of blocks, 1 KB of consecutive bytes per wave.
-template <int NB>
-__device__ __forceinline__ void fetch_tile_q8(const TMat& m, size_t t16, uint4 (&a)[NB / 2]) {
-  const uint4* p = reinterpret_cast<const uint4*>(m.q) + t16 * (NB / 2) * 64 + (threadIdx.x & 63);
-#pragma unroll
-  for (int q = 0; q < NB / 2; q++) a[q] = p[q * 64];
-}
-
-// Member activations: rows row(c) for c in [0, ne) of the hi/lo planes (row length K) and their K/32 block scales;
-// row(c) = off + c (member slots, contiguous) or the c-th set bit of `bits` (member positions).
-template <int K, int NM, int NT>
-struct Members {
-  static constexpr int C16 = K / 16;
-  static constexpr int PER = (NM * C16 + NT - 1) / NT;
-  static constexpr int PERD = (NM * (K / 32) + NT - 1) / NT;
-  uint4 h[PER], l[PER];
-  float d[PERD];
-};
-
-__device__ __forceinline__ int nth_set_bit(unsigned bits, int c) {
-  for (int i = 0; i < c; i++) bits &= bits - 1u;
-  return __ffs(bits) - 1;
-}
-
-template <int K, int NM, int NT, bool CONTIG>
-__device__ __forceinline__ void fetch_members(const int8_t* __restrict__ srch, const int8_t* __restrict__ srcl,
-                                              const float* __restrict__ srcd, unsigned bits, int off, int ne,
-                                              Members<K, NM, NT>& mb) {
-  using M = Members<K, NM, NT>;
-#pragma unroll
-  for (int q = 0; q < M::PER; q++) {
-    const int i = threadIdx.x + q * NT, c = i / M::C16, j = i % M::C16;
-    mb.h[q] = make_uint4(0, 0, 0, 0);
-    mb.l[q] = make_uint4(0, 0, 0, 0);
-    if (i < NM * M::C16 && c < ne) {
-      const size_t r = CONTIG ? (size_t)(off + c) : (size_t)nth_set_bit(bits, c);
-      mb.h[q] = reinterpret_cast<const uint4*>(srch + r * K)[j];
-      mb.l[q] = reinterpret_cast<const uint4*>(srcl + r * K)[j];
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < M::PERD; q++) {
-    const int i = threadIdx.x + q * NT, c = i / (K / 32), b = i % (K / 32);
-    mb.d[q] = 0.0f;
-    if (i < NM * (K / 32) && c < ne) mb.d[q] = srcd[(CONTIG ? (size_t)(off + c) : (size_t)nth_set_bit(bits, c)) * (K / 32) + b];
-  }
-}
-
-template <int K, int NM, int NT>
-__device__ __forceinline__ void store_members(const Members<K, NM, NT>& mb, int8_t* bh, int8_t* bl, int stride,
-                                              float* dx) {
-  using M = Members<K, NM, NT>;
-#pragma unroll
-  for (int q = 0; q < M::PER; q++) {
-    const int i = threadIdx.x + q * NT, c = i / M::C16, j = i % M::C16;
-    if (i < NM * M::C16) {
-      *reinterpret_cast<uint4*>(bh + (size_t)c * stride + 16 * j) = mb.h[q];
-      *reinterpret_cast<uint4*>(bl + (size_t)c * stride + 16 * j) = mb.l[q];
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < M::PERD; q++) {
-    const int i = threadIdx.x + q * NT;
-    if (i < NM * (K / 32)) dx[i] = mb.d[q];
-  }
-}
-
-// ------------------------------------------------------------------------------------------------------------
 // Gate/up of list expert u = blockIdx.y for its members, rows [RT t, RT t + RT) of gate and of up (t = blockIdx.x,
 // RT = 16 * NT / 128): the first half of the waves computes 16 gate rows each, the second half the same up rows, so
 // the members' codes staged in LDS serve every wave. Then act = silu(g)*u and its hi/lo codes (each 32 rows are
@@ -402,16 +254,16 @@ __global__ __launch_bounds__(NT) void k_grp_up(int m, int k, int inter, GroupBuf
   // this wave's 16 rows: gate (first half) or up (second half) rows [RT tile + 16 (wave % WH), +16) of expert e
   const size_t t16 = ((size_t)e * 2 * inter + (size_t)(wave / WH) * inter + RT * tile + 16 * (wave % WH)) / 16;
   TileScales<NB> sc;
-  fetch_scales<NB>(g.gu, t16, sc);
+  fetch_scales<NB>(g.gu, t16, NB, 0, sc);
   Members<H, NM, NT> mb;
   fetch_members<H, NM, NT, false>(g.xh, g.xl, g.xd, bits, 0, ne, mb);
   uint4 a[NB / 2];
-  fetch_tile_q8<NB>(g.gu, t16, a);
+  fetch_tile_q8<NB>(g.gu, t16, NB, 0, a);
   store_scales<NB>(sc, sdt[wave]);
   store_members<H, NM, NT>(mb, bh, bl, STR, dx);
   __syncthreads();
   float acc[NM / 16][4];
-  mfma_tile<NB, NM>(a, bh, bl, STR, sdt[wave], dx, acc);
+  mfma_tile<NB, NM>(a, bh, bl, STR, sdt[wave], dx, NB, acc);
   const int grp = lane >> 4;
 #pragma unroll
   for (int ct = 0; ct < NM / 16; ct++)
@@ -469,16 +321,16 @@ __global__ __launch_bounds__(256, NM == 16 ? 2 : 1) void k_grp_down(int hidden, 
   const int e = g.grp[GRP_LIST + u], ne = g.grp[GRP_CNT + u], off = g.grp[GRP_OFF + u];
   const size_t t16 = ((size_t)e * hidden + 64 * tile + 16 * wave) / 16;  // this wave's 16 output rows
   TileScales<NB> sc;
-  fetch_scales<NB>(g.dn, t16, sc);
+  fetch_scales<NB>(g.dn, t16, NB, 0, sc);
   Members<I, NM, 256> mb;
   fetch_members<I, NM, 256, true>(g.ah, g.al, g.ad, 0u, off, ne, mb);
   uint4 a[NB / 2];
-  fetch_tile_q8<NB>(g.dn, t16, a);
+  fetch_tile_q8<NB>(g.dn, t16, NB, 0, a);
   store_scales<NB>(sc, sdt[wave]);
   store_members<I, NM, 256>(mb, bh, bl, STR, dx);
   __syncthreads();
   float acc[NM / 16][4];
-  mfma_tile<NB, NM>(a, bh, bl, STR, sdt[wave], dx, acc);
+  mfma_tile<NB, NM>(a, bh, bl, STR, sdt[wave], dx, NB, acc);
   const int grp = lane >> 4;
 #pragma unroll
   for (int ct = 0; ct < NM / 16; ct++) {
@@ -518,8 +370,6 @@ __global__ __launch_bounds__(256) void k_grp_combine(int k, int hidden, GroupBuf
 }
 
 // ------------------------------------------------------------------------------------------------------------
-static hipError_t launch_grouped_core(hipStream_t s, int H, int E, int m, int k, int inter, GroupBufs g, float* y,
-                                      const hipEvent_t* ev);
 
 hipError_t launch_grouped_block(hipStream_t s, const LayerDev& L, int m, int k, int inter, const float* x,
                                 GroupBufs g, float* y, const hipEvent_t* ev) {
@@ -534,38 +384,57 @@ hipError_t launch_grouped_block(hipStream_t s, const LayerDev& L, int m, int k, 
     return hipErrorInvalidValue;
   arm(0);
   switch (H) {
-    case 1024: klaunch(k_grp_route<DT_Q8_0, 1024>, m, kRouteThreads, 0, s, L.router, L.router_bias, x, k, g); break;
-    case 1536: klaunch(k_grp_route<DT_Q8_0, 1536>, m, kRouteThreads, 0, s, L.router, L.router_bias, x, k, g); break;
+    case 1024:
+      klaunch(k_grp_route<DT_Q8_0, 1024, false>, m, kRouteThreads, 0, s, L.router, L.router_bias, x, nullptr, 0.0f, k, g);
+      break;
+    case 1536:
+      klaunch(k_grp_route<DT_Q8_0, 1536, false>, m, kRouteThreads, 0, s, L.router, L.router_bias, x, nullptr, 0.0f, k, g);
+      break;
     default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  return launch_grouped_core(s, H, E, m, k, inter, g, y, ev);
+  if ((e = launch_grp_experts(s, H, E, m, k, inter, g, ev)) != hipSuccess) return e;
+  arm(3);
+  klaunch(k_grp_combine, dim3(m, H / 256), 256, 0, s, k, H, g, y);
+  return hipGetLastError();
 }
 
-hipError_t launch_grouped_experts(hipStream_t s, const LayerDev& L, int m, int k, int inter, const float* xn,
-                                  GroupBufs g, float* y) {
-  const int H = L.gate_up.cols, E = L.router.rows;
-  if (m < 1 || m > kGrpMaxPos || k < 1 || k > 8 || E > 64 || L.gate_up.dtype != DT_Q8_0 ||
-      L.down.dtype != DT_Q8_0 || L.down.cols != inter || inter % 64 || H % 256 || !g.gu.q || !g.dn.q ||
-      g.gu.rows != L.gate_up.rows || g.gu.cols != H || g.dn.rows != L.down.rows || g.dn.cols != inter)
+hipError_t launch_grp_codes(hipStream_t s, int K, int m, const float* x, const GroupBufs& g) {
+  if (m < 1 || m > kGrpMaxPos) return hipErrorInvalidValue;
+  switch (K) {
+    case 1024: klaunch(k_grp_codes<1024>, m, 256, 0, s, x, g); break;
+    case 1536: klaunch(k_grp_codes<1536>, m, 256, 0, s, x, g); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_grp_route_norm(hipStream_t s, const LayerDev& L, int m, int k, const float* h, const float* lnw,
+                                 float eps, const GroupBufs& g) {
+  const int H = L.router.cols;
+  if (m < 1 || m > kGrpMaxPos || k < 1 || k > 8 || L.router.rows > 64 || L.router.dtype != DT_Q8_0 || !lnw)
     return hipErrorInvalidValue;
   switch (H) {
-    case 1024: klaunch(k_grp_codes<1024>, m, 256, 0, s, xn, g); break;
-    case 1536: klaunch(k_grp_codes<1536>, m, 256, 0, s, xn, g); break;
+    case 1024:
+      klaunch(k_grp_route<DT_Q8_0, 1024, true>, m, kRouteThreads, 0, s, L.router, L.router_bias, h, lnw, eps, k, g);
+      break;
+    case 1536:
+      klaunch(k_grp_route<DT_Q8_0, 1536, true>, m, kRouteThreads, 0, s, L.router, L.router_bias, h, lnw, eps, k, g);
+      break;
     default: return hipErrorInvalidValue;
   }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  return launch_grouped_core(s, H, E, m, k, inter, g, y, nullptr);
+  return hipGetLastError();
 }
 
-// gate/up, down and combine of a grouped step whose ids, weights and input codes are in g
-static hipError_t launch_grouped_core(hipStream_t s, int H, int E, int m, int k, int inter, GroupBufs g, float* y,
-                                      const hipEvent_t* ev) {
+hipError_t launch_grp_experts(hipStream_t s, int H, int E, int m, int k, int inter, const GroupBufs& g,
+                              const hipEvent_t* ev) {
   auto arm = [&](int i) {
     if (ev) arm_launch_events(ev[2 * i], ev[2 * i + 1]);
   };
+  if (m < 1 || m > kGrpMaxPos || k < 1 || k > 8 || E > 64 || (H != 1024 && H != 1536) || !g.gu.q || !g.dn.q ||
+      g.gu.cols != H || g.gu.rows != E * 2 * inter || g.dn.cols != inter || g.dn.rows != E * H)
+    return hipErrorInvalidValue;
   hipError_t e;
   const int U = m * k < E ? m * k : E;
   const bool wide = m > 16;
@@ -596,9 +465,6 @@ static hipError_t launch_grouped_core(hipStream_t s, int H, int E, int m, int k,
 #undef DOWN_CASE
     default: return hipErrorInvalidValue;
   }
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  arm(3);
-  klaunch(k_grp_combine, dim3(m, H / 256), 256, 0, s, k, H, g, y);
   return hipGetLastError();
 }
 

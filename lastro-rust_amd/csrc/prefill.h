@@ -27,10 +27,14 @@ struct PfBufs {
 };
 
 hipError_t launch_embed_b(hipStream_t s, const DMat& emb, const Dims& d, const PfBufs& p, int nv);
-// One layer for positions pos0 .. pos0 + nv - 1 (*lenp == pos0 on the device), rope: the [max_len, 64] table.
-// With grp (the layer's tiled experts and the grouped step's buffers), the experts go through the grouped int8 MFMA
-// kernels (launch_grouped_experts) instead of the per-row FMA kernels.
+// One layer for positions pos0 .. pos0 + nv - 1 (*lenp == pos0 on the device), rope: the [max_len, 64] table; the
+// per-row FMA kernels, whose results equal nv decode steps bit for bit.
 hipError_t launch_layer_b(hipStream_t s, const LayerDev& L, const Dims& d, const PfBufs& p, const int* lenp, int pos0,
-                          int nv, const float* rope, const GroupBufs* grp = nullptr);
+                          int nv, const float* rope);
+// The same layer in grouped mode: q/k/v, output projection and experts through the int8 MFMA kernels of grouped.h,
+// g holding the layer's tiled matrices. On entry g's codes are those of rmsnorm(h, L.ln_attn) (launch_norm_codes or
+// the previous layer's combine); with next_lnw the layer leaves the codes of rmsnorm(h, next_lnw) for the next one.
+hipError_t launch_layer_grouped(hipStream_t s, const LayerDev& L, const Dims& d, const PfBufs& p, const int* lenp,
+                                int pos0, int nv, const float* rope, const GroupBufs& g, const float* next_lnw);
 
 }  // namespace moert

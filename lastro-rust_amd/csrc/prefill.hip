@@ -550,7 +550,7 @@ hipError_t launch_embed_b(hipStream_t s, const DMat& emb, const Dims& d, const P
 }
 
 hipError_t launch_layer_b(hipStream_t s, const LayerDev& L, const Dims& d, const PfBufs& p, const int* lenp, int pos0,
-                          int nv, const float* rope, const GroupBufs* grp) {
+                          int nv, const float* rope) {
   if (nv < 1 || nv > kPfMaxPos || d.top_k > 8 || d.experts > 64 || d.head_dim != 64) return hipErrorInvalidValue;
 #define BODY(KK)                                                                                         \
   case KK: {                                                                                             \
@@ -582,15 +582,6 @@ hipError_t launch_layer_b(hipStream_t s, const LayerDev& L, const Dims& d, const
   MOERT_DISPATCH(L.router.dtype, L.router.cols, BODY)
 #undef BODY
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  if (grp) {
-    // grouped mode: the routed experts through the int8 MFMA kernels (codes of xn, gate/up, down, sum in list
-    // order into o[0 .. nv*H)), then the residual
-    GroupBufs g = *grp;
-    g.ids = p.ids;
-    g.w = p.w;
-    if ((e = launch_grouped_experts(s, L, nv, d.top_k, d.inter, p.xn, g, p.o)) != hipSuccess) return e;
-    return launch_add_scaled(s, p.h, p.o, d.res_mult, nv * d.hidden);
-  }
   const int U = std::min(nv * d.top_k, d.experts);
 #define BODY(KK)                                                                                         \
   case KK: {                                                                                             \
@@ -626,6 +617,23 @@ hipError_t launch_layer_b(hipStream_t s, const LayerDev& L, const Dims& d, const
   if ((e = hipGetLastError()) != hipSuccess) return e;
   klaunch(k_moe_comb_b, dim3((d.hidden + 255) / 256, nv), 256, 0, s, p.o, p.w, d.top_k, d.hidden, d.res_mult, p.h);
   return hipGetLastError();
+}
+
+hipError_t launch_layer_grouped(hipStream_t s, const LayerDev& L, const Dims& d, const PfBufs& p, const int* lenp,
+                                int pos0, int nv, const float* rope, const GroupBufs& g, const float* next_lnw) {
+  if (nv < 1 || nv > kPfMaxPos || d.top_k > 8 || d.experts > 64 || d.head_dim != 64) return hipErrorInvalidValue;
+  GroupBufs gg = g;
+  gg.ids = p.ids;
+  gg.w = p.w;
+  hipError_t e;
+  if ((e = launch_gd_qkv(s, d, nv, pos0, rope, p.q, L.k_cache, L.v_cache, gg)) != hipSuccess) return e;
+  // position v attends to pos0 + v + 1 positions: *lenp = pos0 on the device, len_add = 1
+  if ((e = launch_attn_batched(s, L, d, lenp, 1, nv, p.q, p.part, p.att)) != hipSuccess) return e;
+  if ((e = launch_grp_codes(s, d.heads * 64, nv, p.att, gg)) != hipSuccess) return e;
+  if ((e = launch_gd_oproj(s, nv, d.res_mult, p.h, gg)) != hipSuccess) return e;
+  if ((e = launch_grp_route_norm(s, L, nv, d.top_k, p.h, L.ln_moe, d.eps, gg)) != hipSuccess) return e;
+  if ((e = launch_grp_experts(s, d.hidden, d.experts, nv, d.top_k, d.inter, gg)) != hipSuccess) return e;
+  return launch_gd_combine(s, d.hidden, nv, d.top_k, d.res_mult, p.h, next_lnw, d.eps, gg);
 }
 
 }  // namespace moert
