@@ -228,8 +228,8 @@ int moert_time_steps(moert_model* m, int warmup, int iters, double* ms_per_step)
 
 /* Per-kernel timing: replays the step `iters` times as individual launches; every launch of kernel class `kind`
  * (see moert_kernel_kind) is made with start/stop events taken from its own dispatch (hipExtLaunchKernelGGL), and
- * the mean duration of one launch in microseconds and the number of launches timed are returned. The position
- * advances by iters. */
+ * the mean duration of one launch in microseconds and the number of launches timed are returned (0 launches and
+ * 0 us for a class the step does not launch). The position advances by iters. */
 typedef enum {
   MOERT_K_EMBED = 0,        /* embedding row */
   MOERT_K_QKV = 1,          /* rmsnorm + q/k/v + RoPE + KV write */
@@ -240,7 +240,9 @@ typedef enum {
   MOERT_K_EXPERT_DOWN = 6,  /* down of the routed experts + weighted combine + residual */
   MOERT_K_HEAD = 7,         /* final rmsnorm + LM head + per-block argmax */
   MOERT_K_HEAD_ARGMAX = 8,  /* argmax over the head blocks, token and position update */
-  MOERT_K_COUNT = 9
+  MOERT_K_ATTN_BLOCK = 9,   /* q/k/v + RoPE + KV write, split-KV attention and merge in one launch (replaces
+                               MOERT_K_QKV, MOERT_K_ATTN_SPLIT and MOERT_K_ATTN_COMBINE where its shape applies) */
+  MOERT_K_COUNT = 10
 } moert_kernel_kind;
 int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch, int* launches);
 

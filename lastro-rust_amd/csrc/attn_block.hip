@@ -1,0 +1,339 @@
+// Attention block of the decode step in one launch: rmsnorm -> [q; k; v] rows -> rotate_half RoPE -> KV append,
+// the split-KV GQA attention, and the merge of the splits. It does the work of k_qkv, k_attn_tiles and
+// k_attn_combine (kernels.hip) with their operations in their order, so its results are the same bit for bit; the
+// reference sequence it replaces is gpu_model.rs:341-384 (rmsnorm, gemv q/k/v, rope_kv, the KV copies,
+// attention_b = attn_split + attn_combine, gpu.rs:133-292; paths relative to rust/moe-rt/src).
+//
+// The chip dispatches the workgroups of a launch to its 8 XCDs in round-robin order, continuing from where the
+// previous launch left off: workgroup b runs on XCD (c + b) % 8 for some c. So the workgroups 8s + r (s = 0, 1, ...)
+// of one residue r share an XCD, and workgroup b serves KV head g = its XCD (hardware register XCC_ID) and split
+// s = b / 8: all workgroups of KV head g run on XCD g and share its L2. They exchange their data through that L2
+// (attn_dev.h) and meet at per-split flags, which costs far less than a kernel boundary:
+//   1. the group's q/k/v row pairs ((G + 2) * 32 of them: G query heads, one K and one V head) are dealt out over
+//      its splits; each workgroup normalises h, computes its pairs with RoPE, writes q into the group's L2 area and
+//      K, V into row `pos` of the cache, and sets its flag;
+//   2. meanwhile its split's K and V tiles have been loaded and staged in LDS; once every flag of the group is set
+//      it reads its queries and (when the split holds position pos) the new K/V row, and computes the split's
+//      partials (m, l, acc) per query head as k_attn_tiles does, into the group's L2 area, and sets a second flag;
+//   3. workgroup s < G then merges query head g*G + s over the used splits as k_attn_combine does, into `att`.
+// Every wait is bounded: a flag that does not arrive in time (which is what a dispatch that is not round-robin, or
+// a group that is not all resident at once, would cause) sets a bit of `err` and the kernel still ends; the host
+// turns a set bit into an error.
+#include "attn_dev.h"
+#include "dev_rows.h"
+#include "kernels.h"
+#include "launch.h"
+#include "timeline.h"
+
+namespace moert {
+
+namespace {
+
+constexpr int kAbSpin = 1 << 18;  // polls of a flag set before a wait gives up (each poll is an L2 round trip)
+
+// Wave-level wait until flags[i] == epoch for every i < n (n <= 64), read from the XCD's L2. Returns false when the
+// wait gave up.
+__device__ __forceinline__ bool wait_flags(const unsigned* flags, int n, unsigned epoch, int lane) {
+  const __amdgpu_buffer_rsrc_t r = l2_buffer(flags, kAbMaxSplits * 4);
+  for (int it = 0; it < kAbSpin; it++) {
+    const unsigned f = lane < n ? l2_load_u32(r, 4u * lane) : epoch;
+    if (__ballot(f != epoch) == 0) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return false;
+}
+
+}  // namespace
+
+template <int DT, int K, int G, int T, int NP, int SP>
+__global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* __restrict__ h,
+                                                          const float* __restrict__ lnw, float eps,
+                                                          const int* __restrict__ st, const float* __restrict__ rope,
+                                                          int heads, int max_len, uint16_t* __restrict__ kc,
+                                                          uint16_t* __restrict__ vc, float scale, int splits, int pp,
+                                                          AbGroup* __restrict__ xg_all,
+                                                          const unsigned* __restrict__ step_ctr, unsigned layer,
+                                                          unsigned* __restrict__ err, float* __restrict__ att, Tl tl) {
+  TL_START(tl);
+  using Ge = Geo<DT, K>;
+  static_assert(Ge::RPW == 1, "one q/k/v row per wave and pass");
+  constexpr int NW = G * T, NT = NW * 64, P = 2 * NP;
+  constexpr int TR = 8 % G == 0 ? 64 : 72;  // tile rows (64..71: padding for VShare when G does not divide 8)
+  constexpr int KS = 68;                     // K row stride in floats: 16-byte rows, conflict-free row reads
+  __shared__ __align__(16) float Vs[T][TR][64];
+  __shared__ __align__(16) float Ks[T][TR][KS];
+  __shared__ float rs;
+  static_assert(T * TR * 64 >= K, "the normalised input is staged in the V tiles' LDS");
+  float* xs = &Vs[0][0][0];  // the normalised input, until the V tiles are staged
+  __shared__ float Qs[G][64];
+  __shared__ float Ps[G][T][64];
+  __shared__ float Pv[G][T][64];
+  __shared__ float Tm[G][T], Al[G][T], Ts[G][T];
+  __shared__ float Cw[2][64];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int g = (int)xcc_id() & 7, s = blockIdx.x >> 3;
+  const int wh = wid % G, wt = wid / G;
+  AbGroup* xg = xg_all + g;
+  uint16_t* Kc = kc + (size_t)g * max_len * 64;
+  uint16_t* Vc = vc + (size_t)g * max_len * 64;
+  const float NEG_INF = __int_as_float(0xff800000);
+
+  // this wave's q/k/v row pairs: pair l of the group (l = s * pp + wid + NW * a) is row pair (jp, jp + 32) of the
+  // group's head l / 32 (query heads g*G .. g*G + G - 1, then K head g, then V head g)
+  constexpr int NPAIR = (G + 2) * 32;
+  size_t row[P];
+  bool ok[P];
+  int lh[NP], jp[NP];
+#pragma unroll
+  for (int a = 0; a < NP; a++) {
+    const int li = wid + NW * a, l = s * pp + li;
+    const bool v = li < pp && l < NPAIR;
+    const int lc = v ? l : 0;
+    lh[a] = lc / 32;
+    jp[a] = lc % 32;
+    const int gh = lh[a] < G ? g * G + lh[a] : lh[a] == G ? heads + g : heads + 8 + g;
+    row[2 * a] = (size_t)gh * 64 + jp[a];
+    row[2 * a + 1] = row[2 * a] + 32;
+    ok[2 * a] = ok[2 * a + 1] = v;
+  }
+  // loads in the order they are needed (they complete in issue order): the position and the step counter, the
+  // activation, this lane's cos/sin, the q/k/v rows, then the split's K and V tiles (used after the first barrier)
+  const int pos = st[ST_POS];
+  const unsigned epoch = *step_ctr * 64u + layer + 1u;
+  NormIn<K, NT> hin;
+  norm_fetch<K, NT>(h, lnw, hin);
+  const float* cs = rope + (size_t)pos * 64;
+  float cv[NP], sv[NP];
+#pragma unroll
+  for (int a = 0; a < NP; a++) {
+    cv[a] = cs[jp[a]];
+    sv[a] = cs[32 + jp[a]];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  Rows<DT, K, P> rr;
+  rows_load<DT, K, P>(rr, m, row, ok, lane);
+  __builtin_amdgcn_sched_barrier(0);
+  const int t0 = s * T, t = t0 + wt;
+  const int tc = min(t, max_len / 64 - 1);  // a tile past the cache's end (never used) reads the last tile
+  VShare<G> ksh, vsh;
+  ksh.load(Kc, tc, lane, wh);
+  vsh.load(Vc, tc, lane, wh);
+
+  // 1. q/k/v pairs of the group
+  norm_finish<K, NT>(hin, eps, xs, &rs);
+  XReg<DT, K> xr;
+  load_x<DT, K>(xr, xs, lane);
+  float out[P];
+  rows_fma<DT, K, P>(rr, ok, xr, lane, out);
+  TL_PHASE(tl, 2);
+  if (lane == 0) {
+#pragma unroll
+    for (int a = 0; a < NP; a++) {
+      if (!ok[2 * a]) continue;
+      const float x1 = out[2 * a], x2 = out[2 * a + 1], c = cv[a], sn = sv[a];
+      if (lh[a] < G) {
+        xg->q[lh[a]][jp[a]] = x1 * c - x2 * sn;
+        xg->q[lh[a]][jp[a] + 32] = x2 * c + x1 * sn;
+      } else if (lh[a] == G) {
+        Kc[(size_t)pos * 64 + jp[a]] = f2h(x1 * c - x2 * sn);
+        Kc[(size_t)pos * 64 + jp[a] + 32] = f2h(x2 * c + x1 * sn);
+      } else {
+        Vc[(size_t)pos * 64 + jp[a]] = f2h(x1);
+        Vc[(size_t)pos * 64 + jp[a] + 32] = f2h(x2);
+      }
+    }
+  }
+  // the split's tiles into LDS while the other workgroups finish their pairs (every wave has read xs)
+  __syncthreads();
+  const int len = pos + 1;
+  const int nb = (len + 63) / 64;
+  const int used = min(T, nb - t0);  // tiles of this split inside the length (>= 1 when the split is used)
+  const bool active = wt < used;
+  const int nv = active ? min(64, len - t * 64) : 0;
+  ksh.template store<KS>(&Ks[wt][0][0], lane, wh, nv);
+  vsh.template store<64>(&Vs[wt][0][0], lane, wh, nv);
+  wait_mem();  // this wave's q/k/v stores have reached the L2
+  __syncthreads();
+  if (threadIdx.x == 0) xg->flag_qkv[s] = epoch;
+  if (wid == 0 && !wait_flags(xg->flag_qkv, splits, epoch, lane) && lane == 0) atomicOr(err, 2u);
+  __syncthreads();
+  TL_PHASE(tl, 3);
+
+  // 2. the split's partials: queries of the group from the L2, the new K/V row (written by this group in phase 1)
+  // over the stale row `pos` of the staged tiles
+  {
+    const __amdgpu_buffer_rsrc_t rq = l2_buffer(&xg->q[0][0], sizeof(xg->q));
+    Qs[wh][lane] = l2_load_f32(rq, 4u * (wh * 64 + lane));  // every wave of head wh stores the same q
+    const int tp = pos / 64 - t0;
+    if (tp >= 0 && tp < T && wid == tp * G) {
+      const __amdgpu_buffer_rsrc_t rk = l2_buffer(Kc + (size_t)pos * 64, 128);
+      const __amdgpu_buffer_rsrc_t rv = l2_buffer(Vc + (size_t)pos * 64, 128);
+      Ks[tp][pos & 63][lane] = h2f(l2_load_u16(rk, 2u * lane));
+      Vs[tp][pos & 63][lane] = h2f(l2_load_u16(rv, 2u * lane));
+    }
+  }
+  __syncthreads();  // Qs, the new row
+  // scores: lane = position, chain over the 64 dims in order (an inactive tile's scores are discarded)
+  float sc;
+  {
+    float dt = 0.0f;
+    const float* krow = &Ks[wt][lane][0];
+#pragma unroll
+    for (int d4 = 0; d4 < 16; d4++) {
+      const float4 kk = *reinterpret_cast<const float4*>(krow + 4 * d4);
+      const float4 qq = *reinterpret_cast<const float4*>(&Qs[wh][4 * d4]);
+      dt = __builtin_fmaf(qq.x, kk.x, dt);
+      dt = __builtin_fmaf(qq.y, kk.y, dt);
+      dt = __builtin_fmaf(qq.z, kk.z, dt);
+      dt = __builtin_fmaf(qq.w, kk.w, dt);
+    }
+    sc = lane < nv ? dt * scale : NEG_INF;  // nv = 0 for an inactive tile
+  }
+  const float tmax = group_max<64>(sc);
+  if (lane == 0) Tm[wh][wt] = tmax;
+  __syncthreads();  // tile maxima
+  float pv = 0.0f;
+  if (active) {
+    float mprev = NEG_INF;
+    for (int u = 0; u < wt; u++) mprev = mprev > Tm[wh][u] ? mprev : Tm[wh][u];
+    const float mn = mprev > tmax ? mprev : tmax;
+    const float alpha = dexp(mprev - mn);
+    const float p = dexp(sc - mn);
+    const float ts = group_sum<64>(p);
+    Ps[wh][wt][lane] = p;
+    if (lane == 0) {
+      Al[wh][wt] = alpha;
+      Ts[wh][wt] = ts;
+    }
+  }
+  __syncthreads();  // P written
+  if (active) {
+    // p.v: lane = dim, chain over the positions in order; past the length p = 0 and V = +0, so those steps leave
+    // pv unchanged (the chain equals the one over the valid positions only)
+    const float* vcol = &Vs[wt][0][lane];
+#pragma unroll
+    for (int i0 = 0; i0 < 64; i0 += 4) {
+      const float4 p4 = *reinterpret_cast<const float4*>(&Ps[wh][wt][i0]);
+      const float pa[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+      for (int u = 0; u < 4; u++) pv = __builtin_fmaf(pa[u], vcol[(i0 + u) * 64], pv);
+    }
+    if (wt > 0) Pv[wh][wt][lane] = pv;
+  }
+  __syncthreads();  // p.v of every tile
+  if (wt == 0 && used > 0) {
+    float mm = NEG_INF, l = 0.0f, acc = 0.0f;
+    for (int u = 0; u < used; u++) {
+      const float a = Al[wh][u];
+      l = __builtin_fmaf(l, a, Ts[wh][u]);
+      acc = __builtin_fmaf(acc, a, u == 0 ? pv : Pv[wh][u][lane]);
+      mm = mm > Tm[wh][u] ? mm : Tm[wh][u];
+    }
+    float* pp_ = xg->part[s][wh];
+    if (lane == 0) {
+      pp_[0] = mm;
+      pp_[1] = l;
+    }
+    pp_[2 + lane] = acc;
+  }
+  TL_PHASE(tl, 4);
+  wait_mem();  // the partials have reached the L2
+  __syncthreads();
+  if (threadIdx.x == 0) xg->flag_part[s] = epoch;
+  if (s >= G || wid != 0) {
+    TL_END(tl);
+    return;
+  }
+
+  // 3. workgroup s < G merges query head g*G + s: M = max m_s; w_s = exp(m_s - M); den and num are fma chains
+  // over the used splits in order; out = num / den (k_attn_combine)
+  const int hh = s;
+  const int nsplit = (nb + T - 1) / T;  // used splits
+  if (!wait_flags(xg->flag_part, nsplit, epoch, lane) && lane == 0) atomicOr(err, 4u);
+  const __amdgpu_buffer_rsrc_t rp = l2_buffer(&xg->part[0][0][0], sizeof(xg->part));
+  constexpr unsigned REC = sizeof(xg->part[0][0]), SREC = sizeof(xg->part[0]);
+  float av[SP];
+#pragma unroll
+  for (int s2 = 0; s2 < SP; s2++)
+    av[s2] = l2_load_f32(rp, (unsigned)min(s2, splits - 1) * SREC + hh * REC + 4u * (2 + lane));
+  const unsigned sl = (unsigned)min(lane, splits - 1);
+  float ms = l2_load_f32(rp, sl * SREC + hh * REC);
+  float ls = l2_load_f32(rp, sl * SREC + hh * REC + 4u);
+  if (lane >= nsplit) {
+    ms = NEG_INF;
+    ls = 0.0f;
+  }
+  const float M = group_max<64>(ms);
+  Cw[0][lane] = lane < nsplit ? dexp(ms - M) : 0.0f;
+  Cw[1][lane] = ls;
+  wave_lds_sync();
+  float den = 0.0f, num = 0.0f;
+#pragma unroll
+  for (int s2 = 0; s2 < SP; s2++) {
+    if (s2 < nsplit) {
+      const float ws = Cw[0][s2];
+      den = __builtin_fmaf(ws, Cw[1][s2], den);
+      num = __builtin_fmaf(ws, av[s2], num);
+    }
+  }
+  att[(g * G + hh) * 64 + lane] = num / den;
+  TL_PHASE(tl, 5);
+  TL_END(tl);
+}
+
+// ------------------------------------------------------------------------------------------------------------
+namespace {
+
+struct AbShape {
+  int G, T, splits, pp, np;
+};
+
+// The launch shape of the attention block for these dimensions, or false when the fused path does not apply.
+bool ab_shape(const Dims& d, const DMat& qkv, int cus, AbShape* out) {
+  // one q/k/v row per wave pass (Q8_0 rows of 1024 or 1536, Q4_0 rows of 1536)
+  const bool rows_ok = (qkv.dtype == DT_Q8_0 && (qkv.cols == 1024 || qkv.cols == 1536)) ||
+                       (qkv.dtype == DT_Q4_0 && qkv.cols == 1536);
+  if (d.kv_heads != 8 || d.head_dim != 64 || d.heads % 8 || !rows_ok || qkv.cols != d.hidden ||
+      qkv.rows != (d.heads + 16) * 64)
+    return false;
+  const int G = d.heads / 8, T = d.tps;
+  if (G < 2 || G > 3 || T < 2 || T > 4 || d.max_len % 64) return false;  // the compiled shapes
+  const int splits = attn_splits_for(d.max_len, T);
+  // every workgroup of a group must be resident at once (they wait for each other): one workgroup per compute
+  // unit (the LDS of a workgroup is above half of a compute unit's), at most cus / 8 splits
+  if (splits < G || splits > kAbMaxSplits || splits > 32 || 8 * splits > cus) return false;
+  const int npair = (G + 2) * 32, pp = (npair + splits - 1) / splits, np = (pp + G * T - 1) / (G * T);
+  if (np > 2) return false;
+  *out = AbShape{G, T, splits, pp, np};
+  return true;
+}
+
+}  // namespace
+
+bool attn_block_fits(const Dims& d, const DMat& qkv, int cus) {
+  AbShape sh;
+  return ab_shape(d, qkv, cus, &sh);
+}
+
+hipError_t launch_attn_block(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int cus, int layer,
+                             const AbBufs& x, Tl tl) {
+  AbShape sh;
+  if (!ab_shape(d, L.qkv, cus, &sh)) return hipErrorInvalidValue;
+  const int grid = 8 * sh.splits;
+#define AB_CASE(DD, KK, GG, TT, NN)                                                                                \
+  if (L.qkv.dtype == DD && L.qkv.cols == KK && sh.G == GG && sh.T == TT && sh.np == NN) {                         \
+    klaunch(k_attn_block<DD, KK, GG, TT, NN, 32>, grid, GG * TT * 64, 0, s, L.qkv, b.h, L.ln_attn, d.eps,         \
+            b.state, b.rope, d.heads, d.max_len, L.k_cache, L.v_cache, d.attn_mult, sh.splits, sh.pp, x.groups,    \
+            x.step_ctr, (unsigned)layer, x.err, b.att, tl);                                                        \
+    return hipGetLastError();                                                                                      \
+  }
+#define AB_T(DD, KK, GG) AB_CASE(DD, KK, GG, 2, 1) AB_CASE(DD, KK, GG, 2, 2) AB_CASE(DD, KK, GG, 3, 1) \
+                         AB_CASE(DD, KK, GG, 3, 2) AB_CASE(DD, KK, GG, 4, 1) AB_CASE(DD, KK, GG, 4, 2)
+  AB_T(DT_Q8_0, 1536, 3) AB_T(DT_Q8_0, 1536, 2) AB_T(DT_Q8_0, 1024, 2) AB_T(DT_Q8_0, 1024, 3)
+  AB_T(DT_Q4_0, 1536, 3) AB_T(DT_Q4_0, 1536, 2)
+#undef AB_T
+#undef AB_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace moert

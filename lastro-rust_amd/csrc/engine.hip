@@ -202,6 +202,11 @@ struct moert_model {
   float* norm = nullptr;
   StepBufs b{};
   int n_head_blocks = 0;
+  // attention block in one launch (attn_block.hip) when the shape allows it; otherwise q/k/v, split attention and
+  // combine as three kernels. MOERT_ATTN_BLOCK=0 at create keeps the three kernels.
+  bool use_ab = false;
+  int cus = 0;
+  AbBufs ab{};
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   // expert cache (ExpertCache, rust/moe-rt/src/cache.rs): experts live in the pinned host store, `cache.slots` of
@@ -261,7 +266,7 @@ struct moert_model {
       tl_layer.push_back(layer);
       return t;
     };
-    CHECK_HIP(launch_embed(stream, embed, dims, b, arm(MOERT_K_EMBED, -1)));
+    CHECK_HIP(launch_embed(stream, embed, dims, b, ab.step_ctr, arm(MOERT_K_EMBED, -1)));
     for (size_t l = 0; l < layers.size(); l++) {
       const LayerDev& L = layers[l];
       const int li = (int)l;
@@ -277,9 +282,13 @@ struct moert_model {
         CHECK_HIP(launch_prefetch_copy(pf_stream, cache));
         CHECK_HIP(hipEventRecord(ev_copy, pf_stream));
       }
-      CHECK_HIP(launch_qkv(stream, L, dims, b, arm(MOERT_K_QKV, li)));
-      CHECK_HIP(launch_attn_split(stream, L, dims, b, arm(MOERT_K_ATTN_SPLIT, li)));
-      CHECK_HIP(launch_attn_combine(stream, dims, b, arm(MOERT_K_ATTN_COMBINE, li)));
+      if (use_ab) {
+        CHECK_HIP(launch_attn_block(stream, L, dims, b, cus, li, ab, arm(MOERT_K_ATTN_BLOCK, li)));
+      } else {
+        CHECK_HIP(launch_qkv(stream, L, dims, b, arm(MOERT_K_QKV, li)));
+        CHECK_HIP(launch_attn_split(stream, L, dims, b, arm(MOERT_K_ATTN_SPLIT, li)));
+        CHECK_HIP(launch_attn_combine(stream, dims, b, arm(MOERT_K_ATTN_COMBINE, li)));
+      }
       if (pf) CHECK_HIP(hipStreamWaitEvent(stream, ev_pred, 0));
       CHECK_HIP(launch_oproj(stream, L, dims, b, arm(MOERT_K_OPROJ, li)));
       if (pf) CHECK_HIP(hipStreamWaitEvent(stream, ev_copy, 0));
@@ -341,14 +350,18 @@ struct moert_model {
     CHECK_HIP(hipMemcpy(&pos, b.state + ST_POS, 4, hipMemcpyDeviceToHost));
     std::memcpy(hy_table_pin, P.table().data(), (size_t)L * E * 4);
     CHECK_HIP(hipMemcpyAsync(hy_table, hy_table_pin, (size_t)L * E * 4, hipMemcpyHostToDevice, stream));
-    CHECK_HIP(launch_embed(stream, embed, dims, b));
+    CHECK_HIP(launch_embed(stream, embed, dims, b, ab.step_ctr));
     std::vector<int> keys, n_e;
     std::vector<char> gpu;
     for (int l = 0; l < L; l++) {
       const LayerDev& Ld = layers[l];
-      CHECK_HIP(launch_qkv(stream, Ld, dims, b));
-      CHECK_HIP(launch_attn_split(stream, Ld, dims, b));
-      CHECK_HIP(launch_attn_combine(stream, dims, b));
+      if (use_ab) {
+        CHECK_HIP(launch_attn_block(stream, Ld, dims, b, cus, l, ab));
+      } else {
+        CHECK_HIP(launch_qkv(stream, Ld, dims, b));
+        CHECK_HIP(launch_attn_split(stream, Ld, dims, b));
+        CHECK_HIP(launch_attn_combine(stream, dims, b));
+      }
       CHECK_HIP(launch_oproj(stream, Ld, dims, b));
       CHECK_HIP(launch_route_up_cached(stream, Ld, dims, b, l, cache));
       CHECK_HIP(hipMemcpyAsync(hy_ids_pin, b.route_ids + l * K, (size_t)K * 4, hipMemcpyDeviceToHost, stream));
@@ -808,6 +821,24 @@ static int model_create(const moert_config* c, const moert_model_weights* w, int
       (rc = zeros(a, s, max_len, &b.seq)) || (rc = zeros(a, s, max_len, &b.argmax_hist)) ||
       (rc = zeros(a, s, ST_WORDS, &b.state)))
     return bail(rc);
+  {
+    int dev = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+      set_err("hipGetDeviceProperties failed");
+      return bail(MOERT_E_DEVICE);
+    }
+    m->cus = prop.multiProcessorCount;
+    const char* ev = getenv("MOERT_ATTN_BLOCK");
+    const bool allow = !(ev && ev[0] == '0');
+    unsigned* grp = nullptr;
+    if ((rc = zeros(a, s, 8 * sizeof(AbGroup) / 4, &grp)) || (rc = zeros(a, s, (size_t)1, &m->ab.step_ctr)) ||
+        (rc = zeros(a, s, (size_t)1, &m->ab.err)))
+      return bail(rc);
+    m->ab.groups = reinterpret_cast<AbGroup*>(grp);
+    m->use_ab = allow && c->layers <= 63 && std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 &&
+                attn_block_fits(m->dims, m->layers[0].qkv, m->cus);
+  }
   if (hipStreamSynchronize(s) != hipSuccess) {
     set_err("upload failed");
     return bail(MOERT_E_DEVICE);
@@ -1035,9 +1066,21 @@ static int model_launch(moert_model* m) {
   CHECK_HIP(hipGraphLaunch(m->exec, m->stream));
   return MOERT_OK;
 }
+// A bit the attention block kernel set (a wait that gave up) is a device error.
+static int ab_check(moert_model* m) {
+  if (!m->use_ab) return MOERT_OK;
+  unsigned e = 0;
+  CHECK_HIP(hipMemcpy(&e, m->ab.err, 4, hipMemcpyDeviceToHost));
+  if (e) {
+    set_err("attention block: a wait for the workgroups of a KV head gave up (error bits %#x): the launch's "
+            "workgroups were not dispatched round-robin over the XCDs or not all resident at once", e);
+    return MOERT_E_DEVICE;
+  }
+  return MOERT_OK;
+}
 static int model_sync(moert_model* m) {
   CHECK_HIP(hipStreamSynchronize(m->stream));
-  return MOERT_OK;
+  return ab_check(m);
 }
 
 // ---- runtime metrics during moert_generate ----
@@ -1562,6 +1605,7 @@ static int time_steps_impl(moert_model* m, int warmup, int iters, double* ms) {
   for (int i = 0; i < iters; i++) TRY(model_launch(m));
   CHECK_HIP(hipEventRecord(e1, m->stream));
   CHECK_HIP(hipEventSynchronize(e1));
+  TRY(ab_check(m));
   float t = 0.0f;
   CHECK_HIP(hipEventElapsedTime(&t, e0, e1));
   *ms = iters > 0 ? t / iters : 0.0;
@@ -1584,14 +1628,16 @@ int moert_time_steps(moert_model* m, int warmup, int iters, double* ms_per_step)
 }
 
 static int time_kernel_impl(moert_model* m, int kind, int iters, double* us, int* launches) {
-  int per_step = (kind == MOERT_K_EMBED || kind == MOERT_K_HEAD || kind == MOERT_K_HEAD_ARGMAX) ? 1 : m->cfg.layers;
-  std::vector<hipEvent_t> ev(2 * per_step);
+  // at most one launch of a class per layer; a class the step does not launch gives no launches
+  std::vector<hipEvent_t> ev(2 * (size_t)m->cfg.layers + 2);
   for (auto& e : ev) CHECK_HIP(hipEventCreate(&e));
   double total = 0.0;
   int n = 0;
   for (int it = 0; it < iters; it++) {
     TRY(m->enqueue(kind, &ev));
+    const int per_step = m->ev_i / 2;
     CHECK_HIP(hipStreamSynchronize(m->stream));
+    TRY(ab_check(m));
     for (int i = 0; i < per_step; i++) {
       float t = 0.0f;
       CHECK_HIP(hipEventElapsedTime(&t, ev[2 * i], ev[2 * i + 1]));

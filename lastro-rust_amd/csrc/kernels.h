@@ -48,11 +48,35 @@ struct StepBufs {
   const float* rope; // [max_len, d]: cos of the d/2 frequencies, then sin
 };
 
-// tl: the launch's timeline record (measurement build; null otherwise).
-hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const StepBufs& b, Tl tl = {});
+// Exchange area of the attention block kernel (attn_block.hip) for one KV head, used only by the workgroups that
+// run on the XCD of that head: per-split flags (the launch's epoch once the split's q/k/v rows, then its partials,
+// are stored), the head group's queries after RoPE, and the partials (m, l, acc[64]) of every split and query head.
+constexpr int kAbMaxSplits = 64;
+struct AbGroup {
+  unsigned flag_qkv[kAbMaxSplits];
+  unsigned flag_part[kAbMaxSplits];
+  float q[4][64];
+  float part[kAbMaxSplits][4][68];
+};
+struct AbBufs {
+  AbGroup* groups;     // [8]
+  unsigned* step_ctr;  // decode steps started (k_embed adds one); a launch's epoch is step_ctr * 64 + layer + 1
+  unsigned* err;       // bits 1, 2: a wait for the workgroups of a KV head (their q/k/v rows, their partials) gave up
+};
+
+// tl: the launch's timeline record (measurement build; null otherwise). step_ctr (may be null): incremented once.
+hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const StepBufs& b, unsigned* step_ctr,
+                        Tl tl = {});
 hipError_t launch_qkv(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl = {});
 hipError_t launch_attn_split(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl = {});
 hipError_t launch_attn_combine(hipStream_t s, const Dims& d, const StepBufs& b, Tl tl = {});
+// The attention block (q/k/v + RoPE + KV append, split-KV attention, merge) in one launch, or false / an error when
+// its shape does not apply: 8 KV heads of dim 64, 2-3 query heads each, q/k/v rows of 1024 or 1536 (Q8_0) or 1536
+// (Q4_0), 2-4 tiles
+// per split, at most min(32, cus / 8) splits (cus: compute units of the device), layer < 63.
+bool attn_block_fits(const Dims& d, const DMat& qkv, int cus);
+hipError_t launch_attn_block(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int cus, int layer,
+                             const AbBufs& x, Tl tl = {});
 // Both attention kernels for ny consecutive positions of a multi-position step: position y has its query at
 // q + y * heads * 64, attends to *lenp + len_add + y cached positions and writes att + y * heads * 64 (part holds
 // ny * heads * splits * 66 floats).

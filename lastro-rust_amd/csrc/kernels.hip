@@ -9,6 +9,7 @@
 #include "kernels.h"
 #include "launch.h"
 #include "moe_norm.h"
+#include "attn_dev.h"
 #include "timeline.h"
 
 namespace moert {
@@ -62,8 +63,10 @@ __global__ __launch_bounds__(kBlock) void k_gemv(DMat m, const float* __restrict
 // Embedding row times embedding_multiplier (model.rs:134-138); the token is seq[pos] on the device.
 template <int DT>
 __global__ __launch_bounds__(kBlock) void k_embed(DMat e, const int* __restrict__ seq, const int* __restrict__ st,
-                                                  float mult, float* __restrict__ h, Tl tl) {
+                                                  float mult, float* __restrict__ h, unsigned* __restrict__ step_ctr,
+                                                  Tl tl) {
   TL_START(tl);
+  if (step_ctr && threadIdx.x == 0) *step_ctr += 1u;
   int tok = seq[st[ST_POS]];
   int H = e.cols;
   for (int i = threadIdx.x; i < H; i += kBlock) {
@@ -290,52 +293,6 @@ __global__ __launch_bounds__(256) void k_attn_split(const float* __restrict__ q,
   }
   pp[2 + lane] = acc;
 }
-
-// One wave's share of a V tile moved into LDS through registers, by the G waves that serve the same tile: piece e
-// (e = wave, wave + G, ...) is rows 8e..8e+7, lane l carrying 16 bytes of row 8e + l/8, so each piece reads 1 KB of
-// consecutive cache rows. The LDS tile is row-major [64][64] f32, converted once for the G heads, with the rows at
-// and past the tile's valid length `nv` stored as +0. Plain loads (not LDS DMA) keep the wait for the tile separate
-// from the waits for the kernel's other loads. A piece index past 7 (only for G = 3) loads piece 7 again and stores
-// it into rows 64..71 of the tile, which are padding and never read.
-template <int G>
-struct VShare {
-  static constexpr int N = (8 + G - 1) / G;
-  uint4 a, b, c, d, e, f, g, h;  // pieces 0..N-1 of this wave (named members: no private array)
-  __device__ __forceinline__ void load(const uint16_t* V, int t, int lane, int wave) {
-    const uint4* src = reinterpret_cast<const uint4*>(V + ((size_t)t * 64 + (lane >> 3)) * 64 + (lane & 7) * 8);
-    auto at = [&](int i) { return src[(size_t)min(wave + G * i, 7) * 64]; };
-    a = at(0);
-    if (N > 1) b = at(1);
-    if (N > 2) c = at(2);
-    if (N > 3) d = at(3);
-    if (N > 4) e = at(4);
-    if (N > 5) f = at(5);
-    if (N > 6) g = at(6);
-    if (N > 7) h = at(7);
-  }
-  template <int STRIDE>
-  __device__ __forceinline__ void store(float* dst, int lane, int wave, int nv) const {
-    auto put = [&](int i, const uint4& v) {
-      const int row = 8 * (wave + G * i) + (lane >> 3);
-      const bool z = row >= nv;
-      float4* o = reinterpret_cast<float4*>(dst + row * STRIDE + (lane & 7) * 8);
-      o[0] = z ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
-               : make_float4(h2f((uint16_t)(v.x & 0xffffu)), h2f((uint16_t)(v.x >> 16)), h2f((uint16_t)(v.y & 0xffffu)),
-                             h2f((uint16_t)(v.y >> 16)));
-      o[1] = z ? make_float4(0.0f, 0.0f, 0.0f, 0.0f)
-               : make_float4(h2f((uint16_t)(v.z & 0xffffu)), h2f((uint16_t)(v.z >> 16)), h2f((uint16_t)(v.w & 0xffffu)),
-                             h2f((uint16_t)(v.w >> 16)));
-    };
-    put(0, a);
-    if (N > 1) put(1, b);
-    if (N > 2) put(2, c);
-    if (N > 3) put(3, d);
-    if (N > 4) put(4, e);
-    if (N > 5) put(5, f);
-    if (N > 6) put(6, g);
-    if (N > 7) put(7, h);
-  }
-};
 
 // Tile-parallel form of k_attn_split for a split of exactly T tiles: workgroup = G x T waves, wave (wh, wt) takes
 // query head g*G + wh and tile t0 + wt. Every wave computes its tile's scores and tile max at once; the running max
@@ -1385,11 +1342,12 @@ hipError_t launch_gemv(hipStream_t s, const DMat& w, const float* x, float* y) {
   return hipGetLastError();
 }
 
-hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const StepBufs& b, Tl tl) {
+hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const StepBufs& b, unsigned* step_ctr,
+                        Tl tl) {
   switch (emb.dtype) {
-    case DT_Q8_0: klaunch(k_embed<DT_Q8_0>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h, tl); break;
-    case DT_Q4_0: klaunch(k_embed<DT_Q4_0>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h, tl); break;
-    case DT_F32: klaunch(k_embed<DT_F32>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h, tl); break;
+    case DT_Q8_0: klaunch(k_embed<DT_Q8_0>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h, step_ctr, tl); break;
+    case DT_Q4_0: klaunch(k_embed<DT_Q4_0>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h, step_ctr, tl); break;
+    case DT_F32: klaunch(k_embed<DT_F32>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h, step_ctr, tl); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -38,6 +38,7 @@ PHASES = {
     "expert_down": ["activations staged", "down rows fma"],
     "head": ["norm of h"],
     "head_argmax": [],
+    "attn_block": ["q/k/v rows fma", "group barrier passed", "partials stored", "merge done"],
 }
 
 

@@ -1,0 +1,123 @@
+"""CPU transcription of the attention block kernel's index arithmetic (lastro-rust_amd/csrc/attn_block.hip): for
+every launch shape the eligibility rule admits, the q/k/v row pairs of each KV head group are computed exactly
+once and every row index stays inside the [q; k; v] matrix, every tile read stays inside the cache, exactly one
+workgroup of the group takes the new K/V row for every position, each query head is merged by exactly one
+workgroup, and every flag and partial offset stays inside the group's exchange area."""
+import itertools
+
+import pytest
+
+MAX_SPLITS = 64          # kAbMaxSplits
+PART_REC = 68 * 4        # bytes of one (split, head) partial record
+PART_SPLIT = 4 * PART_REC
+PART_BYTES = MAX_SPLITS * PART_SPLIT
+
+
+def tiles_per_split(max_len, splits):
+    return (max_len // 64 + splits - 1) // splits
+
+
+def attn_splits_for(max_len, tps):
+    return ((max_len + 63) // 64 + tps - 1) // tps
+
+
+def ab_shape(heads, kv_heads, hidden, max_len, tps, cus=256, dtype="q8_0"):
+    """Restatement of ab_shape(): the launch shape, or None when the three-kernel path is used."""
+    rows_ok = (dtype == "q8_0" and hidden in (1024, 1536)) or (dtype == "q4_0" and hidden == 1536)
+    if kv_heads != 8 or heads % 8 or not rows_ok:
+        return None
+    G, T = heads // 8, tps
+    if not (2 <= G <= 3 and 2 <= T <= 4) or max_len % 64:
+        return None
+    splits = attn_splits_for(max_len, T)
+    if splits < G or splits > MAX_SPLITS or splits > 32 or 8 * splits > cus:
+        return None
+    npair = (G + 2) * 32
+    pp = (npair + splits - 1) // splits
+    np_ = (pp + G * T - 1) // (G * T)
+    if np_ > 2:
+        return None
+    return G, T, splits, pp, np_
+
+
+def shapes():
+    out = []
+    for heads, hidden in ((16, 1024), (24, 1536), (16, 1536), (24, 1024)):
+        for max_len in range(64, 8192 + 1, 64):
+            for req in range(1, 65):
+                tps = tiles_per_split(max_len, req)
+                sh = ab_shape(heads, 8, hidden, max_len, tps)
+                if sh:
+                    out.append((heads, hidden, max_len, sh))
+    # one entry per distinct (heads, hidden, max_len, shape)
+    return sorted(set(out))
+
+
+SHAPES = shapes()
+
+
+def test_the_bench_and_test_shapes_are_eligible():
+    assert ab_shape(24, 8, 1536, 4416, tiles_per_split(4416, 32)) == (3, 3, 23, 7, 1)
+    assert ab_shape(16, 8, 1024, 4416, tiles_per_split(4416, 32)) == (2, 3, 23, 6, 1)
+    assert ab_shape(24, 8, 1536, 4352, tiles_per_split(4352, 64)) is None  # 34 splits: three kernels
+    assert ab_shape(16, 8, 1024, 448, tiles_per_split(448, 64)) is None    # one tile per split
+    assert ab_shape(24, 8, 1536, 4416, tiles_per_split(4416, 32), dtype="q4_0") == (3, 3, 23, 7, 1)
+    assert ab_shape(16, 8, 1024, 4416, tiles_per_split(4416, 32), dtype="q4_0") is None  # two rows per wave
+    assert len(SHAPES) > 100
+
+
+@pytest.mark.parametrize("heads,hidden,max_len,sh", SHAPES[:: max(1, len(SHAPES) // 400)])
+def test_indices_stay_in_bounds_and_cover_the_work_once(heads, hidden, max_len, sh):
+    G, T, splits, pp, NP = sh
+    NW = G * T
+    npair = (G + 2) * 32
+    rows = (heads + 16) * 64
+    TR = 64 if 8 % G == 0 else 72
+    assert T * TR * 64 >= hidden  # the normalised input fits the V tiles' LDS
+    ntiles = max_len // 64
+    for g in range(8):
+        seen = []
+        for s in range(splits):
+            assert s < MAX_SPLITS  # flag_qkv[s], flag_part[s], part[s]
+            for wid, a in itertools.product(range(NW), range(NP)):
+                li = wid + NW * a
+                l = s * pp + li
+                v = li < pp and l < npair
+                lc = l if v else 0
+                lh, jp = lc // 32, lc % 32
+                gh = g * G + lh if lh < G else heads + g if lh == G else heads + 8 + g
+                r0, r1 = gh * 64 + jp, gh * 64 + jp + 32
+                assert 0 <= r0 < rows and 0 <= r1 < rows  # rows are loaded even when unused
+                assert lh < G + 2 and jp < 32  # q[lh][jp + 32] for lh < G; K/V row pos of head g otherwise
+                if v:
+                    seen.append(l)
+                    # the right head: q of this group, then the group's K, then its V
+                    assert (lh < G and gh // G == g) or gh in (heads + g, heads + 8 + g)
+            for wid in range(NW):
+                t = s * T + wid // G
+                tc = min(t, ntiles - 1)
+                assert 0 <= tc < ntiles
+        assert sorted(seen) == list(range(npair)), "every pair of the group exactly once"
+    # per position: the patched tile, the used splits, the merge reads
+    for pos in sorted({0, 1, 63, 64, 65, max_len // 2, max_len - 65, max_len - 64, max_len - 2, max_len - 1}):
+        if not 0 <= pos < max_len:
+            continue
+        nb = (pos + 1 + 63) // 64
+        nsplit = (nb + T - 1) // T
+        assert 1 <= nsplit <= splits
+        patch = [s for s in range(splits) if 0 <= pos // 64 - s * T < T]
+        assert len(patch) == 1 and patch[0] < nsplit
+        tp = pos // 64 - patch[0] * T
+        assert (pos & 63) < min(64, pos + 1 - (patch[0] * T + tp) * 64)  # the patched row is a valid row
+        for hh in range(G):  # workgroup s = hh merges query head g*G + hh
+            assert hh < splits
+            for s2 in range(32):
+                off = min(s2, splits - 1) * PART_SPLIT + hh * PART_REC + 4 * (2 + 63)
+                assert off + 4 <= PART_BYTES
+            for lane in range(64):
+                sl = min(lane, splits - 1)
+                assert sl * PART_SPLIT + hh * PART_REC + 8 <= PART_BYTES
+        # every used split holds at least one valid tile; the unused ones write no partial
+        for s in range(splits):
+            used = min(T, nb - s * T)
+            assert (used > 0) == (s < nsplit)

@@ -1,0 +1,165 @@
+"""The attention block kernel (q/k/v + RoPE + KV append, split-KV attention and merge in one launch, exchanging
+through the L2 of each KV head's XCD) against the oracle's session and against the three-kernel path
+(MOERT_ATTN_BLOCK=0), bit for bit: logits, routes and weights of every step, hidden state and KV rows. Shapes: the
+3B model at the bench's 32 requested splits (23 splits of 3 tiles) across a tile and a split boundary, the 1B model
+from position 0 (one used split), a Q4_0 expert-cache model, and the launch counts of both paths."""
+import os
+
+import numpy as np
+import pytest
+
+import moert
+import oracle
+
+pytestmark = pytest.mark.gpu
+THREADS = min(16, os.cpu_count() or 1)
+MAX_LEN, SPLITS = 4416, 32  # the bench's cache: 23 splits of 3 tiles
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def bits_equal(a, b):
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def three_kernel_model(m, max_len, splits, **kw):
+    os.environ["MOERT_ATTN_BLOCK"] = "0"
+    try:
+        return moert.GpuModel(m, max_len, attn_splits=splits, **kw)
+    finally:
+        del os.environ["MOERT_ATTN_BLOCK"]
+
+
+def launches(g, kind):
+    """Launches of a kernel class in one step (run at the cache's last position, after the parity checks)."""
+    g.set_position(g.max_len - 1)
+    return g.time_kernel(kind, 1)[1]
+
+
+@pytest.fixture(scope="module")
+def granite_3b():
+    cfg = moert.Config(**moert.GRANITE_3B)
+    say("3B build")
+    m = moert.SynthModel(cfg, seed=3003, wdtype=moert.Q8_0, embed_dtype=moert.Q8_0)
+    return cfg, m, [moert.kv_prefill_data(cfg, 3003, l, 4096) for l in range(cfg.layers)]
+
+
+def test_attn_block_3b_forced_tokens_across_tile_and_split_boundaries(gpu, granite_3b):
+    """3B, KV pre-filled to 4096: forced tokens at positions 4088..4103 (the tile boundary at 4096, inside split 21)
+    and 4218..4229 (the split boundary at 4224): every step's logits, routes and weights equal the oracle's, then
+    the hidden state and every KV row written."""
+    cfg, m, kv = granite_3b
+    g = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
+    s = oracle.CpuSession(m, MAX_LEN, attn_splits=SPLITS, threads=THREADS)
+    for l, (k, v) in enumerate(kv):
+        g.kv_prefill(l, k, v)
+        s.kv_prefill(l, k, v)
+    rng = np.random.default_rng(41)
+    for start, n in ((4088, 16), (4218, 12)):
+        g.set_position(start)
+        s.set_position(start)
+        for t, tok in enumerate(rng.integers(0, cfg.vocab, n)):
+            say(f"3B attention block pos={start + t}")
+            lg, ids, w, am = g.step(int(tok))
+            olg, oids, ow, oh = s.step(int(tok))
+            assert np.array_equal(ids, oids) and bits_equal(w, ow), start + t
+            assert bits_equal(lg, olg) and am == oracle.argmax(olg), start + t
+        assert bits_equal(g.hidden(), oh)
+    for l in range(cfg.layers):
+        gk, gv = g.read_kv(l, 4230)
+        ok, ov = s.read_kv(l, 4230)
+        assert np.array_equal(gk, ok) and np.array_equal(gv, ov), l
+    assert launches(g, moert.K_ATTN_BLOCK) == cfg.layers
+    assert launches(g, moert.K_QKV) == 0 and launches(g, moert.K_ATTN_COMBINE) == 0
+    g.close()
+
+
+def test_attn_block_1b_from_position_zero_greedy_identical(gpu):
+    """1B shape (2 query heads per KV head) with the bench's cache shape: a 128-token prompt and 64 greedy tokens
+    from position 0 (only the first split is used, the new row moves through its three tiles): identical tokens,
+    last logits and hidden state, every KV row."""
+    cfg = moert.Config(**moert.GRANITE_1B)
+    say("1B build")
+    m = moert.SynthModel(cfg, seed=2024, wdtype=moert.Q8_0, embed_dtype=moert.F32, std=0.1)
+    g = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
+    s = oracle.CpuSession(m, MAX_LEN, attn_splits=SPLITS, threads=THREADS)
+    prompt = np.random.default_rng(2025).integers(0, cfg.vocab, 128)
+    say("1B attention block generate")
+    out = g.generate(prompt, 64)
+    want, _ = s.generate(prompt, 64)
+    assert out.tolist() == want.tolist()
+    assert bits_equal(g.read_logits(), s.last_logits)
+    assert bits_equal(g.hidden(), s.last_hidden)
+    for l in range(cfg.layers):
+        gk, gv = g.read_kv(l, 192)
+        ok, ov = s.read_kv(l, 192)
+        assert np.array_equal(gk, ok) and np.array_equal(gv, ov), l
+    assert launches(g, moert.K_ATTN_BLOCK) == cfg.layers
+    g.close()
+
+
+def test_attn_block_equals_the_three_kernel_path(gpu, granite_3b):
+    """The same 3B model with and without the attention block: 64 forced steps after 4096 cached positions, logits
+    and hidden state bit for bit; the three-kernel model launches q/k/v, split and combine and no block."""
+    cfg, m, kv = granite_3b
+    a = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
+    b = three_kernel_model(m, MAX_LEN, SPLITS)
+    for l, (k, v) in enumerate(kv):
+        a.kv_prefill(l, k, v)
+        b.kv_prefill(l, k, v)
+    a.set_position(4096)
+    b.set_position(4096)
+    for t, tok in enumerate(np.random.default_rng(43).integers(0, cfg.vocab, 64)):
+        if t % 16 == 0:
+            say(f"3B block vs three kernels step {t}")
+        la, ia, wa, ma = a.step(int(tok))
+        lb, ib, wb, mb = b.step(int(tok))
+        assert bits_equal(la, lb) and np.array_equal(ia, ib) and bits_equal(wa, wb) and ma == mb, t
+    assert bits_equal(a.hidden(), b.hidden())
+    assert launches(b, moert.K_ATTN_BLOCK) == 0 and launches(b, moert.K_QKV) == cfg.layers
+    a.close()
+    b.close()
+
+
+def test_attn_block_in_the_expert_cache_model(gpu):
+    """1B shape with its experts in a 192-slot pool (25% of 768) and the Zipf router bias: 48 forced steps with
+    the attention block equal the resident three-kernel model's logits bit for bit."""
+    cfg = moert.Config(**moert.GRANITE_1B)
+    say("1B cached build")
+    m = moert.SynthModel(cfg, seed=77, wdtype=moert.Q8_0, embed_dtype=moert.Q8_0, zipf_s=1.1)
+    res = three_kernel_model(m, MAX_LEN, SPLITS)
+    cac = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS, cache_slots=192)
+    for t, tok in enumerate(np.random.default_rng(45).integers(0, cfg.vocab, 48)):
+        lr, ir, wr, _ = res.step(int(tok))
+        lc, ic, wc, _ = cac.step(int(tok))
+        assert bits_equal(lr, lc) and np.array_equal(ir, ic) and bits_equal(wr, wc), t
+    assert launches(cac, moert.K_ATTN_BLOCK) == cfg.layers
+    res.close()
+    cac.close()
+
+
+def test_attn_block_q4_0_rows_equal_the_three_kernel_path(gpu):
+    """Q4_0 q/k/v rows of the 3B shape (the expert-cache workload's dtype), four layers: 40 forced steps after 4096
+    cached positions with and without the attention block, logits bit for bit."""
+    cfg = moert.Config(**{**moert.GRANITE_3B, "layers": 4})
+    say("3B-shaped Q4_0 build")
+    m = moert.SynthModel(cfg, seed=5, wdtype=moert.Q4_0, embed_dtype=moert.Q8_0, zipf_s=1.1)
+    a = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
+    b = three_kernel_model(m, MAX_LEN, SPLITS)
+    for l in range(cfg.layers):
+        k, v = moert.kv_prefill_data(cfg, 5, l, 4096)
+        a.kv_prefill(l, k, v)
+        b.kv_prefill(l, k, v)
+    a.set_position(4096)
+    b.set_position(4096)
+    for t, tok in enumerate(np.random.default_rng(47).integers(0, cfg.vocab, 40)):
+        la, ia, wa, _ = a.step(int(tok))
+        lb, ib, wb, _ = b.step(int(tok))
+        assert bits_equal(la, lb) and np.array_equal(ia, ib) and bits_equal(wa, wb), t
+    assert launches(a, moert.K_ATTN_BLOCK) == cfg.layers
+    a.close()
+    b.close()
