@@ -48,6 +48,9 @@ def kernel_bytes(kind, cfg, ctx, wd, ed, nsplit):
         moert.K_HEAD_ARGMAX: 0,
         # q/k/v weights and the KV it reads; its queries and split partials stay in the L2 of their XCD
         moert.K_ATTN_BLOCK: b(wd, (qd + 2 * kvd) * H) + 2 * kvd * 2 * ctx,
+        # the MoE-norm partials, the k routed experts' gate/up and down rows, the down outputs it leaves
+        moert.K_MOE_XCD: 65 * 256 * 4 + cfg.top_k * b(wd, 3 * I * H) + cfg.top_k * H * 4,
+        moert.K_MOE_COMBINE: 0,
     }[kind]
 
 
@@ -325,7 +328,7 @@ def main():
     dk = kernels[dom]
     log("kernels: " + ", ".join(f"{k} {v['us']:.2f}us x{v['launches_per_step']} {v['gbs'] or 0:.0f}GB/s"
                                 for k, v in kernels.items()))
-    moe = {k: kernels[k] for k in ("route_up", "expert_down")}
+    moe = {k: kernels[k] for k in ("route_up", "expert_down", "moe_xcd") if k in kernels}
     prefill = prefill_block(g, cfg, args.seed, CTX, tok_s, reps=args.prefill_reps) if args.prefill_reps > 0 else None
     g.close()
     copy_bytes = 1 << 30

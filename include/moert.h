@@ -242,7 +242,10 @@ typedef enum {
   MOERT_K_HEAD_ARGMAX = 8,  /* argmax over the head blocks, token and position update */
   MOERT_K_ATTN_BLOCK = 9,   /* q/k/v + RoPE + KV write, split-KV attention and merge in one launch (replaces
                                MOERT_K_QKV, MOERT_K_ATTN_SPLIT and MOERT_K_ATTN_COMBINE where its shape applies) */
-  MOERT_K_COUNT = 10
+  MOERT_K_MOE_XCD = 10,     /* rmsnorm + router + top-8 + gate/up + down with the routed experts spread over the 8
+                               XCDs (replaces MOERT_K_ROUTE_UP and MOERT_K_EXPERT_DOWN where it applies) */
+  MOERT_K_MOE_COMBINE = 11, /* weighted combine of the last layer's experts + residual, before the head */
+  MOERT_K_COUNT = 12
 } moert_kernel_kind;
 int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch, int* launches);
 

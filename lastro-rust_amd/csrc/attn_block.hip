@@ -45,7 +45,9 @@ __device__ __forceinline__ bool wait_flags(const unsigned* flags, int n, unsigne
 
 }  // namespace
 
-template <int DT, int K, int G, int T, int NP, int SP>
+// CMB: the input is h + res * (sum over j < 8, in order, of yw[j] * ys[j]) (the previous layer's experts left by
+// k_moe_xcd; k_expert_down's epilogue arithmetic), and workgroup 0 writes it to hc.
+template <int DT, int K, int G, int T, int NP, int SP, bool CMB>
 __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* __restrict__ h,
                                                           const float* __restrict__ lnw, float eps,
                                                           const int* __restrict__ st, const float* __restrict__ rope,
@@ -53,7 +55,9 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
                                                           uint16_t* __restrict__ vc, float scale, int splits, int pp,
                                                           AbGroup* __restrict__ xg_all,
                                                           const unsigned* __restrict__ step_ctr, unsigned layer,
-                                                          unsigned* __restrict__ err, float* __restrict__ att, Tl tl) {
+                                                          unsigned* __restrict__ err, float* __restrict__ att,
+                                                          const float* __restrict__ ys, const float* __restrict__ yw,
+                                                          float res, float* __restrict__ hc, Tl tl) {
   TL_START(tl);
   using Ge = Geo<DT, K>;
   static_assert(Ge::RPW == 1, "one q/k/v row per wave and pass");
@@ -101,7 +105,24 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
   const int pos = st[ST_POS];
   const unsigned epoch = *step_ctr * 64u + layer + 1u;
   NormIn<K, NT> hin;
-  norm_fetch<K, NT>(h, lnw, hin);
+  constexpr int PER = NormIn<K, NT>::PER;
+  float yv[CMB ? 8 : 1][PER], wj[8];
+  if (CMB) {
+    // this thread's elements of h, the norm weights and the 8 experts' down outputs (clamped, not guarded)
+#pragma unroll
+    for (int e = 0; e < PER; e++) {
+      const int i = threadIdx.x + e * NT, ic = i < K ? i : K - 1;
+      hin.hv[e] = h[ic];
+      hin.wv[e] = lnw[ic];
+#pragma unroll
+      for (int j = 0; j < 8; j++) yv[j][e] = ys[(size_t)j * K + ic];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) wj[j] = yw[j];
+    __builtin_amdgcn_sched_barrier(0);
+  } else {
+    norm_fetch<K, NT>(h, lnw, hin);
+  }
   const float* cs = rope + (size_t)pos * 64;
   float cv[NP], sv[NP];
 #pragma unroll
@@ -120,6 +141,17 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
   vsh.load(Vc, tc, lane, wh);
 
   // 1. q/k/v pairs of the group
+  if (CMB) {
+#pragma unroll
+    for (int e = 0; e < PER; e++) {
+      float y = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; j++) y = y + wj[j] * yv[j][e];
+      hin.hv[e] = hin.hv[e] + res * y;
+      const int i = threadIdx.x + e * NT;
+      if (blockIdx.x == 0 && i < K) hc[i] = hin.hv[e];
+    }
+  }
   norm_finish<K, NT>(hin, eps, xs, &rs);
   XReg<DT, K> xr;
   load_x<DT, K>(xr, xs, lane);
@@ -297,7 +329,9 @@ bool ab_shape(const Dims& d, const DMat& qkv, int cus, AbShape* out) {
       qkv.rows != (d.heads + 16) * 64)
     return false;
   const int G = d.heads / 8, T = d.tps;
-  if (G < 2 || G > 3 || T < 2 || T > 4 || d.max_len % 64) return false;  // the compiled shapes
+  // the compiled shapes: 2 query heads per KV head with rows of 1024, 3 with rows of 1536
+  if (!((G == 2 && qkv.cols == 1024) || (G == 3 && qkv.cols == 1536)) || T < 2 || T > 4 || d.max_len % 64)
+    return false;
   const int splits = attn_splits_for(d.max_len, T);
   // every workgroup of a group must be resident at once (they wait for each other): one workgroup per compute
   // unit (the LDS of a workgroup is above half of a compute unit's), at most cus / 8 splits
@@ -316,23 +350,29 @@ bool attn_block_fits(const Dims& d, const DMat& qkv, int cus) {
 }
 
 hipError_t launch_attn_block(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int cus, int layer,
-                             const AbBufs& x, Tl tl) {
+                             const AbBufs& x, bool combine, Tl tl) {
   AbShape sh;
-  if (!ab_shape(d, L.qkv, cus, &sh)) return hipErrorInvalidValue;
+  if (!ab_shape(d, L.qkv, cus, &sh) || (combine && (d.top_k != 8 || layer < 1))) return hipErrorInvalidValue;
   const int grid = 8 * sh.splits;
+  const float* yw = b.route_w + (size_t)(layer > 0 ? layer - 1 : 0) * d.top_k;
+#define AB_LAUNCH(DD, KK, GG, TT, NN, CC)                                                                          \
+  klaunch(k_attn_block<DD, KK, GG, TT, NN, 32, CC>, grid, GG * TT * 64, 0, s, L.qkv, b.h, L.ln_attn, d.eps,        \
+          b.state, b.rope, d.heads, d.max_len, L.k_cache, L.v_cache, d.attn_mult, sh.splits, sh.pp, x.groups,      \
+          x.step_ctr, (unsigned)layer, x.err, b.att, (const float*)x.ys, yw, d.res_mult, b.hc, tl)
 #define AB_CASE(DD, KK, GG, TT, NN)                                                                                \
   if (L.qkv.dtype == DD && L.qkv.cols == KK && sh.G == GG && sh.T == TT && sh.np == NN) {                         \
-    klaunch(k_attn_block<DD, KK, GG, TT, NN, 32>, grid, GG * TT * 64, 0, s, L.qkv, b.h, L.ln_attn, d.eps,         \
-            b.state, b.rope, d.heads, d.max_len, L.k_cache, L.v_cache, d.attn_mult, sh.splits, sh.pp, x.groups,    \
-            x.step_ctr, (unsigned)layer, x.err, b.att, tl);                                                        \
+    if (combine)                                                                                                   \
+      AB_LAUNCH(DD, KK, GG, TT, NN, true);                                                                         \
+    else                                                                                                           \
+      AB_LAUNCH(DD, KK, GG, TT, NN, false);                                                                        \
     return hipGetLastError();                                                                                      \
   }
 #define AB_T(DD, KK, GG) AB_CASE(DD, KK, GG, 2, 1) AB_CASE(DD, KK, GG, 2, 2) AB_CASE(DD, KK, GG, 3, 1) \
                          AB_CASE(DD, KK, GG, 3, 2) AB_CASE(DD, KK, GG, 4, 1) AB_CASE(DD, KK, GG, 4, 2)
-  AB_T(DT_Q8_0, 1536, 3) AB_T(DT_Q8_0, 1536, 2) AB_T(DT_Q8_0, 1024, 2) AB_T(DT_Q8_0, 1024, 3)
-  AB_T(DT_Q4_0, 1536, 3) AB_T(DT_Q4_0, 1536, 2)
+  AB_T(DT_Q8_0, 1536, 3) AB_T(DT_Q8_0, 1024, 2) AB_T(DT_Q4_0, 1536, 3)
 #undef AB_T
 #undef AB_CASE
+#undef AB_LAUNCH
   return hipErrorInvalidValue;
 }
 

@@ -205,6 +205,10 @@ struct moert_model {
   // attention block in one launch (attn_block.hip) when the shape allows it; otherwise q/k/v, split attention and
   // combine as three kernels. MOERT_ATTN_BLOCK=0 at create keeps the three kernels.
   bool use_ab = false;
+  // the MoE half spread over the XCDs (moe_block.hip; resident experts with the attention block): k_moe_xcd leaves
+  // the experts' down outputs for the next attention block (or k_moe_combine) to combine. MOERT_MOE_XCD=0 at create
+  // keeps k_route_up + k_expert_down.
+  bool use_mx = false;
   int cus = 0;
   AbBufs ab{};
   hipGraph_t graph = nullptr;
@@ -282,17 +286,20 @@ struct moert_model {
         CHECK_HIP(launch_prefetch_copy(pf_stream, cache));
         CHECK_HIP(hipEventRecord(ev_copy, pf_stream));
       }
+      const bool cmb = use_mx && li > 0;  // the previous layer's experts are combined by this attention block
       if (use_ab) {
-        CHECK_HIP(launch_attn_block(stream, L, dims, b, cus, li, ab, arm(MOERT_K_ATTN_BLOCK, li)));
+        CHECK_HIP(launch_attn_block(stream, L, dims, b, cus, li, ab, cmb, arm(MOERT_K_ATTN_BLOCK, li)));
       } else {
         CHECK_HIP(launch_qkv(stream, L, dims, b, arm(MOERT_K_QKV, li)));
         CHECK_HIP(launch_attn_split(stream, L, dims, b, arm(MOERT_K_ATTN_SPLIT, li)));
         CHECK_HIP(launch_attn_combine(stream, dims, b, arm(MOERT_K_ATTN_COMBINE, li)));
       }
       if (pf) CHECK_HIP(hipStreamWaitEvent(stream, ev_pred, 0));
-      CHECK_HIP(launch_oproj(stream, L, dims, b, arm(MOERT_K_OPROJ, li)));
+      CHECK_HIP(launch_oproj(stream, L, dims, b, arm(MOERT_K_OPROJ, li), cmb));
       if (pf) CHECK_HIP(hipStreamWaitEvent(stream, ev_copy, 0));
-      if (cached) {
+      if (use_mx) {
+        CHECK_HIP(launch_moe_xcd(stream, L, dims, b, cus, li, ab, arm(MOERT_K_MOE_XCD, li)));
+      } else if (cached) {
         CHECK_HIP(launch_route_up_cached(stream, L, dims, b, li, cache, arm(MOERT_K_ROUTE_UP, li)));
         CHECK_HIP(launch_expert_down_cached(stream, dims, b, li, cache, arm(MOERT_K_EXPERT_DOWN, li)));
       } else {
@@ -300,6 +307,8 @@ struct moert_model {
         CHECK_HIP(launch_expert_down(stream, L, dims, b, li, true, arm(MOERT_K_EXPERT_DOWN, li)));
       }
     }
+    if (use_mx)
+      CHECK_HIP(launch_moe_combine(stream, dims, b, (int)layers.size() - 1, ab, arm(MOERT_K_MOE_COMBINE, -1)));
     CHECK_HIP(launch_head(stream, embed, norm, dims, b, arm(MOERT_K_HEAD, -1)));
     CHECK_HIP(launch_head_argmax(stream, embed, dims, b, arm(MOERT_K_HEAD_ARGMAX, -1)));
     return MOERT_OK;
@@ -356,7 +365,7 @@ struct moert_model {
     for (int l = 0; l < L; l++) {
       const LayerDev& Ld = layers[l];
       if (use_ab) {
-        CHECK_HIP(launch_attn_block(stream, Ld, dims, b, cus, l, ab));
+        CHECK_HIP(launch_attn_block(stream, Ld, dims, b, cus, l, ab, false));
       } else {
         CHECK_HIP(launch_qkv(stream, Ld, dims, b));
         CHECK_HIP(launch_attn_split(stream, Ld, dims, b));
@@ -831,13 +840,17 @@ static int model_create(const moert_config* c, const moert_model_weights* w, int
     m->cus = prop.multiProcessorCount;
     const char* ev = getenv("MOERT_ATTN_BLOCK");
     const bool allow = !(ev && ev[0] == '0');
-    unsigned* grp = nullptr;
-    if ((rc = zeros(a, s, 8 * sizeof(AbGroup) / 4, &grp)) || (rc = zeros(a, s, (size_t)1, &m->ab.step_ctr)) ||
-        (rc = zeros(a, s, (size_t)1, &m->ab.err)))
+    unsigned *grp = nullptr, *mx = nullptr;
+    if ((rc = zeros(a, s, 8 * sizeof(AbGroup) / 4, &grp)) || (rc = zeros(a, s, 8 * sizeof(MxGroup) / 4, &mx)) ||
+        (rc = zeros(a, s, (size_t)8 * H, &m->ab.ys)) || (rc = zeros(a, s, (size_t)H, &b.hc)) ||
+        (rc = zeros(a, s, (size_t)1, &m->ab.step_ctr)) || (rc = zeros(a, s, (size_t)1, &m->ab.err)))
       return bail(rc);
     m->ab.groups = reinterpret_cast<AbGroup*>(grp);
+    m->ab.moe = reinterpret_cast<MxGroup*>(mx);
     m->use_ab = allow && c->layers <= 63 && std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 &&
                 attn_block_fits(m->dims, m->layers[0].qkv, m->cus);
+    const char* mv = getenv("MOERT_MOE_XCD");
+    m->use_mx = m->use_ab && cache_slots == 0 && !(mv && mv[0] == '0') && moe_xcd_fits(m->dims, m->layers[0], m->cus);
   }
   if (hipStreamSynchronize(s) != hipSuccess) {
     set_err("upload failed");

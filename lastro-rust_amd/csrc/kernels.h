@@ -33,6 +33,7 @@ struct Dims {
 // Scratch buffers of one decode step (device).
 struct StepBufs {
   float* h;          // [H] residual stream
+  float* hc;         // [H] residual stream with the previous layer's experts combined (attention block -> o-proj)
   float* q;          // [heads*d]
   float* att;        // [heads*d]
   float* part;       // [heads, splits, 2 + d] split-KV partials
@@ -58,10 +59,20 @@ struct AbGroup {
   float q[4][64];
   float part[kAbMaxSplits][4][68];
 };
+// Exchange area of the MoE kernel spread over the XCDs (moe_block.hip) for one XCD: a flag per workgroup (the
+// launch's epoch once its act values are stored) and the act vector of the XCD's expert.
+constexpr int kMxWgs = 32;  // workgroups per XCD
+struct MxGroup {
+  unsigned flag[kMxWgs];
+  float act[512];
+};
 struct AbBufs {
   AbGroup* groups;     // [8]
+  MxGroup* moe;        // [8]
+  float* ys;           // [8][hidden]: down output of the expert of each routing rank (k_moe_xcd)
   unsigned* step_ctr;  // decode steps started (k_embed adds one); a launch's epoch is step_ctr * 64 + layer + 1
-  unsigned* err;       // bits 1, 2: a wait for the workgroups of a KV head (their q/k/v rows, their partials) gave up
+  unsigned* err;       // bits 1, 2: a wait for the workgroups of a KV head (their q/k/v rows, their partials) gave up;
+                       // bit 3: a wait for the act values of an XCD's expert gave up
 };
 
 // tl: the launch's timeline record (measurement build; null otherwise). step_ctr (may be null): incremented once.
@@ -71,19 +82,32 @@ hipError_t launch_qkv(hipStream_t s, const LayerDev& L, const Dims& d, const Ste
 hipError_t launch_attn_split(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl = {});
 hipError_t launch_attn_combine(hipStream_t s, const Dims& d, const StepBufs& b, Tl tl = {});
 // The attention block (q/k/v + RoPE + KV append, split-KV attention, merge) in one launch, or false / an error when
-// its shape does not apply: 8 KV heads of dim 64, 2-3 query heads each, q/k/v rows of 1024 or 1536 (Q8_0) or 1536
-// (Q4_0), 2-4 tiles
+// its shape does not apply: 8 KV heads of dim 64 with 2 query heads each and q/k/v rows of 1024 (Q8_0) or 3 query
+// heads each and rows of 1536 (Q8_0 or Q4_0), 2-4 tiles
 // per split, at most min(32, cus / 8) splits (cus: compute units of the device), layer < 63.
 bool attn_block_fits(const Dims& d, const DMat& qkv, int cus);
+// combine: the previous layer's experts are in x.ys (k_moe_xcd); the block forms h + res * sum_j w_j ys[j] (weights
+// of layer - 1) as its input and workgroup 0 writes it to b.hc, the output projection's input.
 hipError_t launch_attn_block(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int cus, int layer,
-                             const AbBufs& x, Tl tl = {});
+                             const AbBufs& x, bool combine, Tl tl = {});
+// The MoE half with the 8 routed experts spread over the 8 XCDs (router + gate/up + down in one launch, the down
+// outputs left in x.ys for the next reader of h), or false / an error when it does not apply: top-8 routing, ffn
+// 512, hidden 1024 or 1536, Q8_0 or Q4_0 experts and router, 256 compute units.
+bool moe_xcd_fits(const Dims& d, const LayerDev& L, int cus);
+hipError_t launch_moe_xcd(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int cus, int layer,
+                          const AbBufs& x, Tl tl = {});
+// h += res * sum_j w_j ys[j] for the last layer (before the head).
+hipError_t launch_moe_combine(hipStream_t s, const Dims& d, const StepBufs& b, int layer, const AbBufs& x,
+                              Tl tl = {});
 // Both attention kernels for ny consecutive positions of a multi-position step: position y has its query at
 // q + y * heads * 64, attends to *lenp + len_add + y cached positions and writes att + y * heads * 64 (part holds
 // ny * heads * splits * 66 floats).
 hipError_t launch_attn_batched(hipStream_t s, const LayerDev& L, const Dims& d, const int* lenp, int len_add, int ny,
                                const float* q, float* part, float* att);
-// Output projection + residual; the epilogue writes the MoE-norm partials of the new h into b.zpart.
-hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl = {});
+// Output projection + residual; the epilogue writes the MoE-norm partials of the new h into b.zpart. from_hc: the
+// residual input is b.hc (the attention block's combined h) instead of b.h; the result goes to b.h either way.
+hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl = {},
+                        bool from_hc = false);
 // Router + gate/up of the routed experts (every workgroup ranks the experts, workgroup 0 publishes the routing).
 // partials: the rmsnorm of h and the router logits from the MoE-norm partials that launch_oproj wrote (decode
 // step); otherwise h is the normalised block input and the router's dots are computed in full.

@@ -702,8 +702,8 @@ __global__ __launch_bounds__(64) void k_attn_combine(const float* __restrict__ p
 // router has the output projection's dtype DT.
 template <int DT, int K, int P>
 __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restrict__ att, float res,
-                                                  float* __restrict__ h, DMat router, const float* __restrict__ lnw,
-                                                  float* __restrict__ zp, Tl tl) {
+                                                  const float* hin, float* __restrict__ h, DMat router,
+                                                  const float* __restrict__ lnw, float* __restrict__ zp, Tl tl) {
   TL_START(tl);
   using G = Geo<DT, K>;
   constexpr int RB = kWavesPerBlock * P * G::RPW;  // rows of the workgroup: [r0, r0 + RB)
@@ -725,7 +725,7 @@ __global__ __launch_bounds__(kBlock) void k_oproj(DMat m, const float* __restric
   copy_fetch<K, kBlock>(att, ain);
   float hold[P];
 #pragma unroll
-  for (int p = 0; p < P; p++) hold[p] = h[ok[p] ? row[p] : 0];  // clamped, not guarded: no branch in the load run
+  for (int p = 0; p < P; p++) hold[p] = hin[ok[p] ? row[p] : 0];  // clamped, not guarded: no branch in the load run
   Rows<DT, K, P> rr;
   rows_load<DT, K, P>(rr, m, row, ok, sub);
   copy_finish<K, kBlock>(ain, xs);
@@ -1468,12 +1468,13 @@ hipError_t launch_attn_unit(hipStream_t s, const float* q, const uint16_t* kc, c
   return attn_combine_dispatch(s, heads, tps, max_len, len_dev, 0, part, out);
 }
 
-hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl) {
+hipError_t launch_oproj(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl, bool from_hc) {
+  const float* hin = from_hc ? b.hc : b.h;
 #define BODY(KK)                                                                            \
   case KK: {                                                                                \
     constexpr int RB = rows_per_block<DTC, KK, kOprojP>();                                  \
-    klaunch(k_oproj<DTC, KK, kOprojP>, cdiv(L.o.rows, RB), kBlock, 0, s, L.o, b.att, d.res_mult, b.h, L.router, \
-            L.ln_moe, b.zpart, tl);                                                                 \
+    klaunch(k_oproj<DTC, KK, kOprojP>, cdiv(L.o.rows, RB), kBlock, 0, s, L.o, b.att, d.res_mult, hin, b.h,     \
+            L.router, L.ln_moe, b.zpart, tl);                                                       \
   } break;
   MOERT_DISPATCH(L.o.dtype, L.o.cols, BODY)
 #undef BODY

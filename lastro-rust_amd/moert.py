@@ -25,9 +25,9 @@ F32, Q8_0, Q4_0 = 0, 1, 2
 DTYPE_NAMES = {F32: "f32", Q8_0: "q8_0", Q4_0: "q4_0"}
 
 (K_EMBED, K_QKV, K_ATTN_SPLIT, K_ATTN_COMBINE, K_OPROJ, K_ROUTE_UP, K_EXPERT_DOWN, K_HEAD,
- K_HEAD_ARGMAX, K_ATTN_BLOCK) = range(10)
+ K_HEAD_ARGMAX, K_ATTN_BLOCK, K_MOE_XCD, K_MOE_COMBINE) = range(12)
 KERNEL_NAMES = ["embed", "qkv", "attn_split", "attn_combine", "oproj", "route_up", "expert_down", "head",
-                "head_argmax", "attn_block"]   # kernel classes of a decode step (the same for a cached model)
+                "head_argmax", "attn_block", "moe_xcd", "moe_combine"]   # kernel classes of a decode step (the same for a cached model)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmoert.so")

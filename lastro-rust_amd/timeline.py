@@ -39,6 +39,8 @@ PHASES = {
     "head": ["norm of h"],
     "head_argmax": [],
     "attn_block": ["q/k/v rows fma", "group barrier passed", "partials stored", "merge done"],
+    "moe_xcd": ["norm of h, router logits in LDS", "rank + ids", "gate/up rows fma", "act of the XCD's expert in"],
+    "moe_combine": [],
 }
 
 

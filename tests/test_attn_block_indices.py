@@ -27,7 +27,7 @@ def ab_shape(heads, kv_heads, hidden, max_len, tps, cus=256, dtype="q8_0"):
     if kv_heads != 8 or heads % 8 or not rows_ok:
         return None
     G, T = heads // 8, tps
-    if not (2 <= G <= 3 and 2 <= T <= 4) or max_len % 64:
+    if not ((G == 2 and hidden == 1024) or (G == 3 and hidden == 1536)) or not 2 <= T <= 4 or max_len % 64:
         return None
     splits = attn_splits_for(max_len, T)
     if splits < G or splits > MAX_SPLITS or splits > 32 or 8 * splits > cus:

@@ -26,12 +26,14 @@ def bits_equal(a, b):
     return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-def three_kernel_model(m, max_len, splits, **kw):
-    os.environ["MOERT_ATTN_BLOCK"] = "0"
+def three_kernel_model(m, max_len, splits, var="MOERT_ATTN_BLOCK", **kw):
+    """A model created with `var`=0 (MOERT_ATTN_BLOCK: q/k/v, split attention and combine as three kernels, and the
+    MoE half as k_route_up + k_expert_down; MOERT_MOE_XCD: only the MoE half as those two kernels)."""
+    os.environ[var] = "0"
     try:
         return moert.GpuModel(m, max_len, attn_splits=splits, **kw)
     finally:
-        del os.environ["MOERT_ATTN_BLOCK"]
+        del os.environ[var]
 
 
 def launches(g, kind):
@@ -73,7 +75,8 @@ def test_attn_block_3b_forced_tokens_across_tile_and_split_boundaries(gpu, grani
         gk, gv = g.read_kv(l, 4230)
         ok, ov = s.read_kv(l, 4230)
         assert np.array_equal(gk, ok) and np.array_equal(gv, ov), l
-    assert launches(g, moert.K_ATTN_BLOCK) == cfg.layers
+    assert launches(g, moert.K_ATTN_BLOCK) == cfg.layers and launches(g, moert.K_MOE_XCD) == cfg.layers
+    assert launches(g, moert.K_MOE_COMBINE) == 1 and launches(g, moert.K_ROUTE_UP) == 0
     assert launches(g, moert.K_QKV) == 0 and launches(g, moert.K_ATTN_COMBINE) == 0
     g.close()
 
@@ -161,5 +164,31 @@ def test_attn_block_q4_0_rows_equal_the_three_kernel_path(gpu):
         lb, ib, wb, _ = b.step(int(tok))
         assert bits_equal(la, lb) and np.array_equal(ia, ib) and bits_equal(wa, wb), t
     assert launches(a, moert.K_ATTN_BLOCK) == cfg.layers
+    a.close()
+    b.close()
+
+
+def test_moe_spread_over_the_xcds_equals_route_up_and_down(gpu, granite_3b):
+    """The MoE half with the routed experts spread over the XCDs (k_moe_xcd, combined by the next attention block)
+    against k_route_up + k_expert_down, both with the attention block: 48 forced steps after 4096 cached positions,
+    logits, routes, weights and hidden state bit for bit; the launch counts of both."""
+    cfg, m, kv = granite_3b
+    a = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
+    b = three_kernel_model(m, MAX_LEN, SPLITS, var="MOERT_MOE_XCD")
+    for l, (k, v) in enumerate(kv):
+        a.kv_prefill(l, k, v)
+        b.kv_prefill(l, k, v)
+    a.set_position(4096)
+    b.set_position(4096)
+    for t, tok in enumerate(np.random.default_rng(49).integers(0, cfg.vocab, 48)):
+        if t % 16 == 0:
+            say(f"3B experts over the XCDs vs route_up + down step {t}")
+        la, ia, wa, ma = a.step(int(tok))
+        lb, ib, wb, mb = b.step(int(tok))
+        assert bits_equal(la, lb) and np.array_equal(ia, ib) and bits_equal(wa, wb) and ma == mb, t
+    assert bits_equal(a.hidden(), b.hidden())
+    assert launches(b, moert.K_MOE_XCD) == 0 and launches(b, moert.K_ROUTE_UP) == cfg.layers
+    assert launches(b, moert.K_ATTN_BLOCK) == cfg.layers
+    assert launches(a, moert.K_MOE_XCD) == cfg.layers and launches(a, moert.K_EXPERT_DOWN) == 0
     a.close()
     b.close()
