@@ -8,16 +8,18 @@
 // previous launch left off: workgroup b runs on XCD (c + b) % 8 for some c. So the workgroups 8s + r (s = 0, 1, ...)
 // of one residue r share an XCD, and workgroup b serves KV head g = its XCD (hardware register XCC_ID) and split
 // s = b / 8: all workgroups of KV head g run on XCD g and share its L2. They exchange their data through that L2
-// (attn_dev.h) and meet at per-split flags, which costs far less than a kernel boundary:
+// (attn_dev.h) as 8-byte entries that carry the launch's epoch beside the value, so a consumer polls exactly the
+// entries it needs, and a producer stores and goes on; this costs far less than a kernel boundary:
 //   1. the group's q/k/v row pairs ((G + 2) * 32 of them: G query heads, one K and one V head) are dealt out over
-//      its splits; each workgroup normalises h, computes its pairs with RoPE, writes q into the group's L2 area and
-//      K, V into row `pos` of the cache, and sets its flag;
-//   2. meanwhile its split's K and V tiles have been loaded and staged in LDS; once every flag of the group is set
-//      it reads its queries and (when the split holds position pos) the new K/V row, and computes the split's
-//      partials (m, l, acc) per query head as k_attn_tiles does, into the group's L2 area, and sets a second flag;
-//   3. workgroup s < G then merges query head g*G + s over the used splits as k_attn_combine does, into `att`.
-// Every wait is bounded: a flag that does not arrive in time (which is what a dispatch that is not round-robin, or
-// a group that is not all resident at once, would cause) sets a bit of `err` and the kernel still ends; the host
+//      its splits; each workgroup normalises h, computes its pairs with RoPE, and writes q and the new K/V row into
+//      the group's L2 area (and K, V into row `pos` of the cache);
+//   2. meanwhile its split's K and V tiles have been loaded and staged in LDS; it polls its queries and (when the
+//      split holds position pos) the new K/V row until they carry the epoch, and computes the split's partials
+//      (m, l, acc) per query head as k_attn_tiles does, into the group's L2 area;
+//   3. workgroup s < G then polls the partials of query head g*G + s over the used splits and merges them as
+//      k_attn_combine does, into `att`.
+// Every wait is bounded: an entry that does not arrive in time (which is what a dispatch that is not round-robin,
+// or a group that is not all resident at once, would cause) sets a bit of `err` and the kernel still ends; the host
 // turns a set bit into an error.
 #include "attn_dev.h"
 #include "dev_rows.h"
@@ -29,18 +31,22 @@ namespace moert {
 
 namespace {
 
-constexpr int kAbSpin = 1 << 18;  // polls of a flag set before a wait gives up (each poll is an L2 round trip)
+constexpr int kAbSpin = 1 << 18;  // polls before a wait gives up (each poll is an L2 round trip)
 
-// Wave-level wait until flags[i] == epoch for every i < n (n <= 64), read from the XCD's L2. Returns false when the
-// wait gave up.
-__device__ __forceinline__ bool wait_flags(const unsigned* flags, int n, unsigned epoch, int lane) {
-  const __amdgpu_buffer_rsrc_t r = l2_buffer(flags, kAbMaxSplits * 4);
+// Wave-level wait until the entry at byte offset off0 of r (and with TWO the one at off1) carries `epoch`, read from
+// the XCD's L2; returns the values. Clears *ok when the wait gave up.
+template <bool TWO>
+__device__ __forceinline__ uint2 poll_entries(__amdgpu_buffer_rsrc_t r, unsigned off0, unsigned off1, unsigned epoch,
+                                              bool* ok) {
   for (int it = 0; it < kAbSpin; it++) {
-    const unsigned f = lane < n ? l2_load_u32(r, 4u * lane) : epoch;
-    if (__ballot(f != epoch) == 0) return true;
+    poll_fence();
+    const uint2 a = l2_load_u64(r, off0);
+    const uint2 b = TWO ? l2_load_u64(r, off1) : make_uint2(0u, epoch);
+    if (__ballot(a.y != epoch || b.y != epoch) == 0) return make_uint2(a.x, b.x);
     __builtin_amdgcn_s_sleep(1);
   }
-  return false;
+  *ok = false;
+  return make_uint2(0u, 0u);
 }
 
 }  // namespace
@@ -105,17 +111,18 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
   const int pos = st[ST_POS];
   const unsigned epoch = *step_ctr * 64u + layer + 1u;
   NormIn<K, NT> hin;
-  constexpr int PER = NormIn<K, NT>::PER;
-  float yv[CMB ? 8 : 1][PER], wj[8];
+  constexpr int PER = NormIn<K, NT>::PER, NQ = NormIn<K, NT>::Q;
+  float4 yv[CMB ? 8 : 1][PER];
+  float wj[8];
   if (CMB) {
-    // this thread's elements of h, the norm weights and the 8 experts' down outputs (clamped, not guarded)
+    // this thread's quads of h, the norm weights and the 8 experts' down outputs (clamped, not guarded)
 #pragma unroll
     for (int e = 0; e < PER; e++) {
-      const int i = threadIdx.x + e * NT, ic = i < K ? i : K - 1;
-      hin.hv[e] = h[ic];
-      hin.wv[e] = lnw[ic];
+      const int q = threadIdx.x + e * NT, qc = q < NQ ? q : NQ - 1;
+      hin.hv[e] = reinterpret_cast<const float4*>(h)[qc];
+      hin.wv[e] = reinterpret_cast<const float4*>(lnw)[qc];
 #pragma unroll
-      for (int j = 0; j < 8; j++) yv[j][e] = ys[(size_t)j * K + ic];
+      for (int j = 0; j < 8; j++) yv[j][e] = reinterpret_cast<const float4*>(ys)[(size_t)j * NQ + qc];
     }
 #pragma unroll
     for (int j = 0; j < 8; j++) wj[j] = yw[j];
@@ -135,7 +142,7 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
   rows_load<DT, K, P>(rr, m, row, ok, lane);
   __builtin_amdgcn_sched_barrier(0);
   const int t0 = s * T, t = t0 + wt;
-  const int tc = min(t, max_len / 64 - 1);  // a tile past the cache's end (never used) reads the last tile
+  const int tc = min(t, pos / 64);  // a tile past the length (never used: staged as zeros) reads the last tile in use
   VShare<G> ksh, vsh;
   ksh.load(Kc, tc, lane, wh);
   vsh.load(Vc, tc, lane, wh);
@@ -144,12 +151,18 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
   if (CMB) {
 #pragma unroll
     for (int e = 0; e < PER; e++) {
-      float y = 0.0f;
+      float4 y = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-      for (int j = 0; j < 8; j++) y = y + wj[j] * yv[j][e];
-      hin.hv[e] = hin.hv[e] + res * y;
-      const int i = threadIdx.x + e * NT;
-      if (blockIdx.x == 0 && i < K) hc[i] = hin.hv[e];
+      for (int j = 0; j < 8; j++) {
+        y.x = y.x + wj[j] * yv[j][e].x;
+        y.y = y.y + wj[j] * yv[j][e].y;
+        y.z = y.z + wj[j] * yv[j][e].z;
+        y.w = y.w + wj[j] * yv[j][e].w;
+      }
+      float4& hv = hin.hv[e];
+      hv = make_float4(hv.x + res * y.x, hv.y + res * y.y, hv.z + res * y.z, hv.w + res * y.w);
+      const int q = threadIdx.x + e * NT;
+      if (blockIdx.x == 0 && q < NQ) reinterpret_cast<float4*>(hc)[q] = hv;
     }
   }
   norm_finish<K, NT>(hin, eps, xs, &rs);
@@ -163,15 +176,18 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
     for (int a = 0; a < NP; a++) {
       if (!ok[2 * a]) continue;
       const float x1 = out[2 * a], x2 = out[2 * a + 1], c = cv[a], sn = sv[a];
+      const int j = jp[a];
       if (lh[a] < G) {
-        xg->q[lh[a]][jp[a]] = x1 * c - x2 * sn;
-        xg->q[lh[a]][jp[a] + 32] = x2 * c + x1 * sn;
-      } else if (lh[a] == G) {
-        Kc[(size_t)pos * 64 + jp[a]] = f2h(x1 * c - x2 * sn);
-        Kc[(size_t)pos * 64 + jp[a] + 32] = f2h(x2 * c + x1 * sn);
+        put_entry(&xg->q[lh[a]][j], __float_as_uint(x1 * c - x2 * sn), epoch);
+        put_entry(&xg->q[lh[a]][j + 32], __float_as_uint(x2 * c + x1 * sn), epoch);
       } else {
-        Vc[(size_t)pos * 64 + jp[a]] = f2h(x1);
-        Vc[(size_t)pos * 64 + jp[a] + 32] = f2h(x2);
+        const bool isk = lh[a] == G;
+        const uint16_t e1 = f2h(isk ? x1 * c - x2 * sn : x1), e2 = f2h(isk ? x2 * c + x1 * sn : x2);
+        put_entry(&xg->kv[isk ? 0 : 1][j], e1, epoch);
+        put_entry(&xg->kv[isk ? 0 : 1][j + 32], e2, epoch);
+        uint16_t* row = (isk ? Kc : Vc) + (size_t)pos * 64;
+        row[j] = e1;
+        row[j + 32] = e2;
       }
     }
   }
@@ -184,27 +200,29 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
   const int nv = active ? min(64, len - t * 64) : 0;
   ksh.template store<KS>(&Ks[wt][0][0], lane, wh, nv);
   vsh.template store<64>(&Vs[wt][0][0], lane, wh, nv);
-  wait_mem();  // this wave's q/k/v stores have reached the L2
-  __syncthreads();
-  if (threadIdx.x == 0) xg->flag_qkv[s] = epoch;
-  if (wid == 0 && !wait_flags(xg->flag_qkv, splits, epoch, lane) && lane == 0) atomicOr(err, 2u);
-  __syncthreads();
   TL_PHASE(tl, 3);
+  __syncthreads();  // the staged tiles, before the new row goes over row pos
 
   // 2. the split's partials: queries of the group from the L2, the new K/V row (written by this group in phase 1)
   // over the stale row `pos` of the staged tiles
   {
-    const __amdgpu_buffer_rsrc_t rq = l2_buffer(&xg->q[0][0], sizeof(xg->q));
-    Qs[wh][lane] = l2_load_f32(rq, 4u * (wh * 64 + lane));  // every wave of head wh stores the same q
+    bool okw = true;
+    if (wt == 0) {  // the queries of head wh
+      const __amdgpu_buffer_rsrc_t rq = l2_buffer(&xg->q[0][0], sizeof(xg->q));
+      const uint2 qv = poll_entries<false>(rq, 8u * (wh * 64 + lane), 0u, epoch, &okw);
+      Qs[wh][lane] = __uint_as_float(qv.x);
+    }
     const int tp = pos / 64 - t0;
     if (tp >= 0 && tp < T && wid == tp * G) {
-      const __amdgpu_buffer_rsrc_t rk = l2_buffer(Kc + (size_t)pos * 64, 128);
-      const __amdgpu_buffer_rsrc_t rv = l2_buffer(Vc + (size_t)pos * 64, 128);
-      Ks[tp][pos & 63][lane] = h2f(l2_load_u16(rk, 2u * lane));
-      Vs[tp][pos & 63][lane] = h2f(l2_load_u16(rv, 2u * lane));
+      const __amdgpu_buffer_rsrc_t rk = l2_buffer(&xg->kv[0][0], sizeof(xg->kv));
+      const uint2 kv = poll_entries<true>(rk, 8u * lane, 8u * (64 + lane), epoch, &okw);
+      Ks[tp][pos & 63][lane] = h2f((uint16_t)kv.x);
+      Vs[tp][pos & 63][lane] = h2f((uint16_t)kv.y);
     }
+    if (!okw && lane == 0) atomicOr(err, 2u);
   }
   __syncthreads();  // Qs, the new row
+  TL_PHASE(tl, 4);
   // scores: lane = position, chain over the 64 dims in order (an inactive tile's scores are discarded)
   float sc;
   {
@@ -261,17 +279,14 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
       acc = __builtin_fmaf(acc, a, u == 0 ? pv : Pv[wh][u][lane]);
       mm = mm > Tm[wh][u] ? mm : Tm[wh][u];
     }
-    float* pp_ = xg->part[s][wh];
+    uint2* pe = xg->part[s][wh];
+    put_entry(pe + 2 + lane, __float_as_uint(acc), epoch);
     if (lane == 0) {
-      pp_[0] = mm;
-      pp_[1] = l;
+      put_entry(pe, __float_as_uint(mm), epoch);
+      put_entry(pe + 1, __float_as_uint(l), epoch);
     }
-    pp_[2 + lane] = acc;
   }
-  TL_PHASE(tl, 4);
-  wait_mem();  // the partials have reached the L2
-  __syncthreads();
-  if (threadIdx.x == 0) xg->flag_part[s] = epoch;
+  TL_PHASE(tl, 5);
   if (s >= G || wid != 0) {
     TL_END(tl);
     return;
@@ -281,16 +296,30 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
   // over the used splits in order; out = num / den (k_attn_combine)
   const int hh = s;
   const int nsplit = (nb + T - 1) / T;  // used splits
-  if (!wait_flags(xg->flag_part, nsplit, epoch, lane) && lane == 0) atomicOr(err, 4u);
   const __amdgpu_buffer_rsrc_t rp = l2_buffer(&xg->part[0][0][0], sizeof(xg->part));
   constexpr unsigned REC = sizeof(xg->part[0][0]), SREC = sizeof(xg->part[0]);
-  float av[SP];
-#pragma unroll
-  for (int s2 = 0; s2 < SP; s2++)
-    av[s2] = l2_load_f32(rp, (unsigned)min(s2, splits - 1) * SREC + hh * REC + 4u * (2 + lane));
+  // lane d reads acc[d] of every split (s2 >= nsplit: a clamped, unused entry) and lane s2 reads (m, l) of split s2;
+  // all of them again until every entry of a used split carries the epoch
+  float av[SP], ms = 0.0f, ls = 0.0f;
   const unsigned sl = (unsigned)min(lane, splits - 1);
-  float ms = l2_load_f32(rp, sl * SREC + hh * REC);
-  float ls = l2_load_f32(rp, sl * SREC + hh * REC + 4u);
+  bool done = false;
+  for (int it = 0; it < kAbSpin && !done; it++) {
+    bool stale = false;
+    poll_fence();
+#pragma unroll
+    for (int s2 = 0; s2 < SP; s2++) {
+      const uint2 e = l2_load_u64(rp, (unsigned)min(s2, splits - 1) * SREC + hh * REC + 8u * (2 + lane));
+      av[s2] = __uint_as_float(e.x);
+      stale |= s2 < nsplit && e.y != epoch;
+    }
+    const uint2 em = l2_load_u64(rp, sl * SREC + hh * REC), el = l2_load_u64(rp, sl * SREC + hh * REC + 8u);
+    ms = __uint_as_float(em.x);
+    ls = __uint_as_float(el.x);
+    stale |= lane < nsplit && (em.y != epoch || el.y != epoch);
+    done = __ballot(stale) == 0;
+    if (!done) __builtin_amdgcn_s_sleep(1);
+  }
+  if (!done && lane == 0) atomicOr(err, 4u);
   if (lane >= nsplit) {
     ms = NEG_INF;
     ls = 0.0f;
@@ -309,7 +338,7 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
     }
   }
   att[(g * G + hh) * 64 + lane] = num / den;
-  TL_PHASE(tl, 5);
+  TL_PHASE(tl, 6);
   TL_END(tl);
 }
 

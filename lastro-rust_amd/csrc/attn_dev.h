@@ -69,6 +69,10 @@ __device__ __forceinline__ unsigned xcc_id() {
 // counted by vmcnt).
 __device__ __forceinline__ void wait_mem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// A compiler-only fence for polling loops: the compiler takes a buffer load inside a loop that stores nothing as a
+// read of unchanging memory and hoists it out of the loop; placed in the loop, this keeps a fresh load per pass.
+__device__ __forceinline__ void poll_fence() { asm volatile("" ::: "memory"); }
+
 // A raw buffer over `bytes` bytes at p; loads through it take an explicit cache policy, and a load past the end
 // returns 0.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t l2_buffer(const void* p, unsigned bytes) {
@@ -85,6 +89,17 @@ __device__ __forceinline__ float l2_load_f32(__amdgpu_buffer_rsrc_t r, unsigned 
 }
 __device__ __forceinline__ unsigned short l2_load_u16(__amdgpu_buffer_rsrc_t r, unsigned off) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, kL2Policy);
+}
+__device__ __forceinline__ uint2 l2_load_u64(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kL2Policy);
+  return make_uint2(v[0], v[1]);
+}
+
+// An exchange entry: a value's 32 bits and the epoch of the launch that wrote it, stored as one 8-byte word (a
+// relaxed atomic store, so it is one store instruction and a reader never sees half of it).
+__device__ __forceinline__ void put_entry(uint2* p, unsigned val, unsigned epoch) {
+  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), ((unsigned long long)epoch << 32) | val,
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 }  // namespace moert

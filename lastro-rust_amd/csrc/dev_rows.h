@@ -187,29 +187,33 @@ __device__ __forceinline__ void rows_fma(const Rows<DT, K, P>& r, const bool (&o
 // branch join forces an early wait.
 template <int K, int NT>
 struct NormIn {
-  static constexpr int PER = (K + NT - 1) / NT;
-  float hv[PER], wv[PER];
+  static_assert(K % 4 == 0, "the activation is fetched in 16-byte quads");
+  static constexpr int Q = K / 4;                 // quads of the vector
+  static constexpr int PER = (Q + NT - 1) / NT;   // quads per thread: quad threadIdx.x + e * NT
+  float4 hv[PER], wv[PER];
 };
 
 template <int K, int NT>
 __device__ __forceinline__ void norm_fetch(const float* __restrict__ x, const float* __restrict__ lnw,
                                            NormIn<K, NT>& in) {
+  constexpr int Q = NormIn<K, NT>::Q;
 #pragma unroll
   for (int e = 0; e < NormIn<K, NT>::PER; e++) {
-    const int i = threadIdx.x + e * NT;
-    in.hv[e] = x[i < K ? i : K - 1];
-    in.wv[e] = lnw[i < K ? i : K - 1];
+    const int q = threadIdx.x + e * NT, qc = q < Q ? q : Q - 1;
+    in.hv[e] = reinterpret_cast<const float4*>(x)[qc];
+    in.wv[e] = reinterpret_cast<const float4*>(lnw)[qc];
   }
   __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the kernel's weight loads
 }
 
 template <int K, int NT>
 __device__ __forceinline__ void norm_finish(const NormIn<K, NT>& in, float eps, float* xs, float* rs) {
-  constexpr int NCH = K / 16;
+  constexpr int NCH = K / 16, Q = NormIn<K, NT>::Q;
+  float4* xq = reinterpret_cast<float4*>(xs);
 #pragma unroll
   for (int e = 0; e < NormIn<K, NT>::PER; e++) {
-    const int i = threadIdx.x + e * NT;
-    if (i < K) xs[i] = in.hv[e];
+    const int q = threadIdx.x + e * NT;
+    if (q < Q) xq[q] = in.hv[e];
   }
   __syncthreads();
   if (threadIdx.x < 64) {
@@ -236,8 +240,9 @@ __device__ __forceinline__ void norm_finish(const NormIn<K, NT>& in, float eps, 
   const float r = *rs;
 #pragma unroll
   for (int e = 0; e < NormIn<K, NT>::PER; e++) {
-    const int i = threadIdx.x + e * NT;
-    if (i < K) xs[i] = in.wv[e] * (in.hv[e] * r);
+    const int q = threadIdx.x + e * NT;
+    const float4 h = in.hv[e], w = in.wv[e];
+    if (q < Q) xq[q] = make_float4(w.x * (h.x * r), w.y * (h.y * r), w.z * (h.z * r), w.w * (h.w * r));
   }
   __syncthreads();
 }

@@ -50,14 +50,14 @@ struct StepBufs {
 };
 
 // Exchange area of the attention block kernel (attn_block.hip) for one KV head, used only by the workgroups that
-// run on the XCD of that head: per-split flags (the launch's epoch once the split's q/k/v rows, then its partials,
-// are stored), the head group's queries after RoPE, and the partials (m, l, acc[64]) of every split and query head.
+// run on the XCD of that head. Every entry is an 8-byte word (value bits, epoch of the launch that wrote it), written
+// and read whole, so a reader knows a value is the current launch's by its epoch alone: the head group's queries
+// after RoPE, the new K and V rows (fp16 bits), and the partials (m, l, acc[64]) of every split and query head.
 constexpr int kAbMaxSplits = 64;
 struct AbGroup {
-  unsigned flag_qkv[kAbMaxSplits];
-  unsigned flag_part[kAbMaxSplits];
-  float q[4][64];
-  float part[kAbMaxSplits][4][68];
+  uint2 q[4][64];
+  uint2 kv[2][64];
+  uint2 part[kAbMaxSplits][4][66];
 };
 // Exchange area of the MoE kernel spread over the XCDs (moe_block.hip) for one XCD: a flag per workgroup (the
 // launch's epoch once its act values are stored) and the act vector of the XCD's expert.
@@ -71,7 +71,7 @@ struct AbBufs {
   MxGroup* moe;        // [8]
   float* ys;           // [8][hidden]: down output of the expert of each routing rank (k_moe_xcd)
   unsigned* step_ctr;  // decode steps started (k_embed adds one); a launch's epoch is step_ctr * 64 + layer + 1
-  unsigned* err;       // bits 1, 2: a wait for the workgroups of a KV head (their q/k/v rows, their partials) gave up;
+  unsigned* err;       // bits 1, 2: a wait for values of a KV head's workgroups (queries and K/V row, partials) gave up;
                        // bit 3: a wait for the act values of an XCD's expert gave up
 };
 

@@ -33,6 +33,7 @@ constexpr int kMxUpWaves = 8;  // waves 0..7: gate/up pairs; waves 8..15: down r
 __device__ __forceinline__ bool mx_wait(const unsigned* flags, int n, unsigned epoch, int lane) {
   const __amdgpu_buffer_rsrc_t r = l2_buffer(flags, kMxWgs * 4);
   for (int it = 0; it < kMxSpin; it++) {
+    poll_fence();
     const unsigned f = lane < n ? l2_load_u32(r, 4u * lane) : epoch;
     if (__ballot(f != epoch) == 0) return true;
     __builtin_amdgcn_s_sleep(1);

@@ -11,6 +11,7 @@ stamping the 100 MHz real-time clock at its phase boundaries, and prints a markd
   wave skew   first to last wave start inside a workgroup
   life        a workgroup's first wave start to its last wave end
   phases      time from a workgroup's first wave start to the end of each phase, as its wave 0 sees it
+  latest      time from a launch's first workgroup start to the end of each phase in its latest workgroup
 
 All figures are medians over the workgroups (or launches) of --steps steps after --warmup untimed ones.
 Usage: python lastro-rust_amd/timeline.py [--steps 8] [--out FILE]
@@ -38,7 +39,7 @@ PHASES = {
     "expert_down": ["activations staged", "down rows fma"],
     "head": ["norm of h"],
     "head_argmax": [],
-    "attn_block": ["q/k/v rows fma", "group barrier passed", "partials stored", "merge done"],
+    "attn_block": ["q/k/v rows fma", "tiles staged", "queries in", "partials stored", "merge done"],
     "moe_xcd": ["norm of h, router logits in LDS", "rank + ids", "gate/up rows fma", "act of the XCD's expert in"],
     "moe_combine": [],
 }
@@ -60,7 +61,7 @@ def summarize(records, kinds):
             ends.append(end.max())
             name = moert.KERNEL_NAMES[kd[i]]
             d = rows.setdefault(name, {"span": [], "gap": [], "ramp": [], "skew": [], "life": [], "blocks": [],
-                                       "phases": [[] for _ in range(5)]})
+                                       "phases": [[] for _ in range(5)], "last": [[] for _ in range(5)]})
             d["span"].append(end.max() - first.min())
             d["ramp"].append(first.max() - first.min())
             d["skew"].extend((last_start - first).tolist())
@@ -71,6 +72,7 @@ def summarize(records, kinds):
                 ok = col != 0
                 if ok.any():
                     d["phases"][ph].extend((col[ok] - first[ok]).tolist())
+                    d["last"][ph].append(int(col[ok].max() - first.min()))
             if i > 0:
                 d["gap"].append(starts[-1] - ends[-2])
         totals.append(ends[-1] - starts[0])
@@ -86,8 +88,8 @@ def render(rows, totals, steps, launches):
     out.append(f"Step (first workgroup start to last workgroup end): median {med(totals):.1f} us over {steps} steps; "
                f"{launches} launches per step.\n")
     out.append("| kernel | launches/step | workgroups | span us | gap before us | start ramp us | wave skew us | "
-               "life us | phase ends (us from workgroup start) |")
-    out.append("|---|---|---|---|---|---|---|---|---|")
+               "life us | phase ends (us from workgroup start) | latest phase ends (us from launch start) |")
+    out.append("|---|---|---|---|---|---|---|---|---|---|")
     order = [k for k in moert.KERNEL_NAMES if k in rows]
     per_step = {}
     for name in order:
@@ -96,8 +98,9 @@ def render(rows, totals, steps, launches):
         per_step[name] = n
         ph = "; ".join(f"{lab} {med(d['phases'][i]):.2f}" for i, lab in enumerate(PHASES.get(name, []))
                        if d["phases"][i])
+        last = "; ".join(f"{med(d['last'][i]):.2f}" for i, _ in enumerate(PHASES.get(name, [])) if d["last"][i])
         out.append(f"| {name} | {n} | {int(np.median(d['blocks']))} | {med(d['span']):.2f} | {med(d['gap']):.2f} | "
-                   f"{med(d['ramp']):.2f} | {med(d['skew']):.2f} | {med(d['life']):.2f} | {ph} |")
+                   f"{med(d['ramp']):.2f} | {med(d['skew']):.2f} | {med(d['life']):.2f} | {ph} | {last} |")
     span_sum = sum(med(rows[k]["span"]) * per_step[k] for k in order)
     gap_sum = sum(med(rows[k]["gap"]) * per_step[k] for k in order if rows[k]["gap"])
     out.append("")

@@ -2,13 +2,17 @@
 every launch shape the eligibility rule admits, the q/k/v row pairs of each KV head group are computed exactly
 once and every row index stays inside the [q; k; v] matrix, every tile read stays inside the cache, exactly one
 workgroup of the group takes the new K/V row for every position, each query head is merged by exactly one
-workgroup, and every flag and partial offset stays inside the group's exchange area."""
+workgroup, and every query, K/V row and partial entry offset stays inside the group's exchange area (8-byte
+entries: value bits and epoch)."""
 import itertools
 
 import pytest
 
 MAX_SPLITS = 64          # kAbMaxSplits
-PART_REC = 68 * 4        # bytes of one (split, head) partial record
+ENTRY = 8                # bytes of an exchange entry
+Q_BYTES = 4 * 64 * ENTRY
+KV_BYTES = 2 * 64 * ENTRY
+PART_REC = 66 * ENTRY    # bytes of one (split, head) partial record: m, l, acc[64]
 PART_SPLIT = 4 * PART_REC
 PART_BYTES = MAX_SPLITS * PART_SPLIT
 
@@ -78,7 +82,7 @@ def test_indices_stay_in_bounds_and_cover_the_work_once(heads, hidden, max_len, 
     for g in range(8):
         seen = []
         for s in range(splits):
-            assert s < MAX_SPLITS  # flag_qkv[s], flag_part[s], part[s]
+            assert s < MAX_SPLITS  # part[s]
             for wid, a in itertools.product(range(NW), range(NP)):
                 li = wid + NW * a
                 l = s * pp + li
@@ -88,15 +92,25 @@ def test_indices_stay_in_bounds_and_cover_the_work_once(heads, hidden, max_len, 
                 gh = g * G + lh if lh < G else heads + g if lh == G else heads + 8 + g
                 r0, r1 = gh * 64 + jp, gh * 64 + jp + 32
                 assert 0 <= r0 < rows and 0 <= r1 < rows  # rows are loaded even when unused
-                assert lh < G + 2 and jp < 32  # q[lh][jp + 32] for lh < G; K/V row pos of head g otherwise
+                assert lh < G + 2 and jp < 32  # q[lh][jp + 32] for lh < G; kv[lh - G][jp + 32] otherwise
+                if lh < G:
+                    assert (lh * 64 + jp + 32) * ENTRY + ENTRY <= Q_BYTES
+                else:
+                    assert ((lh - G) * 64 + jp + 32) * ENTRY + ENTRY <= KV_BYTES
                 if v:
                     seen.append(l)
                     # the right head: q of this group, then the group's K, then its V
                     assert (lh < G and gh // G == g) or gh in (heads + g, heads + 8 + g)
             for wid in range(NW):
                 t = s * T + wid // G
-                tc = min(t, ntiles - 1)
-                assert 0 <= tc < ntiles
+                for pos in (0, 63, 64, max_len // 2, max_len - 1):
+                    tc = min(t, pos // 64)  # past the length: the last tile in use
+                    assert 0 <= tc < ntiles and tc * 64 <= pos
+                wh = wid % G
+                for lane in range(64):  # the query poll of head wh, the K/V row poll, the partial store
+                    assert (wh * 64 + lane) * ENTRY + ENTRY <= Q_BYTES
+                    assert (64 + lane) * ENTRY + ENTRY <= KV_BYTES
+                    assert s * PART_SPLIT + wh * PART_REC + (2 + lane) * ENTRY + ENTRY <= PART_BYTES
         assert sorted(seen) == list(range(npair)), "every pair of the group exactly once"
     # per position: the patched tile, the used splits, the merge reads
     for pos in sorted({0, 1, 63, 64, 65, max_len // 2, max_len - 65, max_len - 64, max_len - 2, max_len - 1}):
@@ -112,11 +126,11 @@ def test_indices_stay_in_bounds_and_cover_the_work_once(heads, hidden, max_len, 
         for hh in range(G):  # workgroup s = hh merges query head g*G + hh
             assert hh < splits
             for s2 in range(32):
-                off = min(s2, splits - 1) * PART_SPLIT + hh * PART_REC + 4 * (2 + 63)
-                assert off + 4 <= PART_BYTES
+                off = min(s2, splits - 1) * PART_SPLIT + hh * PART_REC + ENTRY * (2 + 63)
+                assert off + ENTRY <= PART_BYTES
             for lane in range(64):
                 sl = min(lane, splits - 1)
-                assert sl * PART_SPLIT + hh * PART_REC + 8 <= PART_BYTES
+                assert sl * PART_SPLIT + hh * PART_REC + 2 * ENTRY <= PART_BYTES
         # every used split holds at least one valid tile; the unused ones write no partial
         for s in range(splits):
             used = min(T, nb - s * T)
