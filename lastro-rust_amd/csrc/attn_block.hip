@@ -56,7 +56,7 @@ __device__ __forceinline__ uint2 poll_entries(__amdgpu_buffer_rsrc_t r, unsigned
 template <int DT, int K, int G, int T, int NP, int SP, bool CMB>
 __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* __restrict__ h,
                                                           const float* __restrict__ lnw, float eps,
-                                                          const int* __restrict__ st, const float* __restrict__ rope,
+                                                          const int* __restrict__ st, const float* __restrict__ rope_cur,
                                                           int heads, int max_len, uint16_t* __restrict__ kc,
                                                           uint16_t* __restrict__ vc, float scale, int splits, int pp,
                                                           AbGroup* __restrict__ xg_all,
@@ -80,7 +80,8 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
   __shared__ float Pv[G][T][64];
   __shared__ float Tm[G][T], Al[G][T], Ts[G][T];
   __shared__ float Cw[2][64];
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  // wid as a wave-uniform value, so that what derives from it (the wave's row pairs, their cos/sin) is scalar
+  const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int g = (int)xcc_id() & 7, s = blockIdx.x >> 3;
   const int wh = wid % G, wt = wid / G;
   AbGroup* xg = xg_all + g;
@@ -106,46 +107,62 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
     row[2 * a + 1] = row[2 * a] + 32;
     ok[2 * a] = ok[2 * a + 1] = v;
   }
-  // loads in the order they are needed (they complete in issue order): the position and the step counter, the
-  // activation, this lane's cos/sin, the q/k/v rows, then the split's K and V tiles (used after the first barrier)
-  const int pos = st[ST_POS];
-  const unsigned epoch = *step_ctr * 64u + layer + 1u;
+  // The values earlier launches wrote that every wave needs as scalars (the position, the step counter, the
+  // previous layer's routing weights) are the first vector loads (lane j: weight j), so waiting for them waits for
+  // nothing else (vector loads complete in issue order); read back as scalars after the bulk loads are issued.
+  const unsigned pos_v = __builtin_amdgcn_raw_buffer_load_b32(l2_buffer(st, 4 * ST_WORDS), 4 * ST_POS, 0, 0);
+  const unsigned sctr_v = __builtin_amdgcn_raw_buffer_load_b32(l2_buffer(step_ctr, 4), 0, 0, 0);
+  const float yw_v = CMB ? yw[lane & 7] : 0.0f;
+  const float rc_v = rope_cur[lane];  // the rope row of the position: cos 0..31, sin 32..63
+  __builtin_amdgcn_sched_barrier(0);
+  // Vector loads in the order they are needed: the activation, the q/k/v rows, then the split's K and V tiles
+  // (used after the first barrier). A compute unit passes requests to its L1 at a fixed rate of bytes, so the
+  // activation loads of every wave go first (a bare workgroup barrier orders them before any wave's rows), and a
+  // wave whose threads hold no quad of the activation issues none.
   NormIn<K, NT> hin;
   constexpr int PER = NormIn<K, NT>::PER, NQ = NormIn<K, NT>::Q;
   float4 yv[CMB ? 8 : 1][PER];
-  float wj[8];
-  if (CMB) {
-    // this thread's quads of h, the norm weights and the 8 experts' down outputs (clamped, not guarded)
 #pragma unroll
-    for (int e = 0; e < PER; e++) {
-      const int q = threadIdx.x + e * NT, qc = q < NQ ? q : NQ - 1;
+  for (int e = 0; e < PER; e++) {
+    const int q = threadIdx.x + e * NT, qc = q < NQ ? q : NQ - 1;
+    const float4 z4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    hin.hv[e] = hin.wv[e] = z4;
+#pragma unroll
+    for (int j = 0; j < (CMB ? 8 : 1); j++) yv[j][e] = z4;
+    if (wid * 64 + e * NT < NQ) {  // wave-uniform: some thread of the wave holds a quad (clamped, not guarded)
       hin.hv[e] = reinterpret_cast<const float4*>(h)[qc];
       hin.wv[e] = reinterpret_cast<const float4*>(lnw)[qc];
+      if (CMB) {
 #pragma unroll
-      for (int j = 0; j < 8; j++) yv[j][e] = reinterpret_cast<const float4*>(ys)[(size_t)j * NQ + qc];
+        for (int j = 0; j < 8; j++) yv[j][e] = reinterpret_cast<const float4*>(ys)[(size_t)j * NQ + qc];
+      }
     }
-#pragma unroll
-    for (int j = 0; j < 8; j++) wj[j] = yw[j];
-    __builtin_amdgcn_sched_barrier(0);
-  } else {
-    norm_fetch<K, NT>(h, lnw, hin);
   }
-  const float* cs = rope + (size_t)pos * 64;
-  float cv[NP], sv[NP];
-#pragma unroll
-  for (int a = 0; a < NP; a++) {
-    cv[a] = cs[jp[a]];
-    sv[a] = cs[32 + jp[a]];
-  }
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
   Rows<DT, K, P> rr;
-  rows_load<DT, K, P>(rr, m, row, ok, lane);
+  if (ok[0]) rows_load<DT, K, P>(rr, m, row, ok, lane);  // a wave with no pair (wave-uniform) loads no row
   __builtin_amdgcn_sched_barrier(0);
   const int t0 = s * T, t = t0 + wt;
-  const int tc = min(t, pos / 64);  // a tile past the length (never used: staged as zeros) reads the last tile in use
+  const int tc = min(t, max_len / 64 - 1);  // a tile past the cache's end (never used) reads the last tile
   VShare<G> ksh, vsh;
   ksh.load(Kc, tc, lane, wh);
   vsh.load(Vc, tc, lane, wh);
+  __builtin_amdgcn_sched_barrier(0);
+  // the scalars, and the wave's cos/sin
+  const int pos = (int)__builtin_amdgcn_readfirstlane(pos_v);
+  const unsigned sctr = __builtin_amdgcn_readfirstlane(sctr_v);
+  float wj[8];
+#pragma unroll
+  for (int j = 0; j < 8; j++) wj[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(yw_v), j));
+  float cv[NP], sv[NP];
+#pragma unroll
+  for (int a = 0; a < NP; a++) {
+    cv[a] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(rc_v), jp[a]));
+    sv[a] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(rc_v), 32 + jp[a]));
+  }
+  const unsigned epoch = sctr * 64u + layer + 1u;
 
   // 1. q/k/v pairs of the group
   if (CMB) {
@@ -386,7 +403,7 @@ hipError_t launch_attn_block(hipStream_t s, const LayerDev& L, const Dims& d, co
   const float* yw = b.route_w + (size_t)(layer > 0 ? layer - 1 : 0) * d.top_k;
 #define AB_LAUNCH(DD, KK, GG, TT, NN, CC)                                                                          \
   klaunch(k_attn_block<DD, KK, GG, TT, NN, 32, CC>, grid, GG * TT * 64, 0, s, L.qkv, b.h, L.ln_attn, d.eps,        \
-          b.state, b.rope, d.heads, d.max_len, L.k_cache, L.v_cache, d.attn_mult, sh.splits, sh.pp, x.groups,      \
+          b.state, x.rope_cur, d.heads, d.max_len, L.k_cache, L.v_cache, d.attn_mult, sh.splits, sh.pp, x.groups,      \
           x.step_ctr, (unsigned)layer, x.err, b.att, (const float*)x.ys, yw, d.res_mult, b.hc, tl)
 #define AB_CASE(DD, KK, GG, TT, NN)                                                                                \
   if (L.qkv.dtype == DD && L.qkv.cols == KK && sh.G == GG && sh.T == TT && sh.np == NN) {                         \

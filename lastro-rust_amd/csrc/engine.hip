@@ -270,7 +270,8 @@ struct moert_model {
       tl_layer.push_back(layer);
       return t;
     };
-    CHECK_HIP(launch_embed(stream, embed, dims, b, ab.step_ctr, arm(MOERT_K_EMBED, -1)));
+    CHECK_HIP(
+        launch_embed(stream, embed, dims, b, ab.step_ctr, use_ab ? ab.rope_cur : nullptr, arm(MOERT_K_EMBED, -1)));
     for (size_t l = 0; l < layers.size(); l++) {
       const LayerDev& L = layers[l];
       const int li = (int)l;
@@ -359,7 +360,7 @@ struct moert_model {
     CHECK_HIP(hipMemcpy(&pos, b.state + ST_POS, 4, hipMemcpyDeviceToHost));
     std::memcpy(hy_table_pin, P.table().data(), (size_t)L * E * 4);
     CHECK_HIP(hipMemcpyAsync(hy_table, hy_table_pin, (size_t)L * E * 4, hipMemcpyHostToDevice, stream));
-    CHECK_HIP(launch_embed(stream, embed, dims, b, ab.step_ctr));
+    CHECK_HIP(launch_embed(stream, embed, dims, b, ab.step_ctr, use_ab ? ab.rope_cur : nullptr));
     std::vector<int> keys, n_e;
     std::vector<char> gpu;
     for (int l = 0; l < L; l++) {
@@ -843,7 +844,8 @@ static int model_create(const moert_config* c, const moert_model_weights* w, int
     unsigned *grp = nullptr, *mx = nullptr;
     if ((rc = zeros(a, s, 8 * sizeof(AbGroup) / 4, &grp)) || (rc = zeros(a, s, 8 * sizeof(MxGroup) / 4, &mx)) ||
         (rc = zeros(a, s, (size_t)8 * H, &m->ab.ys)) || (rc = zeros(a, s, (size_t)H, &b.hc)) ||
-        (rc = zeros(a, s, (size_t)1, &m->ab.step_ctr)) || (rc = zeros(a, s, (size_t)1, &m->ab.err)))
+        (rc = zeros(a, s, (size_t)1, &m->ab.step_ctr)) || (rc = zeros(a, s, (size_t)1, &m->ab.err)) ||
+        (rc = zeros(a, s, (size_t)64, &m->ab.rope_cur)))
       return bail(rc);
     m->ab.groups = reinterpret_cast<AbGroup*>(grp);
     m->ab.moe = reinterpret_cast<MxGroup*>(mx);

@@ -71,13 +71,15 @@ struct AbBufs {
   MxGroup* moe;        // [8]
   float* ys;           // [8][hidden]: down output of the expert of each routing rank (k_moe_xcd)
   unsigned* step_ctr;  // decode steps started (k_embed adds one); a launch's epoch is step_ctr * 64 + layer + 1
+  float* rope_cur;     // [64]: the rope row (cos, then sin) of the step's position (k_embed copies it)
   unsigned* err;       // bits 1, 2: a wait for values of a KV head's workgroups (queries and K/V row, partials) gave up;
                        // bit 3: a wait for the act values of an XCD's expert gave up
 };
 
 // tl: the launch's timeline record (measurement build; null otherwise). step_ctr (may be null): incremented once.
+// rope_cur (may be null): receives the 64-float rope row of the step's position (head_dim 64).
 hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const StepBufs& b, unsigned* step_ctr,
-                        Tl tl = {});
+                        float* rope_cur = nullptr, Tl tl = {});
 hipError_t launch_qkv(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl = {});
 hipError_t launch_attn_split(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, Tl tl = {});
 hipError_t launch_attn_combine(hipStream_t s, const Dims& d, const StepBufs& b, Tl tl = {});

@@ -64,9 +64,12 @@ __global__ __launch_bounds__(kBlock) void k_gemv(DMat m, const float* __restrict
 template <int DT>
 __global__ __launch_bounds__(kBlock) void k_embed(DMat e, const int* __restrict__ seq, const int* __restrict__ st,
                                                   float mult, float* __restrict__ h, unsigned* __restrict__ step_ctr,
+                                                  const float* __restrict__ rope, float* __restrict__ rope_cur,
                                                   Tl tl) {
   TL_START(tl);
   if (step_ctr && threadIdx.x == 0) *step_ctr += 1u;
+  static_assert(kBlock >= 64, "one thread per rope element");
+  if (rope_cur && threadIdx.x < 64) rope_cur[threadIdx.x] = rope[(size_t)st[ST_POS] * 64 + threadIdx.x];
   int tok = seq[st[ST_POS]];
   int H = e.cols;
   for (int i = threadIdx.x; i < H; i += kBlock) {
@@ -1343,13 +1346,16 @@ hipError_t launch_gemv(hipStream_t s, const DMat& w, const float* x, float* y) {
 }
 
 hipError_t launch_embed(hipStream_t s, const DMat& emb, const Dims& d, const StepBufs& b, unsigned* step_ctr,
-                        Tl tl) {
+                        float* rope_cur, Tl tl) {
+  if (rope_cur && d.head_dim != 64) return hipErrorInvalidValue;
+#define EMB(DD) klaunch(k_embed<DD>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h, step_ctr, b.rope, rope_cur, tl)
   switch (emb.dtype) {
-    case DT_Q8_0: klaunch(k_embed<DT_Q8_0>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h, step_ctr, tl); break;
-    case DT_Q4_0: klaunch(k_embed<DT_Q4_0>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h, step_ctr, tl); break;
-    case DT_F32: klaunch(k_embed<DT_F32>, 1, kBlock, 0, s, emb, b.seq, b.state, d.emb_mult, b.h, step_ctr, tl); break;
+    case DT_Q8_0: EMB(DT_Q8_0); break;
+    case DT_Q4_0: EMB(DT_Q4_0); break;
+    case DT_F32: EMB(DT_F32); break;
     default: return hipErrorInvalidValue;
   }
+#undef EMB
   return hipGetLastError();
 }
 
