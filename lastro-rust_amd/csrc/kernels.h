@@ -59,12 +59,11 @@ struct AbGroup {
   uint2 kv[2][64];
   uint2 part[kAbMaxSplits][4][66];
 };
-// Exchange area of the MoE kernel spread over the XCDs (moe_block.hip) for one XCD: a flag per workgroup (the
-// launch's epoch once its act values are stored) and the act vector of the XCD's expert.
+// Exchange area of the MoE kernel spread over the XCDs (moe_block.hip) for one XCD: the act vector of the XCD's
+// expert, each value with the epoch of the launch that stored it.
 constexpr int kMxWgs = 32;  // workgroups per XCD
 struct MxGroup {
-  unsigned flag[kMxWgs];
-  float act[512];
+  uint2 act[512];  // (value bits, epoch of the launch that wrote it), written and read as one 8-byte word
 };
 struct AbBufs {
   AbGroup* groups;     // [8]

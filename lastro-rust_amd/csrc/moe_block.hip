@@ -3,19 +3,18 @@
 // rank j = x. Every workgroup computes the rmsnorm and the router from the output projection's MoE-norm partials and
 // ranks the experts (as k_route_up does); then
 //   1. its gate/up row pairs of expert j (pairs [w * PW, (w + 1) * PW), PW = inter / 32): act = silu(gate . xn) *
-//      (up . xn), stored into XCD x's L2 area, and a flag;
-//   2. once the flags of the XCD's 32 workgroups are set, the expert's whole act vector from that L2, and its down
-//      rows [w * RB, (w + 1) * RB) (RB = hidden / 32), loaded right after routing so that they arrive while the
-//      act vector is formed: ys[j][r] = down_r . act.
-// Waves 0..7 take the gate/up pairs and waves 8..15 the down rows: a wave's wait for its act stores to complete
-// also waits for every load it issued before them (vmcnt counts both, in order), so the waves that signal hold no
-// down rows in flight.
+//      (up . xn), stored with the launch's epoch into XCD x's L2 area (one 8-byte word per value);
+//   2. the expert's whole act vector from that L2, polled until every value carries the epoch, and its down rows
+//      [w * RB, (w + 1) * RB) (RB = hidden / 32), loaded right after routing so that they arrive while the act
+//      vector is formed: ys[j][r] = down_r . act.
+// Waves 0..7 take the gate/up pairs and waves 8..15 the down rows and the act poll (a wave's loads complete in
+// issue order, so the polls of a wave that holds down rows in flight return once those rows are in).
 // The weighted combine h += res * (sum over j in top-k order of w_j * ys[j]) is done by the next kernel that reads h
 // (the attention block of the next layer, or k_moe_combine before the head), with the operations and order of
 // k_expert_down's epilogue. Each (row, expert) dot is the canonical chain of k_route_up / k_expert_down, so the
 // results are the same bit for bit. Replaces k_route_up + k_expert_down (gemv + route_topk, moe_gate_up, moe_down,
 // rust/moe-rt/src/cuda_backend.rs:804-835, hits.rs:67-148; Cpu::experts, cpu.rs:116-150).
-// The act wait is bounded; a wait that gives up sets bit 3 of `err` and the kernel still ends.
+// The act poll is bounded; a poll that gives up sets bit 3 of `err` and the kernel still ends.
 #include "attn_dev.h"
 #include "dev_rows.h"
 #include "kernels.h"
@@ -30,15 +29,17 @@ constexpr int kMxSpin = 1 << 18;
 constexpr int kMxWaves = 16;
 constexpr int kMxUpWaves = 8;  // waves 0..7: gate/up pairs; waves 8..15: down rows
 
-__device__ __forceinline__ bool mx_wait(const unsigned* flags, int n, unsigned epoch, int lane) {
-  const __amdgpu_buffer_rsrc_t r = l2_buffer(flags, kMxWgs * 4);
+// Wave-level poll of act entry i (one per lane) from the XCD's L2 until every lane's entry carries `epoch`; returns
+// the value. Clears *ok when the poll gave up.
+__device__ __forceinline__ float mx_poll(__amdgpu_buffer_rsrc_t r, int i, unsigned epoch, bool* ok) {
   for (int it = 0; it < kMxSpin; it++) {
     poll_fence();
-    const unsigned f = lane < n ? l2_load_u32(r, 4u * lane) : epoch;
-    if (__ballot(f != epoch) == 0) return true;
+    const uint2 e = l2_load_u64(r, 8u * i);
+    if (__ballot(e.y != epoch) == 0) return __uint_as_float(e.x);
     __builtin_amdgcn_s_sleep(1);
   }
-  return false;
+  *ok = false;
+  return 0.0f;
 }
 }  // namespace
 
@@ -156,24 +157,20 @@ __global__ __launch_bounds__(kMxWaves * 64) void k_moe_xcd(DMat router, const fl
     if (sub == 0) {
 #pragma unroll
       for (int a = 0; a < NP; a++)
-        if (ok[2 * a]) xg->act[pi[a]] = silu_mul(out[2 * a], out[2 * a + 1]);
+        if (ok[2 * a]) put_entry(&xg->act[pi[a]], __float_as_uint(silu_mul(out[2 * a], out[2 * a + 1])), epoch);
     }
     TL_PHASE(tl, 4);
-    wait_mem();  // this wave's act values have reached the L2
   } else {
     rows_load<DT, I, DP>(dd, dn, drow, dok, dsub);
+    // the expert's act vector from the L2 (down thread i polls act[i]), then the down rows
+    static_assert(I == ND * 64, "one act value per down thread");
+    const int i = threadIdx.x - NU * 64;
+    bool got = true;
+    as[i] = mx_poll(l2_buffer(xg->act, sizeof(xg->act)), i, epoch, &got);
+    if (!got && lane == 0) atomicOr(err, 8u);
   }
-  __syncthreads();
-  if (threadIdx.x == 0) xg->flag[w] = epoch;
-  if (wave == 0 && !mx_wait(xg->flag, kMxWgs, epoch, lane) && lane == 0) atomicOr(err, 8u);
   __syncthreads();
   TL_PHASE(tl, 5);
-  // the expert's act vector from the L2, then the down rows
-  {
-    const __amdgpu_buffer_rsrc_t ra = l2_buffer(xg->act, sizeof(xg->act));
-    for (int i = threadIdx.x; i < I; i += NT) as[i] = l2_load_f32(ra, 4u * i);
-  }
-  __syncthreads();
   if (!up) {
     XReg<DT, I> xa;
     load_x<DT, I>(xa, as, dsub);

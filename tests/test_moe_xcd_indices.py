@@ -1,7 +1,7 @@
 """CPU transcription of the index arithmetic of the MoE kernel spread over the XCDs (lastro-rust_amd/csrc/
 moe_block.hip, k_moe_xcd): for every compiled shape, the 32 workgroups of an XCD compute each gate/up pair and each
 down row of their expert exactly once, every row index stays inside the layer's matrices, and every exchange and
-output index stays inside its buffer."""
+output index stays inside its buffer (the act vector: one epoch-tagged entry per value, polled by the down threads)."""
 import pytest
 
 WGS, WAVES, WAVE = 32, 16, 64      # kMxWgs, kMxWaves, lanes
@@ -61,6 +61,7 @@ def test_pairs_and_down_rows_once_and_in_bounds(dt, K, E):
                             if ok and dsub == 0:
                                 rows.append(dr)
                                 assert x * K + dr < 8 * K  # ys[x][dr]
-                assert w < WGS  # flag[w]
+                for t in range(NU * 64, WAVES * 64):  # down thread t polls act[t - NU * 64]
+                    assert 0 <= t - NU * 64 < I
             assert sorted(pairs) == list(range(I)), "every gate/up pair of the expert once"
             assert sorted(rows) == list(range(K)), "every down row of the expert once"
