@@ -68,15 +68,17 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
   using Ge = Geo<DT, K>;
   static_assert(Ge::RPW == 1, "one q/k/v row per wave and pass");
   constexpr int NW = G * T, NT = NW * 64, P = 2 * NP;
-  constexpr int TR = 8 % G == 0 ? 64 : 72;  // tile rows (64..71: padding for VShare when G does not divide 8)
-  constexpr int KS = 68;                     // K row stride in floats: 16-byte rows, conflict-free row reads
-  __shared__ __align__(16) float Vs[T][TR][64];
-  __shared__ __align__(16) float Ks[T][TR][KS];
+  constexpr int TR = 8 % G == 0 ? 64 : 72;  // K tile rows (64..71: padding for VShare when G does not divide 8)
+  constexpr int KHS = 72;                    // K row stride in halves: 144-byte rows, conflict-free row reads
+  // The K and V tiles stay fp16 in LDS (the FMAs take a half operand exactly, v_fma_mix): K row-major, V transposed
+  // (dim-major, VShare::vt_col), so that a lane reads its position's K row and its dim's V column 8 halves at a time.
+  __shared__ __align__(16) uint16_t Vt[T][64][64];
+  __shared__ __align__(16) uint16_t Kh[T][TR][KHS];
   __shared__ float rs;
-  static_assert(T * TR * 64 >= K, "the normalised input is staged in the V tiles' LDS");
-  float* xs = &Vs[0][0][0];  // the normalised input, until the V tiles are staged
-  __shared__ float Qs[G][64];
-  __shared__ float Ps[G][T][64];
+  static_assert(T * 64 * 64 / 2 >= K, "the normalised input is staged in the V tiles' LDS");
+  float* xs = reinterpret_cast<float*>(&Vt[0][0][0]);  // the normalised input, until the V tiles are staged
+  __shared__ __align__(16) float Qs[G][64];
+  __shared__ __align__(16) float Ps[G][T][64];
   __shared__ float Pv[G][T][64];
   __shared__ float Tm[G][T], Al[G][T], Ts[G][T];
   __shared__ float Cw[2][64];
@@ -215,8 +217,8 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
   const int used = min(T, nb - t0);  // tiles of this split inside the length (>= 1 when the split is used)
   const bool active = wt < used;
   const int nv = active ? min(64, len - t * 64) : 0;
-  ksh.template store<KS>(&Ks[wt][0][0], lane, wh, nv);
-  vsh.template store<64>(&Vs[wt][0][0], lane, wh, nv);
+  ksh.template store_h<KHS>(&Kh[wt][0][0], lane, wh, nv);
+  vsh.store_ht(&Vt[wt][0][0], lane, wh, nv);
   TL_PHASE(tl, 3);
   __syncthreads();  // the staged tiles, before the new row goes over row pos
 
@@ -233,8 +235,8 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
     if (tp >= 0 && tp < T && wid == tp * G) {
       const __amdgpu_buffer_rsrc_t rk = l2_buffer(&xg->kv[0][0], sizeof(xg->kv));
       const uint2 kv = poll_entries<true>(rk, 8u * lane, 8u * (64 + lane), epoch, &okw);
-      Ks[tp][pos & 63][lane] = h2f((uint16_t)kv.x);
-      Vs[tp][pos & 63][lane] = h2f((uint16_t)kv.y);
+      Kh[tp][pos & 63][lane] = (uint16_t)kv.x;
+      Vt[tp][lane][VShare<G>::vt_col(pos & 63, lane)] = (uint16_t)kv.y;
     }
     if (!okw && lane == 0) atomicOr(err, 2u);
   }
@@ -244,15 +246,20 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
   float sc;
   {
     float dt = 0.0f;
-    const float* krow = &Ks[wt][lane][0];
+    const uint4* krow = reinterpret_cast<const uint4*>(&Kh[wt][lane][0]);
 #pragma unroll
-    for (int d4 = 0; d4 < 16; d4++) {
-      const float4 kk = *reinterpret_cast<const float4*>(krow + 4 * d4);
-      const float4 qq = *reinterpret_cast<const float4*>(&Qs[wh][4 * d4]);
-      dt = __builtin_fmaf(qq.x, kk.x, dt);
-      dt = __builtin_fmaf(qq.y, kk.y, dt);
-      dt = __builtin_fmaf(qq.z, kk.z, dt);
-      dt = __builtin_fmaf(qq.w, kk.w, dt);
+    for (int c = 0; c < 8; c++) {
+      const uint4 k8 = krow[c];
+      const float4 q0 = *reinterpret_cast<const float4*>(&Qs[wh][8 * c]);
+      const float4 q1 = *reinterpret_cast<const float4*>(&Qs[wh][8 * c + 4]);
+      dt = __builtin_fmaf(q0.x, h2f((uint16_t)k8.x), dt);
+      dt = __builtin_fmaf(q0.y, h2f((uint16_t)(k8.x >> 16)), dt);
+      dt = __builtin_fmaf(q0.z, h2f((uint16_t)k8.y), dt);
+      dt = __builtin_fmaf(q0.w, h2f((uint16_t)(k8.y >> 16)), dt);
+      dt = __builtin_fmaf(q1.x, h2f((uint16_t)k8.z), dt);
+      dt = __builtin_fmaf(q1.y, h2f((uint16_t)(k8.z >> 16)), dt);
+      dt = __builtin_fmaf(q1.z, h2f((uint16_t)k8.w), dt);
+      dt = __builtin_fmaf(q1.w, h2f((uint16_t)(k8.w >> 16)), dt);
     }
     sc = lane < nv ? dt * scale : NEG_INF;  // nv = 0 for an inactive tile
   }
@@ -277,13 +284,21 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
   if (active) {
     // p.v: lane = dim, chain over the positions in order; past the length p = 0 and V = +0, so those steps leave
     // pv unchanged (the chain equals the one over the valid positions only)
-    const float* vcol = &Vs[wt][0][lane];
+    const uint4* vrow = reinterpret_cast<const uint4*>(&Vt[wt][lane][0]);
+    const int sd = (lane ^ (lane >> 3)) & 7;  // positions 8cj..8cj+7 of dim `lane` sit in 16-byte slot cj ^ sd
 #pragma unroll
-    for (int i0 = 0; i0 < 64; i0 += 4) {
-      const float4 p4 = *reinterpret_cast<const float4*>(&Ps[wh][wt][i0]);
-      const float pa[4] = {p4.x, p4.y, p4.z, p4.w};
-#pragma unroll
-      for (int u = 0; u < 4; u++) pv = __builtin_fmaf(pa[u], vcol[(i0 + u) * 64], pv);
+    for (int cj = 0; cj < 8; cj++) {
+      const uint4 v8 = vrow[cj ^ sd];
+      const float4 p0 = *reinterpret_cast<const float4*>(&Ps[wh][wt][8 * cj]);
+      const float4 p1 = *reinterpret_cast<const float4*>(&Ps[wh][wt][8 * cj + 4]);
+      pv = __builtin_fmaf(p0.x, h2f((uint16_t)v8.x), pv);
+      pv = __builtin_fmaf(p0.y, h2f((uint16_t)(v8.x >> 16)), pv);
+      pv = __builtin_fmaf(p0.z, h2f((uint16_t)v8.y), pv);
+      pv = __builtin_fmaf(p0.w, h2f((uint16_t)(v8.y >> 16)), pv);
+      pv = __builtin_fmaf(p1.x, h2f((uint16_t)v8.z), pv);
+      pv = __builtin_fmaf(p1.y, h2f((uint16_t)(v8.z >> 16)), pv);
+      pv = __builtin_fmaf(p1.z, h2f((uint16_t)v8.w), pv);
+      pv = __builtin_fmaf(p1.w, h2f((uint16_t)(v8.w >> 16)), pv);
     }
     if (wt > 0) Pv[wh][wt][lane] = pv;
   }

@@ -49,6 +49,52 @@ struct VShare {
     if (N > 6) put(6, g);
     if (N > 7) put(7, h);
   }
+  // The tile kept in fp16, row-major with rows of RS halves, as loaded (rows at and past nv stored as +0).
+  template <int RS>
+  __device__ __forceinline__ void store_h(uint16_t* dst, int lane, int wave, int nv) const {
+    auto put = [&](int i, const uint4& v) {
+      const int row = 8 * (wave + G * i) + (lane >> 3);
+      *reinterpret_cast<uint4*>(dst + row * RS + (lane & 7) * 8) = row >= nv ? make_uint4(0u, 0u, 0u, 0u) : v;
+    };
+    put(0, a);
+    if (N > 1) put(1, b);
+    if (N > 2) put(2, c);
+    if (N > 3) put(3, d);
+    if (N > 4) put(4, e);
+    if (N > 5) put(5, f);
+    if (N > 6) put(6, g);
+    if (N > 7) put(7, h);
+  }
+  // The tile kept in fp16 and transposed: element (row, dim) at dst[dim * 64 + vt_col(row, dim)] (rows 0..63; the
+  // padding piece past row 63 is not stored), rows at and past nv stored as +0.
+  __device__ __forceinline__ void store_ht(uint16_t* dst, int lane, int wave, int nv) const {
+    auto put = [&](int i, const uint4& v) {
+      const int row = 8 * (wave + G * i) + (lane >> 3);
+      if (row >= 64) return;
+      const bool z = row >= nv;
+      const int c0 = (lane & 7) * 8;
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int k = 0; k < 8; k++) {
+        const int dm = c0 + k;
+        dst[dm * 64 + vt_col(row, dm)] = z ? (uint16_t)0 : (uint16_t)(w[k >> 1] >> (16 * (k & 1)));
+      }
+    };
+    put(0, a);
+    if (N > 1) put(1, b);
+    if (N > 2) put(2, c);
+    if (N > 3) put(3, d);
+    if (N > 4) put(4, e);
+    if (N > 5) put(5, f);
+    if (N > 6) put(6, g);
+    if (N > 7) put(7, h);
+  }
+  // Column of position `row` in dim row `dm` of the transposed tile: 8-position chunks permuted by
+  // (dm ^ dm / 8) % 8, so that the 16-byte reads of one chunk by 8 consecutive dims, and the writes of one element
+  // of a piece by its 64 lanes, fall in different LDS banks.
+  __device__ static __forceinline__ int vt_col(int row, int dm) {
+    return 8 * ((row >> 3) ^ ((dm ^ (dm >> 3)) & 7)) + (row & 7);
+  }
 };
 
 // ------------------------------------------------------------------------------------------------------------

@@ -59,7 +59,7 @@ __global__ __launch_bounds__(kPfNW * 64) void k_prefetch_decide(DMat router, con
   __shared__ float xs[K];
   __shared__ float rs;
   __shared__ __align__(16) float lg[64];
-  __shared__ int part[64][kPfNW];
+  __shared__ int part[kPfNW][64];
   __shared__ int skey[kCacheMaxSlots];
   __shared__ int slast[kCacheMaxSlots];
   __shared__ int lfound[8];

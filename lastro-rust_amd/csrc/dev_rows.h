@@ -294,10 +294,11 @@ __device__ __forceinline__ void wg_copy(const float* __restrict__ x, float* xs) 
 
 // Ranks of n <= 64 logits held in LDS (lg[64], visible to the whole workgroup), by all NW waves: wave w counts, for
 // every lane e, the 64-bit sort keys of logits [w * 64 / NW, (w + 1) * 64 / NW) above lane e's key (total-order key,
-// then 63 - e: descending value, ties to the lower index); the counts meet in LDS and every wave adds them in wave
-// order. Returns the rank of lane e's logit (the same in every wave); contains a workgroup barrier.
+// then 63 - e: descending value, ties to the lower index); the counts meet in LDS (part[wave][lane]: a wave's counts
+// in consecutive words, free of bank conflicts) and every wave adds them in wave order. Returns the rank of lane e's
+// logit (the same in every wave); contains a workgroup barrier.
 template <int NW>
-__device__ __forceinline__ int wg_rank(const float* lg, int n, int lane, int wave, int (*part)[NW]) {
+__device__ __forceinline__ int wg_rank(const float* lg, int n, int lane, int wave, int (*part)[64]) {
   constexpr int PER = 64 / NW;
   static_assert(64 % NW == 0, "waves must divide 64");
   // lg[e] is read for every e < 64 and the entries at and past n are discarded afterwards: a read under the
@@ -311,11 +312,11 @@ __device__ __forceinline__ int wg_rank(const float* lg, int n, int lane, int wav
   int cnt = 0;
 #pragma unroll
   for (int u = 0; u < PER; u++) cnt += key(wave * PER + u) > mine;
-  part[lane][wave] = cnt;
+  part[wave][lane] = cnt;
   __syncthreads();
   int rank = 0;
 #pragma unroll
-  for (int w = 0; w < NW; w++) rank += part[lane][w];
+  for (int w = 0; w < NW; w++) rank += part[w][lane];
   return rank;
 }
 

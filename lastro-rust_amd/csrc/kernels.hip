@@ -788,7 +788,7 @@ __global__ __launch_bounds__(route_waves(DT) * 64) void k_route_up(DMat router, 
   constexpr int SMAX = CACHED ? kCacheMaxSlots : 1;
   __shared__ float xs[K];
   __shared__ __align__(16) float lg[64];
-  __shared__ int part[64][NW];
+  __shared__ int part[NW][64];
   __shared__ int skey[SMAX];
   __shared__ int slast[SMAX];
   __shared__ int lslot[8], lmiss[8], lfound[8];

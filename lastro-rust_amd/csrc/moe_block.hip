@@ -63,7 +63,7 @@ __global__ __launch_bounds__(kMxWaves * 64) void k_moe_xcd(DMat router, const fl
   __shared__ float xs[K];
   __shared__ __align__(16) float as[I];
   __shared__ __align__(16) float lg[64];
-  __shared__ int part[64][NW];
+  __shared__ int part[NW][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int x = (int)xcc_id() & 7, w = blockIdx.x >> 3;
   MxGroup* xg = xg_all + x;

@@ -311,7 +311,7 @@ __global__ __launch_bounds__(route_b_waves(DT) * 64) void k_route_b(DMat router,
   constexpr int IPW = (64 + NW - 1) / NW;  // router items per wave
   constexpr int XP = (K + NT - 1) / NT;    // elements of h per thread
   __shared__ __align__(16) float lg[64];
-  __shared__ int part[64][NW];
+  __shared__ int part[NW][64];
   const int v = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int E = router.rows, nb = K / kNormBlk;

@@ -134,3 +134,31 @@ def test_indices_stay_in_bounds_and_cover_the_work_once(heads, hidden, max_len, 
         for s in range(splits):
             used = min(T, nb - s * T)
             assert (used > 0) == (s < nsplit)
+
+
+def vt_col(row, dm):
+    """VShare::vt_col: column of position `row` in dim row `dm` of the transposed fp16 V tile."""
+    return 8 * ((row >> 3) ^ ((dm ^ (dm >> 3)) & 7)) + (row & 7)
+
+
+def test_transposed_v_tile_layout_is_a_permutation_read_in_order_without_bank_conflicts():
+    for dm in range(64):
+        assert sorted(vt_col(r, dm) for r in range(64)) == list(range(64))
+        sd = (dm ^ (dm >> 3)) & 7
+        for cj in range(8):  # p.v reads positions 8cj..8cj+7 of dim dm from 16-byte slot cj ^ sd, in order
+            assert [vt_col(8 * cj + t, dm) for t in range(8)] == [8 * (cj ^ sd) + t for t in range(8)]
+    # 16-byte reads of one chunk by 8 consecutive dims: 8 different 4-bank groups (row stride 128 B, 32 banks)
+    for g in range(8):
+        for cj in range(8):
+            starts = {(dm * 32 + 4 * (cj ^ ((dm ^ (dm >> 3)) & 7))) % 32 for dm in range(8 * g, 8 * g + 8)}
+            assert len(starts) == 8
+    # 2-byte writes of element k of a piece (rows 8e..8e+7, lane l: row 8e + l // 8, dims 8 (l % 8) + k): the 64
+    # lanes write 32 different dwords in 32 different banks (two lanes share each dword, one half each)
+    for e in range(8):
+        for k in range(8):
+            words = {}
+            for lane in range(64):
+                row, dm = 8 * e + lane // 8, 8 * (lane % 8) + k
+                w = (dm * 64 + vt_col(row, dm)) // 2
+                words.setdefault(w, []).append(lane)
+            assert len(words) == 32 and len({w % 32 for w in words}) == 32
