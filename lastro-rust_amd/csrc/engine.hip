@@ -1081,14 +1081,17 @@ static int model_launch(moert_model* m) {
   CHECK_HIP(hipGraphLaunch(m->exec, m->stream));
   return MOERT_OK;
 }
-// A bit the attention block kernel set (a wait that gave up) is a device error.
+// A bit that k_attn_block or k_moe_xcd set (a bounded wait that gave up) is a device error: 2 = the queries or the
+// new K/V row of a KV head, 4 = the split partials of a merge, 8 = the act vector of an expert.
 static int ab_check(moert_model* m) {
   if (!m->use_ab) return MOERT_OK;
   unsigned e = 0;
   CHECK_HIP(hipMemcpy(&e, m->ab.err, 4, hipMemcpyDeviceToHost));
   if (e) {
-    set_err("attention block: a wait for the workgroups of a KV head gave up (error bits %#x): the launch's "
-            "workgroups were not dispatched round-robin over the XCDs or not all resident at once", e);
+    set_err("%s%s%sgave up (error bits %#x): the launch's workgroups were not dispatched round-robin over the XCDs "
+            "or not all resident at once", (e & 2u) ? "attention block: the wait for queries / the new K/V row " : "",
+            (e & 4u) ? "attention block: the wait for split partials " : "",
+            (e & 8u) ? "MoE kernel: the wait for an expert's act vector " : "", e);
     return MOERT_E_DEVICE;
   }
   return MOERT_OK;
