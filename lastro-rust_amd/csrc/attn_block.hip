@@ -279,9 +279,7 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
       Al[wh][wt] = alpha;
       Ts[wh][wt] = ts;
     }
-  }
-  __syncthreads();  // P written
-  if (active) {
+    wave_lds_sync();  // the wave's own p row, read back below by every lane of the same wave
     // p.v: lane = dim, chain over the positions in order; past the length p = 0 and V = +0, so those steps leave
     // pv unchanged (the chain equals the one over the valid positions only)
     const uint4* vrow = reinterpret_cast<const uint4*>(&Vt[wt][lane][0]);

@@ -109,14 +109,16 @@ __global__ __launch_bounds__(kMxWaves * 64) void k_moe_xcd(DMat router, const fl
   __syncthreads();
   TL_PHASE(tl, 2);
   // routed ids as wave-uniform values; workgroup 0 publishes ids and weights
-  int eid[8];
   const int rank = wg_rank<NW>(lg, E, lane, wave, part);
   const bool sel = lane < E && rank < 8;
-  ids_by_rank(sel, rank, 8, eid);
-  if (blockIdx.x == 0 && wave == 0) route_weights(lg, sel, rank, 8, lane, eid, ids_out, w_out);
-  int ej = eid[0];
-#pragma unroll
-  for (int q = 1; q < 8; q++) ej = x == q ? eid[q] : ej;
+  if (blockIdx.x == 0 && wave == 0) {
+    int eid[8];
+    ids_by_rank(sel, rank, 8, eid);
+    route_weights(lg, sel, rank, 8, lane, eid, ids_out, w_out);
+  }
+  // the expert of rank x (ids_by_rank's entry x, one ballot instead of eight per wave)
+  const unsigned long long bx = __ballot(sel && rank == x);
+  const int ej = bx ? __ffsll((long long)bx) - 1 : 0;
   TL_PHASE(tl, 3);
 
   // gate/up waves: their pairs of expert ej; down waves: their down rows of ej, requested right away
