@@ -1108,22 +1108,26 @@ __device__ __forceinline__ void wave_argmax(int& bk, int& bi) {
 
 // The rows are cut into slots of RPW rows (one pass of a wave) and the slots are dealt out to the grid's waves in
 // contiguous runs, as evenly as possible (the first S % W waves take one more): with at most as many workgroups as
-// are resident at once, 49155 rows on 3072 waves is 16 slots each and 17 for three waves, instead of a 769th
-// workgroup waiting for a free slot. A wave streams its run in batches of P slots, the next batch's loads issued
+// are resident at once, 49155 rows on 3072 waves is 16 slots each and 17 for three waves, instead of a workgroup
+// waiting for a free compute unit. A wave streams its run in batches of P slots, the next batch's loads issued
 // before the current batch's arithmetic.
-template <int DT, int K, int P>
-__global__ __launch_bounds__(kBlock) void k_head(DMat m, const float* __restrict__ h, const float* __restrict__ lnw,
-                                                 float eps, float ls, float* __restrict__ logits,
-                                                 int2* __restrict__ best, Tl tl) {
+// One workgroup of NT threads per compute unit: its activation loads are the first requests of the compute unit
+// (every wave's, ahead of any row, through a bare barrier), so the norm completes at once instead of behind the rows
+// of other workgroups on the same compute unit.
+template <int DT, int K, int P, int NT>
+__global__ __launch_bounds__(NT) void k_head(DMat m, const float* __restrict__ h, const float* __restrict__ lnw,
+                                             float eps, float ls, float* __restrict__ logits,
+                                             int2* __restrict__ best, Tl tl) {
   TL_START(tl);
   using G = Geo<DT, K>;
+  constexpr int NWB = NT / kWave;
   __shared__ float xs[K];
   __shared__ float rs;
-  __shared__ int sk[kWavesPerBlock], si[kWavesPerBlock];
+  __shared__ int sk[NWB], si[NWB];
   int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   int sub = lane % G::LPR, rw = lane / G::LPR;
-  const int slots = (m.rows + G::RPW - 1) / G::RPW, waves = gridDim.x * kWavesPerBlock;
-  const int wv = blockIdx.x * kWavesPerBlock + wave;
+  const int slots = (m.rows + G::RPW - 1) / G::RPW, waves = gridDim.x * NWB;
+  const int wv = blockIdx.x * NWB + wave;
   const int base = slots / waves, extra = slots % waves;
   const int s0 = wv * base + min(wv, extra), ns = base + (wv < extra ? 1 : 0);
   const int nbat = (ns + P - 1) / P;
@@ -1137,11 +1141,13 @@ __global__ __launch_bounds__(kBlock) void k_head(DMat m, const float* __restrict
     }
   };
   batch_rows(0);
-  NormIn<K, kBlock> hin;
-  norm_fetch<K, kBlock>(h, lnw, hin);
+  NormIn<K, NT> hin;
+  norm_fetch<K, NT>(h, lnw, hin);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
   Rows<DT, K, P> cur, nxt;
   rows_load<DT, K, P>(cur, m, row, ok, sub);
-  norm_finish<K, kBlock>(hin, eps, xs, &rs);
+  norm_finish<K, NT>(hin, eps, xs, &rs);
   TL_PHASE(tl, 2);
   XReg<DT, K> xr;
   load_x<DT, K>(xr, xs, sub);
@@ -1181,7 +1187,7 @@ __global__ __launch_bounds__(kBlock) void k_head(DMat m, const float* __restrict
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < kWavesPerBlock; w++)
+    for (int w = 1; w < NWB; w++)
       if (later_better(sk[w], si[w], bk, bi)) {
         bk = sk[w];
         bi = si[w];
@@ -1576,22 +1582,24 @@ hipError_t launch_expert_down(hipStream_t s, const LayerDev& L, const Dims& d, c
 #undef DOWN_DISPATCH
 
 constexpr int kHeadNB = 4;
+constexpr int kHeadNT = 768;  // threads of a k_head workgroup
 
 // Rows of the head per workgroup at kHeadNB batches per wave (the grid's upper bound: the rows are then dealt out
 // to the resident waves).
 static int head_groups(const DMat& head) {
   int ce = head.dtype == DT_Q8_0 ? 16 : head.dtype == DT_Q4_0 ? 32 : 4;
   int rpw = kWave / lanes_per_row(head.cols / ce);
-  return cdiv(head.rows, kWavesPerBlock * kHeadNB * kHeadP * rpw);
+  return cdiv(head.rows, kHeadNT / kWave * kHeadNB * kHeadP * rpw);
 }
 
-// Workgroups of k_head<DT, K> resident on the device at once (occupancy x compute units).
+// Workgroups of k_head<DT, K> resident on the device at once (occupancy x compute units; one per compute unit at
+// 768 threads).
 template <int DT, int K>
 static int head_resident() {
   int dev = 0, cus = 0, per_cu = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_head<DT, K, kHeadP>, kBlock, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_head<DT, K, kHeadP, kHeadNT>, kHeadNT, 0) != hipSuccess ||
       cus < 1 || per_cu < 1)
     return 1 << 30;  // unknown: the group count alone
   return cus * per_cu;
@@ -1616,7 +1624,7 @@ hipError_t launch_head(hipStream_t s, const DMat& head, const float* norm, const
   const int grid = head_blocks(head);
 #define BODY(KK)                                                                                        \
   case KK:                                                                                              \
-    klaunch(k_head<DTC, KK, kHeadP>, grid, kBlock, 0, s, head, b.h, norm, d.eps, d.logits_scaling, b.logits, \
+    klaunch(k_head<DTC, KK, kHeadP, kHeadNT>, grid, kHeadNT, 0, s, head, b.h, norm, d.eps, d.logits_scaling, b.logits, \
             b.best, tl);                                                                                \
     break;
   MOERT_DISPATCH(head.dtype, head.cols, BODY)
