@@ -249,6 +249,21 @@ typedef enum {
 } moert_kernel_kind;
 int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch, int* launches);
 
+/* Which kernels the model's decode step launches: *attn_block = 1 when the attention half is the one-launch
+ * attention block (MOERT_K_ATTN_BLOCK) rather than q/k/v + split attention + combine, *moe_xcd = 1 when the MoE
+ * half is the kernel spread over the XCDs (MOERT_K_MOE_XCD) rather than router + gate/up and down. Both depend on
+ * the shapes, the model kind and its modes (the cache's prefetch branch uses neither). No reference counterpart. */
+int moert_model_path(const moert_model* m, int* attn_block, int* moe_xcd);
+
+/* Test hook for the failure path of the fused kernels (MOERT_K_ATTN_BLOCK, MOERT_K_MOE_XCD); it has no counterpart
+ * in the reference. `bits` (a subset of 2 = the wait for queries / the new K/V row, 4 = the wait for split partials,
+ * 8 = the wait for an expert's act vector; 0 clears the mask) makes the named waits of the following launches look
+ * for an epoch no launch writes, with every wait of those launches bounded to a few hundred polls, so that the wait
+ * gives up and the kernels still end normally; the next synchronising call then reports MOERT_E_DEVICE naming the
+ * wait, and the model is poisoned. MOERT_E_CONFIG for an expert-cache or hybrid model, or one that does not use
+ * the fused kernels. */
+int moert_fault_inject(moert_model* m, unsigned bits);
+
 /* Phase timeline of one decode step (measurement build libmoert_tl.so only; MOERT_E_CONFIG otherwise): one graph
  * replay in which every workgroup of every launch stamps the 100 MHz real-time clock at its phase boundaries.
  * out receives [launches][1024][8] u64 records: word 0 = ~(earliest wave start), word 1 = latest wave start,

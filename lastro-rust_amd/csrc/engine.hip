@@ -270,8 +270,11 @@ struct moert_model {
       tl_layer.push_back(layer);
       return t;
     };
+    // the prefetch branch's kernels run beside the attention half on a second stream, so the attention block
+    // (whose workgroups must all be resident at once, dispatched round-robin over the XCDs) is not used with it
+    const bool use_blk = use_ab && !(cached && prefetch);
     CHECK_HIP(
-        launch_embed(stream, embed, dims, b, ab.step_ctr, use_ab ? ab.rope_cur : nullptr, arm(MOERT_K_EMBED, -1)));
+        launch_embed(stream, embed, dims, b, ab.step_ctr, use_blk ? ab.rope_cur : nullptr, arm(MOERT_K_EMBED, -1)));
     for (size_t l = 0; l < layers.size(); l++) {
       const LayerDev& L = layers[l];
       const int li = (int)l;
@@ -288,7 +291,7 @@ struct moert_model {
         CHECK_HIP(hipEventRecord(ev_copy, pf_stream));
       }
       const bool cmb = use_mx && li > 0;  // the previous layer's experts are combined by this attention block
-      if (use_ab) {
+      if (use_blk) {
         CHECK_HIP(launch_attn_block(stream, L, dims, b, cus, li, ab, cmb, arm(MOERT_K_ATTN_BLOCK, li)));
       } else {
         CHECK_HIP(launch_qkv(stream, L, dims, b, arm(MOERT_K_QKV, li)));
@@ -315,6 +318,7 @@ struct moert_model {
     return MOERT_OK;
   }
   int ev_i = 0;
+  unsigned long long steps_since_clear = 0;  // steps launched since the exchange areas were last cleared
   // timeline records (measurement build): kTlRecord words per launch of a step
   static constexpr size_t kTlRecord = (size_t)kTlMaxBlocks * kTlPhases;
   unsigned long long* tl_buf = nullptr;
@@ -844,7 +848,7 @@ static int model_create(const moert_config* c, const moert_model_weights* w, int
     unsigned *grp = nullptr, *mx = nullptr;
     if ((rc = zeros(a, s, 8 * sizeof(AbGroup) / 4, &grp)) || (rc = zeros(a, s, 8 * sizeof(MxGroup) / 4, &mx)) ||
         (rc = zeros(a, s, (size_t)8 * H, &m->ab.ys)) || (rc = zeros(a, s, (size_t)H, &b.hc)) ||
-        (rc = zeros(a, s, (size_t)1, &m->ab.step_ctr)) || (rc = zeros(a, s, (size_t)1, &m->ab.err)) ||
+        (rc = zeros(a, s, (size_t)1, &m->ab.step_ctr)) || (rc = zeros(a, s, (size_t)2, &m->ab.err)) ||
         (rc = zeros(a, s, (size_t)64, &m->ab.rope_cur)))
       return bail(rc);
     m->ab.groups = reinterpret_cast<AbGroup*>(grp);
@@ -1075,7 +1079,22 @@ static bool use_graph() {
   return on;
 }
 
+// A launch's epoch is step_ctr * 64 + layer + 1 in 32 bits. Before the step counter could reach 2^26 - 1 (where
+// epochs would wrap, and an exchange entry left by a launch of long ago could carry a current epoch), the exchange
+// areas and the counter are cleared in stream order: every entry back to epoch 0, which no launch writes.
+constexpr unsigned long long kEpochSteps = (1ull << 26) - 2;
+static int epoch_guard(moert_model* m) {
+  if (++m->steps_since_clear < kEpochSteps) return MOERT_OK;
+  CHECK_HIP(hipMemsetAsync(m->ab.groups, 0, 8 * sizeof(AbGroup), m->stream));
+  CHECK_HIP(hipMemsetAsync(m->ab.moe, 0, 8 * sizeof(MxGroup), m->stream));
+  CHECK_HIP(hipMemsetAsync(m->ab.step_ctr, 0, 4, m->stream));
+  m->steps_since_clear = 1;
+  return MOERT_OK;
+}
+
 static int model_launch(moert_model* m) {
+  int rc = epoch_guard(m);
+  if (rc) return rc;
   if (m->hybrid) return m->hybrid_step();
   if (!use_graph()) return m->enqueue(-1, nullptr);
   CHECK_HIP(hipGraphLaunch(m->exec, m->stream));
@@ -1652,6 +1671,7 @@ static int time_kernel_impl(moert_model* m, int kind, int iters, double* us, int
   double total = 0.0;
   int n = 0;
   for (int it = 0; it < iters; it++) {
+    TRY(epoch_guard(m));
     TRY(m->enqueue(kind, &ev));
     const int per_step = m->ev_i / 2;
     CHECK_HIP(hipStreamSynchronize(m->stream));
@@ -1668,6 +1688,29 @@ static int time_kernel_impl(moert_model* m, int kind, int iters, double* us, int
   if (launches) *launches = n;
   m->host_pos += iters;
   return MOERT_OK;
+}
+
+int moert_model_path(const moert_model* m, int* attn_block, int* moe_xcd) {
+  if (!m || !attn_block || !moe_xcd) {
+    set_err("model_path: null argument");
+    return MOERT_E_CONFIG;
+  }
+  const bool blk = m->use_ab && !(m->cached && m->prefetch);
+  *attn_block = blk ? 1 : 0;
+  *moe_xcd = blk && m->use_mx ? 1 : 0;
+  return MOERT_OK;
+}
+
+int moert_fault_inject(moert_model* m, unsigned bits) {
+  MODEL_OK(m);
+  CHECK_CFG((bits & ~14u) == 0, "fault_inject: bits %#x outside 2 | 4 | 8", bits);
+  // resident models only: there every index a failed launch leaves behind (token, routed expert) is still in range,
+  // while the expert cache would take slot-table decisions from the garbage values of a failed launch
+  CHECK_CFG(m->use_ab && !m->hybrid && !m->cached, "fault_inject: a resident model with the fused kernels only");
+  CHECK_CFG(bits == 0 || (bits & 8u) == 0 || m->use_mx, "fault_inject: bit 8 needs the MoE kernel spread over the XCDs");
+  MTRY(m, model_sync(m));
+  MTRY(m, model_copy_in(m, m->ab.err + 1, &bits, 4));
+  return m->fail(model_sync(m));
 }
 
 int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch, int* launches) {

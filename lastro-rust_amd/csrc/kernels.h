@@ -71,9 +71,17 @@ struct AbBufs {
   float* ys;           // [8][hidden]: down output of the expert of each routing rank (k_moe_xcd)
   unsigned* step_ctr;  // decode steps started (k_embed adds one); a launch's epoch is step_ctr * 64 + layer + 1
   float* rope_cur;     // [64]: the rope row (cos, then sin) of the step's position (k_embed copies it)
-  unsigned* err;       // bits 1, 2: a wait for values of a KV head's workgroups (queries and K/V row, partials) gave up;
-                       // bit 3: a wait for the act values of an XCD's expert gave up
+  // err[0]: bits 1, 2: a wait for values of a KV head's workgroups (queries and K/V row, partials) gave up; bit 3: a
+  // wait for the act values of an XCD's expert gave up. A launch that finds a bit set at its start waits for nothing
+  // (its waits give up at once and set no further bit), so a failure costs at most one launch of bounded waits.
+  // err[1]: a test mask that only the host writes (moert_fault_inject): a wait whose bit is set there looks for an
+  // epoch no launch writes (kNoEpoch), and every wait of a launch that sees a nonzero mask polls at most kInjectSpin
+  // times, so the failure path runs with every kernel still ending normally.
+  unsigned* err;
 };
+constexpr unsigned kNoEpoch = 0xffffffffu;  // stored by no launch: epochs stay below 2^32 - 64 (the host clears the
+                                            // exchange areas and the step counter before that)
+constexpr int kInjectSpin = 256;
 
 // tl: the launch's timeline record (measurement build; null otherwise). step_ctr (may be null): incremented once.
 // rope_cur (may be null): receives the 64-float rope row of the step's position (head_dim 64).

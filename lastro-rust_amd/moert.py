@@ -138,6 +138,8 @@ def lib() -> ctypes.CDLL:
             "moert_read_logits": (i, [vp, vp]),
             "moert_time_steps": (i, [vp, i, i, ctypes.POINTER(ctypes.c_double)]),
             "moert_time_kernel": (i, [vp, i, i, ctypes.POINTER(ctypes.c_double), ip]),
+            "moert_fault_inject": (i, [vp, ctypes.c_uint]),
+            "moert_model_path": (i, [vp, ip, ip]),
             "moert_timeline_step": (i, [vp, vp, vp, vp, i, ip]),
             "moert_block_create": (i, [i, i, i, i, ctypes.POINTER(moert_tensor), vp, ctypes.POINTER(moert_tensor),
                                        ctypes.POINTER(moert_tensor), ctypes.POINTER(vp)]),
@@ -224,7 +226,7 @@ EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moer
             "moert_decode_step", "moert_generate", "moert_step_batched", "moert_prefill", "moert_reset_sequence",
             "moert_kv_prefill_fp16",
             "moert_set_position", "moert_get_position", "moert_read_kv_fp16", "moert_read_hidden", "moert_read_logits",
-            "moert_time_steps", "moert_time_kernel", "moert_timeline_step", "moert_block_create", "moert_block_destroy",
+            "moert_time_steps", "moert_time_kernel", "moert_fault_inject", "moert_model_path", "moert_timeline_step", "moert_block_create", "moert_block_destroy",
             "moert_block_forward", "moert_block_time", "moert_block_forward_batched",
             "moert_block_experts_in_step", "moert_block_time_batched", "moert_router_topk", "moert_argmax", "moert_gemv",
             "moert_dequant", "moert_rmsnorm", "moert_rope", "moert_attn_decode", "moert_attn_decode_noalloc",
@@ -585,6 +587,17 @@ class GpuModel:
         us, n = ctypes.c_double(0), ctypes.c_int(0)
         check(lib().moert_time_kernel(self.h, kind, iters, ctypes.byref(us), ctypes.byref(n)))
         return us.value, n.value
+
+    def kernel_path(self):
+        """(attention block used, MoE kernel over the XCDs used) by the decode step (moert_model_path)."""
+        a, x = ctypes.c_int(0), ctypes.c_int(0)
+        check(lib().moert_model_path(self.h, ctypes.byref(a), ctypes.byref(x)))
+        return bool(a.value), bool(x.value)
+
+    def fault_inject(self, bits: int):
+        """Test hook: the fused kernels' waits named by `bits` (2 queries / K/V row, 4 split partials, 8 act vector)
+        give up in the following launches, which still end normally (moert_fault_inject)."""
+        check(lib().moert_fault_inject(self.h, bits))
 
 
 # ---- checkpoints ------------------------------------------------------------------------------------------------

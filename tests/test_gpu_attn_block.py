@@ -192,3 +192,142 @@ def test_moe_spread_over_the_xcds_equals_route_up_and_down(gpu, granite_3b):
     assert launches(a, moert.K_MOE_XCD) == cfg.layers and launches(a, moert.K_EXPERT_DOWN) == 0
     a.close()
     b.close()
+
+
+@pytest.fixture(scope="module")
+def granite_1b_wide():
+    cfg = moert.Config(**moert.GRANITE_1B)
+    say("1B wide build")
+    return cfg, moert.SynthModel(cfg, seed=2024, wdtype=moert.Q8_0, embed_dtype=moert.F32, std=0.1)
+
+
+WAIT_NAMES = {2: "the wait for queries / the new K/V row", 4: "the wait for split partials",
+              8: "the wait for an expert's act vector"}
+
+
+@pytest.mark.parametrize("bit", [2, 4, 8])
+def test_a_wait_that_gives_up_is_reported_and_poisons_the_handle(gpu, granite_1b_wide, bit):
+    """The failure path of the fused kernels, forced from the host (moert_fault_inject: the named wait looks for an
+    epoch no launch writes, every wait of those launches is bounded to a few hundred polls, and every kernel still
+    ends): a 64-step generate reports MOERT_E_DEVICE naming that wait, the launches queued after the failure wait
+    for nothing (the whole call ends within seconds), the handle is poisoned, and a fresh model in the same process
+    decodes bit for bit like the oracle."""
+    import time
+    cfg, m = granite_1b_wide
+    g = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
+    assert g.kernel_path() == (True, True)
+    g.step(5)
+    say(f"fault inject bit {bit}")
+    g.fault_inject(bit)
+    t0 = time.time()
+    with pytest.raises(moert.MoertError) as e:
+        g.generate([7], 64)
+    dt = time.time() - t0
+    assert e.value.code == moert.E_DEVICE, str(e.value)
+    msg = str(e.value)
+    assert WAIT_NAMES[bit] in msg and f"error bits {bit:#x}" in msg, msg
+    for other, name in WAIT_NAMES.items():
+        assert other == bit or name not in msg, msg
+    assert dt < 20, dt
+    with pytest.raises(moert.MoertError) as e:
+        g.step(5)
+    assert e.value.code == moert.E_POISONED
+    g.close()
+    say("fresh model after the failure")
+    f = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
+    s = oracle.CpuSession(m, MAX_LEN, attn_splits=SPLITS, threads=THREADS)
+    for t, tok in enumerate(np.random.default_rng(51).integers(0, cfg.vocab, 12)):
+        lg, ids, w, am = f.step(int(tok))
+        olg, oids, ow, _ = s.step(int(tok))
+        assert bits_equal(lg, olg) and np.array_equal(ids, oids) and bits_equal(w, ow), t
+    f.close()
+
+
+def test_fault_inject_refusals(gpu, granite_1b_wide):
+    cfg, m = granite_1b_wide
+    g = three_kernel_model(m, MAX_LEN, SPLITS)
+    assert g.kernel_path() == (False, False)
+    with pytest.raises(moert.MoertError) as e:
+        g.fault_inject(2)
+    assert e.value.code == moert.E_CONFIG
+    g.close()
+    g = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
+    with pytest.raises(moert.MoertError) as e:
+        g.fault_inject(1)
+    assert e.value.code == moert.E_CONFIG
+    g.fault_inject(0)  # an empty mask is a no-op
+    g.step(3)
+    g.close()
+
+
+def test_prefetch_branch_uses_the_three_kernel_attention(gpu):
+    """The cache's prefetch branch runs its kernels beside the attention half on a second stream, which the attention
+    block (all workgroups resident at once) does not allow: with the branch on, the cached model at the bench's cache
+    shape launches no attention block, and its logits equal the resident three-kernel model's bit for bit; with the
+    branch off again it uses the block again, with the same logits."""
+    cfg = moert.Config(**moert.GRANITE_1B)
+    say("1B cached build (prefetch)")
+    m = moert.SynthModel(cfg, seed=78, wdtype=moert.Q8_0, embed_dtype=moert.Q8_0, zipf_s=1.1)
+    res = three_kernel_model(m, MAX_LEN, SPLITS)
+    cac = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS, cache_slots=192)
+    assert cac.kernel_path() == (True, False)
+    cac.cache_prefetch_mode(True)
+    assert cac.kernel_path() == (False, False)
+    toks = np.random.default_rng(46).integers(0, cfg.vocab, 40)
+    for t, tok in enumerate(toks):
+        if t == 20:
+            cac.cache_prefetch_mode(False)
+            assert cac.kernel_path() == (True, False)
+        lr, ir, wr, _ = res.step(int(tok))
+        lc, ic, wc, _ = cac.step(int(tok))
+        assert bits_equal(lr, lc) and np.array_equal(ir, ic) and bits_equal(wr, wc), t
+    cac.cache_prefetch_mode(True)
+    assert launches(cac, moert.K_ATTN_BLOCK) == 0 and launches(cac, moert.K_QKV) == cfg.layers
+    res.close()
+    cac.close()
+
+
+def test_hybrid_with_the_attention_block_equals_the_three_kernel_hybrid(gpu):
+    """The host-CPU hybrid at the bench's cache shape uses the attention block: 32 forced steps with a 96-slot pool
+    and backlog 4 give the same logits bit for bit as the same hybrid built with the three-kernel attention (the
+    placement decides alike, the host part is computed alike), and the same placement counters."""
+    cfg = moert.Config(**moert.GRANITE_1B)
+    say("1B hybrid build")
+    m = moert.SynthModel(cfg, seed=79, wdtype=moert.Q8_0, embed_dtype=moert.Q8_0, zipf_s=1.1)
+    a = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS, hybrid=(96, 4, 4))
+    b = three_kernel_model(m, MAX_LEN, SPLITS, hybrid=(96, 4, 4))
+    assert a.kernel_path() == (True, False) and b.kernel_path() == (False, False)
+    for t, tok in enumerate(np.random.default_rng(48).integers(0, cfg.vocab, 32)):
+        la, ia, wa, _ = a.step(int(tok))
+        lb, ib, wb, _ = b.step(int(tok))
+        assert bits_equal(la, lb) and np.array_equal(ia, ib) and bits_equal(wa, wb), t
+    assert a.cache_counters() == b.cache_counters()
+    a.close()
+    b.close()
+
+
+def test_prefill_then_fused_decode_equals_the_oracle(gpu, granite_1b_wide):
+    """A 70-token block prefill (multi-position kernels) into the bench's cache shape, then 24 forced decode steps
+    through the fused kernels: the prefill's last logits and every decode step's logits, routes and weights equal
+    the oracle's session, and every KV row."""
+    cfg, m = granite_1b_wide
+    g = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
+    s = oracle.CpuSession(m, MAX_LEN, attn_splits=SPLITS, threads=THREADS)
+    rng = np.random.default_rng(52)
+    prompt = rng.integers(0, cfg.vocab, 70)
+    say("prefill 70 into 4416/32")
+    plg, pam = g.prefill(prompt)
+    for tok in prompt:
+        olg = s.step(int(tok))[0]
+    assert bits_equal(plg, olg) and pam == oracle.argmax(olg)
+    for t, tok in enumerate(rng.integers(0, cfg.vocab, 24)):
+        lg, ids, w, am = g.step(int(tok))
+        olg, oids, ow, _ = s.step(int(tok))
+        assert bits_equal(lg, olg) and np.array_equal(ids, oids) and bits_equal(w, ow), t
+    for l in range(cfg.layers):
+        gk, gv = g.read_kv(l, 94)
+        ok, ov = s.read_kv(l, 94)
+        assert np.array_equal(gk, ok) and np.array_equal(gv, ov), l
+    assert g.kernel_path() == (True, True)
+    assert launches(g, moert.K_ATTN_BLOCK) == cfg.layers and launches(g, moert.K_MOE_XCD) == cfg.layers
+    g.close()

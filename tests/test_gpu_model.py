@@ -1,7 +1,8 @@
 """Whole decode steps through the C ABI against the oracle's CpuSession on the same seeded model: logits, hidden
 state, routing (ids and weights) and the KV cache are compared bit for bit, and greedy sequences token for token.
 Workloads: the reference's synthetic test shapes (tests/model.rs:253-281), the 1B model with a 128-token prompt
-and 256 generated tokens, and the 3B model at 4096 cached positions with 256 decode steps."""
+and 256 generated tokens, and the 3B model at 4096 cached positions with 256 decode steps, each through the fused
+kernels the bench times and through the unfused ones."""
 import os
 
 import numpy as np
@@ -131,6 +132,33 @@ def _forced_identity(g, s, toks, label, every=1):
     assert bits_equal(g.hidden(), oh)
 
 
+# The decode step has two kernel paths: the fused one the bench times (the attention half as one attention-block
+# launch, the MoE half as one launch spread over the XCDs) where the cache shape gives 2..4 tiles per split and at
+# most 32 splits, and the unfused one (q/k/v, split attention, combine; router + gate/up, down) otherwise. Each long
+# run below goes through both, and asserts which one ran.
+PATHS_1B = {"fused": (4416, 32), "unfused": (448, 64)}  # 4416/32: 23 splits of 3 tiles; 448/64: 7 splits of 1 tile
+PATHS_3B = {"fused": (4416, 32), "unfused": (4352, 64)}  # 4352/64: 34 splits of 2 tiles (over the 32-split bound)
+
+
+def assert_kernel_path(g, cfg, path):
+    """The step's kernels: the model's own report, then the launches of one step (run last: it moves the position
+    to the cache's end)."""
+    fused = path == "fused"
+    assert g.kernel_path() == (fused, fused)
+    n = {}
+    for k in (moert.K_ATTN_BLOCK, moert.K_MOE_XCD, moert.K_QKV, moert.K_ROUTE_UP, moert.K_EXPERT_DOWN,
+              moert.K_MOE_COMBINE):
+        g.set_position(g.max_len - 1)
+        n[k] = g.time_kernel(k, 1)[1]
+    L = cfg.layers
+    if fused:
+        assert n == {moert.K_ATTN_BLOCK: L, moert.K_MOE_XCD: L, moert.K_QKV: 0, moert.K_ROUTE_UP: 0,
+                     moert.K_EXPERT_DOWN: 0, moert.K_MOE_COMBINE: 1}, n
+    else:
+        assert n == {moert.K_ATTN_BLOCK: 0, moert.K_MOE_XCD: 0, moert.K_QKV: L, moert.K_ROUTE_UP: L,
+                     moert.K_EXPERT_DOWN: L, moert.K_MOE_COMBINE: 0}, n
+
+
 @pytest.fixture(scope="module")
 def granite_1b():
     cfg = moert.Config(**moert.GRANITE_1B)
@@ -138,42 +166,51 @@ def granite_1b():
     return cfg, moert.SynthModel(cfg, seed=2024, wdtype=moert.Q8_0, embed_dtype=moert.F32)
 
 
-def test_granite_1b_greedy_128_prompt_256_tokens_identical(gpu, granite_1b):
+def _pair_1b(m, path):
+    max_len, splits = PATHS_1B[path]
+    return (moert.GpuModel(m, max_len, attn_splits=splits),
+            oracle.CpuSession(m, max_len, attn_splits=splits, threads=THREADS))
+
+
+@pytest.mark.parametrize("path", ["fused", "unfused"])
+def test_granite_1b_greedy_128_prompt_256_tokens_identical(gpu, granite_1b, path):
     """Granite-1B-A400M shape, Q8_0 weights, fp32 embedding/head; 128-token uniform prompt, 256 greedy tokens:
     identical tokens, last logits and hidden state bit for bit, every KV row the run appended. (With N(0, 0.02)
     weights and a tied head the greedy run settles on one token; the forced and wider-init tests below cover
     trajectories that move.)"""
     cfg, m = granite_1b
     prompt = np.random.default_rng(2024).integers(0, cfg.vocab, 128)
-    g = moert.GpuModel(m, 448, attn_splits=64)
-    s = oracle.CpuSession(m, 448, attn_splits=64, threads=THREADS)
-    _greedy_identity(g, s, prompt, 256, "1B")
+    g, s = _pair_1b(m, path)
+    _greedy_identity(g, s, prompt, 256, f"1B {path}")
     _kv_rows_equal(g, s, cfg, 0, 128 + 255)
+    assert_kernel_path(g, cfg, path)
     g.close()
 
 
-def test_granite_1b_forced_tokens_every_step_bit_identical(gpu, granite_1b):
+@pytest.mark.parametrize("path", ["fused", "unfused"])
+def test_granite_1b_forced_tokens_every_step_bit_identical(gpu, granite_1b, path):
     """The 1B workload with a forced random token stream over its 384 positions (128 prompt + 256): logits, routes
     and weights of every step, the final hidden state and every KV row, bit for bit."""
     cfg, m = granite_1b
     toks = np.random.default_rng(99).integers(0, cfg.vocab, 384)
-    g = moert.GpuModel(m, 448, attn_splits=64)
-    s = oracle.CpuSession(m, 448, attn_splits=64, threads=THREADS)
-    _forced_identity(g, s, toks, "1B")
+    g, s = _pair_1b(m, path)
+    _forced_identity(g, s, toks, f"1B {path}")
     _kv_rows_equal(g, s, cfg, 0, 384)
+    assert_kernel_path(g, cfg, path)
     g.close()
 
 
-def test_granite_1b_wider_init_greedy_moves_and_stays_identical(gpu):
+@pytest.mark.parametrize("path", ["fused", "unfused"])
+def test_granite_1b_wider_init_greedy_moves_and_stays_identical(gpu, path):
     """The 1B shape with N(0, 0.1) weights, whose greedy trajectory does not settle: 128-token prompt, 256 greedy
     tokens identical to the oracle (at least 100 distinct), last logits and hidden state bit for bit."""
     cfg = moert.Config(**moert.GRANITE_1B)
     say("1B wide build")
     m = moert.SynthModel(cfg, seed=2024, wdtype=moert.Q8_0, embed_dtype=moert.F32, std=0.1)
     prompt = np.random.default_rng(2025).integers(0, cfg.vocab, 128)
-    g = moert.GpuModel(m, 448, attn_splits=64)
-    s = oracle.CpuSession(m, 448, attn_splits=64, threads=THREADS)
-    _greedy_identity(g, s, prompt, 256, "1B wide", min_distinct=100)
+    g, s = _pair_1b(m, path)
+    _greedy_identity(g, s, prompt, 256, f"1B wide {path}", min_distinct=100)
+    assert_kernel_path(g, cfg, path)
     g.close()
 
 
@@ -184,9 +221,10 @@ def _granite_3b(std):
     return cfg, m, [moert.kv_prefill_data(cfg, 3003, l, 4096) for l in range(cfg.layers)]
 
 
-def _prefilled_pair(cfg, m, kv, max_len=4352, ctx=4096):
-    g = moert.GpuModel(m, max_len, attn_splits=64)
-    s = oracle.CpuSession(m, max_len, attn_splits=64, threads=THREADS)
+def _prefilled_pair(cfg, m, kv, path, ctx=4096):
+    max_len, splits = PATHS_3B[path]
+    g = moert.GpuModel(m, max_len, attn_splits=splits)
+    s = oracle.CpuSession(m, max_len, attn_splits=splits, threads=THREADS)
     for l, (k, v) in enumerate(kv):
         g.kv_prefill(l, k, v)
         s.kv_prefill(l, k, v)
@@ -200,42 +238,53 @@ def granite_3b():
     return _granite_3b(0.02)
 
 
-def test_granite_3b_long_context_256_steps_identical(gpu, granite_3b):
+@pytest.mark.parametrize("path", ["fused", "unfused"])
+def test_granite_3b_long_context_256_steps_identical(gpu, granite_3b, path):
     """Granite-3B-A800M shape, Q8_0 weights and head; KV cache pre-filled to 4096 positions with fp16 N(0,1);
     256 decode steps: the first step's logits and routes, the greedy tokens, the last step's logits and hidden state,
     and the 256 KV rows of every layer, bit for bit."""
     cfg, m, kv = granite_3b
-    g, s = _prefilled_pair(cfg, m, kv)
+    g, s = _prefilled_pair(cfg, m, kv, path)
     tok = int(np.random.default_rng(3003).integers(0, cfg.vocab))
-    say("3B first step")
+    say(f"3B {path} first step")
     lg, ids, w, am = g.step(tok)
     olg, oids, ow, _ = s.step(tok)
     assert bits_equal(lg, olg) and np.array_equal(ids, oids) and bits_equal(w, ow)
     assert am == oracle.argmax(olg)
-    _greedy_identity(g, s, [am], 255, "3B")
+    _greedy_identity(g, s, [am], 255, f"3B {path}")
     _kv_rows_equal(g, s, cfg, 4096, 4352)
+    assert_kernel_path(g, cfg, path)
     g.close()
 
 
-def test_granite_3b_forced_tokens_at_4096_every_step_bit_identical(gpu, granite_3b):
+@pytest.mark.parametrize("path", ["fused", "unfused"])
+def test_granite_3b_forced_tokens_at_4096_every_step_bit_identical(gpu, granite_3b, path):
     """The 3B workload with a forced random token stream: 256 steps after the 4096 cached positions, logits, routes
     and weights of every step, the final hidden state and the appended KV rows, bit for bit."""
     cfg, m, kv = granite_3b
-    g, s = _prefilled_pair(cfg, m, kv)
+    g, s = _prefilled_pair(cfg, m, kv, path)
     toks = np.random.default_rng(31).integers(0, cfg.vocab, 256)
-    _forced_identity(g, s, toks, "3B")
+    _forced_identity(g, s, toks, f"3B {path}")
     _kv_rows_equal(g, s, cfg, 4096, 4352)
+    assert_kernel_path(g, cfg, path)
     g.close()
 
 
-def test_granite_3b_wider_init_greedy_moves_and_stays_identical(gpu):
+@pytest.fixture(scope="module")
+def granite_3b_wide():
+    return _granite_3b(0.1)
+
+
+@pytest.mark.parametrize("path", ["fused", "unfused"])
+def test_granite_3b_wider_init_greedy_moves_and_stays_identical(gpu, granite_3b_wide, path):
     """The 3B long-context workload with N(0, 0.1) weights, whose greedy trajectory does not settle: 256 greedy steps
     after 4096 cached positions, identical tokens (at least 100 distinct), last logits and hidden state bit for
     bit."""
-    cfg, m, kv = _granite_3b(0.1)
-    g, s = _prefilled_pair(cfg, m, kv)
+    cfg, m, kv = granite_3b_wide
+    g, s = _prefilled_pair(cfg, m, kv, path)
     tok = int(np.random.default_rng(7).integers(0, cfg.vocab))
-    _greedy_identity(g, s, [tok], 256, "3B wide", min_distinct=100)
+    _greedy_identity(g, s, [tok], 256, f"3B wide {path}", min_distinct=100)
+    assert_kernel_path(g, cfg, path)
     g.close()
 
 
