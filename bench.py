@@ -7,7 +7,8 @@ pre-filled with N(0, 1) to 4096 positions. A step is one decode token (the whole
 device); the timed region replays the captured step graph K times with the token fed back on the device.
 
 Prints one JSON line: tok/s, the HBM roofline of the dominant kernel (HIP events around its launches on the
-engine's stream) and the oracle's CPU decode rate on this host as the CPU baseline.
+engine's stream) and, as the CPU baseline, the decode rate on this host of a C++ port of the reference's CPU path
+(oracle/cpu_port.cpp).
 """
 import argparse
 import json
@@ -255,14 +256,39 @@ def expert_cache(cfg, seed, steps, frac=0.25, hybrid_steps=128):
     return out
 
 
+def host_cpu():
+    """The host's logical CPU count, the cores this process may run on, the per-GPU share the host sets through
+    OMP_NUM_THREADS (when set), and the CPU model name."""
+    nproc = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = nproc
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    usable = min(affinity, int(share)) if share.isdigit() and int(share) > 0 else affinity
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": nproc, "affinity": affinity, "usable": usable, "model": model}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--kernel-iters", type=int, default=6)
-    ap.add_argument("--cpu-steps", type=int, default=32, help="oracle decode steps timed for the CPU baseline")
-    ap.add_argument("--cpu-threads", type=int, default=min(16, os.cpu_count() or 1))
+    ap.add_argument("--cpu-steps", type=int, default=32,
+                    help="decode steps of the CPU port of the reference CPU path timed for the CPU baseline")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="threads of the CPU baseline (0: every core this process may run on, within the host's "
+                         "per-GPU share given by OMP_NUM_THREADS when it is set)")
     ap.add_argument("--seed", type=int, default=3003)
     ap.add_argument("--attn-splits", type=int, default=32,
                     help="KV splits requested for decode attention (tiles per split = ceil(tiles / splits))")
@@ -351,7 +377,9 @@ def main():
     if args.cpu_steps > 0:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle
-        s = oracle.CpuSession(model, max_len, attn_splits=args.attn_splits, threads=args.cpu_threads)
+        hw = host_cpu()
+        threads = args.cpu_threads or hw["usable"]
+        s = oracle.PortSession(model, max_len, threads=threads)
         for l, (k, v) in enumerate(kv):
             s.kv_prefill(l, k, v)
         s.set_position(CTX)
@@ -362,11 +390,13 @@ def main():
             lg = s.step(nxt)[0]
             nxt = oracle.argmax(lg)
         cw = time.perf_counter() - t0
-        cpu = {"value": round(args.cpu_steps / cw, 3), "unit": "tok/s", "cores": args.cpu_threads, "kind": "port",
-               "sample": f"{args.cpu_steps} greedy decode steps of the same 3B model at context {CTX + 1}.."
-                         f"{CTX + args.cpu_steps}, oracle C++ restatement of the reference CPU path, "
-                         f"{args.cpu_threads} threads ({cw:.1f} s)"}
-        log(f"cpu baseline {cpu['value']} tok/s on {args.cpu_threads} threads")
+        cpu = {"value": round(args.cpu_steps / cw, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+               "nproc": hw["nproc"], "affinity": hw["affinity"], "cpu_model": hw["model"],
+               "sample": f"{args.cpu_steps} greedy decode steps of the same 3B Q8_0 model at context {CTX + 1}.."
+                         f"{CTX + args.cpu_steps}: C++ port of the reference CPU path (CpuSession::step, dot_avx2's "
+                         f"4x8-lane accumulation on Q8_0 blocks, 16-row pool tasks, f32 KV, attention on the "
+                         f"calling thread), {threads} threads ({cw:.1f} s)"}
+        log(f"cpu baseline {cpu['value']} tok/s on {threads} threads of {hw['model']} (nproc {hw['nproc']})")
 
     out = {
         "metric": "decode tok/s batch1 (3B-A800M shape); MoE GEMV achieved HBM GB/s vs peak",

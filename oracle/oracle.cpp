@@ -15,6 +15,7 @@
 //   rust/moe-rt/src/gpu.rs:205-292     attn_split / attn_combine      -> orc_attention
 //   rust/moe-rt/src/bin/m1b-gulosa.rs:22-24  argmax (last index wins) -> orc_argmax
 #include "oracle.h"
+#include "pool.h"
 
 #include <atomic>
 #include <cmath>
@@ -26,6 +27,8 @@
 #include <vector>
 
 namespace {
+
+using orc::Pool;
 
 // Rows per pool task (rust/moe-rt/src/cpu.rs:10).
 constexpr int kRowsPerTask = 16;
@@ -164,71 +167,6 @@ struct Dotter {
     dequant_row_lanes(w, dtype, cols, row, wt.data());
     return dot_t(wt.data(), xt.data(), cols, C);
   }
-};
-
-// Fixed set of workers over an atomic task counter; the caller works too (rust/moe-rt/src/pool.rs:96-199).
-class Pool {
- public:
-  explicit Pool(int threads) {
-    for (int i = 1; i < threads; i++) ws_.emplace_back([this] { worker(); });
-  }
-  ~Pool() {
-    {
-      std::lock_guard<std::mutex> l(mu_);
-      stop_ = true;
-    }
-    cv_.notify_all();
-    for (auto& t : ws_) t.join();
-  }
-  int threads() const { return (int)ws_.size() + 1; }
-  void run(size_t n, const std::function<void(size_t)>& f) {
-    if (ws_.empty() || n <= 1) {
-      for (size_t i = 0; i < n; i++) f(i);
-      return;
-    }
-    {
-      std::lock_guard<std::mutex> l(mu_);
-      f_ = &f;
-      n_ = n;
-      next_.store(0);
-      busy_ = (int)ws_.size();
-      gen_++;
-    }
-    cv_.notify_all();
-    for (size_t i; (i = next_.fetch_add(1)) < n;) f(i);
-    std::unique_lock<std::mutex> l(mu_);
-    done_.wait(l, [&] { return busy_ == 0; });
-    f_ = nullptr;
-  }
-
- private:
-  void worker() {
-    uint64_t seen = 0;
-    for (;;) {
-      const std::function<void(size_t)>* f;
-      size_t n;
-      {
-        std::unique_lock<std::mutex> l(mu_);
-        cv_.wait(l, [&] { return stop_ || gen_ != seen; });
-        if (stop_) return;
-        seen = gen_;
-        f = f_;
-        n = n_;
-      }
-      for (size_t i; (i = next_.fetch_add(1)) < n;) (*f)(i);
-      std::lock_guard<std::mutex> l(mu_);
-      if (--busy_ == 0) done_.notify_one();
-    }
-  }
-  std::vector<std::thread> ws_;
-  std::mutex mu_;
-  std::condition_variable cv_, done_;
-  const std::function<void(size_t)>* f_ = nullptr;
-  size_t n_ = 0;
-  std::atomic<size_t> next_{0};
-  int busy_ = 0;
-  uint64_t gen_ = 0;
-  bool stop_ = false;
 };
 
 // y[r] = f(r) in 16-row tasks (Cpu::fill_rows, rust/moe-rt/src/cpu.rs:93-105).
@@ -1026,6 +964,211 @@ int orc_session_step(orc_session* s, int token, float* logits, int* route_ids, f
     for (int v = 0; v < c.vocab; v++) logits[v] = logits[v] / c.logits_scaling;
   }
   s->pos++;
+  return MOERT_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------------------------------------------------
+// The grouped mode of the engine's multi-position step (moert_batched_mode 1): n <= 32 consecutive positions through
+// every layer with each weight GEMM on 15-bit activation codes (the block prefill of rust/moe-rt/src/cuda_dense.rs:
+// 236-288 and motor/leitura.rs:79-85, with the arithmetic of rust/moe-rt/src/cpu.rs:239-296 for the experts). Per
+// layer and position p, in this order:
+//   1. xn = rmsnorm(h_p, ln_attn) in the 256-thread order of norm_codes_256 below, then its codes (orc_quant_hilo);
+//   2. each q/k/v row: dot_hilo_quarters (the row's blocks cut into four quarters, each an fmaf chain over its
+//      blocks of (float)S_b * (d_w * d_x), the quarters added in order); rows (j, j + 32) of a head rotated as RoPE
+//      at position p (x1 c - x2 s, x2 c + x1 s); K and V rounded to fp16 into the cache;
+//   3. split-KV attention over the first pos0 + p + 1 positions (the decode order);
+//   4. the codes of the attention output, then h_p += res * dot_hilo_quarters(o row, codes);
+//   5. xn = rmsnorm(h_p, ln_moe) in the 1024-thread order of norm_1024 below; router logits = canonical dot (+ bias),
+//      Routing::from_logits; the experts of all n positions grouped (orc_experts_grouped: codes of xn, exact block
+//      products, first-appearance list order); h_p += res * y_p.
+// Then the final norm, tied head and logits_scaling of the last position, in the decode order.
+namespace {
+
+// Sum of squares over h[0, H) as 256 threads hold it: thread t the elements 1024 j + 4 t + i (j, then i, in
+// increasing order, those below H), each an fmaf chain from +0; the 64 sums of a wave through the pairwise lane
+// tree; the 4 wave sums added in order.
+float ss_256(const float* h, int H) {
+  float wsum[4];
+  for (int w = 0; w < 4; w++) {
+    float lane[kLanes];
+    for (int l = 0; l < kLanes; l++) {
+      const int t = 64 * w + l;
+      float ss = 0.0f;
+      for (int j = 0; j < (H + 1023) / 1024; j++)
+        for (int i = 0; i < 4; i++) {
+          const int e = 1024 * j + 4 * t + i;
+          const float v = e < H ? h[e] : 0.0f;
+          ss = std::fmaf(v, v, ss);
+        }
+      lane[l] = ss;
+    }
+    for (int st = 1; st < kLanes; st *= 2)
+      for (int l = 0; l < kLanes; l += 2 * st) lane[l] = lane[l] + lane[l + st];
+    wsum[w] = lane[0];
+  }
+  return ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3];
+}
+
+// The same over 1024 threads (16 waves): thread t the elements t, t + 1024, ..., the 16 wave sums added in order
+// from +0.
+float ss_1024(const float* h, int H) {
+  float tot = 0.0f;
+  for (int w = 0; w < 16; w++) {
+    float lane[kLanes];
+    for (int l = 0; l < kLanes; l++) {
+      float ss = 0.0f;
+      for (int e = 64 * w + l; e < H; e += 1024) ss = std::fmaf(h[e], h[e], ss);
+      lane[l] = ss;
+    }
+    for (int st = 1; st < kLanes; st *= 2)
+      for (int l = 0; l < kLanes; l += 2 * st) lane[l] = lane[l] + lane[l + st];
+    tot = tot + lane[0];
+  }
+  return tot;
+}
+
+void norm_with(const float* h, const float* lnw, int H, float eps, float ss, float* xn) {
+  const float r = 1.0f / std::sqrt(ss / (float)H + eps);
+  for (int i = 0; i < H; i++) xn[i] = lnw[i] * (h[i] * r);
+}
+
+float dot_hilo_quarters(const void* w, int dtype, int cols, size_t row, const int8_t* hi, const int8_t* lo,
+                        const float* dx) {
+  const int NB = cols / 32, NBW = NB / 4;
+  int8_t q[32];
+  float part[4];
+  for (int kq = 0; kq < 4; kq++) {
+    float acc = 0.0f;
+    for (int b = kq * NBW; b < (kq + 1) * NBW; b++) {
+      float dw;
+      block_codes(w, dtype, cols, row, b, q, &dw);
+      int32_t sh = 0, sl = 0;
+      for (int i = 0; i < 32; i++) {
+        sh += (int32_t)q[i] * hi[b * 32 + i];
+        sl += (int32_t)q[i] * lo[b * 32 + i];
+      }
+      const int32_t S = 256 * sh + sl;
+      acc = std::fmaf((float)S, dw * dx[b], acc);
+    }
+    part[kq] = acc;
+  }
+  return ((part[0] + part[1]) + part[2]) + part[3];
+}
+
+}  // namespace
+
+extern "C" {
+
+float orc_dot_hilo_quarters(const void* w, int dtype, int cols, size_t row, const int8_t* hi, const int8_t* lo,
+                            const float* dx) {
+  return dot_hilo_quarters(w, dtype, cols, row, hi, lo, dx);
+}
+
+void orc_rmsnorm_threads(const float* h, const float* lnw, int H, float eps, int threads, float* xn) {
+  norm_with(h, lnw, H, eps, threads == 1024 ? ss_1024(h, H) : ss_256(h, H), xn);
+}
+
+int orc_session_step_grouped(orc_session* s, const int* tokens, int n, float* logits, int* route_ids,
+                             float* route_weights, float* hidden) {
+  const moert_config& c = s->cfg;
+  if (n < 1 || n > 32) return MOERT_E_CONFIG;
+  if (s->pos + n > s->max_len) return MOERT_E_FULL;
+  for (int p = 0; p < n; p++)
+    if (tokens[p] < 0 || tokens[p] >= c.vocab) return MOERT_E_RANGE;
+  if (c.head_dim != 64 || (c.hidden % 128) || ((c.heads * 64) % 128)) return MOERT_E_CONFIG;
+  Pool& pool = *s->pool;
+  const int H = c.hidden, d = c.head_dim, qd = c.heads * d, k = c.top_k, E = c.experts, pos0 = s->pos;
+  const int HB = H / 32, QB = qd / 32;
+  std::vector<float> h((size_t)n * H), xn((size_t)n * H), q((size_t)n * qd), att((size_t)n * qd), cs(d), lg(E),
+      y((size_t)n * H);
+  std::vector<int8_t> xh((size_t)n * std::max(H, qd)), xl((size_t)n * std::max(H, qd));
+  std::vector<float> xd((size_t)n * std::max(HB, QB));
+  std::vector<int> ids((size_t)n * k);
+  std::vector<float> wts((size_t)n * k);
+  for (int p = 0; p < n; p++) {
+    dequant_row(s->w.embed.data, s->w.embed.dtype, H, (size_t)tokens[p], &h[(size_t)p * H]);
+    for (int i = 0; i < H; i++) h[(size_t)p * H + i] = h[(size_t)p * H + i] * c.embedding_multiplier;
+  }
+  const int nh = c.heads + 2 * c.kv_heads;
+  for (int l = 0; l < c.layers; l++) {
+    const moert_layer_weights& L = s->layers[l];
+    // 1. norm codes of every position
+    for (int p = 0; p < n; p++) {
+      float* xp = &xn[(size_t)p * H];
+      norm_with(&h[(size_t)p * H], L.ln_attn, H, c.eps, ss_256(&h[(size_t)p * H], H), xp);
+      orc_quant_hilo(xp, H, &xh[(size_t)p * H], &xl[(size_t)p * H], &xd[(size_t)p * HB]);
+    }
+    // 2. q/k/v with RoPE and the KV append, one task per (head, position)
+    pool.run((size_t)nh * n, [&](size_t t) {
+      const int head = (int)(t / n), p = (int)(t % n), pos = pos0 + p;
+      const moert_tensor& W = head < c.heads ? L.q : head < c.heads + c.kv_heads ? L.k : L.v;
+      const int hr = head < c.heads ? head : head < c.heads + c.kv_heads ? head - c.heads : head - c.heads - c.kv_heads;
+      float rc[64];
+      orc_rope_cos_sin(c.rope_theta, d, pos, rc);
+      const int8_t* ph = &xh[(size_t)p * H];
+      const int8_t* pl = &xl[(size_t)p * H];
+      const float* pd = &xd[(size_t)p * HB];
+      for (int jp = 0; jp < 32; jp++) {
+        const float x1 = dot_hilo_quarters(W.data, W.dtype, H, (size_t)hr * 64 + jp, ph, pl, pd);
+        const float x2 = dot_hilo_quarters(W.data, W.dtype, H, (size_t)hr * 64 + jp + 32, ph, pl, pd);
+        const float co = rc[jp], sn = rc[32 + jp];
+        if (head < c.heads) {
+          float* qv = &q[(size_t)p * qd + head * 64];
+          qv[jp] = x1 * co - x2 * sn;
+          qv[jp + 32] = x2 * co + x1 * sn;
+        } else if (head < c.heads + c.kv_heads) {
+          uint16_t* kp = &s->kc[l][((size_t)hr * s->max_len + pos) * 64];
+          kp[jp] = f2h(x1 * co - x2 * sn);
+          kp[jp + 32] = f2h(x2 * co + x1 * sn);
+        } else {
+          uint16_t* vp = &s->vc[l][((size_t)hr * s->max_len + pos) * 64];
+          vp[jp] = f2h(x1);
+          vp[jp + 32] = f2h(x2);
+        }
+      }
+    });
+    // 3. attention of every position over its causal length
+    for (int p = 0; p < n; p++)
+      attention(s->pool, &q[(size_t)p * qd], s->kc[l].data(), s->vc[l].data(), c.heads, c.kv_heads, d, s->max_len,
+                pos0 + p + 1, c.attention_multiplier, s->tps, &att[(size_t)p * qd]);
+    // 4. output projection on the attention output's codes, residual
+    for (int p = 0; p < n; p++)
+      orc_quant_hilo(&att[(size_t)p * qd], qd, &xh[(size_t)p * qd], &xl[(size_t)p * qd], &xd[(size_t)p * QB]);
+    pool.run((size_t)n * ((H + 15) / 16), [&](size_t t) {
+      const int p = (int)(t % n), r0 = (int)(t / n) * 16;
+      for (int r = r0; r < r0 + 16 && r < H; r++) {
+        const float o = dot_hilo_quarters(L.o.data, L.o.dtype, qd, (size_t)r, &xh[(size_t)p * qd],
+                                          &xl[(size_t)p * qd], &xd[(size_t)p * QB]);
+        float& hv = h[(size_t)p * H + r];
+        hv = hv + c.residual_multiplier * o;
+      }
+    });
+    // 5. router of each position on its own rmsnorm, then the experts of all positions grouped
+    for (int p = 0; p < n; p++) {
+      float* xp = &xn[(size_t)p * H];
+      norm_with(&h[(size_t)p * H], L.ln_moe, H, c.eps, ss_1024(&h[(size_t)p * H], H), xp);
+      for (int e = 0; e < E; e++) lg[e] = orc_dot(L.router.data, L.router.dtype, H, (size_t)e, xp);
+      orc_route(lg.data(), L.router_bias, E, k, &ids[(size_t)p * k], &wts[(size_t)p * k]);
+    }
+    orc_experts_grouped(H, c.inter, n, k, &L.gate_up, &L.down, xn.data(), ids.data(), wts.data(), y.data(),
+                        pool.threads());
+    for (size_t i = 0; i < (size_t)n * H; i++) h[i] = h[i] + c.residual_multiplier * y[i];
+    for (int p = 0; p < n; p++)
+      for (int j = 0; j < k; j++) {
+        if (route_ids) route_ids[((size_t)p * c.layers + l) * k + j] = ids[(size_t)p * k + j];
+        if (route_weights) route_weights[((size_t)p * c.layers + l) * k + j] = wts[(size_t)p * k + j];
+      }
+  }
+  const float* last = &h[(size_t)(n - 1) * H];
+  if (hidden) std::memcpy(hidden, last, (size_t)H * 4);
+  if (logits) {
+    orc_rmsnorm(last, s->w.norm, H, c.eps, xn.data());
+    gemv(pool, s->w.embed.data, s->w.embed.dtype, c.vocab, H, xn.data(), logits);
+    for (int v = 0; v < c.vocab; v++) logits[v] = logits[v] / c.logits_scaling;
+  }
+  s->pos += n;
   return MOERT_OK;
 }
 

@@ -110,6 +110,27 @@ int orc_session_pos(orc_session* s);
 int orc_session_kv_prefill(orc_session* s, int layer, const uint16_t* k, const uint16_t* v, int n);
 int orc_session_read_kv(orc_session* s, int layer, uint16_t* k, uint16_t* v, int n);
 
+/* The grouped mode of the engine's multi-position step (moert_batched_mode 1) over n <= 32 positions from the
+ * session's position: q/k/v and output projections as exact integer block products over 15-bit activation codes,
+ * each row's blocks in four quarters (orc_dot_hilo_quarters), the norms in the engine's thread orders
+ * (orc_rmsnorm_threads: 256 for the attention input, 1024 for the router input), the experts grouped
+ * (orc_experts_grouped); route_ids / route_weights [n][layers][k], logits and hidden of the last position. */
+float orc_dot_hilo_quarters(const void* w, int dtype, int cols, size_t row, const int8_t* hi, const int8_t* lo,
+                            const float* dx);
+void orc_rmsnorm_threads(const float* h, const float* lnw, int H, float eps, int threads, float* xn);
+int orc_session_step_grouped(orc_session* s, const int* tokens, int n, float* logits, int* route_ids,
+                             float* route_weights, float* hidden);
+/* CPU port of the reference's CPU decode path (cpu_port.cpp): the reference's own arithmetic shape (dot_avx2's
+ * 4 x 8-lane accumulation, f32 KV cache, attention on the calling thread), timed as bench.py's CPU baseline; it
+ * agrees with the session above within float rounding, not bit for bit. */
+typedef struct port_session port_session;
+int port_session_create(const moert_config* cfg, const moert_model_weights* w, int max_len, int threads,
+                        port_session** out);
+void port_session_destroy(port_session* s);
+void port_session_set_pos(port_session* s, int pos);
+int port_session_kv_prefill(port_session* s, int layer, const uint16_t* k, const uint16_t* v, int n);
+int port_session_step(port_session* s, int token, float* logits, int* route_ids, float* route_weights);
+float port_dot(const void* w, int dtype, int cols, size_t row, const float* x);
 #ifdef __cplusplus
 }
 #endif

@@ -66,6 +66,15 @@ def lib() -> ctypes.CDLL:
             "orc_session_pos": (i, [vp]),
             "orc_session_kv_prefill": (i, [vp, i, vp, vp, i]),
             "orc_session_read_kv": (i, [vp, i, vp, vp, i]),
+            "orc_dot_hilo_quarters": (f, [vp, i, i, sz, vp, vp, vp]),
+            "orc_rmsnorm_threads": (None, [vp, vp, i, f, i, vp]),
+            "orc_session_step_grouped": (i, [vp, vp, i, vp, vp, vp, vp]),
+            "port_session_create": (i, [vp, vp, i, i, ctypes.POINTER(vp)]),
+            "port_session_destroy": (None, [vp]),
+            "port_session_set_pos": (None, [vp, i]),
+            "port_session_kv_prefill": (i, [vp, i, vp, vp, i]),
+            "port_session_step": (i, [vp, i, vp, vp, vp]),
+            "port_dot": (f, [vp, i, i, sz, vp]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -402,6 +411,21 @@ class CpuSession:
             raise RuntimeError(f"orc_session_step failed: {rc}")
         return lg, ids, w, hid
 
+    def step_grouped(self, tokens, want_logits=True):
+        """The engine's grouped multi-position step (moert_batched_mode 1) over n <= 32 tokens: (last logits,
+        routes [n, layers, k], weights [n, layers, k], last hidden state)."""
+        c = self.cfg
+        t = np.ascontiguousarray(tokens, np.int32)
+        n = t.size
+        lg = np.empty(c.vocab, np.float32) if want_logits else None
+        ids = np.empty((n, c.layers, c.top_k), np.int32)
+        w = np.empty((n, c.layers, c.top_k), np.float32)
+        hid = np.empty(c.hidden, np.float32)
+        rc = lib().orc_session_step_grouped(self.h, _p(t), n, _p(lg), _p(ids), _p(w), _p(hid))
+        if rc != 0:
+            raise RuntimeError(f"orc_session_step_grouped failed: {rc}")
+        return lg, ids, w, hid
+
     def set_position(self, pos):
         lib().orc_session_set_pos(self.h, pos)
 
@@ -437,3 +461,62 @@ class CpuSession:
                 lg, _, _, self.last_hidden = self.step(nxt)
         self.last_logits = lg  # the logits the last token was chosen from
         return np.array(out, np.int32), np.array(gaps, np.float32)
+
+
+class PortSession:
+    """The CPU port of the reference's CPU decode path (cpu_port.cpp: CpuSession::step with dot_avx2's accumulation,
+    an f32 KV cache and attention on the calling thread), timed as bench.py's CPU baseline."""
+
+    def __init__(self, model, max_len, threads=None):
+        self.model, self.cfg = model, model.cfg
+        self.threads = threads or (os.cpu_count() or 1)
+        h = ctypes.c_void_p()
+        rc = lib().port_session_create(ctypes.byref(model.cfg.c()), ctypes.byref(model.weights()), max_len,
+                                       self.threads, ctypes.byref(h))
+        if rc != 0:
+            raise RuntimeError(f"port_session_create failed: {rc}")
+        self.h = h
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            lib().port_session_destroy(self.h)
+            self.h = None
+
+    def step(self, token, want_logits=True):
+        c = self.cfg
+        lg = np.empty(c.vocab, np.float32) if want_logits else None
+        ids = np.empty((c.layers, c.top_k), np.int32)
+        w = np.empty((c.layers, c.top_k), np.float32)
+        rc = lib().port_session_step(self.h, int(token), _p(lg), _p(ids), _p(w))
+        if rc != 0:
+            raise RuntimeError(f"port_session_step failed: {rc}")
+        return lg, ids, w
+
+    def set_position(self, pos):
+        lib().port_session_set_pos(self.h, pos)
+
+    def kv_prefill(self, layer, k, v):
+        k = np.ascontiguousarray(k, np.uint16)
+        v = np.ascontiguousarray(v, np.uint16)
+        rc = lib().port_session_kv_prefill(self.h, layer, _p(k), _p(v), k.shape[1])
+        if rc != 0:
+            raise RuntimeError(f"port kv_prefill failed: {rc}")
+
+
+def port_dot(w: np.ndarray, dtype: int, cols: int, row: int, x: np.ndarray) -> float:
+    x = np.ascontiguousarray(x, np.float32)
+    return float(lib().port_dot(_p(w), dtype, cols, row, _p(x)))
+
+
+def dot_hilo_quarters(w, dtype, cols, row, hi, lo, d):
+    return float(lib().orc_dot_hilo_quarters(_p(w), dtype, cols, row, _p(np.ascontiguousarray(hi, np.int8)),
+                                             _p(np.ascontiguousarray(lo, np.int8)),
+                                             _p(np.ascontiguousarray(d, np.float32))))
+
+
+def rmsnorm_threads(h, lnw, eps, threads):
+    h = np.ascontiguousarray(h, np.float32)
+    lnw = np.ascontiguousarray(lnw, np.float32)
+    out = np.empty_like(h)
+    lib().orc_rmsnorm_threads(_p(h), _p(lnw), h.size, eps, threads, _p(out))
+    return out
