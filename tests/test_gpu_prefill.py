@@ -4,6 +4,8 @@ cuda_backend.rs:499-516, 751-917, whose per-position loops make it equal to sing
 position, the hidden state and logits of the last one, bit for bit, and the same greedy continuation. The
 single-position decode is itself pinned bit for bit against the oracle (test_gpu_model.py); the tiny case also
 checks the oracle directly."""
+import os
+
 import numpy as np
 import pytest
 
@@ -11,6 +13,7 @@ import moert
 import oracle
 
 pytestmark = pytest.mark.gpu
+THREADS = min(16, os.cpu_count() or 1)
 
 
 def say(msg):
@@ -180,6 +183,49 @@ def test_grouped_mode_prefill_within_1e2_of_the_fma_path(gpu, shape, seed):
     assert bits_equal(a, b)
     fma.close()
     grp.close()
+
+
+@pytest.mark.parametrize("shape,seed,ctx", [("1b", 41, 0), ("3b", 43, 4096)])
+def test_grouped_mode_blocks_equal_the_oracle_grouped_step(gpu, shape, seed, ctx):
+    """moert_batched_mode(1) against the oracle's restatement of the grouped step (orc_session_step_grouped: 15-bit
+    codes, exact integer block products in four quarters per q/k/v and output row, the engine's norm orders, experts
+    grouped in first-appearance order), bit for bit: blocks of 32, 5 and 17 positions (the 3B model after 4096
+    positions pre-filled with fp16 N(0, 1)), each block's last logits, argmax and hidden state, then every KV row the
+    blocks appended, then 4 decode steps after them (the decode path, against the oracle's decode)."""
+    cfg = moert.Config(**(moert.GRANITE_1B if shape == "1b" else moert.GRANITE_3B))
+    say(f"{shape} build")
+    m = moert.SynthModel(cfg, seed=seed, zipf_s=1.1)
+    max_len = 4416 if ctx else 128
+    g = moert.GpuModel(m, max_len, attn_splits=32)
+    s = oracle.CpuSession(m, max_len, attn_splits=32, threads=THREADS)
+    if ctx:
+        for l in range(cfg.layers):
+            k, v = moert.kv_prefill_data(cfg, seed, l, ctx)
+            g.kv_prefill(l, k, v)
+            s.kv_prefill(l, k, v)
+        g.set_position(ctx)
+        s.set_position(ctx)
+    g.batched_mode(1)
+    rng = np.random.default_rng(seed + 7)
+    pos = ctx
+    for n in (32, 5, 17):
+        toks = rng.integers(0, cfg.vocab, n)
+        say(f"{shape} grouped block of {n} at {pos}")
+        blg, bam = g.step_batched(toks)
+        olg, _, _, ohid = s.step_grouped(toks)
+        assert bits_equal(blg, olg), (n, float(np.abs(blg - olg).max()))
+        assert bam == oracle.argmax(olg)
+        assert bits_equal(g.hidden(), ohid), n
+        pos += n
+    for l in range(cfg.layers):
+        gk, gv = g.read_kv(l, pos)
+        ok, ov = s.read_kv(l, pos)
+        assert np.array_equal(gk[:, ctx:pos], ok[:, ctx:pos]) and np.array_equal(gv[:, ctx:pos], ov[:, ctx:pos]), l
+    for t, tok in enumerate(rng.integers(0, cfg.vocab, 4)):
+        lg, ids, w, _ = g.step(int(tok))
+        olg, oids, ow, _ = s.step(int(tok))
+        assert bits_equal(lg, olg) and np.array_equal(ids, oids) and bits_equal(w, ow), t
+    g.close()
 
 
 def test_grouped_mode_refusals(gpu):
