@@ -52,6 +52,11 @@ def kernel_bytes(kind, cfg, ctx, wd, ed, nsplit):
         # the MoE-norm partials, the k routed experts' gate/up and down rows, the down outputs it leaves
         moert.K_MOE_XCD: 65 * 256 * 4 + cfg.top_k * b(wd, 3 * I * H) + cfg.top_k * H * 4,
         moert.K_MOE_COMBINE: 0,
+        # a whole layer: q/k/v and the KV it reads, the output projection, the router rows, the k routed experts;
+        # its exchanges stay in the XCDs' L2s or are a few KB device-wide
+        moert.K_LAYER: b(wd, (qd + 2 * kvd) * H) + 2 * kvd * 2 * ctx + b(wd, H * qd) + b(wd, cfg.experts * H)
+        + cfg.top_k * b(wd, 3 * I * H),
+        moert.K_LAYER_COMBINE: 0,
     }[kind]
 
 
@@ -354,7 +359,8 @@ def main():
     dk = kernels[dom]
     log("kernels: " + ", ".join(f"{k} {v['us']:.2f}us x{v['launches_per_step']} {v['gbs'] or 0:.0f}GB/s"
                                 for k, v in kernels.items()))
-    moe = {k: kernels[k] for k in ("route_up", "expert_down", "moe_xcd") if k in kernels}
+    # the MoE GEMV of the metric: its own kernels, or (one launch per layer) inside the layer kernel
+    moe = {k: kernels[k] for k in ("route_up", "expert_down", "moe_xcd", "layer") if k in kernels}
     prefill = prefill_block(g, cfg, args.seed, CTX, tok_s, reps=args.prefill_reps) if args.prefill_reps > 0 else None
     g.close()
     copy_bytes = 1 << 30

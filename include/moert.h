@@ -245,15 +245,21 @@ typedef enum {
   MOERT_K_MOE_XCD = 10,     /* rmsnorm + router + top-8 + gate/up + down with the routed experts spread over the 8
                                XCDs (replaces MOERT_K_ROUTE_UP and MOERT_K_EXPERT_DOWN where it applies) */
   MOERT_K_MOE_COMBINE = 11, /* weighted combine of the last layer's experts + residual, before the head */
-  MOERT_K_COUNT = 12
+  MOERT_K_LAYER = 12,       /* a whole layer in one launch: attention, output projection, router and the routed
+                               experts, exchanging through the XCDs' L2s and device-wide (replaces
+                               MOERT_K_ATTN_BLOCK, MOERT_K_OPROJ and MOERT_K_MOE_XCD where its shape applies) */
+  MOERT_K_LAYER_COMBINE = 13, /* the last layer's experts combined into the head's input after MOERT_K_LAYER */
+  MOERT_K_COUNT = 14
 } moert_kernel_kind;
 int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch, int* launches);
 
-/* Which kernels the model's decode step launches: *attn_block = 1 when the attention half is the one-launch
- * attention block (MOERT_K_ATTN_BLOCK) rather than q/k/v + split attention + combine, *moe_xcd = 1 when the MoE
- * half is the kernel spread over the XCDs (MOERT_K_MOE_XCD) rather than router + gate/up and down. Both depend on
- * the shapes, the model kind and its modes (the cache's prefetch branch uses neither). No reference counterpart. */
-int moert_model_path(const moert_model* m, int* attn_block, int* moe_xcd);
+/* Which kernels the model's decode step launches: *layer = 1 when each layer is one launch (MOERT_K_LAYER);
+ * otherwise *attn_block = 1 when the attention half is the one-launch attention block (MOERT_K_ATTN_BLOCK) rather
+ * than q/k/v + split attention + combine, and *moe_xcd = 1 when the MoE half is the kernel spread over the XCDs
+ * (MOERT_K_MOE_XCD) rather than router + gate/up and down. They depend on the shapes, the model kind and its modes
+ * (the cache's prefetch branch uses none of them); MOERT_LAYER=1 at create asks for one launch per layer where the
+ * shape allows it. No reference counterpart. */
+int moert_model_path(const moert_model* m, int* layer, int* attn_block, int* moe_xcd);
 
 /* Test hook for the failure path of the fused kernels (MOERT_K_ATTN_BLOCK, MOERT_K_MOE_XCD); it has no counterpart
  * in the reference. `bits` (a subset of 2 = the wait for queries / the new K/V row, 4 = the wait for split partials,
@@ -266,8 +272,8 @@ int moert_fault_inject(moert_model* m, unsigned bits);
 
 /* Phase timeline of one decode step (measurement build libmoert_tl.so only; MOERT_E_CONFIG otherwise): one graph
  * replay in which every workgroup of every launch stamps the 100 MHz real-time clock at its phase boundaries.
- * out receives [launches][1024][8] u64 records: word 0 = ~(earliest wave start), word 1 = latest wave start,
- * words 2..6 = phase ends seen by wave 0 (0 = no such phase), word 7 = latest wave end; kinds / layers receive each
+ * out receives [launches][1024][12] u64 records: word 0 = ~(earliest wave start), word 1 = latest wave start,
+ * words 2..10 = phase ends seen by wave 0 (0 = no such phase), word 11 = latest wave end; kinds / layers receive each
  * launch's moert_kernel_kind and layer (-1 outside the layers). The position advances by one. No reference
  * counterpart (the reference's phase instrument is perfil_bloco.rs, host-side); used for the latency analysis. */
 int moert_timeline_step(moert_model* m, unsigned long long* out, int* kinds, int* layers, int max_launches,

@@ -17,7 +17,7 @@ struct VShare {
   uint4 a, b, c, d, e, f, g, h;  // pieces 0..N-1 of this wave (named members: no private array)
   __device__ __forceinline__ void load(const uint16_t* V, int t, int lane, int wave) {
     const uint4* src = reinterpret_cast<const uint4*>(V + ((size_t)t * 64 + (lane >> 3)) * 64 + (lane & 7) * 8);
-    auto at = [&](int i) { return src[(size_t)min(wave + G * i, 7) * 64]; };
+    auto at = [&](int i) { return gload_u4(src + (size_t)min(wave + G * i, 7) * 64); };
     a = at(0);
     if (N > 1) b = at(1);
     if (N > 2) c = at(2);

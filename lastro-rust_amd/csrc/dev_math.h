@@ -159,6 +159,37 @@ template <> struct Fmt<DT_F32> {
   __device__ static size_t row_bytes(int cols) { return (size_t)cols * 4; }
 };
 
+// A pointer into device memory as a global-address-space pointer. A load through a plain pointer whose origin the
+// compiler cannot trace to a kernel argument (one read from a table in memory) becomes a flat load, which also
+// counts in the LDS counter (so every LDS wait would wait for it) and needs a 64-bit address per lane; through this
+// cast it is a global load.
+#define MOERT_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ const MOERT_GLOBAL T* gmem(const T* p) {
+  return (const MOERT_GLOBAL T*)p;
+}
+template <class T>
+__device__ __forceinline__ MOERT_GLOBAL T* gmem_w(T* p) {
+  return (MOERT_GLOBAL T*)p;
+}
+// 16- and 8-byte vector loads through a global pointer (the HIP vector classes cannot be copied from a qualified
+// lvalue, so the native vector is loaded and converted).
+typedef unsigned moert_u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned moert_u32x2 __attribute__((ext_vector_type(2)));
+typedef float moert_f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 gload_u4(const void* p) {
+  const moert_u32x4 v = *(const MOERT_GLOBAL moert_u32x4*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 gload_u2(const void* p) {
+  const moert_u32x2 v = *(const MOERT_GLOBAL moert_u32x2*)p;
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ float4 gload_f4(const void* p) {
+  const moert_f32x4 v = *(const MOERT_GLOBAL moert_f32x4*)p;
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // One 16-byte chunk j of a row, loaded raw, with the raw bits of its fp16 scale (converted where it is used, so
 // that a run of chunk loads is not broken by a wait for each scale).
 struct RawChunk {
@@ -170,17 +201,23 @@ template <int DT>
 __device__ __forceinline__ RawChunk load_chunk(const DMat& m, size_t row, int j) {
   RawChunk c;
   const uint8_t* base = m.q + row * Fmt<DT>::row_bytes(m.cols);
-  c.v = *reinterpret_cast<const uint4*>(base + (size_t)j * 16);
+  c.v = gload_u4(base + (size_t)j * 16);
   if (DT == DT_Q8_0)
-    c.d = m.d[row * (size_t)(m.cols / 32) + (j >> 1)];
+    c.d = *gmem(m.d + row * (size_t)(m.cols / 32) + (j >> 1));
   else if (DT == DT_Q4_0)
-    c.d = m.d[row * (size_t)(m.cols / 32) + j];
+    c.d = *gmem(m.d + row * (size_t)(m.cols / 32) + j);
   else
     c.d = 0x3c00u;  // 1.0
   return c;
 }
 
-__device__ __forceinline__ float chunk_scale(const RawChunk& c) { return h2f((uint16_t)c.d); }
+// The empty asm keeps the conversion at its use: hoisted up to its load (the compiler pushes the conversion through
+// the phi of a conditional load), it would make the wave wait there for every load issued before the scale.
+__device__ __forceinline__ float scale_at_use(uint32_t bits) {
+  asm volatile("" : "+v"(bits));
+  return h2f((uint16_t)bits);
+}
+__device__ __forceinline__ float chunk_scale(const RawChunk& c) { return scale_at_use(c.d); }
 
 // acc = fma chain over the chunk's elements in index order; x holds the chunk's Fmt<DT>::kElems activations.
 template <int DT>

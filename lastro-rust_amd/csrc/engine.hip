@@ -25,6 +25,7 @@
 #include "cache.h"
 #include "grouped.h"
 #include "kernels.h"
+#include "layers.h"
 #include "moe_norm.h"
 #include "noalloc.h"
 #include "prefill.h"
@@ -209,6 +210,12 @@ struct moert_model {
   // the experts' down outputs for the next attention block (or k_moe_combine) to combine. MOERT_MOE_XCD=0 at create
   // keeps k_route_up + k_expert_down.
   bool use_mx = false;
+  // every layer as one launch (layers.hip), where the shape allows it with the attention block and the MoE kernel
+  // over the XCDs, when MOERT_LAYER=1 at create (measured no faster than the three launches per layer, which stay
+  // the default)
+  bool use_px = false;
+  PxBufs px{};
+  std::vector<PxLayer> pxl;
   int cus = 0;
   AbBufs ab{};
   hipGraph_t graph = nullptr;
@@ -275,6 +282,14 @@ struct moert_model {
     const bool use_blk = use_ab && !(cached && prefetch);
     CHECK_HIP(
         launch_embed(stream, embed, dims, b, ab.step_ctr, use_blk ? ab.rope_cur : nullptr, arm(MOERT_K_EMBED, -1)));
+    if (use_px) {
+      for (size_t l = 0; l < layers.size(); l++)
+        CHECK_HIP(launch_layer(stream, pxl[l], layers[l], (int)l, dims, b, cus, ab, px, arm(MOERT_K_LAYER, (int)l)));
+      CHECK_HIP(launch_layer_combine(stream, dims, b, (int)layers.size() - 1, ab, px, arm(MOERT_K_LAYER_COMBINE, -1)));
+      CHECK_HIP(launch_head(stream, embed, norm, dims, b, arm(MOERT_K_HEAD, -1)));
+      CHECK_HIP(launch_head_argmax(stream, embed, dims, b, arm(MOERT_K_HEAD_ARGMAX, -1)));
+      return MOERT_OK;
+    }
     for (size_t l = 0; l < layers.size(); l++) {
       const LayerDev& L = layers[l];
       const int li = (int)l;
@@ -857,6 +872,19 @@ static int model_create(const moert_config* c, const moert_model_weights* w, int
                 attn_block_fits(m->dims, m->layers[0].qkv, m->cus);
     const char* mv = getenv("MOERT_MOE_XCD");
     m->use_mx = m->use_ab && cache_slots == 0 && !(mv && mv[0] == '0') && moe_xcd_fits(m->dims, m->layers[0], m->cus);
+    const char* lv = getenv("MOERT_LAYER");
+    if (m->use_mx && lv && lv[0] == '1' && layers_fit(m->dims, m->layers[0], m->cus)) {
+      unsigned *pxx = nullptr, *pxd = nullptr;
+      float* hpp = nullptr;
+      if ((rc = zeros(a, s, 8 * sizeof(PxXcd) / 4, &pxx)) || (rc = zeros(a, s, sizeof(PxDev) / 4, &pxd)) ||
+          (rc = zeros(a, s, (size_t)H, &hpp)))
+        return bail(rc);
+      m->px = PxBufs{reinterpret_cast<PxXcd*>(pxx), reinterpret_cast<PxDev*>(pxd), hpp};
+      for (const LayerDev& L : m->layers)
+        m->pxl.push_back(PxLayer{L.qkv, L.o, L.router, L.gate_up, L.down, L.ln_attn, L.ln_moe, L.router_bias,
+                                 L.k_cache, L.v_cache});
+      m->use_px = true;
+    }
   }
   if (hipStreamSynchronize(s) != hipSuccess) {
     set_err("upload failed");
@@ -1088,6 +1116,10 @@ static int epoch_guard(moert_model* m) {
   CHECK_HIP(hipMemsetAsync(m->ab.groups, 0, 8 * sizeof(AbGroup), m->stream));
   CHECK_HIP(hipMemsetAsync(m->ab.moe, 0, 8 * sizeof(MxGroup), m->stream));
   CHECK_HIP(hipMemsetAsync(m->ab.step_ctr, 0, 4, m->stream));
+  if (m->use_px) {
+    CHECK_HIP(hipMemsetAsync(m->px.xcd, 0, 8 * sizeof(PxXcd), m->stream));
+    CHECK_HIP(hipMemsetAsync(m->px.dev, 0, sizeof(PxDev), m->stream));
+  }
   m->steps_since_clear = 1;
   return MOERT_OK;
 }
@@ -1100,17 +1132,23 @@ static int model_launch(moert_model* m) {
   CHECK_HIP(hipGraphLaunch(m->exec, m->stream));
   return MOERT_OK;
 }
-// A bit that k_attn_block or k_moe_xcd set (a bounded wait that gave up) is a device error: 2 = the queries or the
-// new K/V row of a KV head, 4 = the split partials of a merge, 8 = the act vector of an expert.
+// A bit that k_attn_block, k_moe_xcd or k_layer set (a bounded wait that gave up) is a device error: 2 = the queries
+// or the new K/V row of a KV head, 4 = the split partials of a merge, 8 = the act vector of an expert; k_layer only:
+// 32 = the merged heads (device-wide), 64 = h' (device-wide), 128 = the merged heads or h' in the XCD's L2, or the
+// router items.
 static int ab_check(moert_model* m) {
   if (!m->use_ab) return MOERT_OK;
   unsigned e = 0;
   CHECK_HIP(hipMemcpy(&e, m->ab.err, 4, hipMemcpyDeviceToHost));
   if (e) {
-    set_err("%s%s%sgave up (error bits %#x): the launch's workgroups were not dispatched round-robin over the XCDs "
-            "or not all resident at once", (e & 2u) ? "attention block: the wait for queries / the new K/V row " : "",
-            (e & 4u) ? "attention block: the wait for split partials " : "",
-            (e & 8u) ? "MoE kernel: the wait for an expert's act vector " : "", e);
+    set_err("%s%s%s%s%s%sgave up (error bits %#x): the launch's workgroups were not dispatched round-robin over the "
+            "XCDs or not all resident at once",
+            (e & 2u) ? "attention: the wait for queries / the new K/V row " : "",
+            (e & 4u) ? "attention: the wait for split partials " : "",
+            (e & 8u) ? "MoE: the wait for an expert's act vector " : "",
+            (e & 32u) ? "layer: the wait for the merged heads " : "",
+            (e & 64u) ? "layer: the wait for the post-attention residual " : "",
+            (e & 128u) ? "layer: the wait for values relayed inside an XCD or for router items " : "", e);
     return MOERT_E_DEVICE;
   }
   return MOERT_OK;
@@ -1690,14 +1728,15 @@ static int time_kernel_impl(moert_model* m, int kind, int iters, double* us, int
   return MOERT_OK;
 }
 
-int moert_model_path(const moert_model* m, int* attn_block, int* moe_xcd) {
-  if (!m || !attn_block || !moe_xcd) {
+int moert_model_path(const moert_model* m, int* layer, int* attn_block, int* moe_xcd) {
+  if (!m || !layer || !attn_block || !moe_xcd) {
     set_err("model_path: null argument");
     return MOERT_E_CONFIG;
   }
   const bool blk = m->use_ab && !(m->cached && m->prefetch);
-  *attn_block = blk ? 1 : 0;
-  *moe_xcd = blk && m->use_mx ? 1 : 0;
+  *layer = m->use_px ? 1 : 0;
+  *attn_block = blk && !m->use_px ? 1 : 0;
+  *moe_xcd = blk && m->use_mx && !m->use_px ? 1 : 0;
   return MOERT_OK;
 }
 

@@ -139,24 +139,30 @@ __global__ __launch_bounds__(kMxWaves * 64) void k_moe_xcd(DMat router, const fl
     dok[p] = !up && li < RB;
     drow[p] = (size_t)ej * K + (dok[p] ? dr[p] : 0);
   }
-  Rows<DT, I, DP> dd;
-  if (up) {
-    const int sub = lane % G::LPR, rw = lane / G::LPR;
-    size_t row[P];
-    bool ok[P];
-    int pi[NP];
+  // the gate/up requests go out first (a compute unit passes requests to its L1 at a fixed rate of bytes: a bare
+  // workgroup barrier puts them ahead of the down rows, which are needed only after the act vector)
+  const int sub = lane % G::LPR, rw = lane / G::LPR;
+  size_t row[P];
+  bool ok[P];
+  int pi[NP];
 #pragma unroll
-    for (int a = 0; a < NP; a++) {
-      const int li = (wave * NP + a) * G::RPW + rw;  // pair of the workgroup
-      pi[a] = w * PW + li;
-      const bool v = li < PW;
-      const size_t r0 = (size_t)ej * 2 * I + (v ? pi[a] : 0);
-      row[2 * a] = r0;
-      row[2 * a + 1] = r0 + I;
-      ok[2 * a] = ok[2 * a + 1] = v;
-    }
-    Rows<DT, K, P> rr;
-    rows_load<DT, K, P>(rr, gu, row, ok, sub);
+  for (int a = 0; a < NP; a++) {
+    const int li = (wave * NP + a) * G::RPW + rw;  // pair of the workgroup
+    pi[a] = w * PW + li;
+    const bool v = up && li < PW;
+    const size_t r0 = (size_t)ej * 2 * I + (v ? pi[a] : 0);
+    row[2 * a] = r0;
+    row[2 * a + 1] = r0 + I;
+    ok[2 * a] = ok[2 * a + 1] = v;
+  }
+  Rows<DT, K, P> rr;
+  if (up) rows_load<DT, K, P>(rr, gu, row, ok, sub);
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  Rows<DT, I, DP> dd;
+  if (!up) rows_load<DT, I, DP>(dd, dn, drow, dok, dsub);
+  if (up) {
     XReg<DT, K> xr;
     load_x<DT, K>(xr, xs, sub);
     float out[P];
@@ -168,7 +174,6 @@ __global__ __launch_bounds__(kMxWaves * 64) void k_moe_xcd(DMat router, const fl
     }
     TL_PHASE(tl, 4);
   } else {
-    rows_load<DT, I, DP>(dd, dn, drow, dok, dsub);
     // the expert's act vector from the L2 (down thread i polls act[i]), then the down rows
     static_assert(I == ND * 64, "one act value per down thread");
     const int i = threadIdx.x - NU * 64;

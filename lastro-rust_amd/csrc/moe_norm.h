@@ -34,18 +34,18 @@ __device__ __forceinline__ Col8 load_col8(const DMat& m, int e, int c0) {
   const size_t row = (size_t)e;
   if (DT == DT_F32) {
     const uint4* p = reinterpret_cast<const uint4*>(m.q + (row * m.cols + c0) * 4);
-    const uint4 a = p[0], b = p[1];
+    const uint4 a = gload_u4(p), b = gload_u4(p + 1);
     c.w[0] = a.x; c.w[1] = a.y; c.w[2] = a.z; c.w[3] = a.w;
     c.w[4] = b.x; c.w[5] = b.y; c.w[6] = b.z; c.w[7] = b.w;
     c.d = 0x3c00u;
   } else {
     const size_t off =
         DT == DT_Q8_0 ? row * m.cols + c0 : row * (m.cols / 2) + (size_t)(c0 / 32) * 16 + (c0 & 15);
-    const uint2 v = *reinterpret_cast<const uint2*>(m.q + off);
+    const uint2 v = gload_u2(m.q + off);
     c.w[0] = v.x;
     c.w[1] = v.y;
     c.w[2] = c.w[3] = c.w[4] = c.w[5] = c.w[6] = c.w[7] = 0u;
-    c.d = m.d[row * (size_t)(m.cols / 32) + c0 / 32];
+    c.d = *gmem(m.d + row * (size_t)(m.cols / 32) + c0 / 32);
   }
   return c;
 }
@@ -55,7 +55,7 @@ template <int DT>
 __device__ __forceinline__ float col8_elem(const Col8& c, int t, int c0) {
   if (DT == DT_F32) return __uint_as_float(c.w[t]);
   const uint32_t byte = (c.w[t >> 2] >> (8 * (t & 3))) & 0xffu;
-  const float d = h2f((uint16_t)c.d);
+  const float d = scale_at_use(c.d);
   if (DT == DT_Q8_0) return (float)(int8_t)byte * d;
   const int nib = (c0 & 31) >= 16 ? (int)(byte >> 4) : (int)(byte & 15u);
   return (float)(nib - 8) * d;

@@ -13,7 +13,7 @@
 
 namespace moert {
 
-constexpr int kTlPhases = 8;
+constexpr int kTlPhases = 12;
 constexpr int kTlMaxBlocks = 1024;  // workgroups per launch with a record (later ones are not stamped)
 
 struct Tl {

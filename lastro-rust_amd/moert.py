@@ -25,13 +25,15 @@ F32, Q8_0, Q4_0 = 0, 1, 2
 DTYPE_NAMES = {F32: "f32", Q8_0: "q8_0", Q4_0: "q4_0"}
 
 (K_EMBED, K_QKV, K_ATTN_SPLIT, K_ATTN_COMBINE, K_OPROJ, K_ROUTE_UP, K_EXPERT_DOWN, K_HEAD,
- K_HEAD_ARGMAX, K_ATTN_BLOCK, K_MOE_XCD, K_MOE_COMBINE) = range(12)
+ K_HEAD_ARGMAX, K_ATTN_BLOCK, K_MOE_XCD, K_MOE_COMBINE, K_LAYER, K_LAYER_COMBINE) = range(14)
 KERNEL_NAMES = ["embed", "qkv", "attn_split", "attn_combine", "oproj", "route_up", "expert_down", "head",
-                "head_argmax", "attn_block", "moe_xcd", "moe_combine"]   # kernel classes of a decode step (the same for a cached model)
+                "head_argmax", "attn_block", "moe_xcd", "moe_combine", "layer",
+                "layer_combine"]   # kernel classes of a decode step (the same for a cached model)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libmoert.so")
 TIMELINE_LIB_PATH = os.path.join(_HERE, "libmoert_tl.so")  # measurement build (phase timeline), see timeline.py
+TL_WORDS = 12  # words of a workgroup's timeline record: start, latest start, 9 phase ends, latest end
 
 E_NAMES = {-1: "DEVICE", -2: "CONFIG", -3: "POISONED", -4: "FULL", -5: "RANGE"}
 E_DEVICE, E_CONFIG, E_POISONED, E_FULL, E_RANGE = -1, -2, -3, -4, -5
@@ -139,7 +141,7 @@ def lib() -> ctypes.CDLL:
             "moert_time_steps": (i, [vp, i, i, ctypes.POINTER(ctypes.c_double)]),
             "moert_time_kernel": (i, [vp, i, i, ctypes.POINTER(ctypes.c_double), ip]),
             "moert_fault_inject": (i, [vp, ctypes.c_uint]),
-            "moert_model_path": (i, [vp, ip, ip]),
+            "moert_model_path": (i, [vp, ip, ip, ip]),
             "moert_timeline_step": (i, [vp, vp, vp, vp, i, ip]),
             "moert_block_create": (i, [i, i, i, i, ctypes.POINTER(moert_tensor), vp, ctypes.POINTER(moert_tensor),
                                        ctypes.POINTER(moert_tensor), ctypes.POINTER(vp)]),
@@ -573,10 +575,10 @@ class GpuModel:
         return ms.value
 
     def timeline_step(self):
-        """One step with per-workgroup phase stamps (libmoert_tl.so only): (records [launches, 1024, 8] u64,
+        """One step with per-workgroup phase stamps (libmoert_tl.so only): (records [launches, 1024, 12] u64,
         kinds [launches], layers [launches])."""
         n_max = 3 + 6 * self.cfg.layers
-        out = np.zeros((n_max, 1024, 8), np.uint64)
+        out = np.zeros((n_max, 1024, TL_WORDS), np.uint64)
         kinds = np.zeros(n_max, np.int32)
         layers = np.zeros(n_max, np.int32)
         n = ctypes.c_int(0)
@@ -588,11 +590,17 @@ class GpuModel:
         check(lib().moert_time_kernel(self.h, kind, iters, ctypes.byref(us), ctypes.byref(n)))
         return us.value, n.value
 
-    def kernel_path(self):
-        """(attention block used, MoE kernel over the XCDs used) by the decode step (moert_model_path)."""
-        a, x = ctypes.c_int(0), ctypes.c_int(0)
-        check(lib().moert_model_path(self.h, ctypes.byref(a), ctypes.byref(x)))
-        return bool(a.value), bool(x.value)
+    def kernel_path(self) -> str:
+        """The decode step's kernels (moert_model_path): "layer" (each layer one launch), "fused" (the attention
+        block and the MoE kernel over the XCDs), "block" (the attention block with the two-kernel MoE half) or
+        "unfused"."""
+        y, a, x = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
+        check(lib().moert_model_path(self.h, ctypes.byref(y), ctypes.byref(a), ctypes.byref(x)))
+        if y.value:
+            return "layer"
+        if a.value:
+            return "fused" if x.value else "block"
+        return "unfused"
 
     def fault_inject(self, bits: int):
         """Test hook: the fused kernels' waits named by `bits` (2 queries / K/V row, 4 split partials, 8 act vector)

@@ -29,6 +29,8 @@ sys.path.insert(0, HERE)
 import moert  # noqa: E402
 
 TICK_US = 0.01  # s_memrealtime runs at 100 MHz
+END = moert.TL_WORDS - 1  # word of the latest wave end
+NPH = moert.TL_WORDS - 3  # phase-end words 2 .. END - 1
 PHASES = {
     "embed": [],
     "qkv": ["norm of h (staged, sum of squares)", "q/k/v rows fma"],
@@ -42,32 +44,35 @@ PHASES = {
     "attn_block": ["q/k/v rows fma", "tiles staged", "queries in", "partials stored", "merge done"],
     "moe_xcd": ["norm of h, router logits in LDS", "rank + ids", "gate/up rows fma", "act of the XCD's expert in"],
     "moe_combine": [],
+    "layer": ["input + norm", "partials / merge done", "merged heads in", "o rows done", "h' gathered",
+              "router items out", "logits in", "ranked", "act of the XCD's expert in"],
+    "layer_combine": [],
 }
 
 
 def summarize(records, kinds):
-    """records: list over steps of (rec [launches, 1024, 8] u64, kinds [launches])."""
+    """records: list over steps of (rec [launches, 1024, moert.TL_WORDS] u64, kinds [launches])."""
     rows = {}
     totals = []
     for rec, kd in records:
         starts, ends = [], []
         for i in range(len(kd)):
             r = rec[i]
-            used = r[:, 7] != 0
+            used = r[:, END] != 0
             r = r[used].astype(np.int64)
             first = (~rec[i][used][:, 0]).astype(np.int64)
-            last_start, end = r[:, 1], r[:, 7]
+            last_start, end = r[:, 1], r[:, END]
             starts.append(first.min())
             ends.append(end.max())
             name = moert.KERNEL_NAMES[kd[i]]
             d = rows.setdefault(name, {"span": [], "gap": [], "ramp": [], "skew": [], "life": [], "blocks": [],
-                                       "phases": [[] for _ in range(5)], "last": [[] for _ in range(5)]})
+                                       "phases": [[] for _ in range(NPH)], "last": [[] for _ in range(NPH)]})
             d["span"].append(end.max() - first.min())
             d["ramp"].append(first.max() - first.min())
             d["skew"].extend((last_start - first).tolist())
             d["life"].extend((end - first).tolist())
             d["blocks"].append(int(used.sum()))
-            for ph in range(5):
+            for ph in range(NPH):
                 col = r[:, 2 + ph]
                 ok = col != 0
                 if ok.any():
@@ -115,6 +120,7 @@ def main():
     ap.add_argument("--seed", type=int, default=3003)
     ap.add_argument("--attn-splits", type=int, default=32)
     ap.add_argument("--out", default=None)
+    ap.add_argument("--raw", default=None, help="also save the records of the first 256 workgroups (.npz)")
     args = ap.parse_args()
     moert.LIB_PATH = moert.TIMELINE_LIB_PATH
     n, name = moert.device_info()
@@ -146,6 +152,8 @@ def main():
     text = (f"Device: {name}. Workload: 3B-A800M shape, Q8_0, fp16 KV at {ctx}..{ctx + args.warmup + args.steps}, "
             f"{args.attn_splits} KV splits requested.\n\n" + render(rows, totals, args.steps, len(records[0][1])))
     print(text)
+    if args.raw:
+        np.savez_compressed(args.raw, rec=np.stack([r[:, :256] for r, _ in records]), kinds=records[0][1])
     if args.out:
         with open(args.out, "w") as f:
             f.write(text + "\n")

@@ -26,14 +26,31 @@ def bits_equal(a, b):
     return a.shape == b.shape and np.array_equal(a.view(np.uint32), b.view(np.uint32))
 
 
-def three_kernel_model(m, max_len, splits, var="MOERT_ATTN_BLOCK", **kw):
-    """A model created with `var`=0 (MOERT_ATTN_BLOCK: q/k/v, split attention and combine as three kernels, and the
-    MoE half as k_route_up + k_expert_down; MOERT_MOE_XCD: only the MoE half as those two kernels)."""
-    os.environ[var] = "0"
+def env_model(m, max_len, splits, var, val, **kw):
+    os.environ[var] = val
     try:
         return moert.GpuModel(m, max_len, attn_splits=splits, **kw)
     finally:
         del os.environ[var]
+
+
+def three_kernel_model(m, max_len, splits, var="MOERT_ATTN_BLOCK", **kw):
+    """A model created with `var`=0 (MOERT_ATTN_BLOCK: q/k/v, split attention and combine as three kernels, and the
+    MoE half as k_route_up + k_expert_down; MOERT_MOE_XCD: only the MoE half as those two kernels)."""
+    return env_model(m, max_len, splits, var, "0", **kw)
+
+
+def fused_model(m, max_len, splits, **kw):
+    """The default: the attention block, the output projection and the MoE kernel over the XCDs as separate
+    launches."""
+    return moert.GpuModel(m, max_len, attn_splits=splits, **kw)
+
+
+def path_model(m, max_len, splits, path, **kw):
+    """path "layer": one launch per layer (MOERT_LAYER=1); "fused": the default."""
+    if path == "layer":
+        return env_model(m, max_len, splits, "MOERT_LAYER", "1", **kw)
+    return fused_model(m, max_len, splits, **kw)
 
 
 def launches(g, kind):
@@ -50,12 +67,14 @@ def granite_3b():
     return cfg, m, [moert.kv_prefill_data(cfg, 3003, l, 4096) for l in range(cfg.layers)]
 
 
-def test_attn_block_3b_forced_tokens_across_tile_and_split_boundaries(gpu, granite_3b):
+@pytest.mark.parametrize("path", ["layer", "fused"])
+def test_attn_block_3b_forced_tokens_across_tile_and_split_boundaries(gpu, granite_3b, path):
     """3B, KV pre-filled to 4096: forced tokens at positions 4088..4103 (the tile boundary at 4096, inside split 21)
     and 4218..4229 (the split boundary at 4224): every step's logits, routes and weights equal the oracle's, then
     the hidden state and every KV row written."""
     cfg, m, kv = granite_3b
-    g = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
+    g = path_model(m, MAX_LEN, SPLITS, path)
+    assert g.kernel_path() == path
     s = oracle.CpuSession(m, MAX_LEN, attn_splits=SPLITS, threads=THREADS)
     for l, (k, v) in enumerate(kv):
         g.kv_prefill(l, k, v)
@@ -75,20 +94,27 @@ def test_attn_block_3b_forced_tokens_across_tile_and_split_boundaries(gpu, grani
         gk, gv = g.read_kv(l, 4230)
         ok, ov = s.read_kv(l, 4230)
         assert np.array_equal(gk, ok) and np.array_equal(gv, ov), l
-    assert launches(g, moert.K_ATTN_BLOCK) == cfg.layers and launches(g, moert.K_MOE_XCD) == cfg.layers
-    assert launches(g, moert.K_MOE_COMBINE) == 1 and launches(g, moert.K_ROUTE_UP) == 0
-    assert launches(g, moert.K_QKV) == 0 and launches(g, moert.K_ATTN_COMBINE) == 0
+    if path == "fused":
+        assert launches(g, moert.K_ATTN_BLOCK) == cfg.layers and launches(g, moert.K_MOE_XCD) == cfg.layers
+        assert launches(g, moert.K_MOE_COMBINE) == 1 and launches(g, moert.K_LAYER) == 0
+    else:
+        assert launches(g, moert.K_LAYER) == cfg.layers and launches(g, moert.K_LAYER_COMBINE) == 1
+        assert launches(g, moert.K_ATTN_BLOCK) == 0 and launches(g, moert.K_OPROJ) == 0
+    assert launches(g, moert.K_ROUTE_UP) == 0 and launches(g, moert.K_QKV) == 0
+    assert launches(g, moert.K_ATTN_COMBINE) == 0
     g.close()
 
 
-def test_attn_block_1b_from_position_zero_greedy_identical(gpu):
+@pytest.mark.parametrize("path", ["layer", "fused"])
+def test_attn_block_1b_from_position_zero_greedy_identical(gpu, path):
     """1B shape (2 query heads per KV head) with the bench's cache shape: a 128-token prompt and 64 greedy tokens
     from position 0 (only the first split is used, the new row moves through its three tiles): identical tokens,
     last logits and hidden state, every KV row."""
     cfg = moert.Config(**moert.GRANITE_1B)
     say("1B build")
     m = moert.SynthModel(cfg, seed=2024, wdtype=moert.Q8_0, embed_dtype=moert.F32, std=0.1)
-    g = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
+    g = path_model(m, MAX_LEN, SPLITS, path)
+    assert g.kernel_path() == path
     s = oracle.CpuSession(m, MAX_LEN, attn_splits=SPLITS, threads=THREADS)
     prompt = np.random.default_rng(2025).integers(0, cfg.vocab, 128)
     say("1B attention block generate")
@@ -101,7 +127,7 @@ def test_attn_block_1b_from_position_zero_greedy_identical(gpu):
         gk, gv = g.read_kv(l, 192)
         ok, ov = s.read_kv(l, 192)
         assert np.array_equal(gk, ok) and np.array_equal(gv, ov), l
-    assert launches(g, moert.K_ATTN_BLOCK) == cfg.layers
+    assert launches(g, moert.K_ATTN_BLOCK if path == "fused" else moert.K_LAYER) == cfg.layers
     g.close()
 
 
@@ -109,8 +135,9 @@ def test_attn_block_equals_the_three_kernel_path(gpu, granite_3b):
     """The same 3B model with and without the attention block: 64 forced steps after 4096 cached positions, logits
     and hidden state bit for bit; the three-kernel model launches q/k/v, split and combine and no block."""
     cfg, m, kv = granite_3b
-    a = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
+    a = fused_model(m, MAX_LEN, SPLITS)
     b = three_kernel_model(m, MAX_LEN, SPLITS)
+    assert a.kernel_path() == "fused" and b.kernel_path() == "unfused"
     for l, (k, v) in enumerate(kv):
         a.kv_prefill(l, k, v)
         b.kv_prefill(l, k, v)
@@ -151,21 +178,25 @@ def test_attn_block_q4_0_rows_equal_the_three_kernel_path(gpu):
     cfg = moert.Config(**{**moert.GRANITE_3B, "layers": 4})
     say("3B-shaped Q4_0 build")
     m = moert.SynthModel(cfg, seed=5, wdtype=moert.Q4_0, embed_dtype=moert.Q8_0, zipf_s=1.1)
-    a = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
+    a = fused_model(m, MAX_LEN, SPLITS)
     b = three_kernel_model(m, MAX_LEN, SPLITS)
+    c = path_model(m, MAX_LEN, SPLITS, "layer")
+    assert a.kernel_path() == "fused" and c.kernel_path() == "layer"
     for l in range(cfg.layers):
         k, v = moert.kv_prefill_data(cfg, 5, l, 4096)
-        a.kv_prefill(l, k, v)
-        b.kv_prefill(l, k, v)
-    a.set_position(4096)
-    b.set_position(4096)
+        for g in (a, b, c):
+            g.kv_prefill(l, k, v)
+    for g in (a, b, c):
+        g.set_position(4096)
     for t, tok in enumerate(np.random.default_rng(47).integers(0, cfg.vocab, 40)):
         la, ia, wa, _ = a.step(int(tok))
         lb, ib, wb, _ = b.step(int(tok))
+        lc, ic, wc, _ = c.step(int(tok))
         assert bits_equal(la, lb) and np.array_equal(ia, ib) and bits_equal(wa, wb), t
-    assert launches(a, moert.K_ATTN_BLOCK) == cfg.layers
-    a.close()
-    b.close()
+        assert bits_equal(lc, lb) and np.array_equal(ic, ib) and bits_equal(wc, wb), t
+    assert launches(a, moert.K_ATTN_BLOCK) == cfg.layers and launches(c, moert.K_LAYER) == cfg.layers
+    for g in (a, b, c):
+        g.close()
 
 
 def test_moe_spread_over_the_xcds_equals_route_up_and_down(gpu, granite_3b):
@@ -173,8 +204,9 @@ def test_moe_spread_over_the_xcds_equals_route_up_and_down(gpu, granite_3b):
     against k_route_up + k_expert_down, both with the attention block: 48 forced steps after 4096 cached positions,
     logits, routes, weights and hidden state bit for bit; the launch counts of both."""
     cfg, m, kv = granite_3b
-    a = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
+    a = fused_model(m, MAX_LEN, SPLITS)
     b = three_kernel_model(m, MAX_LEN, SPLITS, var="MOERT_MOE_XCD")
+    assert a.kernel_path() == "fused" and b.kernel_path() == "block"
     for l, (k, v) in enumerate(kv):
         a.kv_prefill(l, k, v)
         b.kv_prefill(l, k, v)
@@ -205,8 +237,9 @@ WAIT_NAMES = {2: "the wait for queries / the new K/V row", 4: "the wait for spli
               8: "the wait for an expert's act vector"}
 
 
+@pytest.mark.parametrize("path", ["layer", "fused"])
 @pytest.mark.parametrize("bit", [2, 4, 8])
-def test_a_wait_that_gives_up_is_reported_and_poisons_the_handle(gpu, granite_1b_wide, bit):
+def test_a_wait_that_gives_up_is_reported_and_poisons_the_handle(gpu, granite_1b_wide, bit, path):
     """The failure path of the fused kernels, forced from the host (moert_fault_inject: the named wait looks for an
     epoch no launch writes, every wait of those launches is bounded to a few hundred polls, and every kernel still
     ends): a 64-step generate reports MOERT_E_DEVICE naming that wait, the launches queued after the failure wait
@@ -214,8 +247,8 @@ def test_a_wait_that_gives_up_is_reported_and_poisons_the_handle(gpu, granite_1b
     decodes bit for bit like the oracle."""
     import time
     cfg, m = granite_1b_wide
-    g = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
-    assert g.kernel_path() == (True, True)
+    g = path_model(m, MAX_LEN, SPLITS, path)
+    assert g.kernel_path() == path
     g.step(5)
     say(f"fault inject bit {bit}")
     g.fault_inject(bit)
@@ -246,7 +279,7 @@ def test_a_wait_that_gives_up_is_reported_and_poisons_the_handle(gpu, granite_1b
 def test_fault_inject_refusals(gpu, granite_1b_wide):
     cfg, m = granite_1b_wide
     g = three_kernel_model(m, MAX_LEN, SPLITS)
-    assert g.kernel_path() == (False, False)
+    assert g.kernel_path() == "unfused"
     with pytest.raises(moert.MoertError) as e:
         g.fault_inject(2)
     assert e.value.code == moert.E_CONFIG
@@ -270,14 +303,14 @@ def test_prefetch_branch_uses_the_three_kernel_attention(gpu):
     m = moert.SynthModel(cfg, seed=78, wdtype=moert.Q8_0, embed_dtype=moert.Q8_0, zipf_s=1.1)
     res = three_kernel_model(m, MAX_LEN, SPLITS)
     cac = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS, cache_slots=192)
-    assert cac.kernel_path() == (True, False)
+    assert cac.kernel_path() == "block"
     cac.cache_prefetch_mode(True)
-    assert cac.kernel_path() == (False, False)
+    assert cac.kernel_path() == "unfused"
     toks = np.random.default_rng(46).integers(0, cfg.vocab, 40)
     for t, tok in enumerate(toks):
         if t == 20:
             cac.cache_prefetch_mode(False)
-            assert cac.kernel_path() == (True, False)
+            assert cac.kernel_path() == "block"
         lr, ir, wr, _ = res.step(int(tok))
         lc, ic, wc, _ = cac.step(int(tok))
         assert bits_equal(lr, lc) and np.array_equal(ir, ic) and bits_equal(wr, wc), t
@@ -296,7 +329,7 @@ def test_hybrid_with_the_attention_block_equals_the_three_kernel_hybrid(gpu):
     m = moert.SynthModel(cfg, seed=79, wdtype=moert.Q8_0, embed_dtype=moert.Q8_0, zipf_s=1.1)
     a = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS, hybrid=(96, 4, 4))
     b = three_kernel_model(m, MAX_LEN, SPLITS, hybrid=(96, 4, 4))
-    assert a.kernel_path() == (True, False) and b.kernel_path() == (False, False)
+    assert a.kernel_path() == "block" and b.kernel_path() == "unfused"
     for t, tok in enumerate(np.random.default_rng(48).integers(0, cfg.vocab, 32)):
         la, ia, wa, _ = a.step(int(tok))
         lb, ib, wb, _ = b.step(int(tok))
@@ -306,12 +339,13 @@ def test_hybrid_with_the_attention_block_equals_the_three_kernel_hybrid(gpu):
     b.close()
 
 
-def test_prefill_then_fused_decode_equals_the_oracle(gpu, granite_1b_wide):
+@pytest.mark.parametrize("path", ["layer", "fused"])
+def test_prefill_then_fused_decode_equals_the_oracle(gpu, granite_1b_wide, path):
     """A 70-token block prefill (multi-position kernels) into the bench's cache shape, then 24 forced decode steps
     through the fused kernels: the prefill's last logits and every decode step's logits, routes and weights equal
     the oracle's session, and every KV row."""
     cfg, m = granite_1b_wide
-    g = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS)
+    g = path_model(m, MAX_LEN, SPLITS, path)
     s = oracle.CpuSession(m, MAX_LEN, attn_splits=SPLITS, threads=THREADS)
     rng = np.random.default_rng(52)
     prompt = rng.integers(0, cfg.vocab, 70)
@@ -328,6 +362,9 @@ def test_prefill_then_fused_decode_equals_the_oracle(gpu, granite_1b_wide):
         gk, gv = g.read_kv(l, 94)
         ok, ov = s.read_kv(l, 94)
         assert np.array_equal(gk, ok) and np.array_equal(gv, ov), l
-    assert g.kernel_path() == (True, True)
-    assert launches(g, moert.K_ATTN_BLOCK) == cfg.layers and launches(g, moert.K_MOE_XCD) == cfg.layers
+    assert g.kernel_path() == path
+    if path == "layer":
+        assert launches(g, moert.K_LAYER) == cfg.layers and launches(g, moert.K_LAYER_COMBINE) == 1
+    else:
+        assert launches(g, moert.K_ATTN_BLOCK) == cfg.layers and launches(g, moert.K_MOE_XCD) == cfg.layers
     g.close()

@@ -1,8 +1,8 @@
 """Whole decode steps through the C ABI against the oracle's CpuSession on the same seeded model: logits, hidden
 state, routing (ids and weights) and the KV cache are compared bit for bit, and greedy sequences token for token.
 Workloads: the reference's synthetic test shapes (tests/model.rs:253-281), the 1B model with a 128-token prompt
-and 256 generated tokens, and the 3B model at 4096 cached positions with 256 decode steps, each through the fused
-kernels the bench times and through the unfused ones."""
+and 256 generated tokens, and the 3B model at 4096 cached positions with 256 decode steps, each through the one
+launch per layer the bench times, the three fused launches per layer, and the unfused kernels."""
 import os
 
 import numpy as np
@@ -132,31 +132,46 @@ def _forced_identity(g, s, toks, label, every=1):
     assert bits_equal(g.hidden(), oh)
 
 
-# The decode step has two kernel paths: the fused one the bench times (the attention half as one attention-block
-# launch, the MoE half as one launch spread over the XCDs) where the cache shape gives 2..4 tiles per split and at
-# most 32 splits, and the unfused one (q/k/v, split attention, combine; router + gate/up, down) otherwise. Each long
-# run below goes through both, and asserts which one ran.
-PATHS_1B = {"fused": (4416, 32), "unfused": (448, 64)}  # 4416/32: 23 splits of 3 tiles; 448/64: 7 splits of 1 tile
-PATHS_3B = {"fused": (4416, 32), "unfused": (4352, 64)}  # 4352/64: 34 splits of 2 tiles (over the 32-split bound)
+# The decode step has three kernel paths, each run below with its launch counts asserted:
+#   layer   each layer one launch (attention, output projection and MoE exchanging through the XCDs' L2s and
+#           device-wide), where the cache shape gives 2..3 tiles per split and at most 32 splits (MOERT_LAYER=1);
+#   fused   the same shapes with three launches per layer (the attention block, the output projection, the MoE
+#           kernel over the XCDs): the default, and the bench's path;
+#   unfused q/k/v, split attention, combine, output projection, router + gate/up, down.
+PATHS_1B = {"layer": (4416, 32), "fused": (4416, 32), "unfused": (448, 64)}  # 4416/32: 23 splits of 3 tiles
+PATHS_3B = {"layer": (4416, 32), "fused": (4416, 32), "unfused": (4352, 64)}  # 4352/64: 34 splits (over 32)
+ALL_PATHS = ["layer", "fused", "unfused"]
+
+
+def make_model(m, path, max_len, splits):
+    if path != "layer":
+        return moert.GpuModel(m, max_len, attn_splits=splits)
+    os.environ["MOERT_LAYER"] = "1"
+    try:
+        return moert.GpuModel(m, max_len, attn_splits=splits)
+    finally:
+        del os.environ["MOERT_LAYER"]
 
 
 def assert_kernel_path(g, cfg, path):
     """The step's kernels: the model's own report, then the launches of one step (run last: it moves the position
     to the cache's end)."""
-    fused = path == "fused"
-    assert g.kernel_path() == (fused, fused)
+    assert g.kernel_path() == path
+    kinds = (moert.K_LAYER, moert.K_LAYER_COMBINE, moert.K_ATTN_BLOCK, moert.K_MOE_XCD, moert.K_QKV,
+             moert.K_ROUTE_UP, moert.K_EXPERT_DOWN, moert.K_MOE_COMBINE, moert.K_OPROJ)
     n = {}
-    for k in (moert.K_ATTN_BLOCK, moert.K_MOE_XCD, moert.K_QKV, moert.K_ROUTE_UP, moert.K_EXPERT_DOWN,
-              moert.K_MOE_COMBINE):
+    for k in kinds:
         g.set_position(g.max_len - 1)
         n[k] = g.time_kernel(k, 1)[1]
     L = cfg.layers
-    if fused:
-        assert n == {moert.K_ATTN_BLOCK: L, moert.K_MOE_XCD: L, moert.K_QKV: 0, moert.K_ROUTE_UP: 0,
-                     moert.K_EXPERT_DOWN: 0, moert.K_MOE_COMBINE: 1}, n
+    want = dict.fromkeys(kinds, 0)
+    if path == "layer":
+        want.update({moert.K_LAYER: L, moert.K_LAYER_COMBINE: 1})
+    elif path == "fused":
+        want.update({moert.K_ATTN_BLOCK: L, moert.K_MOE_XCD: L, moert.K_MOE_COMBINE: 1, moert.K_OPROJ: L})
     else:
-        assert n == {moert.K_ATTN_BLOCK: 0, moert.K_MOE_XCD: 0, moert.K_QKV: L, moert.K_ROUTE_UP: L,
-                     moert.K_EXPERT_DOWN: L, moert.K_MOE_COMBINE: 0}, n
+        want.update({moert.K_QKV: L, moert.K_ROUTE_UP: L, moert.K_EXPERT_DOWN: L, moert.K_OPROJ: L})
+    assert n == want, n
 
 
 @pytest.fixture(scope="module")
@@ -168,11 +183,11 @@ def granite_1b():
 
 def _pair_1b(m, path):
     max_len, splits = PATHS_1B[path]
-    return (moert.GpuModel(m, max_len, attn_splits=splits),
+    return (make_model(m, path, max_len, splits),
             oracle.CpuSession(m, max_len, attn_splits=splits, threads=THREADS))
 
 
-@pytest.mark.parametrize("path", ["fused", "unfused"])
+@pytest.mark.parametrize("path", ALL_PATHS)
 def test_granite_1b_greedy_128_prompt_256_tokens_identical(gpu, granite_1b, path):
     """Granite-1B-A400M shape, Q8_0 weights, fp32 embedding/head; 128-token uniform prompt, 256 greedy tokens:
     identical tokens, last logits and hidden state bit for bit, every KV row the run appended. (With N(0, 0.02)
@@ -187,7 +202,7 @@ def test_granite_1b_greedy_128_prompt_256_tokens_identical(gpu, granite_1b, path
     g.close()
 
 
-@pytest.mark.parametrize("path", ["fused", "unfused"])
+@pytest.mark.parametrize("path", ALL_PATHS)
 def test_granite_1b_forced_tokens_every_step_bit_identical(gpu, granite_1b, path):
     """The 1B workload with a forced random token stream over its 384 positions (128 prompt + 256): logits, routes
     and weights of every step, the final hidden state and every KV row, bit for bit."""
@@ -200,7 +215,7 @@ def test_granite_1b_forced_tokens_every_step_bit_identical(gpu, granite_1b, path
     g.close()
 
 
-@pytest.mark.parametrize("path", ["fused", "unfused"])
+@pytest.mark.parametrize("path", ALL_PATHS)
 def test_granite_1b_wider_init_greedy_moves_and_stays_identical(gpu, path):
     """The 1B shape with N(0, 0.1) weights, whose greedy trajectory does not settle: 128-token prompt, 256 greedy
     tokens identical to the oracle (at least 100 distinct), last logits and hidden state bit for bit."""
@@ -223,7 +238,7 @@ def _granite_3b(std):
 
 def _prefilled_pair(cfg, m, kv, path, ctx=4096):
     max_len, splits = PATHS_3B[path]
-    g = moert.GpuModel(m, max_len, attn_splits=splits)
+    g = make_model(m, path, max_len, splits)
     s = oracle.CpuSession(m, max_len, attn_splits=splits, threads=THREADS)
     for l, (k, v) in enumerate(kv):
         g.kv_prefill(l, k, v)
@@ -238,7 +253,7 @@ def granite_3b():
     return _granite_3b(0.02)
 
 
-@pytest.mark.parametrize("path", ["fused", "unfused"])
+@pytest.mark.parametrize("path", ALL_PATHS)
 def test_granite_3b_long_context_256_steps_identical(gpu, granite_3b, path):
     """Granite-3B-A800M shape, Q8_0 weights and head; KV cache pre-filled to 4096 positions with fp16 N(0,1);
     256 decode steps: the first step's logits and routes, the greedy tokens, the last step's logits and hidden state,
@@ -257,7 +272,7 @@ def test_granite_3b_long_context_256_steps_identical(gpu, granite_3b, path):
     g.close()
 
 
-@pytest.mark.parametrize("path", ["fused", "unfused"])
+@pytest.mark.parametrize("path", ALL_PATHS)
 def test_granite_3b_forced_tokens_at_4096_every_step_bit_identical(gpu, granite_3b, path):
     """The 3B workload with a forced random token stream: 256 steps after the 4096 cached positions, logits, routes
     and weights of every step, the final hidden state and the appended KV rows, bit for bit."""
@@ -275,7 +290,7 @@ def granite_3b_wide():
     return _granite_3b(0.1)
 
 
-@pytest.mark.parametrize("path", ["fused", "unfused"])
+@pytest.mark.parametrize("path", ALL_PATHS)
 def test_granite_3b_wider_init_greedy_moves_and_stays_identical(gpu, granite_3b_wide, path):
     """The 3B long-context workload with N(0, 0.1) weights, whose greedy trajectory does not settle: 256 greedy steps
     after 4096 cached positions, identical tokens (at least 100 distinct), last logits and hidden state bit for
