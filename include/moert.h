@@ -257,8 +257,8 @@ int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch
  * otherwise *attn_block = 1 when the attention half is the one-launch attention block (MOERT_K_ATTN_BLOCK) rather
  * than q/k/v + split attention + combine, and *moe_xcd = 1 when the MoE half is the kernel spread over the XCDs
  * (MOERT_K_MOE_XCD) rather than router + gate/up and down. They depend on the shapes, the model kind and its modes
- * (the cache's prefetch branch uses none of them); MOERT_LAYER=1 at create asks for one launch per layer where the
- * shape allows it. No reference counterpart. */
+ * (the cache's prefetch branch uses none of them); MOERT_LAYER=0 at create keeps the three launches per layer. No
+ * reference counterpart. */
 int moert_model_path(const moert_model* m, int* layer, int* attn_block, int* moe_xcd);
 
 /* Test hook for the failure path of the fused kernels (MOERT_K_ATTN_BLOCK, MOERT_K_MOE_XCD); it has no counterpart

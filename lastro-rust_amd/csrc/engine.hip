@@ -211,8 +211,7 @@ struct moert_model {
   // keeps k_route_up + k_expert_down.
   bool use_mx = false;
   // every layer as one launch (layers.hip), where the shape allows it with the attention block and the MoE kernel
-  // over the XCDs, when MOERT_LAYER=1 at create (measured no faster than the three launches per layer, which stay
-  // the default)
+  // over the XCDs; MOERT_LAYER=0 at create keeps three launches per layer
   bool use_px = false;
   PxBufs px{};
   std::vector<PxLayer> pxl;
@@ -284,7 +283,8 @@ struct moert_model {
         launch_embed(stream, embed, dims, b, ab.step_ctr, use_blk ? ab.rope_cur : nullptr, arm(MOERT_K_EMBED, -1)));
     if (use_px) {
       for (size_t l = 0; l < layers.size(); l++)
-        CHECK_HIP(launch_layer(stream, pxl[l], layers[l], (int)l, dims, b, cus, ab, px, arm(MOERT_K_LAYER, (int)l)));
+        CHECK_HIP(launch_layer(stream, pxl[l], layers[l], (int)l, dims, b, cus, ab, px,
+                               l + 1 < layers.size() ? &pxl[l + 1] : nullptr, arm(MOERT_K_LAYER, (int)l)));
       CHECK_HIP(launch_layer_combine(stream, dims, b, (int)layers.size() - 1, ab, px, arm(MOERT_K_LAYER_COMBINE, -1)));
       CHECK_HIP(launch_head(stream, embed, norm, dims, b, arm(MOERT_K_HEAD, -1)));
       CHECK_HIP(launch_head_argmax(stream, embed, dims, b, arm(MOERT_K_HEAD_ARGMAX, -1)));
@@ -873,7 +873,7 @@ static int model_create(const moert_config* c, const moert_model_weights* w, int
     const char* mv = getenv("MOERT_MOE_XCD");
     m->use_mx = m->use_ab && cache_slots == 0 && !(mv && mv[0] == '0') && moe_xcd_fits(m->dims, m->layers[0], m->cus);
     const char* lv = getenv("MOERT_LAYER");
-    if (m->use_mx && lv && lv[0] == '1' && layers_fit(m->dims, m->layers[0], m->cus)) {
+    if (m->use_mx && !(lv && lv[0] == '0') && layers_fit(m->dims, m->layers[0], m->cus)) {
       unsigned *pxx = nullptr, *pxd = nullptr;
       float* hpp = nullptr;
       if ((rc = zeros(a, s, 8 * sizeof(PxXcd) / 4, &pxx)) || (rc = zeros(a, s, sizeof(PxDev) / 4, &pxd)) ||

@@ -42,8 +42,11 @@ struct PxBufs {
 bool layers_fit(const Dims& d, const LayerDev& L, int cus);
 // One layer as one launch: layer 0 reads the embedding row from b.h; a later layer reads the previous launch's h'
 // (p.hp), expert outputs (x.ys) and routing weights (b.route_w); its own routing goes to b.route_ids / b.route_w.
+// With `next` (the following layer), the launch's last phase also reads the next launch's q/k/v and output rows and
+// K/V tiles once, into the XCDs' L2s.
 hipError_t launch_layer(hipStream_t s, const PxLayer& L, const LayerDev& Ld, int layer, const Dims& d,
-                        const StepBufs& b, int cus, const AbBufs& x, const PxBufs& p, Tl tl = {});
+                        const StepBufs& b, int cus, const AbBufs& x, const PxBufs& p, const PxLayer* next,
+                        Tl tl = {});
 // The last layer's experts combined into b.h for the head.
 hipError_t launch_layer_combine(hipStream_t s, const Dims& d, const StepBufs& b, int last_layer, const AbBufs& x,
                                 const PxBufs& p, Tl tl = {});

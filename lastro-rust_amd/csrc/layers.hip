@@ -73,11 +73,16 @@ __device__ __forceinline__ bool poll_m(const LD& ld, const int (&idx)[M], const 
   return false;
 }
 
+// A dword read of a 128-byte line that leaves the line in the XCD's L2 for the next launch; the value is kept only
+// so that the read is not dropped.
+__device__ __forceinline__ unsigned warm(const void* line) { return *gmem(reinterpret_cast<const unsigned*>(line)); }
+
 }  // namespace
 
 // DT: dtype of every projection; K: hidden (= heads * 64); G: query heads per KV head; T: tiles per split.
 template <int DT, int K, int G, int T>
-__global__ __launch_bounds__(kPxThreads) void k_layer(PxLayer L, int l, float eps, float res, float scale, int max_len,
+__global__ __launch_bounds__(kPxThreads) void k_layer(PxLayer L, PxLayer Ln, int pf, int l, float eps, float res,
+                                                     float scale, int max_len,
                                                      int splits, int pp, const int* __restrict__ st,
                                                      const float* __restrict__ rope_cur, const float* __restrict__ h,
                                                      float* __restrict__ hpp, float* __restrict__ ysp,
@@ -460,10 +465,40 @@ __global__ __launch_bounds__(kPxThreads) void k_layer(PxLayer L, int l, float ep
     const bool orow = w < NOW && wid < 8;
     const int orw = x * (K / 8) + 8 * w + wid;
     Rows<DT, K, 1> ro;
-    {
+    unsigned keep0 = 0, keep1 = 0;
+    if (wid < 8) {
+      // (a workgroup without output rows loads row 0, unused)
       size_t r1[1] = {(size_t)(orow ? orw : 0)};
       bool ok1[1] = {orow};
-      if (orow) rows_load<DT, K, 1>(ro, L.o, r1, ok1, lane);
+      rows_load<DT, K, 1>(ro, L.o, r1, ok1, lane);
+      // behind the output row: one read of each 128-byte line that the next launch's workgroup of this split loads
+      // first (its q/k/v pair rows and output row, slot A; its K/V tiles, slot B), so that they come from the XCD's
+      // L2 there (the reads go out while the exchanges of phases C and D leave HBM idle). They are unconditional (a
+      // lane without a line reads the head's first one), so that the wait for the output row counts exactly them.
+      const PxLayer& N = pf ? Ln : L;
+      constexpr int RL = (int)(K * (DT == DT_Q4_0 ? 1 : 2) / 2 / 128);  // lines of a row's payload
+      const int pa = w * pp + wid;
+      const int ah = min(pa, NPAIR - 1) / 32, aj = min(pa, NPAIR - 1) % 32;
+      const int agh = ah < G ? g * G + ah : ah == G ? 8 * G + g : 8 * G + 8 + g;
+      const size_t arow0 = (size_t)agh * 64 + aj, orow0 = (size_t)(x * (K / 8) + 8 * w + wid);
+      const bool apair = wid < pp && pa < NPAIR;
+      const int ar = lane < 3 * RL ? lane / RL : lane - 3 * RL;  // payload lines of rows 0..2, then their scales
+      const bool apay = lane < 3 * RL;
+      const bool aval = ar <= 1 ? apair : ar == 2 && w < NOW;
+      const size_t rsel = ar == 0 ? arow0 : ar == 1 ? arow0 + 32 : orow0;
+      const uint8_t* aq = ar == 2 ? N.o.q : N.qkv.q;
+      const uint16_t* ad = ar == 2 ? N.o.d : N.qkv.d;
+      const uint8_t* la = apay ? aq + rsel * (size_t)(RL * 128) + (size_t)(lane % RL) * 128
+                               : reinterpret_cast<const uint8_t*>(ad + rsel * (size_t)(K / 32));
+      const int ntl = s < splits ? min(T, max_len / 64 - t0) : 0;
+      const int u = wid * 64 + lane;
+      const bool bk = u < ntl * 64, bv = !bk && u < 2 * ntl * 64;
+      const size_t tbase = ((size_t)g * max_len + (size_t)t0 * 64) * 64;
+      const uint8_t* lb = reinterpret_cast<const uint8_t*>(bk ? N.kc + tbase : N.vc + tbase) +
+                          (size_t)(bk ? u : bv ? u - ntl * 64 : 0) * 128;
+      const uint8_t* l0 = reinterpret_cast<const uint8_t*>(N.kc + (size_t)g * max_len * 64);  // head g's first line
+      keep0 = warm(aval ? la : l0);
+      keep1 = warm(bk || bv ? lb : l0);
     }
     __builtin_amdgcn_sched_barrier(0);
     // the merged heads of the 8 XCDs: wave 8 of workgroup w < 8 relays XCD w's G heads from the device-wide area
@@ -745,6 +780,7 @@ __global__ __launch_bounds__(kPxThreads) void k_layer(PxLayer L, int l, float ep
           if (dok[p]) *gmem_w(ysp + (size_t)x * K + dr[p]) = dout[p];
       }
     }
+    asm volatile("" ::"v"(keep0), "v"(keep1));
   }
 
   TL_END(tl);
@@ -810,13 +846,13 @@ __global__ __launch_bounds__(256) void k_layer_combine(const float* __restrict__
 }
 
 hipError_t launch_layer(hipStream_t s, const PxLayer& L, const LayerDev& Ld, int layer, const Dims& d,
-                        const StepBufs& b, int cus, const AbBufs& x, const PxBufs& p, Tl tl) {
+                        const StepBufs& b, int cus, const AbBufs& x, const PxBufs& p, const PxLayer* next, Tl tl) {
   PxShape sh;
   if (!px_shape(d, Ld, cus, &sh) || layer < 0 || layer > 62) return hipErrorInvalidValue;
 #define PX_LAUNCH(DD, KK, GG, TT)                                                                              \
-  klaunch(k_layer<DD, KK, GG, TT>, 256, kPxThreads, 0, s, L, layer, d.eps, d.res_mult, d.attn_mult, d.max_len,   \
-          sh.splits, sh.pp, b.state, x.rope_cur, b.h, p.hp, x.ys, x.groups, x.moe, p.xcd, p.dev, x.step_ctr, x.err, \
-          b.route_ids, b.route_w, tl)
+  klaunch(k_layer<DD, KK, GG, TT>, 256, kPxThreads, 0, s, L, next ? *next : L, next ? 1 : 0, layer, d.eps,      \
+          d.res_mult, d.attn_mult, d.max_len, sh.splits, sh.pp, b.state, x.rope_cur, b.h, p.hp, x.ys, x.groups, x.moe, \
+          p.xcd, p.dev, x.step_ctr, x.err, b.route_ids, b.route_w, tl)
 #define PX_CASE(DD, KK, GG, TT)                                                             \
   if (Ld.qkv.dtype == DD && d.hidden == KK && sh.G == GG && sh.T == TT) {                   \
     PX_LAUNCH(DD, KK, GG, TT);                                                              \

@@ -41,16 +41,16 @@ def three_kernel_model(m, max_len, splits, var="MOERT_ATTN_BLOCK", **kw):
 
 
 def fused_model(m, max_len, splits, **kw):
-    """The default: the attention block, the output projection and the MoE kernel over the XCDs as separate
-    launches."""
-    return moert.GpuModel(m, max_len, attn_splits=splits, **kw)
+    """The attention block, the output projection and the MoE kernel over the XCDs as separate launches
+    (MOERT_LAYER=0), not one launch per layer."""
+    return env_model(m, max_len, splits, "MOERT_LAYER", "0", **kw)
 
 
 def path_model(m, max_len, splits, path, **kw):
-    """path "layer": one launch per layer (MOERT_LAYER=1); "fused": the default."""
-    if path == "layer":
-        return env_model(m, max_len, splits, "MOERT_LAYER", "1", **kw)
-    return fused_model(m, max_len, splits, **kw)
+    """path "layer": one launch per layer (the default where the shape allows it); "fused": MOERT_LAYER=0."""
+    if path == "fused":
+        return fused_model(m, max_len, splits, **kw)
+    return moert.GpuModel(m, max_len, attn_splits=splits, **kw)
 
 
 def launches(g, kind):

@@ -134,9 +134,9 @@ def _forced_identity(g, s, toks, label, every=1):
 
 # The decode step has three kernel paths, each run below with its launch counts asserted:
 #   layer   each layer one launch (attention, output projection and MoE exchanging through the XCDs' L2s and
-#           device-wide), where the cache shape gives 2..3 tiles per split and at most 32 splits (MOERT_LAYER=1);
+#           device-wide), where the cache shape gives 2..3 tiles per split and at most 32 splits: the bench's path;
 #   fused   the same shapes with three launches per layer (the attention block, the output projection, the MoE
-#           kernel over the XCDs): the default, and the bench's path;
+#           kernel over the XCDs; MOERT_LAYER=0);
 #   unfused q/k/v, split attention, combine, output projection, router + gate/up, down.
 PATHS_1B = {"layer": (4416, 32), "fused": (4416, 32), "unfused": (448, 64)}  # 4416/32: 23 splits of 3 tiles
 PATHS_3B = {"layer": (4416, 32), "fused": (4416, 32), "unfused": (4352, 64)}  # 4352/64: 34 splits (over 32)
@@ -144,9 +144,9 @@ ALL_PATHS = ["layer", "fused", "unfused"]
 
 
 def make_model(m, path, max_len, splits):
-    if path != "layer":
+    if path != "fused":
         return moert.GpuModel(m, max_len, attn_splits=splits)
-    os.environ["MOERT_LAYER"] = "1"
+    os.environ["MOERT_LAYER"] = "0"
     try:
         return moert.GpuModel(m, max_len, attn_splits=splits)
     finally:
