@@ -145,7 +145,12 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
   __builtin_amdgcn_s_barrier();
   __builtin_amdgcn_sched_barrier(0);
   Rows<DT, K, P> rr;
-  if (ok[0]) rows_load<DT, K, P>(rr, m, row, ok, lane);  // a wave with no pair (wave-uniform) loads no row
+  if (ok[0]) {  // a wave with no pair (wave-uniform) loads no row
+    rows_load<DT, K, P>(rr, m, row, ok, lane);
+    // the wave's rows in before its tiles are requested (vmcnt(0)): the rows come first, and the pairs' dot does not
+    // wait for the tiles
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+  }
   __builtin_amdgcn_sched_barrier(0);
   const int t0 = s * T, t = t0 + wt;
   const int tc = min(t, max_len / 64 - 1);  // a tile past the cache's end (never used) reads the last tile

@@ -124,6 +124,7 @@ __global__ __launch_bounds__(kPxThreads) void k_layer(PxLayer L, PxLayer Ln, int
   __shared__ __align__(16) float lg[64];
   __shared__ int part[NW][64];
   __shared__ float rs;
+  __shared__ float hp8_s[8];  // the workgroup's output rows of h' (phase C)
   __shared__ int dead_s;
 
   const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -196,7 +197,12 @@ __global__ __launch_bounds__(kPxThreads) void k_layer(PxLayer L, PxLayer Ln, int
     row[1] = row[0] + 32;
   }
   Rows<DT, K, 2> rr;
-  if (pok) rows_load<DT, K, 2>(rr, L.qkv, row, rok, lane);
+  if (pok) {
+    rows_load<DT, K, 2>(rr, L.qkv, row, rok, lane);
+    // the wave's rows in before its tiles are requested (vmcnt(0)): the rows come first, and the pair's dot does
+    // not wait for the tiles
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+  }
   const int tc = min(t, max_len / 64 - 1);
   VShare<G> ksh, vsh;
   if (wid < G * T) {
@@ -549,10 +555,13 @@ __global__ __launch_bounds__(kPxThreads) void k_layer(PxLayer L, PxLayer Ln, int
         rows_fma<DT, K, 1>(ro, ok1, xr, lane, out);
         if (lane == 0) {
           const float hv = hin[orw] + res * out[0];
-          put_dev(&dv->hp[orw], __float_as_uint(hv), epoch);
+          hp8_s[wid] = hv;
           *gmem_w(hpp + orw) = hv;  // for the next launch
         }
       }
+      __syncthreads();
+      // the workgroup's 8 rows of h' go out device-wide as one 64-byte store (8 lanes), not 8 single entries
+      if (wid == 0 && lane < 8) put_dev(&dv->hp[x * (K / 8) + 8 * w + lane], __float_as_uint(hp8_s[lane]), epoch);
       TL_PHASE(tl, 5);
     }
 
