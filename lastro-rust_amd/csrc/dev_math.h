@@ -185,6 +185,12 @@ __device__ __forceinline__ uint2 gload_u2(const void* p) {
   const moert_u32x2 v = *(const MOERT_GLOBAL moert_u32x2*)p;
   return make_uint2(v.x, v.y);
 }
+// The same 16-byte load with the non-temporal hint: the line goes into the L2 as the first to be evicted, so that a
+// stream read once does not push out lines that a later launch will read.
+__device__ __forceinline__ uint4 gload_u4_nt(const void* p) {
+  const moert_u32x4 v = __builtin_nontemporal_load((const MOERT_GLOBAL moert_u32x4*)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 __device__ __forceinline__ float4 gload_f4(const void* p) {
   const moert_f32x4 v = *(const MOERT_GLOBAL moert_f32x4*)p;
   return make_float4(v.x, v.y, v.z, v.w);
@@ -197,16 +203,16 @@ struct RawChunk {
   uint32_t d;
 };
 
-template <int DT>
+// NT: with the non-temporal hint (rows streamed once per step).
+template <int DT, bool NT = false>
 __device__ __forceinline__ RawChunk load_chunk(const DMat& m, size_t row, int j) {
   RawChunk c;
   const uint8_t* base = m.q + row * Fmt<DT>::row_bytes(m.cols);
-  c.v = gload_u4(base + (size_t)j * 16);
-  if (DT == DT_Q8_0)
-    c.d = *gmem(m.d + row * (size_t)(m.cols / 32) + (j >> 1));
-  else if (DT == DT_Q4_0)
-    c.d = *gmem(m.d + row * (size_t)(m.cols / 32) + j);
-  else
+  c.v = NT ? gload_u4_nt(base + (size_t)j * 16) : gload_u4(base + (size_t)j * 16);
+  if (DT == DT_Q8_0 || DT == DT_Q4_0) {
+    const uint16_t* sp = m.d + row * (size_t)(m.cols / 32) + (DT == DT_Q8_0 ? (j >> 1) : j);
+    c.d = NT ? __builtin_nontemporal_load(gmem(sp)) : *gmem(sp);
+  } else
     c.d = 0x3c00u;  // 1.0
   return c;
 }

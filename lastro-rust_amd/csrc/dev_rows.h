@@ -113,7 +113,8 @@ struct Rows {
 
 // Loads are unconditional (a row that is not used loads row 0, a chunk past the row end loads the last chunk) so
 // that they form one straight run of independent loads; rows_fma skips what is not used.
-template <int DT, int K, int P>
+// NT: the loads carry the non-temporal hint.
+template <int DT, int K, int P, bool NT = false>
 __device__ __forceinline__ void rows_load(Rows<DT, K, P>& r, const DMat& m, const size_t (&row)[P],
                                           const bool (&ok)[P], int sub) {
   using G = Geo<DT, K>;
@@ -122,7 +123,7 @@ __device__ __forceinline__ void rows_load(Rows<DT, K, P>& r, const DMat& m, cons
 #pragma unroll
     for (int jj = 0; jj < G::NJ; jj++) {
       const int j = sub + G::LPR * jj;
-      r.c[p][jj] = load_chunk<DT>(m, ok[p] ? row[p] : 0, j < G::NCH ? j : G::NCH - 1);
+      r.c[p][jj] = load_chunk<DT, NT>(m, ok[p] ? row[p] : 0, j < G::NCH ? j : G::NCH - 1);
     }
 }
 

@@ -741,12 +741,12 @@ __global__ __launch_bounds__(kPxThreads) void k_layer(PxLayer L, PxLayer Ln, int
       uok[2 * a] = uok[2 * a + 1] = v;
     }
     Rows<DT, K, 2 * NPU> ur;
-    if (up) rows_load<DT, K, 2 * NPU>(ur, L.gu, urow, uok, lane);
+    if (up) rows_load<DT, K, 2 * NPU, true>(ur, L.gu, urow, uok, lane);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     Rows<DT, 512, DP> dd;
-    if (!up) rows_load<DT, 512, DP>(dd, L.dn, drow, dok, dsub);
+    if (!up) rows_load<DT, 512, DP, true>(dd, L.dn, drow, dok, dsub);
     if (up) {
       XReg<DT, K> xr;
       load_x<DT, K>(xr, xm, lane);
