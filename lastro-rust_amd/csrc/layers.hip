@@ -692,22 +692,6 @@ __global__ __launch_bounds__(kPxThreads) void k_layer(PxLayer L, PxLayer Ln, int
       for (int v2 = 0; v2 < NW; v2++) rank += part[v2][lane];
     }
     const bool sel = lane < E && rank < 8;
-    if (wid == 0) {
-      int eid[8];
-      ids_by_rank(sel, rank, 8, eid);
-      // the weights in rank order for the next layer's input (and, from workgroup 0, the step's routing record)
-      const float lv = lg[lane];
-      const float ex = sel ? dexp(lv - lg[eid[0]]) : 0.0f;
-      float sum = 0.0f;
-#pragma unroll
-      for (int r2 = 0; r2 < 8; r2++) sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), eid[r2]));
-      if (sel) {
-        if (blockIdx.x == 0) {
-          *gmem_w(route_ids + l * 8 + rank) = lane;
-          *gmem_w(route_w + l * 8 + rank) = ex / sum;
-        }
-      }
-    }
     TL_PHASE(tl, 9);
     const unsigned long long bx = __ballot(sel && rank == x);
     const int ej = bx ? __ffsll((long long)bx) - 1 : 0;
@@ -758,6 +742,22 @@ __global__ __launch_bounds__(kPxThreads) void k_layer(PxLayer L, PxLayer Ln, int
           if (uok[2 * a]) put_entry(&mg->act[pi[a]], __float_as_uint(silu_mul(out[2 * a], out[2 * a + 1])), epoch);
       }
     } else {
+      // the step's routing record and the weights in rank order for the next layer's input: workgroup 0's last
+      // wave, a down wave, after its down rows are requested (no gate/up wave waits for it)
+      if (blockIdx.x == 0 && wid == NW - 1) {
+        int eid[8];
+        ids_by_rank(sel, rank, 8, eid);
+        const float lv = lg[lane];
+        const float ex = sel ? dexp(lv - lg[eid[0]]) : 0.0f;
+        float sum = 0.0f;
+#pragma unroll
+        for (int r2 = 0; r2 < 8; r2++)
+          sum = sum + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), eid[r2]));
+        if (sel) {
+          *gmem_w(route_ids + l * 8 + rank) = lane;
+          *gmem_w(route_w + l * 8 + rank) = ex / sum;
+        }
+      }
       const int i = tx - NU * 64;
       const __amdgpu_buffer_rsrc_t ra = l2_buffer(mg->act, sizeof(mg->act));
       int idx[MA];
