@@ -220,7 +220,7 @@ __device__ __forceinline__ RawChunk load_chunk(const DMat& m, size_t row, int j)
 // The empty asm keeps the conversion at its use: hoisted up to its load (the compiler pushes the conversion through
 // the phi of a conditional load), it would make the wave wait there for every load issued before the scale.
 __device__ __forceinline__ float scale_at_use(uint32_t bits) {
-  asm volatile("" : "+v"(bits));
+  asm("" : "+v"(bits));
   return h2f((uint16_t)bits);
 }
 __device__ __forceinline__ float chunk_scale(const RawChunk& c) { return scale_at_use(c.d); }
