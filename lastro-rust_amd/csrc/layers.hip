@@ -120,7 +120,6 @@ __global__ __launch_bounds__(kPxThreads) void k_layer(PxLayer L, PxLayer Ln, int
   __shared__ __align__(16) float Ps[G][T][64];
   __shared__ float Pv[G][T][64];
   __shared__ float Tm[G][T], Al[G][T], Ts[G][T];
-  __shared__ float Cw[2][64];
   __shared__ __align__(16) float lg[64];
   __shared__ int part[NW][64];
   __shared__ float rs;
@@ -451,15 +450,15 @@ __global__ __launch_bounds__(kPxThreads) void k_layer(PxLayer L, PxLayer Ln, int
         lsv = 0.0f;
       }
       const float M = group_max<64>(ms);
-      Cw[0][lane] = lane < nsplit ? dexp(ms - M) : 0.0f;
-      Cw[1][lane] = lsv;
-      wave_lds_sync();
+      // split s2's weight and sum from lane s2 by readlane (no LDS round trips between the FMAs)
+      const float wsl = lane < nsplit ? dexp(ms - M) : 0.0f;
       float den = 0.0f, num = 0.0f;
 #pragma unroll
       for (int s2 = 0; s2 < 32; s2++) {
         if (s2 < nsplit) {
-          const float ws = Cw[0][s2];
-          den = __builtin_fmaf(ws, Cw[1][s2], den);
+          const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(wsl), s2));
+          const float ls = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__float_as_uint(lsv), s2));
+          den = __builtin_fmaf(ws, ls, den);
           num = __builtin_fmaf(ws, av[s2], num);
         }
       }
