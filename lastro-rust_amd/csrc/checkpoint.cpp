@@ -116,14 +116,14 @@ int open_file(moert_checkpoint* ck, const std::string& path) {
     if (!off || off->kind != JVal::ARR)
       return set_error(MOERT_E_CONFIG, "safetensors: %s: no data_offsets", name.c_str());
     if (off->arr.size() != 2)
-      return set_error(MOERT_E_CONFIG, "safetensors: %s: data_offsets with %zu values (expected 2)", name.c_str(),
+      return set_error(MOERT_E_CONFIG, "safetensors: %s: data_offsets must be [begin, end], got %zu numbers", name.c_str(),
                        off->arr.size());
     const JVal &a = off->arr[0], &b = off->arr[1];
     if (a.kind != JVal::NUM || !a.is_uint || b.kind != JVal::NUM || !b.is_uint)
       return set_error(MOERT_E_CONFIG, "safetensors: %s: data_offsets not numeric", name.c_str());
     const uint64_t base = 8 + n;
     if (a.u > UINT64_MAX - base || b.u > UINT64_MAX - base || a.u > b.u || base + b.u > size)
-      return set_error(MOERT_E_CONFIG, "safetensors: %s: offsets outside the file", name.c_str());
+      return set_error(MOERT_E_CONFIG, "safetensors: %s: the tensor's byte range ends past the data section", name.c_str());
     e.start = base + a.u;
     e.end = base + b.u;
     ck->index[name] = std::move(e);
@@ -151,7 +151,7 @@ int read_bf16(const moert_checkpoint* ck, const char* name, std::vector<uint16_t
     return set_error(MOERT_E_CONFIG, "safetensors: %s: dtype %s (expected BF16)", name, e.dtype.c_str());
   uint64_t bytes = 0;
   if (!shape_bytes(e.shape, 2, &bytes) || bytes != e.end - e.start)
-    return set_error(MOERT_E_CONFIG, "safetensors: %s: size does not match the shape", name);
+    return set_error(MOERT_E_CONFIG, "safetensors: %s: byte count differs from dtype size x product of the shape", name);
   out.resize(bytes / 2);
   if (!read_at(ck->files[e.file].second, out.data(), bytes, e.start))
     return set_error(MOERT_E_CONFIG, "safetensors: %s: short read", name);

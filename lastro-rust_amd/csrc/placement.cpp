@@ -82,7 +82,8 @@ void Placement::serve_layer(int l, const int* ids, int m, std::vector<int>* unio
         n_e[it - keys.begin()]++;
       }
     }
-  // the frequency counts every request at the same instant, before any decision of the layer; the clock moves m
+  // all of this layer's requests are recorded in the frequency table with one timestamp (step_), ahead of the
+  // placement decisions below; afterwards the timestamp advances by the m positions of the block
   for (size_t i = 0; i < keys.size(); i++)
     for (int r = 0; r < n_e[i]; r++) freq_.touch(keys[i], step_);
   step_ += (uint64_t)m;
