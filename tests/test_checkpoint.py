@@ -49,7 +49,7 @@ def test_reader_reads_bf16_and_refuses_other_dtypes_missing_tensors_and_bad_offs
     ck.close()
     raw = path.read_bytes()
     path.write_bytes(raw[:-6])  # offsets past the end of the file
-    with pytest.raises(moert.MoertError, match="outside the file"):
+    with pytest.raises(moert.MoertError, match="ends past the data section"):
         moert.Checkpoint(tmp_path)
 
 
