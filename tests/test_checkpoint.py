@@ -81,7 +81,7 @@ def test_reader_refuses_an_overflowing_shape_on_read_and_broken_files_on_open(tm
     p.write_bytes(len(head).to_bytes(8, "little") + head + bytes(16))
     ck = moert.Checkpoint(tmp_path)
     buf = np.zeros(2, np.uint16)
-    with pytest.raises(moert.MoertError, match="size does not match"):
+    with pytest.raises(moert.MoertError, match="byte count differs"):
         moert.check(moert.lib().moert_checkpoint_read_bf16(ck.h, b"a", moert.ptr(buf), 2))
     ck.close()
     for raw in (b"\x05\x00\x00\x00\x00\x00\x00\x00{abc}", (200 << 20).to_bytes(8, "little") + b"{}", b"\x01\x00"):
