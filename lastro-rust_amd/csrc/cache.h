@@ -56,6 +56,10 @@ hipError_t launch_expert_down_cached(hipStream_t s, const Dims& d, const StepBuf
                                      Tl tl = {});
 // h[i] += res * y[i] for i < n (hybrid: the host-computed experts of a layer step)
 hipError_t launch_add_scaled(hipStream_t s, float* h, const float* y, float res, int n);
+// A hybrid layer's doorbell: waits (bounded) for the host's flag word *flag to carry `seq` (flag = seq << 1 | any),
+// then adds res * y when any; a flag that never comes sets bit 256 of *err.
+hipError_t launch_hy_doorbell_add(hipStream_t s, float* h, const float* y, float res, int n, const unsigned* flag,
+                                  unsigned seq, unsigned* err);
 
 // Prefetch branch of a cached step, for layer `layer` (run on a side stream while the layer's attention runs):
 // launch_prefetch_decide predicts the layer's experts from its input h (the layer's router on rmsnorm(h, ln_moe),

@@ -8,6 +8,7 @@
 // same graph serves every position and greedy generation needs no host synchronisation between tokens.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <chrono>
 #include <cmath>
 #include <memory>
@@ -242,8 +243,9 @@ struct moert_model {
   double mx_wait_s = 0;
   double mx_speed_last[2] = {};  // decode and prefill tok/s of the last finished request
   // host-CPU hybrid (moert_model_create_hybrid): the placement state machine, the token's table on the device, the
-  // pinned read-backs of each layer's routing and normalised input, the host experts' sum (mapped for the add
-  // kernel), and per position and layer: hits, copies, dropped, host-computed requests
+  // pinned read-backs of each layer's routing and normalised input (two layers' worth: the next layer's are queued
+  // while this one is served), the host experts' sum (coherent mapped memory, read by the doorbell kernel), and per
+  // position and layer: hits, copies, dropped, host-computed requests
   bool hybrid = false;
   std::unique_ptr<Placement> place;
   int hy_threads = 1;
@@ -255,7 +257,14 @@ struct moert_model {
   float* hy_y_pin = nullptr;
   float* hy_y_dev = nullptr;
   float* hy_xn_dev = nullptr;
-  hipEvent_t hy_ev = nullptr;
+  // the doorbell: per layer a flag word in coherent host memory (token sequence << 1 | any host expert) that the
+  // layer's add kernel waits for, the routing event of every layer, the token's sequence number, and the device word
+  // a doorbell that never rang sets
+  unsigned* hy_flag_pin = nullptr;
+  unsigned* hy_flag_dev = nullptr;
+  unsigned* hy_err = nullptr;
+  std::vector<hipEvent_t> hy_evs;
+  unsigned hy_seq = 0;
   std::vector<float> hy_act, hy_y;
   std::vector<int> hy_tok;  // [max_len][layers][4]
 
@@ -364,25 +373,36 @@ struct moert_model {
     return MOERT_OK;
   }
 
-  // One hybrid decode step (the D1 protocol in its deterministic mode, driven from this thread): the token's table
-  // to the device; per layer the attention half and the gate/up kernel (experts in the table from their slots), the
-  // routing and the normalised input read back, the down kernel; then, on the host, the layer's requests served
-  // (placement), the experts outside the table computed and added into the residual stream by a small kernel, and
-  // the admissions' copies queued (or held until their victim's layer has passed); at the end of the token every
-  // copy queued precedes the next token's work in stream order (the barrier), and the next table is published.
+  // One hybrid decode step (the D1 protocol in its deterministic mode; cuda_backend.rs:919-1014 with the doorbell of
+  // motor/backend.rs:17-25): the token's table to the device, then the GPU work of every layer queued one layer ahead
+  // of the host: the attention half and the gate/up kernel (experts in the table from their slots), the routing and
+  // the normalised input read back behind the layer's event, the down kernel, and the doorbell kernel that waits for
+  // the layer's flag and adds the host experts' sum. This thread serves each layer as its event completes: the
+  // layer's requests (placement), the experts outside the table computed into the mapped sum, the flag rung, the
+  // admissions' copies queued (behind the next layer's queued work; held ones once their victim's layer has passed).
+  // The GPU never waits for an enqueue, only for the host experts. At the end of the token every copy queued precedes
+  // the next token's work in stream order (the barrier), and the next table is published.
   int hybrid_step() {
     Placement& P = *place;
-    const int L = cfg.layers, E = cfg.experts, K = cfg.top_k, H = cfg.hidden, I = cfg.inter;
+    const int L = cfg.layers, E = cfg.experts, K = cfg.top_k, H = cfg.hidden;
     // the previous token has ended (so its table copy has been read, and its position is final)
     CHECK_HIP(hipStreamSynchronize(stream));
+    unsigned herr = 0;
+    CHECK_HIP(hipMemcpy(&herr, hy_err, 4, hipMemcpyDeviceToHost));
+    if (herr) {
+      set_err("hybrid step: a layer's doorbell was not rung in time (error bits %#x)", herr);
+      return MOERT_E_DEVICE;
+    }
     int pos = 0;
     CHECK_HIP(hipMemcpy(&pos, b.state + ST_POS, 4, hipMemcpyDeviceToHost));
     std::memcpy(hy_table_pin, P.table().data(), (size_t)L * E * 4);
     CHECK_HIP(hipMemcpyAsync(hy_table, hy_table_pin, (size_t)L * E * 4, hipMemcpyHostToDevice, stream));
     CHECK_HIP(launch_embed(stream, embed, dims, b, ab.step_ctr, use_ab ? ab.rope_cur : nullptr));
-    std::vector<int> keys, n_e;
-    std::vector<char> gpu;
-    for (int l = 0; l < L; l++) {
+    // the token's sequence number in 31 bits, never 0 (the flags start at 0)
+    hy_seq = (hy_seq + 1u) & 0x7fffffffu;
+    if (hy_seq == 0u) hy_seq = 1u;
+    const unsigned seq = hy_seq;
+    auto enqueue_layer = [&](int l) -> int {
       const LayerDev& Ld = layers[l];
       if (use_ab) {
         CHECK_HIP(launch_attn_block(stream, Ld, dims, b, cus, l, ab, false));
@@ -393,37 +413,68 @@ struct moert_model {
       }
       CHECK_HIP(launch_oproj(stream, Ld, dims, b));
       CHECK_HIP(launch_route_up_cached(stream, Ld, dims, b, l, cache));
-      CHECK_HIP(hipMemcpyAsync(hy_ids_pin, b.route_ids + l * K, (size_t)K * 4, hipMemcpyDeviceToHost, stream));
-      CHECK_HIP(hipMemcpyAsync(hy_w_pin, b.route_w + l * K, (size_t)K * 4, hipMemcpyDeviceToHost, stream));
-      CHECK_HIP(hipMemcpyAsync(hy_xn_pin, hy_xn_dev, (size_t)H * 4, hipMemcpyDeviceToHost, stream));
-      CHECK_HIP(hipEventRecord(hy_ev, stream));
+      CHECK_HIP(hipMemcpyAsync(hy_ids_pin + 8 * (l & 1), b.route_ids + l * K, (size_t)K * 4, hipMemcpyDeviceToHost,
+                               stream));
+      CHECK_HIP(hipMemcpyAsync(hy_w_pin + 8 * (l & 1), b.route_w + l * K, (size_t)K * 4, hipMemcpyDeviceToHost,
+                               stream));
+      CHECK_HIP(hipMemcpyAsync(hy_xn_pin + (size_t)H * (l & 1), hy_xn_dev, (size_t)H * 4, hipMemcpyDeviceToHost,
+                               stream));
+      CHECK_HIP(hipEventRecord(hy_evs[l], stream));
       CHECK_HIP(launch_expert_down_cached(stream, dims, b, l, cache));
-      CHECK_HIP(hipEventSynchronize(hy_ev));
+      CHECK_HIP(launch_hy_doorbell_add(stream, b.h, hy_y_dev, dims.res_mult, H, hy_flag_dev + l, seq, hy_err));
+      return MOERT_OK;
+    };
+    // on a host-side failure the layers already queued must not wait out their doorbells: ring them all, empty
+    auto release = [&]() {
+      std::atomic_thread_fence(std::memory_order_release);
+      for (int l = 0; l < L; l++) reinterpret_cast<volatile unsigned*>(hy_flag_pin)[l] = seq << 1;
+    };
+    int rc = enqueue_layer(0);
+    if (!rc && L > 1) rc = enqueue_layer(1);
+    if (rc) {
+      release();
+      return rc;
+    }
+    std::vector<int> keys, n_e;
+    std::vector<char> gpu;
+    for (int l = 0; l < L; l++) {
+      if (hipEventSynchronize(hy_evs[l]) != hipSuccess) {
+        release();
+        set_err("hybrid step: layer %d routing event", l);
+        return MOERT_E_DEVICE;
+      }
+      const int* ids = hy_ids_pin + 8 * (l & 1);
+      const float* wts_l = hy_w_pin + 8 * (l & 1);
       for (int j = 0; j < K; j++)
-        if (hy_ids_pin[j] < 0 || hy_ids_pin[j] >= E) {
-          set_err("hybrid step: routed expert %d outside [0, %d)", hy_ids_pin[j], E);
+        if (ids[j] < 0 || ids[j] >= E) {
+          release();
+          set_err("hybrid step: routed expert %d outside [0, %d)", ids[j], E);
           return MOERT_E_DEVICE;
         }
       const PlacementStats s0 = P.stats();
-      P.serve_layer(l, hy_ids_pin, 1, &keys, &n_e, &gpu);
+      P.serve_layer(l, ids, 1, &keys, &n_e, &gpu);
       // the host experts in top-k order (CPU-served requests, HostExperts::compute)
       const uint8_t* recs[8];
       float wts[8];
       int n_host = 0;
       for (int j = 0; j < K; j++) {
-        const int key = l * E + hy_ids_pin[j];
+        const int key = l * E + ids[j];
         if (P.table()[key] >= 0) continue;
         recs[n_host] = (const uint8_t*)host_store + (size_t)key * cache.record_bytes;
-        wts[n_host++] = hy_w_pin[j];
+        wts[n_host++] = wts_l[j];
       }
       const bool any = n_host > 0;
       if (any) {
         std::fill(hy_y.begin(), hy_y.end(), 0.0f);
-        const HostRecordGeo geo{cache.pool_gu.dtype, H, I, cache.gu_q, cache.gu_d, cache.dn_q};
-        host_experts_layer(geo, recs, wts, n_host, hy_xn_pin, hy_act.data(), hy_y.data(), hy_threads);
+        const HostRecordGeo geo{cache.pool_gu.dtype, H, cfg.inter, cache.gu_q, cache.gu_d, cache.dn_q};
+        host_experts_layer(geo, recs, wts, n_host, hy_xn_pin + (size_t)H * (l & 1), hy_act.data(), hy_y.data(),
+                           hy_threads);
+        // (the previous layer's doorbell kernel has read the sum: it precedes this layer's routing event)
         std::memcpy(hy_y_pin, hy_y.data(), (size_t)H * 4);
-        CHECK_HIP(launch_add_scaled(stream, b.h, hy_y_dev, dims.res_mult, H));
       }
+      // ring the layer's doorbell: the sum is in host memory before the flag (release fence, then the store)
+      std::atomic_thread_fence(std::memory_order_release);
+      reinterpret_cast<volatile unsigned*>(hy_flag_pin)[l] = (seq << 1) | (any ? 1u : 0u);
       P.admit_layer();
       const PlacementStats& s1 = P.stats();
       if (pos >= 0 && pos < max_len) {
@@ -433,13 +484,17 @@ struct moert_model {
         t[2] = (int)(s1.dropped - s0.dropped);
         t[3] = (int)(s1.cpu - s0.cpu);
       }
-      // (the next layer's sum is written into the same pinned buffer only after its routing event, which follows
-      // this layer's add kernel in stream order)
-      int rc = hy_copies();
-      if (rc) return rc;
+      // the admissions' copies land behind layer l + 1's queued reads (a slot a later layer of this token reads is
+      // held by the placement until that layer has passed)
+      rc = hy_copies();
+      if (!rc && l + 2 < L) rc = enqueue_layer(l + 2);
+      if (rc) {
+        release();
+        return rc;
+      }
     }
     P.end_token();
-    int rc = hy_copies();
+    rc = hy_copies();
     if (rc) return rc;
     CHECK_HIP(launch_head(stream, embed, norm, dims, b));
     CHECK_HIP(launch_head_argmax(stream, embed, dims, b));
@@ -677,8 +732,10 @@ struct moert_model {
     for (hipEvent_t e : {ev_fork, ev_pred, ev_copy, mx_ev, mx_t[0], mx_t[1], mx_t[2]})
       if (e) (void)hipEventDestroy(e);
     if (mx_pin) (void)hipHostFree(mx_pin);
-    if (hy_ev) (void)hipEventDestroy(hy_ev);
-    for (void* p : {(void*)hy_table_pin, (void*)hy_ids_pin, (void*)hy_w_pin, (void*)hy_xn_pin, (void*)hy_y_pin})
+    for (hipEvent_t e : hy_evs)
+      if (e) (void)hipEventDestroy(e);
+    for (void* p : {(void*)hy_table_pin, (void*)hy_ids_pin, (void*)hy_w_pin, (void*)hy_xn_pin, (void*)hy_y_pin,
+                    (void*)hy_flag_pin})
       if (p) (void)hipHostFree(p);
     if (pf_stream) (void)hipStreamDestroy(pf_stream);
     if (stream) (void)hipStreamDestroy(stream);
@@ -1049,15 +1106,25 @@ int moert_model_create_hybrid(const moert_config* cfg, const moert_model_weights
   if ((rc = m->arena.alloc(&p, (size_t)H * 4))) return bail(rc);
   m->hy_xn_dev = (float*)p;
   if (hipHostMalloc((void**)&m->hy_table_pin, (size_t)L * E * 4, hipHostMallocDefault) != hipSuccess ||
-      hipHostMalloc((void**)&m->hy_ids_pin, 8 * 4, hipHostMallocDefault) != hipSuccess ||
-      hipHostMalloc((void**)&m->hy_w_pin, 8 * 4, hipHostMallocDefault) != hipSuccess ||
-      hipHostMalloc((void**)&m->hy_xn_pin, (size_t)H * 4, hipHostMallocDefault) != hipSuccess ||
-      hipHostMalloc((void**)&m->hy_y_pin, (size_t)H * 4, hipHostMallocMapped) != hipSuccess ||
+      hipHostMalloc((void**)&m->hy_ids_pin, 2 * 8 * 4, hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void**)&m->hy_w_pin, 2 * 8 * 4, hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void**)&m->hy_xn_pin, 2 * (size_t)H * 4, hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void**)&m->hy_y_pin, (size_t)H * 4, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
       hipHostGetDevicePointer((void**)&m->hy_y_dev, m->hy_y_pin, 0) != hipSuccess ||
-      hipEventCreateWithFlags(&m->hy_ev, hipEventDisableTiming) != hipSuccess) {
+      hipHostMalloc((void**)&m->hy_flag_pin, (size_t)L * 4, hipHostMallocMapped | hipHostMallocCoherent) !=
+          hipSuccess ||
+      hipHostGetDevicePointer((void**)&m->hy_flag_dev, m->hy_flag_pin, 0) != hipSuccess) {
     set_err("hybrid: pinned host buffers or event");
     return bail(MOERT_E_DEVICE);
   }
+  std::memset(m->hy_flag_pin, 0, (size_t)L * 4);
+  m->hy_evs.assign((size_t)L, nullptr);
+  for (hipEvent_t& e : m->hy_evs)
+    if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+      set_err("hybrid: events");
+      return bail(MOERT_E_DEVICE);
+    }
+  if ((rc = zeros(m->arena, m->stream, 1, &m->hy_err))) return bail(rc);
   m->cache.table = m->hy_table;
   m->cache.xn = m->hy_xn_dev;
   m->hy_act.assign((size_t)cfg->top_k * cfg->inter, 0.0f);
@@ -1137,6 +1204,14 @@ static int model_launch(moert_model* m) {
 // 32 = the merged heads (device-wide), 64 = h' (device-wide), 128 = the merged heads or h' in the XCD's L2, or the
 // router items.
 static int ab_check(moert_model* m) {
+  if (m->hybrid && m->hy_err) {
+    unsigned he = 0;
+    CHECK_HIP(hipMemcpy(&he, m->hy_err, 4, hipMemcpyDeviceToHost));
+    if (he) {
+      set_err("hybrid step: a layer's doorbell was not rung in time (error bits %#x)", he);
+      return MOERT_E_DEVICE;
+    }
+  }
   if (!m->use_ab) return MOERT_OK;
   unsigned e = 0;
   CHECK_HIP(hipMemcpy(&e, m->ab.err, 4, hipMemcpyDeviceToHost));

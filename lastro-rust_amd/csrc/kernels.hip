@@ -1566,6 +1566,41 @@ hipError_t launch_add_scaled(hipStream_t s, float* h, const float* y, float res,
   return hipGetLastError();
 }
 
+// The doorbell of a hybrid layer (the reference's stream wait on a host-written value, cuda_backend.rs:919-927):
+// thread 0 of each workgroup polls the layer's flag word in coherent host memory until it carries the token's
+// sequence number (flag = seq << 1 | any host expert), then h[i] += res * y[i] when the host computed any expert.
+// The poll is bounded (kHyDoorbellSpin polls of about a microsecond each, far beyond a layer's host work): a flag
+// that never comes sets bit 256 of *err and adds nothing, so the kernel always ends.
+constexpr int kHyDoorbellSpin = 1 << 23;
+__global__ __launch_bounds__(256) void k_hy_doorbell_add(float* __restrict__ h, const float* __restrict__ y,
+                                                         float res, int n, const unsigned* __restrict__ flag,
+                                                         unsigned seq, unsigned* __restrict__ err) {
+  __shared__ unsigned any_s;
+  if (threadIdx.x == 0) {
+    unsigned v = 0;
+    int it = 0;
+    for (; it < kHyDoorbellSpin; it++) {
+      v = __hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM);
+      if ((v >> 1) == seq) break;
+      __builtin_amdgcn_s_sleep(4);
+    }
+    if (it == kHyDoorbellSpin) {
+      if (blockIdx.x == 0) atomicOr(err, 256u);
+      v = 0u;
+    }
+    any_s = v & 1u;
+  }
+  __syncthreads();
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (any_s && i < n) h[i] = h[i] + res * __hip_atomic_load(y + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+hipError_t launch_hy_doorbell_add(hipStream_t s, float* h, const float* y, float res, int n, const unsigned* flag,
+                                  unsigned seq, unsigned* err) {
+  klaunch(k_hy_doorbell_add, cdiv(n, 256), 256, 0, s, h, y, res, n, flag, seq, err);
+  return hipGetLastError();
+}
+
 hipError_t launch_expert_down(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int layer,
                               bool accumulate, Tl tl) {
   const CacheDev none{};
