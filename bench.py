@@ -128,6 +128,17 @@ def batched_step(cfg, seed, iters, m=16, nblocks=4):
         uniq.append(blk.experts_in_step())
         blocks.append(blk)
     t = moert.time_batched(blocks, m, iters)
+    # the same step as one launch of 256 workgroups (moert_block_batched_kernel 1), where the device allows it
+    one = None
+    try:
+        for blk in blocks:
+            blk.batched_kernel(1)
+        t1 = moert.time_batched(blocks, m, iters)
+        one = {"block_step_us": round(t1["step"], 2), "launch_us": round(t1["launch"], 2)}
+    except moert.MoertError as exc:
+        one = {"skipped": str(exc)}
+    for blk in blocks:
+        blk.batched_kernel(0)
     per_pos_us = blocks[0].time(max(4, iters)) * m
     for blk in blocks:
         blk.close()
@@ -144,9 +155,12 @@ def batched_step(cfg, seed, iters, m=16, nblocks=4):
            "down_gbs": round(dn_bytes / (t["down"] * 1e-6) / 1e9, 1),
            "useful_tops": round(flops / ((t["up"] + t["down"]) * 1e-6) / 1e12, 3),
            "per_position_path_us": round(per_pos_us, 2),
-           "speedup_vs_per_position": round(per_pos_us / t["step"], 2)}
+           "speedup_vs_per_position": round(per_pos_us / t["step"], 2),
+           "one_launch": one}
+    if "block_step_us" in one:
+        one["achieved_gbs"] = round(nbytes / (one["block_step_us"] * 1e-6) / 1e9, 1)
     log(f"batched step m={m}: {t['step']:.1f} us per block ({u_mean:.1f} experts, {out['achieved_gbs']} GB/s), "
-        f"per-position path {per_pos_us:.1f} us")
+        f"one launch {one.get('block_step_us', '-')} us, per-position path {per_pos_us:.1f} us")
     return out
 
 

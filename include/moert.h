@@ -301,6 +301,14 @@ int moert_block_time(moert_block* b, int iters, double* us);
  * Replaces Cpu::experts_step (rust/moe-rt/src/cpu.rs:239-296) and the per-position GPU loops of the multi-position
  * step (rust/moe-rt/src/cuda_backend.rs:751-917). */
 int moert_block_forward_batched(moert_block* b, int m, const float* x, float* y, int* ids, float* weights);
+/* The kernels of the block's batched steps: mode 0 (default) the four kernels (route, gate/up, down, combine);
+ * mode 1 one launch of 256 workgroups that must all be resident at once, one per compute unit, dealt round-robin
+ * over the 8 XCDs (router logits and input codes through each XCD's L2; gate/up items and down tiles spread over
+ * all workgroups, act vectors and expert outputs device-wide), bit-identical to mode 0, for m <= 16 positions,
+ * ffn 512, at most 48 experts, Q8_0, on a device with 256 compute units (MOERT_E_CONFIG otherwise). The device
+ * must run nothing else meanwhile: a wait of that launch that gives up makes the step return MOERT_E_DEVICE. In
+ * mode 1, moert_block_time_batched reports the launch in us[1] and 0 in us[2..4]. No reference counterpart. */
+int moert_block_batched_kernel(moert_block* b, int mode);
 /* Number of distinct experts routed by the last batched step on this block (the grouped GEMM's expert count). */
 int moert_block_experts_in_step(moert_block* b, int* n_experts);
 /* Times `iters` rounds of the batched step over `nblocks` blocks in turn (rotating weights beyond the caches),

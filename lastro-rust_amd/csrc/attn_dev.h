@@ -148,4 +148,35 @@ __device__ __forceinline__ void put_entry(uint2* p, unsigned val, unsigned epoch
                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+// Device-wide entries: agent-scope atomic stores and loads, coherent across the XCDs' L2s.
+__device__ __forceinline__ void put_dev(uint2* p, unsigned val, unsigned epoch) {
+  __hip_atomic_store(reinterpret_cast<unsigned long long*>(p), ((unsigned long long)epoch << 32) | val,
+                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint2 get_dev(const uint2* p) {
+  const unsigned long long v = __hip_atomic_load(reinterpret_cast<unsigned long long*>(const_cast<uint2*>(p)),
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_uint2((unsigned)v, (unsigned)(v >> 32));
+}
+
+// Wave-level poll of up to M entries per lane (entry m of this lane at index idx[m], used when use[m]) until every
+// used entry of the wave carries `epoch`; LD(i) loads entry i. Returns false when the poll gave up.
+template <int M, class LD>
+__device__ __forceinline__ bool poll_m(const LD& ld, const int (&idx)[M], const bool (&use)[M], unsigned epoch,
+                                       int spin, unsigned (&val)[M]) {
+  for (int it = 0; it < spin; it++) {
+    poll_fence();
+    bool stale = false;
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const uint2 e = ld(use[m] ? idx[m] : idx[0]);
+      val[m] = e.x;
+      stale |= use[m] && e.y != epoch;
+    }
+    if (__ballot(stale) == 0) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return false;
+}
+
 }  // namespace moert

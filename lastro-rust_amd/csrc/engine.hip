@@ -966,6 +966,56 @@ struct moert_block {
   GroupBufs g{};
   float* gx = nullptr;
   float* gy = nullptr;
+  // the batched step as one launch (moert_block_batched_kernel 1): its exchange buffers (on first use), the launch
+  // epoch (never 0) and the device's compute units
+  int fused = 0;
+  FbBufs fb{};
+  unsigned fb_epoch = 0;
+  int cus = 0;
+  int ensure_fused() {
+    if (fb.err) return MOERT_OK;
+    const size_t H = dims.hidden, P = kFbPos;
+    unsigned *err = nullptr, *lg = nullptr, *xf = nullptr, *act = nullptr, *o = nullptr;
+    int rc;
+    if ((rc = zeros(arena, stream, 1, &err)) || (rc = zeros(arena, stream, 8 * P * 64 * 2, &lg)) ||
+        (rc = zeros(arena, stream, 8 * P * 2, &xf)) || (rc = zeros(arena, stream, 8 * P * H, &fb.xh)) ||
+        (rc = zeros(arena, stream, 8 * P * H, &fb.xl)) || (rc = zeros(arena, stream, 8 * P * (H / 32), &fb.xd)) ||
+        (rc = zeros(arena, stream, (size_t)kFbExperts * (kFbInter / 32) * kFbActW * P * 2, &act)) ||
+        (rc = zeros(arena, stream, P * 8 * H * 2, &o)))
+      return rc;
+    fb.err = err;
+    fb.lg = reinterpret_cast<uint2*>(lg);
+    fb.xflag = reinterpret_cast<uint2*>(xf);
+    fb.act = reinterpret_cast<uint2*>(act);
+    fb.o = reinterpret_cast<uint2*>(o);
+    CHECK_HIP(hipStreamSynchronize(stream));
+    return MOERT_OK;
+  }
+  // one batched step of m positions from gx into gy on stream s; with `ev`, its dispatches record into the event
+  // pairs (the one launch into the first)
+  int launch_batched(hipStream_t s, int m, const hipEvent_t* ev) {
+    if (!fused) {
+      CHECK_HIP(launch_grouped_block(s, L, m, dims.top_k, dims.inter, gx, g, gy, ev));
+      return MOERT_OK;
+    }
+    if (++fb_epoch == 0) fb_epoch = 1;
+    if (ev) arm_launch_events(ev[0], ev[1]);
+    CHECK_HIP(launch_grp_fused(s, L, m, dims.top_k, dims.inter, gx, g, fb, fb_epoch, gy, cus));
+    return MOERT_OK;
+  }
+  // the one-launch step's error word: a wait that gave up
+  int fused_check() {
+    if (!fused) return MOERT_OK;
+    unsigned e = 0;
+    CHECK_HIP(hipMemcpy(&e, fb.err, 4, hipMemcpyDeviceToHost));
+    if (e) {
+      set_err("batched step (one launch) gave up waiting for %s%s%s%s(error bits %#x): its workgroups were not "
+              "all resident at once or not dealt round-robin over the XCDs", (e & 1u) ? "router logits " : "",
+              (e & 2u) ? "act vectors " : "", (e & 4u) ? "expert outputs " : "", (e & 8u) ? "input codes " : "", e);
+      return MOERT_E_DEVICE;
+    }
+    return MOERT_OK;
+  }
   int ensure_grouped() {
     if (gx) return MOERT_OK;
     const int H = dims.hidden, I = dims.inter, M = kGrpMaxPos, S = kGrpMaxPos * 8;
@@ -2075,12 +2125,35 @@ int moert_block_forward_batched(moert_block* b, int m, const float* x, float* y,
   CHECK_CFG(b && x, "null argument");
   TRY(check_grouped(b, m));
   const Dims& d = b->dims;
+  CHECK_CFG(!b->fused || m <= kFbPos, "batched step: the one-launch kernel takes at most %d positions", kFbPos);
   CHECK_HIP(hipMemcpyAsync(b->gx, x, (size_t)m * d.hidden * 4, hipMemcpyHostToDevice, b->stream));
-  CHECK_HIP(launch_grouped_block(b->stream, b->L, m, d.top_k, d.inter, b->gx, b->g, b->gy));
+  TRY(b->launch_batched(b->stream, m, nullptr));
   if (y) CHECK_HIP(hipMemcpyAsync(y, b->gy, (size_t)m * d.hidden * 4, hipMemcpyDeviceToHost, b->stream));
   if (ids) CHECK_HIP(hipMemcpyAsync(ids, b->g.ids, (size_t)m * d.top_k * 4, hipMemcpyDeviceToHost, b->stream));
   if (weights) CHECK_HIP(hipMemcpyAsync(weights, b->g.w, (size_t)m * d.top_k * 4, hipMemcpyDeviceToHost, b->stream));
   CHECK_HIP(hipStreamSynchronize(b->stream));
+  return b->fused_check();
+}
+
+int moert_block_batched_kernel(moert_block* b, int mode) {
+  CHECK_CFG(b && (mode == 0 || mode == 1), "batched kernel mode %d (0: four kernels, 1: one launch)", mode);
+  if (mode == 1) {
+    CHECK_CFG(b->L.router.dtype == MOERT_Q8_0 && b->L.gate_up.dtype == MOERT_Q8_0 && b->L.down.dtype == MOERT_Q8_0,
+              "one-launch batched step: Q8_0 router and experts");
+    CHECK_CFG(b->dims.inter == kFbInter && b->dims.experts <= kFbExperts && b->dims.top_k <= 8,
+              "one-launch batched step: ffn %d (needs %d), %d experts (at most %d)", b->dims.inter, kFbInter,
+              b->dims.experts, kFbExperts);
+    if (!b->cus) {
+      int dev = 0, n = 0;
+      CHECK_HIP(hipGetDevice(&dev));
+      CHECK_HIP(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev));
+      b->cus = n;
+    }
+    CHECK_CFG(b->cus == 256, "one-launch batched step: needs 256 compute units (this device has %d)", b->cus);
+    TRY(check_grouped(b, 1));
+    TRY(b->ensure_fused());
+  }
+  b->fused = mode;
   return MOERT_OK;
 }
 
@@ -2108,7 +2181,8 @@ int moert_block_time_batched(moert_block* const* blocks, int nblocks, int m, int
       for (int i = 0; i < nblocks; i++) {
         moert_block* b = blocks[i];
         const hipEvent_t* e = per_kernel ? &ev[8 * (it * nblocks + i)] : nullptr;
-        CHECK_HIP(launch_grouped_block(s, b->L, m, b->dims.top_k, b->dims.inter, b->gx, b->g, b->gy, e));
+        CHECK_CFG(!b->fused || m <= kFbPos, "time_batched: the one-launch kernel takes at most %d positions", kFbPos);
+        TRY(b->launch_batched(s, m, e));
       }
     return MOERT_OK;
   };
@@ -2124,7 +2198,8 @@ int moert_block_time_batched(moert_block* const* blocks, int nblocks, int m, int
       double tot = 0.0;
       for (int i = 0; i < n; i++) {
         float x = 0.0f;
-        (void)hipEventElapsedTime(&x, ev[8 * i + 2 * k], ev[8 * i + 2 * k + 1]);
+        // a one-launch step records only its first pair
+        if (k == 0 || !blocks[i % nblocks]->fused) (void)hipEventElapsedTime(&x, ev[8 * i + 2 * k], ev[8 * i + 2 * k + 1]);
         tot += x;
       }
       us[1 + k] = tot * 1000.0 / n;
@@ -2132,6 +2207,7 @@ int moert_block_time_batched(moert_block* const* blocks, int nblocks, int m, int
   }
   for (auto& e : ev) (void)hipEventDestroy(e);
   if (rc == MOERT_E_DEVICE && g_err.empty()) set_err("time_batched: device error");
+  for (int i = 0; i < nblocks && !rc; i++) rc = blocks[i]->fused_check();
   return rc;
 }
 

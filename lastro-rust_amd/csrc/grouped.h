@@ -41,6 +41,33 @@ struct GroupBufs {
   TMat qkv, oproj;  // the layer's q/k/v [(heads + 2 kv_heads) * 64, H] and output [H, heads * 64] projections, tiled
 };
 
+// Exchange buffers of the one-launch block (launch_grp_fused), zeroed at allocation. Entries are (value bits,
+// epoch) 8-byte words; the input codes are plain bytes published by a per-position epoch flag.
+constexpr int kFbPos = 16;         // positions per one-launch block step
+constexpr int kFbExperts = 48;     // routed experts at most
+constexpr int kFbInter = 512;      // ffn width of the one-launch block
+constexpr int kFbActW = 17;        // act entries per (expert, 32-row block, position): 8 hi words, 8 lo words, scale
+struct FbBufs {
+  unsigned* err;  // [1] bits of the waits that gave up: 1 router logits, 2 act vectors, 4 expert outputs, 8 codes
+  uint2* lg;      // [8][kFbPos * 64] router logits (position, expert) of each XCD
+  uint2* xflag;   // [8][kFbPos] one flag per (XCD, position) over the XCD's copy of the input codes
+  int8_t* xh;     // [8][kFbPos][hidden] hi codes of the inputs, one copy per XCD
+  int8_t* xl;     // [8][kFbPos][hidden] lo codes
+  float* xd;      // [8][kFbPos][hidden / 32] their block scales
+  uint2* act;     // [kFbExperts][kFbInter / 32][kFbActW][kFbPos] act codes by list index, device-wide
+  uint2* o;       // [kFbPos * 8][hidden] expert outputs by member slot, device-wide
+};
+
+// y[m, H] = the MoE block of launch_grouped_block as one launch of 256 workgroups of 512 threads, all resident (one
+// per compute unit, 8 XCDs): each XCD codes the m inputs once and shares the codes and the router logits through
+// its L2, and every workgroup ranks the experts; the gate/up items and down tiles of all routed experts are dealt
+// over the 256 workgroups, with the m positions as MFMA columns and the act vectors device-wide; the expert outputs
+// go out device-wide and workgroup b combines rows [b H / 256, +H / 256). Same arithmetic and order as the four
+// kernels, bit for bit. m <= 16, k <= 8, E <= 48, ffn 512, Q8_0, 256 compute units; `epoch` >= 1 differs from the
+// previous launch's on these buffers.
+hipError_t launch_grp_fused(hipStream_t s, const LayerDev& L, int m, int k, int inter, const float* x,
+                            const GroupBufs& g, const FbBufs& f, unsigned epoch, float* y, int cus);
+
 // Tiled copy (TMat layout) of the Q8_0 matrix src into q [rows*cols] and d [rows*cols/32].
 hipError_t launch_tile_q8(hipStream_t s, const DMat& src, uint8_t* q, uint16_t* d);
 

@@ -18,6 +18,7 @@
 //   k_grp_combine grid (m, H/256):   y[p] = sum over p's experts in list order of w * o
 #include <climits>
 
+#include "attn_dev.h"
 #include "dev_rows.h"
 #include "grouped.h"
 #include "launch.h"
@@ -463,6 +464,407 @@ hipError_t launch_grp_experts(hipStream_t s, int H, int E, int m, int k, int int
     DOWN_CASE(256)
     DOWN_CASE(512)
 #undef DOWN_CASE
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------------------
+// The block as one launch (launch_grp_fused). Workgroup b runs on XCD x = XCC_ID with index w = b / 8 in it (the
+// chip deals the workgroups of a launch round-robin over its 8 XCDs; all 256 are resident at once):
+//   R. workgroup w < m of each XCD codes input w into the XCD's copy (k_grp_route's codes) and raises its flag;
+//      wave slot s = 8 w + wave of the XCD computes the router dots of position s % 16 with experts s / 16 + 16 i
+//      (one batch of rows), shared through the XCD's L2; every workgroup ranks the experts of each position
+//      (wave_topk), builds the grouping (make_plan) and reads the XCD's codes into LDS;
+//   U. gate/up item q = 2 b + slot (+512 per round) covers act rows [32 blk, +32) of list expert u = q / 16: 32
+//      gate and 32 up rows on four waves, every position an MFMA column; silu(g) * u and its hi/lo codes go out
+//      device-wide for the expert's members;
+//   D. down tile q = 8 b + wave (+2048 per round) covers output rows [16 t, +16) of list expert u = q / (H / 16);
+//      the waves of a workgroup span at most two experts per round, whose members' act codes it gathers into LDS;
+//      the members' outputs go out device-wide by member slot;
+//   C. workgroup b combines rows [b H / 256, +H / 256) of every position from its k slots in list order.
+// Every wait is bounded; one that gives up sets a bit of f.err and the workgroup waits for nothing more.
+constexpr int kFbThreads = 512;
+constexpr int kFbSpin = 1 << 18;
+
+// The hi/lo codes of one 32-element block (block_codes' arithmetic; 8 lanes, 4 elements each, all lanes taking
+// part in the maximum).
+__device__ __forceinline__ void code_block(const float (&v)[4], uint32_t& hw, uint32_t& lw, float& d) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const float a = fabsf(v[i]);
+    amax = a > amax ? a : amax;
+  }
+  amax = group_max<8>(amax);
+  d = amax / 32639.0f;
+  hw = 0;
+  lw = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int q = d > 0.0f ? (int)__builtin_rintf(v[i] / d) : 0;
+    const int h = (q + 128) >> 8;
+    hw |= (uint32_t)(uint8_t)(int8_t)h << (8 * i);
+    lw |= (uint32_t)(uint8_t)(int8_t)(q - 256 * h) << (8 * i);
+  }
+}
+
+// Wave-level poll of one record of W entries per lane (entry i at src + S i, device-wide) until every used record
+// of the wave carries `epoch`; val gets the values. Returns false when the poll gave up (at once for spin 0).
+template <int W, int S>
+__device__ __forceinline__ bool poll_rec(const uint2* src, bool use, unsigned epoch, int spin, unsigned (&val)[W]) {
+  for (int it = 0; it < spin; it++) {
+    poll_fence();
+    bool stale = false;
+#pragma unroll
+    for (int i = 0; i < W; i++) {
+      const uint2 e = get_dev(src + S * i);
+      val[i] = e.x;
+      stale |= use && e.y != epoch;
+    }
+    if (__ballot(stale) == 0) return true;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return false;
+}
+
+template <int H>
+__global__ __launch_bounds__(kFbThreads) void k_grp_fused(DMat router, const float* __restrict__ bias,
+                                                          const float* __restrict__ x, int m, int k, unsigned epoch,
+                                                          GroupBufs g, FbBufs f, float* __restrict__ y) {
+  using GR = Geo<DT_Q8_0, H>;
+  static_assert(GR::RPW == 1, "one router row per wave");
+  constexpr int NT = kFbThreads, NW = NT / 64, P = kFbPos, I = kFbInter, AW = kFbActW;
+  constexpr int NB = H / 32, NBI = I / 32, STR = H + 16, SA = I + 16;
+  constexpr int NTILE = H / 16;                // down tiles (16 rows) of an expert
+  constexpr int R = H / 256;                   // combined rows per workgroup
+  constexpr int LGN = P * 64;                  // logit entries per XCD
+  constexpr int RE = (kFbExperts + 15) / 16;   // router rows per wave
+  constexpr int XB = 2 * P * STR, AB = 2 * 2 * P * SA;
+  static_assert(NB * 8 <= NT && (NB * 8) % 64 == 0, "one pass of whole waves codes an input");
+  static_assert(2 * NBI * P == NT, "one thread per act record of two experts");
+  __shared__ __align__(16) int8_t big[XB > AB ? XB : AB];  // the input codes (R, U), then two experts' act codes
+  __shared__ float xd_s[P * NB];
+  __shared__ float ad_s[2 * P * NBI];
+  __shared__ __align__(16) float lgs[P][64];
+  __shared__ int ids_s[P * 8];
+  __shared__ float w_s[P * 8];
+  __shared__ __align__(16) TopkLds tk[NW];
+  __shared__ Plan plan;
+  __shared__ __align__(16) uint16_t sdt[NW][NB * 16];
+  __shared__ float gout[2][2][32][P + 1];
+  __shared__ int dead_s;
+
+  const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int xc = (int)xcc_id() & 7, w = blockIdx.x >> 3, bid = blockIdx.x;
+  const int E = router.rows, grp = lane >> 4;
+  const unsigned err0 = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_raw_buffer_load_b32(
+      l2_buffer(f.err, 4), 0, 0, kL2Policy));
+  if (threadIdx.x == 0) dead_s = err0 ? 1 : 0;
+  auto fail = [&](bool ok, unsigned bit) {
+    if (!ok && lane == 0) {
+      if (!dead_s && !err0) atomicOr(f.err, bit);
+      dead_s = 1;
+    }
+  };
+  int8_t* xh = big;
+  int8_t* xl = big + P * STR;
+
+  // ---- R. router dots: wave slot s of the XCD, position s % 16, experts s / 16 + 16 i, one batch of rows; their
+  // loads go out first, and workgroup w < m codes input w into the XCD's copy while they are in flight ----
+  const int rs = 8 * w + wid, rp = rs % 16, re0 = rs / 16;
+  const bool rwave = rp < m;
+  size_t rrow[RE];
+  bool rok[RE];
+#pragma unroll
+  for (int i = 0; i < RE; i++) {
+    rok[i] = re0 + 16 * i < E;
+    rrow[i] = rok[i] ? (size_t)(re0 + 16 * i) : 0;
+  }
+  Rows<DT_Q8_0, H, RE> rr;
+  XReg<DT_Q8_0, H> xr;
+  if (rwave) {
+    rows_load<DT_Q8_0, H, RE>(rr, router, rrow, rok, lane);
+    load_x<DT_Q8_0, H>(xr, x + (size_t)rp * H, lane);
+  }
+  const bool coder = w < m && (int)threadIdx.x < NB * 8;
+  if (coder) {
+    const int b = threadIdx.x / 8, part = threadIdx.x % 8;
+    float v[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = x[(size_t)w * H + 32 * b + 4 * part + e];
+    uint32_t hw, lw;
+    float d;
+    code_block(v, hw, lw, d);
+    const size_t row = (size_t)xc * P + w;
+    reinterpret_cast<uint32_t*>(f.xh + row * H)[8 * b + part] = hw;
+    reinterpret_cast<uint32_t*>(f.xl + row * H)[8 * b + part] = lw;
+    if (part == 0) f.xd[row * NB + b] = d;
+  }
+  if (rwave) {
+    float out[RE];
+    rows_fma<DT_Q8_0, H, RE>(rr, rok, xr, lane, out);
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < RE; i++)
+        if (rok[i]) {
+          const int e = re0 + 16 * i;
+          const float lv = bias ? out[i] + bias[e] : out[i];
+          put_entry(&f.lg[xc * LGN + rp * E + e], __float_as_uint(lv), epoch);
+        }
+    }
+  }
+  if (coder) wait_mem();
+  __syncthreads();
+  if (w < m && threadIdx.x == 0) put_entry(&f.xflag[xc * P + w], 0u, epoch);
+  {
+    constexpr int M = (P * 64 + NT - 1) / NT;
+    const int NI = m * E;
+    int idx[M];
+    bool use[M];
+#pragma unroll
+    for (int q = 0; q < M; q++) {
+      idx[q] = (int)threadIdx.x + q * NT;
+      use[q] = idx[q] < NI;
+      idx[q] = use[q] ? idx[q] : 0;
+    }
+    unsigned v[M];
+    const __amdgpu_buffer_rsrc_t rl = l2_buffer(f.lg + xc * LGN, LGN * 8);
+    const bool ok = poll_m<M>([&](int i) { return l2_load_u64(rl, 8u * (unsigned)i); }, idx, use, epoch,
+                              dead_s ? 0 : kFbSpin, v);
+#pragma unroll
+    for (int q = 0; q < M; q++)
+      if (use[q]) lgs[idx[q] / E][idx[q] % E] = __uint_as_float(v[q]);
+    fail(ok, 1u);
+  }
+  // the XCD's input codes: each wave waits for the m flags itself, then loads its share into registers, which
+  // reach LDS after the plan (rows past m are never a member)
+  constexpr int XC = (P * (H / 16) + NT - 1) / NT, XD = (P * NB + NT - 1) / NT;
+  uint4 xhv[XC], xlv[XC];
+  float xdv[XD];
+  {
+    int idx[1] = {lane < m ? lane : 0};
+    bool use[1] = {lane < m};
+    unsigned v[1];
+    const __amdgpu_buffer_rsrc_t rf = l2_buffer(f.xflag + xc * P, P * 8);
+    const bool ok = poll_m<1>([&](int i) { return l2_load_u64(rf, 8u * (unsigned)i); }, idx, use, epoch,
+                              dead_s ? 0 : kFbSpin, v);
+    fail(ok, 8u);
+    const __amdgpu_buffer_rsrc_t rh = l2_buffer(f.xh + (size_t)xc * P * H, P * H);
+    const __amdgpu_buffer_rsrc_t rlo = l2_buffer(f.xl + (size_t)xc * P * H, P * H);
+    const __amdgpu_buffer_rsrc_t rd = l2_buffer(f.xd + (size_t)xc * P * NB, P * NB * 4);
+#pragma unroll
+    for (int j = 0; j < XC; j++) {
+      const int i = (int)threadIdx.x + j * NT;
+      if (i < m * (H / 16)) {
+        const auto hv = __builtin_amdgcn_raw_buffer_load_b128(rh, 16 * i, 0, kL2Policy);
+        const auto lv = __builtin_amdgcn_raw_buffer_load_b128(rlo, 16 * i, 0, kL2Policy);
+        xhv[j] = make_uint4(hv[0], hv[1], hv[2], hv[3]);
+        xlv[j] = make_uint4(lv[0], lv[1], lv[2], lv[3]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < XD; j++) {
+      const int i = (int)threadIdx.x + j * NT;
+      if (i < m * NB) xdv[j] = l2_load_f32(rd, 4u * (unsigned)i);
+    }
+  }
+  __syncthreads();
+  for (int p = wid; p < m; p += NW) wave_topk(lgs[p], E, k, lane, tk[wid], ids_s + p * k, w_s + p * k);
+  __syncthreads();
+  if (bid == 0)
+    for (int i = threadIdx.x; i < m * k; i += NT) {
+      g.ids[i] = ids_s[i];
+      g.w[i] = w_s[i];
+    }
+  make_plan<NT>(ids_s, m, k, plan);
+  if (bid == 0) publish_plan<NT>(plan, w_s, m, k, g.grp);
+  const int nu = plan.nu;
+#pragma unroll
+  for (int j = 0; j < XC; j++) {
+    const int i = (int)threadIdx.x + j * NT;
+    if (i < m * (H / 16)) {
+      const int row = i / (H / 16), c = i % (H / 16);
+      *reinterpret_cast<uint4*>(xh + row * STR + 16 * c) = xhv[j];
+      *reinterpret_cast<uint4*>(xl + row * STR + 16 * c) = xlv[j];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < XD; j++) {
+    const int i = (int)threadIdx.x + j * NT;
+    if (i < m * NB) xd_s[i] = xdv[j];
+  }
+  __syncthreads();
+
+  // ---- U. gate/up items: two per workgroup and round, four waves each ----
+  const int sl = wid >> 2, role = wid & 3;  // item slot; rows [16 (role & 1), +16) of gate (role < 2) or up
+  for (int r = 0; r < (nu * 16 + 511) / 512; r++) {
+    const int q = 2 * bid + sl + 512 * r;
+    const bool has = q < nu * 16;
+    const int u = has ? q / 16 : 0, blk = q % 16;
+    const int e = plan.list[u];
+    const size_t t16 = ((size_t)e * 2 * I + (size_t)(role >> 1) * I + 32 * blk + 16 * (role & 1)) / 16;
+    TileScales<NB> sc;
+    uint4 a[NB / 2];
+    if (has) {
+      fetch_scales<NB>(g.gu, t16, NB, 0, sc);
+      fetch_tile_q8<NB>(g.gu, t16, NB, 0, a);
+    }
+    if (has) {
+      store_scales<NB>(sc, sdt[wid]);
+      float acc[1][4];
+      mfma_tile<NB, P>(a, xh, xl, STR, sdt[wid], xd_s, NB, acc);
+#pragma unroll
+      for (int i = 0; i < 4; i++) gout[sl][role >> 1][16 * (role & 1) + 4 * grp + i][lane & 15] = acc[0][i];
+    }
+    __syncthreads();
+    // act = silu(gate) * up of the two items' members: 8 lanes per (item, position), 4 rows a lane
+    if (threadIdx.x < 2 * P * 8) {
+      const int ss = threadIdx.x / (P * 8), p = (threadIdx.x / 8) % P, part = threadIdx.x & 7;
+      const int qq = 2 * bid + ss + 512 * r;
+      const bool hq = qq < nu * 16;
+      const int uu = hq ? qq / 16 : 0, bb = qq % 16;
+      const bool mem = hq && p < m && ((plan.bits[plan.list[uu]] >> p) & 1u);
+      float av[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        av[i] = mem ? silu_mul(gout[ss][0][4 * part + i][p], gout[ss][1][4 * part + i][p]) : 0.0f;
+      uint32_t hw, lw;
+      float d;
+      code_block(av, hw, lw, d);
+      if (mem) {
+        uint2* ae = f.act + (size_t)(uu * NBI + bb) * AW * P + p;
+        put_dev(ae + part * P, hw, epoch);
+        put_dev(ae + (8 + part) * P, lw, epoch);
+        if (part == 0) put_dev(ae + 16 * P, __float_as_uint(d), epoch);
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- D. down tiles [T b, +T) of the list's nu * (H / 16) (at most two experts, as T <= H / 16); wave w takes
+  // tiles w, w + 8, ..., whose weights it fetches before it gathers the experts' act codes into LDS ----
+  {
+    constexpr int TMAX = (kFbExperts * NTILE + 255) / 256, JD = (TMAX + NW - 1) / NW;  // tiles per wave at most
+    const int total = nu * NTILE, T = (total + 255) / 256;
+    const int t0 = min(bid * T, total), t1 = min(t0 + T, total);
+    const int u0 = min(t0, total - 1) / NTILE, u1 = t1 > t0 ? (t1 - 1) / NTILE : u0;
+    constexpr int JP = JD < 2 ? JD : 2;  // tiles fetched ahead of the gather (a third only past 42 experts)
+    TileScales<NBI> sc[JD];
+    uint4 a[JD][NBI / 2];
+    auto fetch = [&](int j) {
+      const int dq = t0 + wid + NW * j;
+      if (dq < t1) {
+        const int e = plan.list[dq / NTILE];
+        const size_t t16 = ((size_t)e * H + 16 * (dq % NTILE)) / 16;
+        fetch_scales<NBI>(g.dn, t16, NBI, 0, sc[j]);
+        fetch_tile_q8<NBI>(g.dn, t16, NBI, 0, a[j]);
+      }
+    };
+#pragma unroll
+    for (int j = 0; j < JP; j++) fetch(j);
+    int8_t* ahs = big;
+    int8_t* als = big + 2 * P * SA;
+    {
+      // thread (slot, block, position) gathers the 17 entries of one act record; lanes read consecutive positions
+      const int s2 = threadIdx.x / (NBI * P), bb = threadIdx.x / P % NBI, p = threadIdx.x % P;
+      const int uu = s2 == 0 ? u0 : u1;
+      const bool use = t0 < t1 && (s2 == 0 || u1 != u0) && p < m && ((plan.bits[plan.list[uu]] >> p) & 1u);
+      const uint2* src = f.act + (size_t)(uu * NBI + bb) * AW * P + p;
+      unsigned v[AW];
+      const bool ok = poll_rec<AW, P>(src, use, epoch, dead_s ? 0 : kFbSpin, v);
+      if (use) {
+        int8_t* row_h = ahs + (s2 * P + p) * SA + 32 * bb;
+        int8_t* row_l = als + (s2 * P + p) * SA + 32 * bb;
+        *reinterpret_cast<uint4*>(row_h) = make_uint4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<uint4*>(row_h + 16) = make_uint4(v[4], v[5], v[6], v[7]);
+        *reinterpret_cast<uint4*>(row_l) = make_uint4(v[8], v[9], v[10], v[11]);
+        *reinterpret_cast<uint4*>(row_l + 16) = make_uint4(v[12], v[13], v[14], v[15]);
+        ad_s[(s2 * P + p) * NBI + bb] = __uint_as_float(v[16]);
+      }
+      fail(ok, 2u);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < JD; j++) {
+      if (j >= JP) fetch(j);
+      const int dq = t0 + wid + NW * j;
+      if (dq < t1) {
+        const int u = dq / NTILE, t = dq % NTILE, s2 = u == u0 ? 0 : 1;
+        const int e = plan.list[u];
+        store_scales<NBI>(sc[j], sdt[wid]);
+        float acc[1][4];
+        mfma_tile<NBI, P>(a[j], ahs + s2 * P * SA, als + s2 * P * SA, SA, sdt[wid], ad_s + s2 * P * NBI, NBI, acc);
+        const int p = lane & 15;
+        const unsigned bits = plan.bits[e];
+        if (p < m && ((bits >> p) & 1u)) {
+          const int slot = plan.offe[e] + __popc(bits & ((1u << p) - 1u));
+#pragma unroll
+          for (int i = 0; i < 4; i++)
+            put_dev(&f.o[(size_t)slot * H + 16 * t + 4 * grp + i], __float_as_uint(acc[0][i]), epoch);
+        }
+      }
+    }
+  }
+
+  // ---- C. rows [R b, +R) of every position: its k member slots in list order ----
+  if ((int)threadIdx.x < m * R) {
+    const int p = threadIdx.x / R, row = R * bid + (int)threadIdx.x % R;
+    int sls[8];
+    float wt[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      sls[jj] = 0;
+      wt[jj] = 0.0f;
+    }
+    for (int j0 = 0; j0 < k; j0++) {
+      const int e = ids_s[p * k + j0];
+      int rank = 0;
+      for (int j1 = 0; j1 < k; j1++) rank += plan.uof[ids_s[p * k + j1]] < plan.uof[e];
+      const int slot = plan.offe[e] + __popc(plan.bits[e] & ((1u << p) - 1u));
+#pragma unroll
+      for (int jj = 0; jj < 8; jj++)
+        if (jj == rank) {
+          sls[jj] = slot;
+          wt[jj] = w_s[p * k + j0];
+        }
+    }
+    int idx[8];
+    bool use[8];
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++) {
+      idx[jj] = sls[jj] * H + row;
+      use[jj] = jj < k;
+    }
+    unsigned v[8];
+    const bool ok = poll_m<8>([&](int i) { return get_dev(f.o + i); }, idx, use, epoch, dead_s ? 0 : kFbSpin, v);
+    float acc = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < 8; jj++)
+      if (jj < k) {
+        const float tw = wt[jj] * __uint_as_float(v[jj]);
+        acc = acc + tw;
+      }
+    y[(size_t)p * H + row] = acc;
+    if (!ok) {
+      if (!dead_s && !err0) atomicOr(f.err, 4u);
+      dead_s = 1;
+    }
+  }
+}
+
+hipError_t launch_grp_fused(hipStream_t s, const LayerDev& L, int m, int k, int inter, const float* x,
+                            const GroupBufs& g, const FbBufs& f, unsigned epoch, float* y, int cus) {
+  const int H = L.gate_up.cols, E = L.router.rows;
+  if (m < 1 || m > kFbPos || k < 1 || k > 8 || E < 1 || E > kFbExperts || inter != kFbInter || cus != 256 ||
+      epoch == 0 || L.gate_up.dtype != DT_Q8_0 || L.down.dtype != DT_Q8_0 || L.router.dtype != DT_Q8_0 ||
+      L.router.cols != H || L.down.cols != inter || !g.gu.q || !g.dn.q || g.gu.rows != E * 2 * inter ||
+      g.gu.cols != H || g.dn.rows != E * H || g.dn.cols != inter || !f.err || !f.lg || !f.xflag || !f.xh || !f.xl ||
+      !f.xd || !f.act || !f.o)
+    return hipErrorInvalidValue;
+  switch (H) {
+    case 1024: klaunch(k_grp_fused<1024>, 256, kFbThreads, 0, s, L.router, L.router_bias, x, m, k, epoch, g, f, y); break;
+    case 1536: klaunch(k_grp_fused<1536>, 256, kFbThreads, 0, s, L.router, L.router_bias, x, m, k, epoch, g, f, y); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -90,3 +90,64 @@ def test_batched_block_refuses_bad_sizes(gpu):
     with pytest.raises(moert.MoertError):
         blk.forward_batched(np.zeros((33, hidden), np.float32))
     blk.close()
+
+
+@pytest.mark.parametrize("hidden,experts", [(1024, 32), (1536, 40)])
+def test_batched_one_launch_is_bit_identical_to_the_grouped_oracle(gpu, hidden, experts):
+    """moert_block_batched_kernel(1): the step as one launch over the XCDs, against the oracle and the four-kernel
+    step of the same block, bit for bit (routing, weights, outputs, distinct experts), with and without a Zipf
+    router bias, m = 1 .. 16."""
+    inter, k = 512, 8
+    router = moert.synth_quantized(121, hidden, experts * hidden, 0.02, moert.Q8_0)
+    gate_up = moert.synth_quantized(122, hidden, experts * 2 * inter * hidden, 0.02, moert.Q8_0)
+    down = moert.synth_quantized(123, hidden, experts * hidden * inter, 0.02, moert.Q8_0)
+    for zipf in (False, True):
+        bias = moert.zipf_bias(experts, 9) if zipf else None
+        blk = moert.GpuBlock(hidden, inter, experts, k, router, gate_up, down, moert.Q8_0, router_bias=bias)
+        for m in (1, 5, 16):
+            say(f"one-launch block hidden={hidden} E={experts} zipf={zipf} m={m}")
+            x = moert.synth_normal(124 + m, m, m * hidden).reshape(m, hidden)
+            blk.batched_kernel(0)
+            y0, i0, w0 = blk.forward_batched(x)
+            blk.batched_kernel(1)
+            y1, i1, w1 = blk.forward_batched(x)
+            n1 = blk.experts_in_step()
+            oy, oi, ow = oracle.moe_block_batched(hidden, inter, experts, k, router, gate_up, down, moert.Q8_0, x,
+                                                  bias=bias)
+            assert i1.tolist() == oi.tolist() and bits_equal(w1, ow), m
+            assert bits_equal(y1, oy), m
+            assert bits_equal(y1, y0) and i1.tolist() == i0.tolist(), m
+            assert n1 == len(np.unique(oi))
+            # a second launch on the same buffers (the next epoch) gives the same bits
+            y2, _, _ = blk.forward_batched(x)
+            assert bits_equal(y2, y1), m
+        blk.close()
+
+
+def test_batched_one_launch_identical_positions_and_refusals(gpu):
+    """One launch with every position on the same experts (m members each), zero inputs, and the shapes it refuses
+    (more than 16 positions, ffn other than 512) with MOERT_E_CONFIG."""
+    hidden, inter, experts, k = 1536, 512, 40, 8
+    router = moert.synth_quantized(131, 0, experts * hidden, 0.02, moert.Q8_0)
+    gate_up = moert.synth_quantized(132, 0, experts * 2 * inter * hidden, 0.02, moert.Q8_0)
+    down = moert.synth_quantized(133, 0, experts * hidden * inter, 0.02, moert.Q8_0)
+    blk = moert.GpuBlock(hidden, inter, experts, k, router, gate_up, down, moert.Q8_0)
+    blk.batched_kernel(1)
+    for m, zero in ((16, False), (5, True)):
+        say(f"one-launch identical positions m={m} zero={zero}")
+        row = np.zeros(hidden, np.float32) if zero else moert.synth_normal(134, 0, hidden)
+        x = np.tile(row, (m, 1))
+        y, ids, w = blk.forward_batched(x)
+        oy, oi, ow = oracle.moe_block_batched(hidden, inter, experts, k, router, gate_up, down, moert.Q8_0, x)
+        assert ids.tolist() == oi.tolist() and bits_equal(w, ow) and bits_equal(y, oy)
+    with pytest.raises(moert.MoertError) as e:
+        blk.forward_batched(np.zeros((17, hidden), np.float32))
+    assert e.value.code == moert.E_CONFIG
+    blk.close()
+    small = moert.GpuBlock(1024, 256, 8, 2, moert.synth_quantized(135, 0, 8 * 1024, 0.02, moert.Q8_0),
+                           moert.synth_quantized(136, 0, 8 * 2 * 256 * 1024, 0.02, moert.Q8_0),
+                           moert.synth_quantized(137, 0, 8 * 1024 * 256, 0.02, moert.Q8_0), moert.Q8_0)
+    with pytest.raises(moert.MoertError) as e:
+        small.batched_kernel(1)
+    assert e.value.code == moert.E_CONFIG
+    small.close()
