@@ -136,14 +136,16 @@ int moert_cache_fill(moert_model* m, int* copied);
  * with hipMemcpyAsync on a side stream that the model stream waits for. Experts distinct, 1 <= n <= min(slots,
  * experts). *copied = experts that were not in the pool. Returns synchronised; counters not changed. */
 int moert_cache_prefetch(moert_model* m, int layer, const int* experts, int n, int* copied);
-/* Prefetch inside the step (north_star item 6: transfer overlapping attention): with on = 1, each layer step of the
- * cached model also runs, on a side stream of the step graph, a prediction of the layer's experts (the layer's router
- * applied to rmsnorm of the layer's input, top-k) and one uncounted tick of the LRU rule over the predicted keys (as
- * moert_cache_prefetch), then copies the predicted misses from the pinned store into their slots while the layer's
- * attention runs; the router + gate/up kernel waits for the copies. Outputs are unchanged (a misprediction is read
- * from the host as before); the counters count the step's requests as before and the prefetched copies apart.
- * on = 0 restores the plain cached step. No reference counterpart beyond copy_in_background (rust/moe-rt/src/cache/
- * core.rs:380), whose copies start only after the miss. */
+/* Prefetch inside the step (transfers overlapping attention): with on = 1, each layer step of the cached model also
+ * predicts the layer's experts (the layer's router applied to rmsnorm of the layer's input, top-k), takes one
+ * uncounted tick of the LRU rule over the predicted keys (as moert_cache_prefetch), and copies the predicted misses
+ * from the pinned store into their slots before the router + gate/up kernel reads the pool. Where the attention
+ * block applies this runs inside its launch (extra workgroups after the attention workgroups; a wait of theirs that
+ * gives up is reported as MOERT_E_DEVICE); elsewhere, or with MOERT_PF_BLOCK=0 in the environment when the mode is
+ * switched on, on a side stream of the step graph beside the three-kernel attention. Outputs are unchanged (a
+ * misprediction is read from the host as before); the counters count the step's requests as before and the
+ * prefetched copies apart. on = 0 restores the plain cached step. No reference counterpart beyond
+ * copy_in_background (rust/moe-rt/src/cache/core.rs:380), whose copies start only after the miss. */
 int moert_cache_prefetch_mode(moert_model* m, int on);
 /* The experts predicted for positions [pos0, pos0 + n): [n][layers][8] ids in top-k order (-1 past top_k, and for
  * positions not decoded with prefetch since the last clear). */

@@ -22,6 +22,7 @@
 // or a group that is not all resident at once, would cause) sets a bit of `err` and the kernel still ends; the host
 // turns a set bit into an error.
 #include "attn_dev.h"
+#include "cache_pf.h"
 #include "dev_rows.h"
 #include "kernels.h"
 #include "launch.h"
@@ -54,16 +55,16 @@ __device__ __forceinline__ uint2 poll_entries(__amdgpu_buffer_rsrc_t r, unsigned
 // CMB: the input is h + res * (sum over j < 8, in order, of yw[j] * ys[j]) (the previous layer's experts left by
 // k_moe_xcd; k_expert_down's epilogue arithmetic), and workgroup 0 writes it to hc.
 template <int DT, int K, int G, int T, int NP, int SP, bool CMB>
-__global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* __restrict__ h,
-                                                          const float* __restrict__ lnw, float eps,
-                                                          const int* __restrict__ st, const float* __restrict__ rope_cur,
-                                                          int heads, int max_len, uint16_t* __restrict__ kc,
-                                                          uint16_t* __restrict__ vc, float scale, int splits, int pp,
-                                                          AbGroup* __restrict__ xg_all,
-                                                          const unsigned* __restrict__ step_ctr, unsigned layer,
-                                                          unsigned* __restrict__ err, float* __restrict__ att,
-                                                          const float* __restrict__ ys, const float* __restrict__ yw,
-                                                          float res, float* __restrict__ hc, Tl tl) {
+__device__ __forceinline__ void attn_block_body(DMat m, const float* __restrict__ h,
+                                                const float* __restrict__ lnw, float eps,
+                                                const int* __restrict__ st, const float* __restrict__ rope_cur,
+                                                int heads, int max_len, uint16_t* __restrict__ kc,
+                                                uint16_t* __restrict__ vc, float scale, int splits, int pp,
+                                                AbGroup* __restrict__ xg_all,
+                                                const unsigned* __restrict__ step_ctr, unsigned layer,
+                                                unsigned* __restrict__ err, float* __restrict__ att,
+                                                const float* __restrict__ ys, const float* __restrict__ yw,
+                                                float res, float* __restrict__ hc, Tl tl) {
   TL_START(tl);
   using Ge = Geo<DT, K>;
   static_assert(Ge::RPW == 1, "one q/k/v row per wave and pass");
@@ -383,6 +384,53 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* 
   TL_END(tl);
 }
 
+template <int DT, int K, int G, int T, int NP, int SP, bool CMB>
+__global__ __launch_bounds__(G * T * 64) void k_attn_block(DMat m, const float* __restrict__ h,
+                                                          const float* __restrict__ lnw, float eps,
+                                                          const int* __restrict__ st, const float* __restrict__ rope_cur,
+                                                          int heads, int max_len, uint16_t* __restrict__ kc,
+                                                          uint16_t* __restrict__ vc, float scale, int splits, int pp,
+                                                          AbGroup* __restrict__ xg_all,
+                                                          const unsigned* __restrict__ step_ctr, unsigned layer,
+                                                          unsigned* __restrict__ err, float* __restrict__ att,
+                                                          const float* __restrict__ ys, const float* __restrict__ yw,
+                                                          float res, float* __restrict__ hc, Tl tl) {
+  attn_block_body<DT, K, G, T, NP, SP, CMB>(m, h, lnw, eps, st, rope_cur, heads, max_len, kc, vc, scale, splits, pp,
+                                            xg_all, step_ctr, layer, err, att, ys, yw, res, hc, tl);
+}
+
+// The attention block of a cached step with its layer's prefetch (cache_pf.h): workgroups past the 8 * splits of
+// the attention block decide (the first) or copy (the others); the attention workgroups are those of k_attn_block.
+template <int DT, int K, int G, int T, int NP, int SP>
+__global__ __launch_bounds__(G * T * 64) void k_attn_block_pf(DMat m, const float* __restrict__ h,
+                                                          const float* __restrict__ lnw, float eps,
+                                                          const int* __restrict__ st, const float* __restrict__ rope_cur,
+                                                          int heads, int max_len, uint16_t* __restrict__ kc,
+                                                          uint16_t* __restrict__ vc, float scale, int splits, int pp,
+                                                          AbGroup* __restrict__ xg_all,
+                                                          const unsigned* __restrict__ step_ctr, unsigned layer,
+                                                          unsigned* __restrict__ err, float* __restrict__ att,
+                                                          const float* __restrict__ ys, const float* __restrict__ yw,
+                                                          float res, float* __restrict__ hc, Tl tl, PfArgs pf) {
+  constexpr int NT = G * T * 64;
+  const int extra = (int)blockIdx.x - 8 * splits;
+  if (extra < 0) {
+    attn_block_body<DT, K, G, T, NP, SP, false>(m, h, lnw, eps, st, rope_cur, heads, max_len, kc, vc, scale, splits,
+                                                pp, xg_all, step_ctr, layer, err, att, ys, yw, res, hc, tl);
+    return;
+  }
+  const unsigned sctr = __builtin_amdgcn_readfirstlane(
+      __builtin_amdgcn_raw_buffer_load_b32(l2_buffer(step_ctr, 4), 0, 0, 0));
+  const unsigned err0 =
+      __builtin_amdgcn_readfirstlane(__builtin_amdgcn_raw_buffer_load_b32(l2_buffer(err, 8), 0, 0, 0));
+  const unsigned epoch = sctr * 64u + layer + 1u;
+  if (extra == 0) {
+    pf_decide<DT, K, NT>(pf, h, epoch);
+  } else if (!pf_copy<NT>(pf.c, epoch, extra - 1, err0 != 0) && threadIdx.x == 0 && !err0) {
+    atomicOr(err, 16u);
+  }
+}
+
 // ------------------------------------------------------------------------------------------------------------
 namespace {
 
@@ -419,19 +467,29 @@ bool attn_block_fits(const Dims& d, const DMat& qkv, int cus) {
   return ab_shape(d, qkv, cus, &sh);
 }
 
+bool attn_block_prefetch_fits(const Dims& d, const LayerDev& L, const CacheDev& c) {
+  return c.pfx && c.slots >= d.top_k && c.slots <= kCacheMaxSlots && L.router.rows <= 64 && d.top_k <= 8 &&
+         L.router.dtype == L.qkv.dtype && L.router.cols == L.qkv.cols;
+}
+
 hipError_t launch_attn_block(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int cus, int layer,
-                             const AbBufs& x, bool combine, Tl tl) {
+                             const AbBufs& x, bool combine, Tl tl, const CacheDev* pfc) {
   AbShape sh;
   if (!ab_shape(d, L.qkv, cus, &sh) || (combine && (d.top_k != 8 || layer < 1))) return hipErrorInvalidValue;
+  if (pfc && (combine || !attn_block_prefetch_fits(d, L, *pfc))) return hipErrorInvalidValue;
   const int grid = 8 * sh.splits;
   const float* yw = b.route_w + (size_t)(layer > 0 ? layer - 1 : 0) * d.top_k;
-#define AB_LAUNCH(DD, KK, GG, TT, NN, CC)                                                                          \
-  klaunch(k_attn_block<DD, KK, GG, TT, NN, 32, CC>, grid, GG * TT * 64, 0, s, L.qkv, b.h, L.ln_attn, d.eps,        \
-          b.state, x.rope_cur, d.heads, d.max_len, L.k_cache, L.v_cache, d.attn_mult, sh.splits, sh.pp, x.groups,      \
-          x.step_ctr, (unsigned)layer, x.err, b.att, (const float*)x.ys, yw, d.res_mult, b.hc, tl)
+  const PfArgs pf = pfc ? PfArgs{L.router, L.router_bias, L.ln_moe, d.eps, d.top_k, layer, *pfc} : PfArgs{};
+#define AB_ARGS                                                                                                    \
+  L.qkv, b.h, L.ln_attn, d.eps, b.state, x.rope_cur, d.heads, d.max_len, L.k_cache, L.v_cache, d.attn_mult,         \
+      sh.splits, sh.pp, x.groups, x.step_ctr, (unsigned)layer, x.err, b.att, (const float*)x.ys, yw, d.res_mult, b.hc, tl
+#define AB_LAUNCH(DD, KK, GG, TT, NN, CC) \
+  klaunch(k_attn_block<DD, KK, GG, TT, NN, 32, CC>, grid, GG * TT * 64, 0, s, AB_ARGS)
 #define AB_CASE(DD, KK, GG, TT, NN)                                                                                \
   if (L.qkv.dtype == DD && L.qkv.cols == KK && sh.G == GG && sh.T == TT && sh.np == NN) {                         \
-    if (combine)                                                                                                   \
+    if (pfc)                                                                                                       \
+      klaunch(k_attn_block_pf<DD, KK, GG, TT, NN, 32>, grid + 1 + kPfCopyWgs, GG * TT * 64, 0, s, AB_ARGS, pf);   \
+    else if (combine)                                                                                              \
       AB_LAUNCH(DD, KK, GG, TT, NN, true);                                                                         \
     else                                                                                                           \
       AB_LAUNCH(DD, KK, GG, TT, NN, false);                                                                        \
@@ -443,6 +501,7 @@ hipError_t launch_attn_block(hipStream_t s, const LayerDev& L, const Dims& d, co
 #undef AB_T
 #undef AB_CASE
 #undef AB_LAUNCH
+#undef AB_ARGS
   return hipErrorInvalidValue;
 }
 

@@ -37,6 +37,7 @@ struct CacheDev {
                           // key when it missed (read from the host store by the down kernel), -1 when it hit
   // prefetch branch (moert_cache_prefetch_mode)
   int* pf;                // [1 + 2 * 8] experts to copy ahead of the current layer: count, then (slot, key) pairs
+  uint2* pfx;             // [1 + 2 * 8] the same list as epoch-tagged entries (prefetch inside the attention launch)
   int* pred_hist;         // [max_len][layers][8] predicted experts of each position and layer (-1: none)
   int* tok_hist;          // [max_len][layers][4] per position and layer: hits, copies, prefetched, 0
   const int* state;       // the step state (ST_POS: the position being decoded)

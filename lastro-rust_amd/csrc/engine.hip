@@ -227,6 +227,7 @@ struct moert_model {
   void* host_store = nullptr;
   // prefetch branch of the cached step (moert_cache_prefetch_mode): side stream and its fork / join events
   bool prefetch = false;
+  bool pf_blk = false;  // the prefetch inside the attention launch instead of the side branch (cache_pf.h)
   hipStream_t pf_stream = nullptr;
   hipEvent_t ev_fork = nullptr, ev_pred = nullptr, ev_copy = nullptr;
   // runtime metrics (moert_model_attach_metrics): the publisher, the pinned read-back of the device counters and
@@ -285,9 +286,11 @@ struct moert_model {
       tl_layer.push_back(layer);
       return t;
     };
-    // the prefetch branch's kernels run beside the attention half on a second stream, so the attention block
-    // (whose workgroups must all be resident at once, dispatched round-robin over the XCDs) is not used with it
-    const bool use_blk = use_ab && !(cached && prefetch);
+    // the prefetch runs inside the attention launch where the block fits (pf_blk); otherwise the side branch's
+    // kernels run beside the attention half on a second stream, and then the attention block (whose workgroups must
+    // all be resident at once, dispatched round-robin over the XCDs) is not used
+    const bool branch = cached && prefetch && !pf_blk;
+    const bool use_blk = use_ab && !branch;
     CHECK_HIP(
         launch_embed(stream, embed, dims, b, ab.step_ctr, use_blk ? ab.rope_cur : nullptr, arm(MOERT_K_EMBED, -1)));
     if (use_px) {
@@ -302,7 +305,7 @@ struct moert_model {
     for (size_t l = 0; l < layers.size(); l++) {
       const LayerDev& L = layers[l];
       const int li = (int)l;
-      const bool pf = cached && prefetch;
+      const bool pf = branch;
       if (pf) {
         // side branch: predict the layer's experts from its input and copy the predicted misses into the pool while
         // the attention half runs; the output projection (which rewrites h) waits for the prediction, the router +
@@ -316,7 +319,8 @@ struct moert_model {
       }
       const bool cmb = use_mx && li > 0;  // the previous layer's experts are combined by this attention block
       if (use_blk) {
-        CHECK_HIP(launch_attn_block(stream, L, dims, b, cus, li, ab, cmb, arm(MOERT_K_ATTN_BLOCK, li)));
+        CHECK_HIP(launch_attn_block(stream, L, dims, b, cus, li, ab, cmb, arm(MOERT_K_ATTN_BLOCK, li),
+                                    cached && prefetch ? &cache : nullptr));
       } else {
         CHECK_HIP(launch_qkv(stream, L, dims, b, arm(MOERT_K_QKV, li)));
         CHECK_HIP(launch_attn_split(stream, L, dims, b, arm(MOERT_K_ATTN_SPLIT, li)));
@@ -806,6 +810,9 @@ static int cache_create(moert_model* m, const moert_model_weights* w, int slots)
   cd.route = (int*)p;
   if ((rc = a.alloc(&p, 17 * 4))) return rc;
   cd.pf = (int*)p;
+  if ((rc = a.alloc(&p, 17 * 8))) return rc;
+  cd.pfx = (uint2*)p;
+  CHECK_HIP(hipMemsetAsync(cd.pfx, 0, 17 * 8, m->stream));  // epoch 0: written by no launch
   if ((rc = a.alloc(&p, (size_t)m->max_len * L * 8 * 4))) return rc;
   cd.pred_hist = (int*)p;
   if ((rc = a.alloc(&p, (size_t)m->max_len * L * 4 * 4))) return rc;
@@ -1233,6 +1240,7 @@ static int epoch_guard(moert_model* m) {
   CHECK_HIP(hipMemsetAsync(m->ab.groups, 0, 8 * sizeof(AbGroup), m->stream));
   CHECK_HIP(hipMemsetAsync(m->ab.moe, 0, 8 * sizeof(MxGroup), m->stream));
   CHECK_HIP(hipMemsetAsync(m->ab.step_ctr, 0, 4, m->stream));
+  if (m->cached) CHECK_HIP(hipMemsetAsync(m->cache.pfx, 0, 17 * 8, m->stream));
   if (m->use_px) {
     CHECK_HIP(hipMemsetAsync(m->px.xcd, 0, 8 * sizeof(PxXcd), m->stream));
     CHECK_HIP(hipMemsetAsync(m->px.dev, 0, sizeof(PxDev), m->stream));
@@ -1266,11 +1274,12 @@ static int ab_check(moert_model* m) {
   unsigned e = 0;
   CHECK_HIP(hipMemcpy(&e, m->ab.err, 4, hipMemcpyDeviceToHost));
   if (e) {
-    set_err("%s%s%s%s%s%sgave up (error bits %#x): the launch's workgroups were not dispatched round-robin over the "
+    set_err("%s%s%s%s%s%s%sgave up (error bits %#x): the launch's workgroups were not dispatched round-robin over the "
             "XCDs or not all resident at once",
             (e & 2u) ? "attention: the wait for queries / the new K/V row " : "",
             (e & 4u) ? "attention: the wait for split partials " : "",
             (e & 8u) ? "MoE: the wait for an expert's act vector " : "",
+            (e & 16u) ? "prefetch: the wait for the layer's predicted misses " : "",
             (e & 32u) ? "layer: the wait for the merged heads " : "",
             (e & 64u) ? "layer: the wait for the post-attention residual " : "",
             (e & 128u) ? "layer: the wait for values relayed inside an XCD or for router items " : "", e);
@@ -1858,7 +1867,7 @@ int moert_model_path(const moert_model* m, int* layer, int* attn_block, int* moe
     set_err("model_path: null argument");
     return MOERT_E_CONFIG;
   }
-  const bool blk = m->use_ab && !(m->cached && m->prefetch);
+  const bool blk = m->use_ab && !(m->cached && m->prefetch && !m->pf_blk);
   *layer = m->use_px ? 1 : 0;
   *attn_block = blk && !m->use_px ? 1 : 0;
   *moe_xcd = blk && m->use_mx && !m->use_px ? 1 : 0;
@@ -1944,6 +1953,13 @@ int moert_cache_prefetch_mode(moert_model* m, int on) {
   m->exec = nullptr;
   m->graph = nullptr;
   m->prefetch = on != 0;
+  // inside the attention launch when the block and every layer fit (MOERT_PF_BLOCK=0: the side branch)
+  const char* pv = std::getenv("MOERT_PF_BLOCK");
+  bool fits = m->prefetch && m->use_ab && !(pv && pv[0] == '0');
+  for (size_t l = 0; fits && l < m->layers.size(); l++)
+    fits = attn_block_fits(m->dims, m->layers[l].qkv, m->cus) &&
+           attn_block_prefetch_fits(m->dims, m->layers[l], m->cache);
+  m->pf_blk = fits;
   MTRY(m, m->build_graph());
   return MOERT_OK;
 }

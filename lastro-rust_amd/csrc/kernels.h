@@ -97,8 +97,14 @@ hipError_t launch_attn_combine(hipStream_t s, const Dims& d, const StepBufs& b, 
 bool attn_block_fits(const Dims& d, const DMat& qkv, int cus);
 // combine: the previous layer's experts are in x.ys (k_moe_xcd); the block forms h + res * sum_j w_j ys[j] (weights
 // of layer - 1) as its input and workgroup 0 writes it to b.hc, the output projection's input.
+// pfc (a cached model, not with combine): the same launch also predicts the layer's experts from h and copies the
+// predicted misses into the pool (one decide and 64 copy workgroups after the attention workgroups, cache_pf.h);
+// attn_block_prefetch_fits says whether the layer allows it (router of at most 64 rows in the q/k/v rows' format,
+// top_k <= 8, top_k <= slots <= 4096).
+struct CacheDev;
+bool attn_block_prefetch_fits(const Dims& d, const LayerDev& L, const CacheDev& c);
 hipError_t launch_attn_block(hipStream_t s, const LayerDev& L, const Dims& d, const StepBufs& b, int cus, int layer,
-                             const AbBufs& x, bool combine, Tl tl = {});
+                             const AbBufs& x, bool combine, Tl tl = {}, const CacheDev* pfc = nullptr);
 // The MoE half with the 8 routed experts spread over the 8 XCDs (router + gate/up + down in one launch, the down
 // outputs left in x.ys for the next reader of h), or false / an error when it does not apply: top-8 routing, ffn
 // 512, hidden 1024 or 1536, Q8_0 or Q4_0 experts and router, 256 compute units.

@@ -293,31 +293,50 @@ def test_fault_inject_refusals(gpu, granite_1b_wide):
     g.close()
 
 
-def test_prefetch_branch_uses_the_three_kernel_attention(gpu):
-    """The cache's prefetch branch runs its kernels beside the attention half on a second stream, which the attention
-    block (all workgroups resident at once) does not allow: with the branch on, the cached model at the bench's cache
-    shape launches no attention block, and its logits equal the resident three-kernel model's bit for bit; with the
-    branch off again it uses the block again, with the same logits."""
+def test_prefetch_runs_inside_the_attention_block_and_decides_like_the_branch(gpu):
+    """The cache's prefetch at the bench's cache shape runs inside the attention launch (one decide and 64 copy
+    workgroups after the attention workgroups, cache_pf.h): with it on, the cached model still launches the attention
+    block, its logits, ids and weights equal the resident three-kernel model's bit for bit, and its predictions and
+    counters (hits, copies, prefetched) equal those of the same model with the side-stream branch (MOERT_PF_BLOCK=0,
+    which uses the three-kernel attention) over the same forced tokens."""
     cfg = moert.Config(**moert.GRANITE_1B)
-    say("1B cached build (prefetch)")
+    say("1B cached build (prefetch inside the block)")
     m = moert.SynthModel(cfg, seed=78, wdtype=moert.Q8_0, embed_dtype=moert.Q8_0, zipf_s=1.1)
     res = three_kernel_model(m, MAX_LEN, SPLITS)
-    cac = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS, cache_slots=192)
-    assert cac.kernel_path() == "block"
-    cac.cache_prefetch_mode(True)
-    assert cac.kernel_path() == "unfused"
+    blk = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS, cache_slots=192)
+    brn = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS, cache_slots=192)
+    assert blk.kernel_path() == "block"
+    blk.cache_prefetch_mode(True)
+    assert blk.kernel_path() == "block"
+    os.environ["MOERT_PF_BLOCK"] = "0"
+    try:
+        brn.cache_prefetch_mode(True)
+    finally:
+        del os.environ["MOERT_PF_BLOCK"]
+    assert brn.kernel_path() == "unfused"
     toks = np.random.default_rng(46).integers(0, cfg.vocab, 40)
     for t, tok in enumerate(toks):
-        if t == 20:
-            cac.cache_prefetch_mode(False)
-            assert cac.kernel_path() == "block"
         lr, ir, wr, _ = res.step(int(tok))
-        lc, ic, wc, _ = cac.step(int(tok))
-        assert bits_equal(lr, lc) and np.array_equal(ir, ic) and bits_equal(wr, wc), t
-    cac.cache_prefetch_mode(True)
-    assert launches(cac, moert.K_ATTN_BLOCK) == 0 and launches(cac, moert.K_QKV) == cfg.layers
-    res.close()
-    cac.close()
+        for g in (blk, brn):
+            lc, ic, wc, _ = g.step(int(tok))
+            assert bits_equal(lr, lc) and np.array_equal(ir, ic) and bits_equal(wr, wc), t
+    assert np.array_equal(blk.cache_predictions(0, len(toks)), brn.cache_predictions(0, len(toks)))
+    cb, cr = blk.cache_counters(), brn.cache_counters()
+    say(f"prefetch inside the block: {cb['hits']} hits, {cb['copies']} copies, {cb['prefetched']} prefetched")
+    assert cb["prefetched"] > 0
+    assert all(cb[k] == cr[k] for k in ("hits", "copies", "prefetched", "needed")), (cb, cr)
+    # prefetch off again: the same block without the extra workgroups, same logits
+    blk.cache_prefetch_mode(False)
+    assert blk.kernel_path() == "block"
+    for tok in toks[:4]:
+        lr, _, _, _ = res.step(int(tok))
+        lc, _, _, _ = blk.step(int(tok))
+        assert bits_equal(lr, lc)
+    blk.cache_prefetch_mode(True)
+    assert launches(blk, moert.K_ATTN_BLOCK) == cfg.layers and launches(blk, moert.K_QKV) == 0
+    assert launches(brn, moert.K_ATTN_BLOCK) == 0 and launches(brn, moert.K_QKV) == cfg.layers
+    for g in (res, blk, brn):
+        g.close()
 
 
 def test_hybrid_with_the_attention_block_equals_the_three_kernel_hybrid(gpu):

@@ -194,16 +194,20 @@ def test_prefetch_branch_keeps_outputs_and_its_evictions_replay_on_the_lru_oracl
     cac.close()
 
 
-def test_granite_3b_q4_0_prefetch_branch_forced_512_steps(gpu, granite_3b_q4):
-    """The expert-cache workload with the prefetch branch: 512 forced steps from an empty 320-slot pool, outputs
-    equal to the resident model's bit for bit, counters equal to the replay with the recorded predictions, and most
-    predicted experts used (the prediction from the layer's input routes like the layer)."""
+@pytest.mark.parametrize("max_len,splits,path", [(576, 64, "unfused"), (4416, 32, "block")])
+def test_granite_3b_q4_0_prefetch_forced_512_steps(gpu, granite_3b_q4, max_len, splits, path):
+    """The expert-cache workload with the prefetch: 512 forced steps from an empty 320-slot pool, outputs equal to
+    the resident model's bit for bit, counters equal to the replay with the recorded predictions, and most predicted
+    experts used (the prediction from the layer's input routes like the layer). At 576 positions (one tile per split)
+    the prefetch is the side-stream branch beside the three-kernel attention; at the decode bench's 4416 / 32 splits
+    it runs inside the attention block's launch."""
     cfg, m = granite_3b_q4
     toks = np.random.default_rng(512).integers(0, cfg.vocab, 512)
-    res = moert.GpuModel(m, 576, attn_splits=64)
-    cac = moert.GpuModel(m, 576, attn_splits=64, cache_slots=320)
+    res = moert.GpuModel(m, max_len, attn_splits=splits)
+    cac = moert.GpuModel(m, max_len, attn_splits=splits, cache_slots=320)
     cac.cache_prefetch_mode(True)
-    routes = _forced_pair(res, cac, toks, "3b q4_0 prefetch")
+    assert cac.kernel_path() == path
+    routes = _forced_pair(res, cac, toks, f"3b q4_0 prefetch ({path})")
     preds = cac.cache_predictions(0, len(toks))
     (hits, copies, _), pf = _replay_with_predictions(cfg, 320, routes, preds)
     c = cac.cache_counters()
