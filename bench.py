@@ -175,10 +175,12 @@ def expert_cache(cfg, seed, steps, frac=0.25, hybrid_steps=128):
     log("expert cache: building the 3B Q4_0 model")
     m = moert.SynthModel(cfg, seed=seed + 5, wdtype=moert.Q4_0, embed_dtype=moert.Q4_0, zipf_s=1.1)
     slots = int(cfg.layers * cfg.experts * frac)
-    max_len = (steps + 2 + 63) // 64 * 64
+    # the decode bench's cache shape (4416 positions, 32 requested splits: 23 splits of 3 tiles), where the
+    # attention block applies and the prefetch runs inside its launch
+    max_len, splits = max(4416, (steps + 2 + 63) // 64 * 64), 32
     record = moert.dtype_bytes(moert.Q4_0, 3 * cfg.inter * cfg.hidden)
     tok = int(np.random.default_rng(seed).integers(0, cfg.vocab))
-    g = moert.GpuModel(m, max_len, attn_splits=64, cache_slots=slots)
+    g = moert.GpuModel(m, max_len, attn_splits=splits, cache_slots=slots)
     log(f"expert cache: pinned host store and {slots}-slot pool ready; greedy run")
     g.step(tok, want_logits=False)
     g.cache_clear()
@@ -200,31 +202,48 @@ def expert_cache(cfg, seed, steps, frac=0.25, hybrid_steps=128):
     g.generate(forced, 1)
     fwall = time.perf_counter() - t0
     fhits, fcopies = g.cache_stats()
-    # the same forced run with the prefetch branch: each layer's experts predicted from the layer's input (its norm and
-    # router applied to the residual before attention) and copied into the pool on a side stream while attention runs
-    log("expert cache: forced-token run with the prefetch branch")
-    g.cache_prefetch_mode(True)
-    g.cache_clear()
-    g.reset()
-    c0 = g.cache_counters()
-    t0 = time.perf_counter()
-    g.generate(forced, 1)
-    pwall = time.perf_counter() - t0
-    c1 = g.cache_counters()
-    # the cost of the branch itself: the greedy run (all hits after its first steps) with the branch on
+    # the same forced run with the prefetch: each layer's experts predicted from the layer's input (its norm and
+    # router applied to the residual before attention) and copied into the pool, inside the attention launch (the
+    # default where the block applies) and as the side-stream branch beside the three-kernel attention
+    def prefetched_run(label, branch):
+        log(f"expert cache: forced-token run with the prefetch {label}")
+        if branch:
+            os.environ["MOERT_PF_BLOCK"] = "0"
+        try:
+            g.cache_prefetch_mode(True)
+        finally:
+            os.environ.pop("MOERT_PF_BLOCK", None)
+        path = g.kernel_path()
+        g.cache_clear()
+        g.reset()
+        c0 = g.cache_counters()
+        t0 = time.perf_counter()
+        g.generate(forced, 1)
+        pwall = time.perf_counter() - t0
+        c1 = g.cache_counters()
+        # its cost alone: the greedy run (all hits after its first steps) with the prefetch on
+        g.reset()
+        g.step(tok, want_logits=False)
+        t0 = time.perf_counter()
+        g.time_steps(0, steps - 1)
+        pgreedy = (steps - 1) / (time.perf_counter() - t0)
+        g.cache_prefetch_mode(False)
+        pc = {k: c1[k] - c0[k] for k in ("hits", "copies", "prefetched")}
+        # miss bytes overlapped: the records copied ahead, of all records copied in the run
+        return {"kernel_path": path, "tok_s": round((steps + 1) / pwall, 2), "hits": pc["hits"],
+                "copies_in_step": pc["copies"], "prefetched": pc["prefetched"],
+                "overlapped_miss_bytes_frac": round(pc["prefetched"] / max(1, pc["prefetched"] + pc["copies"]), 4),
+                "copied_bytes_per_token": round((pc["copies"] + pc["prefetched"]) * record / steps),
+                "greedy_tok_s": round(pgreedy, 2)}
+
+    prefetch = prefetched_run("inside the attention launch", False)
+    prefetch["side_branch"] = prefetched_run("branch", True)
+    # the greedy run without prefetch on this model again, beside the prefetched ones (same shape and box state)
     g.reset()
     g.step(tok, want_logits=False)
     t0 = time.perf_counter()
     g.time_steps(0, steps - 1)
-    pgreedy = (steps - 1) / (time.perf_counter() - t0)
-    g.cache_prefetch_mode(False)
-    pc = {k: c1[k] - c0[k] for k in ("hits", "copies", "prefetched")}
-    # miss bytes overlapped: the records copied ahead by the branch, of all records copied in the run
-    prefetch = {"tok_s": round((steps + 1) / pwall, 2), "hits": pc["hits"], "copies_in_step": pc["copies"],
-                "prefetched": pc["prefetched"],
-                "overlapped_miss_bytes_frac": round(pc["prefetched"] / max(1, pc["prefetched"] + pc["copies"]), 4),
-                "copied_bytes_per_token": round((pc["copies"] + pc["prefetched"]) * record / steps),
-                "greedy_tok_s": round(pgreedy, 2)}
+    prefetch["greedy_tok_s_without"] = round((steps - 1) / (time.perf_counter() - t0), 2)
     # the empty pool filled from the host between steps (moert_cache_fill: each slot's record copied with
     # hipMemcpyAsync on a side stream, host-timed including the table read-back and write-back)
     g.cache_clear()
@@ -238,7 +257,7 @@ def expert_cache(cfg, seed, steps, frac=0.25, hybrid_steps=128):
     hybrid = None
     if hsteps > 0:
         log(f"expert cache: host-CPU hybrid, {hsteps} forced tokens")
-        hy = moert.GpuModel(m, max_len, attn_splits=64, hybrid=(slots, 4, 16))
+        hy = moert.GpuModel(m, max_len, attn_splits=splits, hybrid=(slots, 4, 16))
         t0 = time.perf_counter()
         hy.generate(forced[:hsteps], 1)
         hwall = time.perf_counter() - t0
@@ -250,11 +269,12 @@ def expert_cache(cfg, seed, steps, frac=0.25, hybrid_steps=128):
     probe_bytes = 256 << 20
     pk, pm = moert.h2d_probe(probe_bytes, 4)
     log("expert cache: resident comparison")
-    r = moert.GpuModel(m, max_len, attn_splits=64)
+    r = moert.GpuModel(m, max_len, attn_splits=splits)
     r.step(tok, want_logits=False)
     res_ms = r.time_steps(2, 64)
     r.close()
-    out = {"slots": slots, "experts_total": cfg.layers * cfg.experts, "steps": steps, "tok_s": round(tok_s, 2),
+    out = {"slots": slots, "experts_total": cfg.layers * cfg.experts, "steps": steps, "max_len": max_len,
+           "attn_splits": splits, "tok_s": round(tok_s, 2),
            "ms_per_step": round(wall * 1e3 / (steps - 1), 4), "hits": hits, "copies": copies,
            "hit_rate": round(hits / max(1, hits + copies), 4), "requests": n,
            "copied_bytes_per_token": round(copies * record / steps),
