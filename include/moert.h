@@ -311,6 +311,12 @@ int moert_block_forward_batched(moert_block* b, int m, const float* x, float* y,
  * must run nothing else meanwhile: a wait of that launch that gives up makes the step return MOERT_E_DEVICE. In
  * mode 1, moert_block_time_batched reports the launch in us[1] and 0 in us[2..4]. No reference counterpart. */
 int moert_block_batched_kernel(moert_block* b, int mode);
+/* Test hook of the one-launch batched step (mode 1): the waits named by `bits` (1 router logits, 2 act vectors,
+ * 4 expert outputs, 8 input codes) look for an epoch no launch writes in the following steps and give up after a few
+ * polls, so the step returns MOERT_E_DEVICE while every workgroup still ends normally; 0 restores normal steps. The
+ * error is cleared once reported (a block step carries no state into the next). No reference counterpart: it
+ * exercises the failure path of the bounded waits. */
+int moert_block_fault_inject(moert_block* b, unsigned bits);
 /* Number of distinct experts routed by the last batched step on this block (the grouped GEMM's expert count). */
 int moert_block_experts_in_step(moert_block* b, int* n_experts);
 /* Times `iters` rounds of the batched step over `nblocks` blocks in turn (rotating weights beyond the caches),

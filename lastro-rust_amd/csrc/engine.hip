@@ -984,7 +984,7 @@ struct moert_block {
     const size_t H = dims.hidden, P = kFbPos;
     unsigned *err = nullptr, *lg = nullptr, *xf = nullptr, *act = nullptr, *o = nullptr;
     int rc;
-    if ((rc = zeros(arena, stream, 1, &err)) || (rc = zeros(arena, stream, 8 * P * 64 * 2, &lg)) ||
+    if ((rc = zeros(arena, stream, 2, &err)) || (rc = zeros(arena, stream, 8 * P * 64 * 2, &lg)) ||
         (rc = zeros(arena, stream, 8 * P * 2, &xf)) || (rc = zeros(arena, stream, 8 * P * H, &fb.xh)) ||
         (rc = zeros(arena, stream, 8 * P * H, &fb.xl)) || (rc = zeros(arena, stream, 8 * P * (H / 32), &fb.xd)) ||
         (rc = zeros(arena, stream, (size_t)kFbExperts * (kFbInter / 32) * kFbActW * P * 2, &act)) ||
@@ -1010,12 +1010,15 @@ struct moert_block {
     CHECK_HIP(launch_grp_fused(s, L, m, dims.top_k, dims.inter, gx, g, fb, fb_epoch, gy, cus));
     return MOERT_OK;
   }
-  // the one-launch step's error word: a wait that gave up
+  // the one-launch step's error word: a wait that gave up. A block step carries nothing into the next one, so the
+  // word is cleared once reported (the stream is idle) and the next step starts clean.
   int fused_check() {
     if (!fused) return MOERT_OK;
     unsigned e = 0;
     CHECK_HIP(hipMemcpy(&e, fb.err, 4, hipMemcpyDeviceToHost));
     if (e) {
+      const unsigned zero = 0;
+      CHECK_HIP(hipMemcpy(fb.err, &zero, 4, hipMemcpyHostToDevice));
       set_err("batched step (one launch) gave up waiting for %s%s%s%s(error bits %#x): its workgroups were not "
               "all resident at once or not dealt round-robin over the XCDs", (e & 1u) ? "router logits " : "",
               (e & 2u) ? "act vectors " : "", (e & 4u) ? "expert outputs " : "", (e & 8u) ? "input codes " : "", e);
@@ -2170,6 +2173,15 @@ int moert_block_batched_kernel(moert_block* b, int mode) {
     TRY(b->ensure_fused());
   }
   b->fused = mode;
+  return MOERT_OK;
+}
+
+int moert_block_fault_inject(moert_block* b, unsigned bits) {
+  CHECK_CFG(b, "null argument");
+  CHECK_CFG((bits & ~15u) == 0, "block fault_inject: bits %#x outside 1 | 2 | 4 | 8", bits);
+  CHECK_CFG(b->fused && b->fb.err, "block fault_inject: the block runs its batched steps as one launch only");
+  CHECK_HIP(hipStreamSynchronize(b->stream));
+  CHECK_HIP(hipMemcpy(b->fb.err + 1, &bits, 4, hipMemcpyHostToDevice));
   return MOERT_OK;
 }
 

@@ -48,7 +48,8 @@ constexpr int kFbExperts = 48;     // routed experts at most
 constexpr int kFbInter = 512;      // ffn width of the one-launch block
 constexpr int kFbActW = 17;        // act entries per (expert, 32-row block, position): 8 hi words, 8 lo words, scale
 struct FbBufs {
-  unsigned* err;  // [1] bits of the waits that gave up: 1 router logits, 2 act vectors, 4 expert outputs, 8 codes
+  unsigned* err;  // [2] bits of the waits that gave up (1 router logits, 2 act vectors, 4 expert outputs, 8 codes),
+                  // then the test mask of waits made to give up (moert_block_fault_inject)
   uint2* lg;      // [8][kFbPos * 64] router logits (position, expert) of each XCD
   uint2* xflag;   // [8][kFbPos] one flag per (XCD, position) over the XCD's copy of the input codes
   int8_t* xh;     // [8][kFbPos][hidden] hi codes of the inputs, one copy per XCD

@@ -558,8 +558,12 @@ __global__ __launch_bounds__(kFbThreads) void k_grp_fused(DMat router, const flo
   const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int xc = (int)xcc_id() & 7, w = blockIdx.x >> 3, bid = blockIdx.x;
   const int E = router.rows, grp = lane >> 4;
-  const unsigned err0 = __builtin_amdgcn_readfirstlane(__builtin_amdgcn_raw_buffer_load_b32(
-      l2_buffer(f.err, 4), 0, 0, kL2Policy));
+  // f.err[0]: bits of waits that gave up; f.err[1]: a test mask only the host writes (moert_block_fault_inject):
+  // a wait whose bit is set looks for an epoch no launch writes, and every wait polls at most kInjectSpin times
+  const auto ew = __builtin_amdgcn_raw_buffer_load_b64(l2_buffer(f.err, 8), 0, 0, kL2Policy);
+  const unsigned err0 = __builtin_amdgcn_readfirstlane(ew[0]), inj = __builtin_amdgcn_readfirstlane(ew[1]);
+  const int spin_max = inj ? kInjectSpin : kFbSpin;
+  auto ep = [&](unsigned bit) { return (inj & bit) ? kNoEpoch : epoch; };
   if (threadIdx.x == 0) dead_s = err0 ? 1 : 0;
   auto fail = [&](bool ok, unsigned bit) {
     if (!ok && lane == 0) {
@@ -630,8 +634,8 @@ __global__ __launch_bounds__(kFbThreads) void k_grp_fused(DMat router, const flo
     }
     unsigned v[M];
     const __amdgpu_buffer_rsrc_t rl = l2_buffer(f.lg + xc * LGN, LGN * 8);
-    const bool ok = poll_m<M>([&](int i) { return l2_load_u64(rl, 8u * (unsigned)i); }, idx, use, epoch,
-                              dead_s ? 0 : kFbSpin, v);
+    const bool ok = poll_m<M>([&](int i) { return l2_load_u64(rl, 8u * (unsigned)i); }, idx, use, ep(1u),
+                              dead_s ? 0 : spin_max, v);
 #pragma unroll
     for (int q = 0; q < M; q++)
       if (use[q]) lgs[idx[q] / E][idx[q] % E] = __uint_as_float(v[q]);
@@ -647,8 +651,8 @@ __global__ __launch_bounds__(kFbThreads) void k_grp_fused(DMat router, const flo
     bool use[1] = {lane < m};
     unsigned v[1];
     const __amdgpu_buffer_rsrc_t rf = l2_buffer(f.xflag + xc * P, P * 8);
-    const bool ok = poll_m<1>([&](int i) { return l2_load_u64(rf, 8u * (unsigned)i); }, idx, use, epoch,
-                              dead_s ? 0 : kFbSpin, v);
+    const bool ok = poll_m<1>([&](int i) { return l2_load_u64(rf, 8u * (unsigned)i); }, idx, use, ep(8u),
+                              dead_s ? 0 : spin_max, v);
     fail(ok, 8u);
     const __amdgpu_buffer_rsrc_t rh = l2_buffer(f.xh + (size_t)xc * P * H, P * H);
     const __amdgpu_buffer_rsrc_t rlo = l2_buffer(f.xl + (size_t)xc * P * H, P * H);
@@ -772,7 +776,7 @@ __global__ __launch_bounds__(kFbThreads) void k_grp_fused(DMat router, const flo
       const bool use = t0 < t1 && (s2 == 0 || u1 != u0) && p < m && ((plan.bits[plan.list[uu]] >> p) & 1u);
       const uint2* src = f.act + (size_t)(uu * NBI + bb) * AW * P + p;
       unsigned v[AW];
-      const bool ok = poll_rec<AW, P>(src, use, epoch, dead_s ? 0 : kFbSpin, v);
+      const bool ok = poll_rec<AW, P>(src, use, ep(2u), dead_s ? 0 : spin_max, v);
       if (use) {
         int8_t* row_h = ahs + (s2 * P + p) * SA + 32 * bb;
         int8_t* row_l = als + (s2 * P + p) * SA + 32 * bb;
@@ -837,7 +841,7 @@ __global__ __launch_bounds__(kFbThreads) void k_grp_fused(DMat router, const flo
       use[jj] = jj < k;
     }
     unsigned v[8];
-    const bool ok = poll_m<8>([&](int i) { return get_dev(f.o + i); }, idx, use, epoch, dead_s ? 0 : kFbSpin, v);
+    const bool ok = poll_m<8>([&](int i) { return get_dev(f.o + i); }, idx, use, ep(4u), dead_s ? 0 : spin_max, v);
     float acc = 0.0f;
 #pragma unroll
     for (int jj = 0; jj < 8; jj++)

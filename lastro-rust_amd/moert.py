@@ -151,6 +151,7 @@ def lib() -> ctypes.CDLL:
             "moert_block_forward_batched": (i, [vp, i, vp, vp, vp, vp]),
             "moert_block_experts_in_step": (i, [vp, ip]),
             "moert_block_batched_kernel": (i, [vp, i]),
+            "moert_block_fault_inject": (i, [vp, ctypes.c_uint]),
             "moert_block_time_batched": (i, [vp, i, i, i, vp]),
             "moert_router_topk": (i, [vp, i, i, vp, vp]),
             "moert_argmax": (i, [vp, i, ip]),
@@ -231,7 +232,7 @@ EXPORTED = ["moert_last_error", "moert_device_info", "moert_model_create", "moer
             "moert_set_position", "moert_get_position", "moert_read_kv_fp16", "moert_read_hidden", "moert_read_logits",
             "moert_time_steps", "moert_time_kernel", "moert_fault_inject", "moert_model_path", "moert_timeline_step", "moert_block_create", "moert_block_destroy",
             "moert_block_forward", "moert_block_time", "moert_block_forward_batched",
-            "moert_block_experts_in_step", "moert_block_batched_kernel", "moert_block_time_batched", "moert_router_topk", "moert_argmax", "moert_gemv",
+            "moert_block_experts_in_step", "moert_block_batched_kernel", "moert_block_fault_inject", "moert_block_time_batched", "moert_router_topk", "moert_argmax", "moert_gemv",
             "moert_dequant", "moert_rmsnorm", "moert_rope", "moert_attn_decode", "moert_attn_decode_noalloc",
             "moert_exp_device",
             "moert_copy_probe", "moert_read_probe", "moert_h2d_probe", "moert_quantize", "moert_dtype_bytes", "moert_synth_normal", "moert_synth_quantized",
@@ -751,6 +752,11 @@ class GpuBlock:
         """0: the batched step as four kernels; 1: as one launch over the XCDs (moert_block_batched_kernel)."""
         check(lib().moert_block_batched_kernel(self.h, int(mode)))
         self.fused = int(mode)
+
+    def fault_inject(self, bits: int):
+        """Test hook of the one-launch step: the waits named by `bits` (1 logits, 2 act vectors, 4 expert outputs,
+        8 input codes) give up in the following steps, which still end normally (moert_block_fault_inject)."""
+        check(lib().moert_block_fault_inject(self.h, bits))
 
     def close(self):
         if self.h:

@@ -151,3 +151,35 @@ def test_batched_one_launch_identical_positions_and_refusals(gpu):
         small.batched_kernel(1)
     assert e.value.code == moert.E_CONFIG
     small.close()
+
+
+def test_batched_one_launch_failure_path_is_reported_and_cleared(gpu):
+    """The one launch's bounded waits, each made to give up from the host (moert_block_fault_inject: the named wait
+    looks for an epoch no launch writes): the step returns MOERT_E_DEVICE naming the wait, every workgroup ends
+    (the next call runs), and with the mask cleared the next step equals the four kernels' bit for bit again. The
+    hook is refused for the four-kernel mode and for unknown bits."""
+    hidden, inter, experts, k, m = 1536, 512, 40, 8, 16
+    router = moert.synth_quantized(141, 0, experts * hidden, 0.02, moert.Q8_0)
+    gate_up = moert.synth_quantized(142, 0, experts * 2 * inter * hidden, 0.02, moert.Q8_0)
+    down = moert.synth_quantized(143, 0, experts * hidden * inter, 0.02, moert.Q8_0)
+    blk = moert.GpuBlock(hidden, inter, experts, k, router, gate_up, down, moert.Q8_0,
+                         router_bias=moert.zipf_bias(experts, 144))
+    x = moert.synth_normal(145, 0, m * hidden).reshape(m, hidden)
+    y0, i0, w0 = blk.forward_batched(x)
+    with pytest.raises(moert.MoertError) as e:
+        blk.fault_inject(2)
+    assert e.value.code == moert.E_CONFIG
+    blk.batched_kernel(1)
+    with pytest.raises(moert.MoertError) as e:
+        blk.fault_inject(16)
+    assert e.value.code == moert.E_CONFIG
+    for bit, name in ((1, "router logits"), (2, "act vectors"), (4, "expert outputs"), (8, "input codes")):
+        say(f"one-launch failure path: bit {bit} ({name})")
+        blk.fault_inject(bit)
+        with pytest.raises(moert.MoertError) as e:
+            blk.forward_batched(x)
+        assert e.value.code == moert.E_DEVICE and name in str(e.value), str(e.value)
+        blk.fault_inject(0)
+        y, ids, w = blk.forward_batched(x)
+        assert ids.tolist() == i0.tolist() and bits_equal(w, w0) and bits_equal(y, y0), bit
+    blk.close()
