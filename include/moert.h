@@ -305,8 +305,8 @@ int moert_block_time(moert_block* b, int iters, double* us);
 int moert_block_forward_batched(moert_block* b, int m, const float* x, float* y, int* ids, float* weights);
 /* The kernels of the block's batched steps: mode 0 (default) the four kernels (route, gate/up, down, combine);
  * mode 1 one launch of 256 workgroups that must all be resident at once, one per compute unit, dealt round-robin
- * over the 8 XCDs (router logits and input codes through each XCD's L2; gate/up items and down tiles spread over
- * all workgroups, act vectors and expert outputs device-wide), bit-identical to mode 0, for m <= 16 positions,
+ * over the 8 XCDs (router logits, top-k and input codes through each XCD's L2; gate/up items and down tiles spread
+ * over all workgroups, act vectors and expert outputs device-wide), bit-identical to mode 0, for m <= 16 positions,
  * ffn 512, at most 48 experts, Q8_0, on a device with 256 compute units (MOERT_E_CONFIG otherwise). The device
  * must run nothing else meanwhile: a wait of that launch that gives up makes the step return MOERT_E_DEVICE. In
  * mode 1, moert_block_time_batched reports the launch in us[1] and 0 in us[2..4]. No reference counterpart. */

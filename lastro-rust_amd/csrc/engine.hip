@@ -982,19 +982,20 @@ struct moert_block {
   int ensure_fused() {
     if (fb.err) return MOERT_OK;
     const size_t H = dims.hidden, P = kFbPos;
-    unsigned *err = nullptr, *lg = nullptr, *xf = nullptr, *act = nullptr, *o = nullptr;
+    unsigned *err = nullptr, *lg = nullptr, *xf = nullptr, *act = nullptr, *o = nullptr, *rk = nullptr;
     int rc;
     if ((rc = zeros(arena, stream, 2, &err)) || (rc = zeros(arena, stream, 8 * P * 64 * 2, &lg)) ||
         (rc = zeros(arena, stream, 8 * P * 2, &xf)) || (rc = zeros(arena, stream, 8 * P * H, &fb.xh)) ||
         (rc = zeros(arena, stream, 8 * P * H, &fb.xl)) || (rc = zeros(arena, stream, 8 * P * (H / 32), &fb.xd)) ||
         (rc = zeros(arena, stream, (size_t)kFbExperts * (kFbInter / 32) * kFbActW * P * 2, &act)) ||
-        (rc = zeros(arena, stream, P * 8 * H * 2, &o)))
+        (rc = zeros(arena, stream, P * 8 * H * 2, &o)) || (rc = zeros(arena, stream, 8 * P * 16 * 2, &rk)))
       return rc;
     fb.err = err;
     fb.lg = reinterpret_cast<uint2*>(lg);
     fb.xflag = reinterpret_cast<uint2*>(xf);
     fb.act = reinterpret_cast<uint2*>(act);
     fb.o = reinterpret_cast<uint2*>(o);
+    fb.rk = reinterpret_cast<uint2*>(rk);
     CHECK_HIP(hipStreamSynchronize(stream));
     return MOERT_OK;
   }

@@ -57,13 +57,14 @@ struct FbBufs {
   float* xd;      // [8][kFbPos][hidden / 32] their block scales
   uint2* act;     // [kFbExperts][kFbInter / 32][kFbActW][kFbPos] act codes by list index, device-wide
   uint2* o;       // [kFbPos * 8][hidden] expert outputs by member slot, device-wide
+  uint2* rk;      // [8][kFbPos][16] per XCD: the top-k ids (8), then weights (8), of each position
 };
 
 // y[m, H] = the MoE block of launch_grouped_block as one launch of 256 workgroups of 512 threads, all resident (one
-// per compute unit, 8 XCDs): each XCD codes the m inputs once and shares the codes and the router logits through
-// its L2, and every workgroup ranks the experts; the gate/up items and down tiles of all routed experts are dealt
-// over the 256 workgroups, with the m positions as MFMA columns and the act vectors device-wide; the expert outputs
-// go out device-wide and workgroup b combines rows [b H / 256, +H / 256). Same arithmetic and order as the four
+// per compute unit, 8 XCDs): each XCD codes and ranks the m positions once and shares the codes, router logits and
+// top-k through its L2; the gate/up items and down tiles of all routed experts are dealt over the 256 workgroups,
+// with the m positions as MFMA columns and the act vectors device-wide; the expert outputs go out device-wide and
+// workgroup b combines rows [b H / 256, +H / 256). Same arithmetic and order as the four
 // kernels, bit for bit. m <= 16, k <= 8, E <= 48, ffn 512, Q8_0, 256 compute units; `epoch` >= 1 differs from the
 // previous launch's on these buffers.
 hipError_t launch_grp_fused(hipStream_t s, const LayerDev& L, int m, int k, int inter, const float* x,

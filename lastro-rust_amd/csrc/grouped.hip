@@ -472,10 +472,11 @@ hipError_t launch_grp_experts(hipStream_t s, int H, int E, int m, int k, int int
 // ------------------------------------------------------------------------------------------------------------
 // The block as one launch (launch_grp_fused). Workgroup b runs on XCD x = XCC_ID with index w = b / 8 in it (the
 // chip deals the workgroups of a launch round-robin over its 8 XCDs; all 256 are resident at once):
-//   R. workgroup w < m of each XCD codes input w into the XCD's copy (k_grp_route's codes) and raises its flag;
-//      wave slot s = 8 w + wave of the XCD computes the router dots of position s % 16 with experts s / 16 + 16 i
-//      (one batch of rows), shared through the XCD's L2; every workgroup ranks the experts of each position
-//      (wave_topk), builds the grouping (make_plan) and reads the XCD's codes into LDS;
+//   R. wave slot s = 8 w + wave of the XCD computes the router dots of position s % 16 with experts s / 16 + 16 i
+//      (one batch of rows), shared through the XCD's L2; workgroup w < m of each XCD codes input w into the XCD's
+//      copy (k_grp_route's codes), raises its flag, ranks the experts of position w (wave_topk) and shares the ids
+//      and weights through the XCD's L2; every workgroup gathers them, builds the grouping (make_plan) and reads the
+//      XCD's codes into LDS;
 //   U. gate/up item q = 2 b + slot (+512 per round) covers act rows [32 blk, +32) of list expert u = q / 16: 32
 //      gate and 32 up rows on four waves, every position an MFMA column; silu(g) * u and its hi/lo codes go out
 //      device-wide for the expert's members;
@@ -546,10 +547,12 @@ __global__ __launch_bounds__(kFbThreads) void k_grp_fused(DMat router, const flo
   __shared__ __align__(16) int8_t big[XB > AB ? XB : AB];  // the input codes (R, U), then two experts' act codes
   __shared__ float xd_s[P * NB];
   __shared__ float ad_s[2 * P * NBI];
-  __shared__ __align__(16) float lgs[P][64];
+  __shared__ __align__(16) float lgs[64];
   __shared__ int ids_s[P * 8];
   __shared__ float w_s[P * 8];
-  __shared__ __align__(16) TopkLds tk[NW];
+  __shared__ __align__(16) TopkLds tk;
+  __shared__ int rk_ids[8];
+  __shared__ float rk_w[8];
   __shared__ Plan plan;
   __shared__ __align__(16) uint16_t sdt[NW][NB * 16];
   __shared__ float gout[2][2][32][P + 1];
@@ -621,25 +624,25 @@ __global__ __launch_bounds__(kFbThreads) void k_grp_fused(DMat router, const flo
   if (coder) wait_mem();
   __syncthreads();
   if (w < m && threadIdx.x == 0) put_entry(&f.xflag[xc * P + w], 0u, epoch);
-  {
-    constexpr int M = (P * 64 + NT - 1) / NT;
-    const int NI = m * E;
-    int idx[M];
-    bool use[M];
-#pragma unroll
-    for (int q = 0; q < M; q++) {
-      idx[q] = (int)threadIdx.x + q * NT;
-      use[q] = idx[q] < NI;
-      idx[q] = use[q] ? idx[q] : 0;
-    }
-    unsigned v[M];
+  // the top-k of position w, once per XCD: wave 0 of workgroup w < m waits for the position's E logits, ranks them
+  // (wave_topk) and shares the ids and weights through the XCD's L2
+  if (w < m && wid == 0) {
+    int idx[1] = {w * E + (lane < E ? lane : 0)};
+    bool use[1] = {lane < E};
+    unsigned v[1];
     const __amdgpu_buffer_rsrc_t rl = l2_buffer(f.lg + xc * LGN, LGN * 8);
-    const bool ok = poll_m<M>([&](int i) { return l2_load_u64(rl, 8u * (unsigned)i); }, idx, use, ep(1u),
+    const bool ok = poll_m<1>([&](int i) { return l2_load_u64(rl, 8u * (unsigned)i); }, idx, use, ep(1u),
                               dead_s ? 0 : spin_max, v);
-#pragma unroll
-    for (int q = 0; q < M; q++)
-      if (use[q]) lgs[idx[q] / E][idx[q] % E] = __uint_as_float(v[q]);
+    lgs[lane] = __uint_as_float(v[0]);
     fail(ok, 1u);
+    wave_lds_sync();
+    wave_topk(lgs, E, k, lane, tk, rk_ids, rk_w);
+    wave_lds_sync();
+    if (lane < k) {
+      uint2* rk = f.rk + (size_t)(xc * P + w) * 16;
+      put_entry(rk + lane, (unsigned)rk_ids[lane], epoch);
+      put_entry(rk + 8 + lane, __float_as_uint(rk_w[lane]), epoch);
+    }
   }
   // the XCD's input codes: each wave waits for the m flags itself, then loads its share into registers, which
   // reach LDS after the plan (rows past m are never a member)
@@ -673,8 +676,24 @@ __global__ __launch_bounds__(kFbThreads) void k_grp_fused(DMat router, const flo
       if (i < m * NB) xdv[j] = l2_load_f32(rd, 4u * (unsigned)i);
     }
   }
-  __syncthreads();
-  for (int p = wid; p < m; p += NW) wave_topk(lgs[p], E, k, lane, tk[wid], ids_s + p * k, w_s + p * k);
+  {
+    // every workgroup: the ids and weights of the m positions (entry 16 p + j: id j, then weight j - 8); an id is
+    // clamped below E so that a wait that gave up (stale entries) keeps every index in range
+    const int t = threadIdx.x, p = t / 16, j = t % 16;
+    int idx[1] = {t < m * 16 ? t : 0};
+    bool use[1] = {t < m * 16 && (j & 7) < k};
+    unsigned v[1];
+    const __amdgpu_buffer_rsrc_t rr = l2_buffer(f.rk + (size_t)xc * P * 16, P * 16 * 8);
+    const bool ok = poll_m<1>([&](int i) { return l2_load_u64(rr, 8u * (unsigned)i); }, idx, use, ep(1u),
+                              dead_s ? 0 : spin_max, v);
+    if (use[0]) {
+      if (j < 8)
+        ids_s[p * k + j] = (int)min(v[0], (unsigned)(E - 1));
+      else
+        w_s[p * k + j - 8] = __uint_as_float(v[0]);
+    }
+    fail(ok, 1u);
+  }
   __syncthreads();
   if (bid == 0)
     for (int i = threadIdx.x; i < m * k; i += NT) {
@@ -864,7 +883,7 @@ hipError_t launch_grp_fused(hipStream_t s, const LayerDev& L, int m, int k, int 
       epoch == 0 || L.gate_up.dtype != DT_Q8_0 || L.down.dtype != DT_Q8_0 || L.router.dtype != DT_Q8_0 ||
       L.router.cols != H || L.down.cols != inter || !g.gu.q || !g.dn.q || g.gu.rows != E * 2 * inter ||
       g.gu.cols != H || g.dn.rows != E * H || g.dn.cols != inter || !f.err || !f.lg || !f.xflag || !f.xh || !f.xl ||
-      !f.xd || !f.act || !f.o)
+      !f.xd || !f.act || !f.o || !f.rk)
     return hipErrorInvalidValue;
   switch (H) {
     case 1024: klaunch(k_grp_fused<1024>, 256, kFbThreads, 0, s, L.router, L.router_bias, x, m, k, epoch, g, f, y); break;

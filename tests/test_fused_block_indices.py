@@ -23,6 +23,7 @@ def alloc_bytes(H, E):
         "xd": 8 * P * (H // 32) * 4,
         "act": EMAX * NBI * AW * P * 2 * 4,
         "o": P * 8 * H * 2 * 4,
+        "rk": 8 * P * 16 * 2 * 4,
         "gu_q": E * 2 * I * H,             # tiled gate_up payload (Q8_0: one byte per weight)
         "gu_d": E * 2 * I * H // 32 * 2,
         "dn_q": E * H * I,
@@ -36,7 +37,7 @@ def alloc_bytes(H, E):
 
 def lds_bytes(H):
     NB, STR, SA = H // 32, H + 16, I + 16
-    return {"big": max(2 * P * STR, 2 * 2 * P * SA), "xd": P * NB * 4, "ad": 2 * P * NBI * 4, "lgs": P * 64 * 4,
+    return {"big": max(2 * P * STR, 2 * 2 * P * SA), "xd": P * NB * 4, "ad": 2 * P * NBI * 4, "lgs": 64 * 4,
             "sdt": NW * NB * 16 * 2, "gout": 2 * 2 * 32 * (P + 1) * 4, "ids": P * 8 * 4, "w": P * 8 * 4}
 
 
@@ -99,12 +100,31 @@ def check_step(H, E, m, k, pool):
                         assert (idx + 1) * ENTRY <= sz["lg"]
                         dots[(xc, p, e)] = dots.get((xc, p, e), 0) + 1
     assert dots == {(xc, p, e): 1 for xc in range(8) for p in range(m) for e in range(E)}
-    # the logits gather and the codes into LDS (same for every workgroup)
-    for q in range((P * 64 + NT - 1) // NT):
-        for t in range(NT):
-            i = t + q * NT
-            if i < m * E:
-                assert i < LGN and i // E < P and i % E < 64
+    # the top-k of position w by wave 0 of workgroup w < m of each XCD: its E logits, then 8 ids and 8 weights
+    ranked = {}
+    for bid in range(256):
+        xc, w = bid % 8, bid // 8
+        if w < m:
+            for lane in range(64):
+                idx = w * E + (lane if lane < E else 0)
+                assert idx < LGN and (xc * LGN + idx + 1) * ENTRY <= sz["lg"] and lane < 64
+                if lane < k:
+                    for off in (lane, 8 + lane):
+                        e = (xc * P + w) * 16 + off
+                        assert (e + 1) * ENTRY <= sz["rk"]
+                        ranked[e] = ranked.get(e, 0) + 1
+    assert ranked == {(xc * P + w) * 16 + o: 1 for xc in range(8) for w in range(m) for o in
+                      list(range(k)) + list(range(8, 8 + k))}
+    # every workgroup gathers the m positions' entries it uses, each once, into ids_s / w_s
+    got = set()
+    for t in range(NT):
+        p, j = t // 16, t % 16
+        if t < m * 16 and (j & 7) < k:
+            assert (t + 1) * ENTRY <= P * 16 * ENTRY
+            tgt = ("id", p * k + j) if j < 8 else ("w", p * k + j - 8)
+            assert tgt[1] < m * k <= P * 8 and tgt not in got
+            got.add(tgt)
+    assert got == {(kind, i) for kind in ("id", "w") for i in range(m * k)}
     XC, XD = (P * (H // 16) + NT - 1) // NT, (P * NB + NT - 1) // NT
     loaded = []
     for t in range(NT):
