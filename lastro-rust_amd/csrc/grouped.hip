@@ -226,10 +226,12 @@ hipError_t launch_tile_q8(hipStream_t s, const DMat& src, uint8_t* q, uint16_t* 
 }
 
 // ------------------------------------------------------------------------------------------------------------
-// Gate/up of list expert u = blockIdx.y for its members, rows [RT t, RT t + RT) of gate and of up (t = blockIdx.x,
-// RT = 16 * NT / 128): the first half of the waves computes 16 gate rows each, the second half the same up rows, so
-// the members' codes staged in LDS serve every wave. Then act = silu(g)*u and its hi/lo codes (each 32 rows are
-// one block of the act vector), written to the members' slots.
+// Gate/up of list expert u = blockIdx.y for its members [NM z, NM z + NM) (z = blockIdx.z; a workgroup past the
+// expert's member count ends at once), rows [RT t, RT t + RT) of gate and of up (t = blockIdx.x, RT = 16 * NT /
+// 128): the first half of the waves computes 16 gate rows each, the second half the same up rows, so the members'
+// codes staged in LDS serve every wave. Then act = silu(g)*u and its hi/lo codes (each 32 rows are one block of the
+// act vector), written to the members' slots. Each member's column and act codes depend on that member alone, so
+// the cut of the members into groups of NM changes no result.
 constexpr int kGrpUpThreads = 512;
 
 template <int H, int NM, int NT>
@@ -249,8 +251,11 @@ __global__ __launch_bounds__(NT) void k_grp_up(int m, int k, int inter, GroupBuf
   const int u = blockIdx.y, tile = blockIdx.x;
   make_plan<NT>(g.ids, m, k, plan);
   if (u >= plan.nu) return;
-  const int e = plan.list[u], off = plan.offe[e];
-  const unsigned bits = plan.bits[e];
+  const int c0 = NM * blockIdx.z;  // this workgroup's first member
+  const int e = plan.list[u], off = plan.offe[e] + c0;
+  unsigned bits = plan.bits[e];
+  if (__popc(bits) <= c0) return;
+  for (int i = 0; i < c0; i++) bits &= bits - 1u;  // the members from c0 on
   const int ne = __popc(bits);
   // this wave's 16 rows: gate (first half) or up (second half) rows [RT tile + 16 (wave % WH), +16) of expert e
   const size_t t16 = ((size_t)e * 2 * inter + (size_t)(wave / WH) * inter + RT * tile + 16 * (wave % WH)) / 16;
@@ -303,11 +308,12 @@ __global__ __launch_bounds__(NT) void k_grp_up(int m, int k, int inter, GroupBuf
       if (part == 0) g.ad[slotv * (inter / 32) + blk] = d;
     }
   }
-  if (u == 0 && tile == 0) publish_plan<NT>(plan, g.w, m, k, g.grp);
+  if (u == 0 && tile == 0 && c0 == 0) publish_plan<NT>(plan, g.w, m, k, g.grp);
 }
 
 // ------------------------------------------------------------------------------------------------------------
-// Down of list expert u = blockIdx.y for its members, output rows [64t, 64t+64): o[slot][row].
+// Down of list expert u = blockIdx.y for its members [NM z, NM z + NM) (z = blockIdx.z; a workgroup past the
+// expert's member count ends at once), output rows [64t, 64t+64): o[slot][row].
 template <int I, int NM>
 __global__ __launch_bounds__(256, NM == 16 ? 2 : 1) void k_grp_down(int hidden, GroupBufs g) {
   constexpr int NB = I / 32;
@@ -319,7 +325,9 @@ __global__ __launch_bounds__(256, NM == 16 ? 2 : 1) void k_grp_down(int hidden, 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int u = blockIdx.y, tile = blockIdx.x;
   if (u >= g.grp[GRP_NU]) return;
-  const int e = g.grp[GRP_LIST + u], ne = g.grp[GRP_CNT + u], off = g.grp[GRP_OFF + u];
+  const int c0 = NM * blockIdx.z;
+  if (g.grp[GRP_CNT + u] <= c0) return;
+  const int e = g.grp[GRP_LIST + u], ne = g.grp[GRP_CNT + u] - c0, off = g.grp[GRP_OFF + u] + c0;
   const size_t t16 = ((size_t)e * hidden + 64 * tile + 16 * wave) / 16;  // this wave's 16 output rows
   TileScales<NB> sc;
   fetch_scales<NB>(g.dn, t16, NB, 0, sc);
@@ -438,27 +446,24 @@ hipError_t launch_grp_experts(hipStream_t s, int H, int E, int m, int k, int int
     return hipErrorInvalidValue;
   hipError_t e;
   const int U = m * k < E ? m * k : E;
-  const bool wide = m > 16;
+  const int CH = (m + 15) / 16;  // member groups of 16: a step's expert has at most m members
   // u is the slow grid index, so the workgroups of list indices past the step's expert count (which end at once)
   // are dispatched last
   constexpr int NT = kGrpUpThreads, RT = 16 * NT / 128;
-  const dim3 gu_grid(inter / RT, U);
+  const dim3 gu_grid(inter / RT, U, CH);
   arm(1);
   if (H == 1024) {
-    if (wide) klaunch(k_grp_up<1024, 32, NT>, gu_grid, NT, 0, s, m, k, inter, g);
-    else klaunch(k_grp_up<1024, 16, NT>, gu_grid, NT, 0, s, m, k, inter, g);
+    klaunch(k_grp_up<1024, 16, NT>, gu_grid, NT, 0, s, m, k, inter, g);
   } else {
-    if (wide) klaunch(k_grp_up<1536, 32, NT>, gu_grid, NT, 0, s, m, k, inter, g);
-    else klaunch(k_grp_up<1536, 16, NT>, gu_grid, NT, 0, s, m, k, inter, g);
+    klaunch(k_grp_up<1536, 16, NT>, gu_grid, NT, 0, s, m, k, inter, g);
   }
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  const dim3 dn_grid(H / 64, U);
+  const dim3 dn_grid(H / 64, U, CH);
   arm(2);
   switch (inter) {
 #define DOWN_CASE(II)                                                                               \
   case II:                                                                                          \
-    if (wide) klaunch(k_grp_down<II, 32>, dn_grid, 256, 0, s, H, g);                            \
-    else klaunch(k_grp_down<II, 16>, dn_grid, 256, 0, s, H, g);                                 \
+    klaunch(k_grp_down<II, 16>, dn_grid, 256, 0, s, H, g);                                      \
     break;
     DOWN_CASE(128)
     DOWN_CASE(256)

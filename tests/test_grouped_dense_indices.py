@@ -170,3 +170,55 @@ def test_norm_and_combine_elements_and_codes(H):
         for j in range(NP):
             v = [1024 * j + 4 * t < H for t in range(t0, t0 + 8)]
             assert all(v) or not any(v)
+
+
+def _nth_set_bit(bits, c):
+    for _ in range(c):
+        bits &= bits - 1
+    return (bits & -bits).bit_length() - 1
+
+
+@pytest.mark.parametrize("m,k,E", [(1, 8, 40), (16, 8, 40), (17, 8, 40), (32, 8, 40), (32, 2, 6), (24, 4, 64)])
+def test_expert_member_groups_cover_every_member_once(m, k, E):
+    """k_grp_up / k_grp_down take an expert's members in groups of 16 (grid z = ceil(m / 16)): workgroup z handles
+    members [16 z, 16 z + 16) and ends at once when the expert has no more. Each (expert, member) is computed once,
+    its position is the member index's set bit of the expert's mask (the group's mask has its first 16 z bits
+    cleared), and its slot off + 16 z + j stays below m * k."""
+    rng = np.random.default_rng(m * 100 + k * 10 + E)
+    ids = [list(rng.choice(E, size=k, replace=False)) for _ in range(m)]
+    # a skewed step: the first expert routed by every position
+    ids = [[0] + [e for e in row if e != 0][:k - 1] for row in ids]
+    order, bits = [], {}
+    for row in ids:
+        for e in row:
+            if e not in bits:
+                order.append(e)
+                bits[e] = 0
+    for p, row in enumerate(ids):
+        for e in row:
+            bits[e] |= 1 << p
+    offe, off = {}, 0
+    for e in order:
+        offe[e] = off
+        off += bin(bits[e]).count("1")
+    CH = (m + 15) // 16
+    done = {}
+    for u, e in enumerate(order):
+        ne_all = bin(bits[e]).count("1")
+        for z in range(CH):
+            c0 = 16 * z
+            if ne_all <= c0:
+                continue  # the workgroup ends at once
+            b = bits[e]
+            for _ in range(c0):
+                b &= b - 1
+            ne = bin(b).count("1")
+            assert ne == ne_all - c0
+            for j in range(min(16, ne)):
+                pos = _nth_set_bit(b, j)
+                assert pos == _nth_set_bit(bits[e], c0 + j)
+                slot = offe[e] + c0 + j
+                assert slot < m * k
+                done[(e, c0 + j)] = done.get((e, c0 + j), 0) + 1
+    assert done == {(e, c): 1 for e in order for c in range(bin(bits[e]).count("1"))}
+    assert max(bin(bits[e]).count("1") for e in order) == m  # expert 0: every position, so z reaches m - 1
