@@ -259,8 +259,8 @@ int moert_time_kernel(moert_model* m, int kind, int iters, double* us_per_launch
  * otherwise *attn_block = 1 when the attention half is the one-launch attention block (MOERT_K_ATTN_BLOCK) rather
  * than q/k/v + split attention + combine, and *moe_xcd = 1 when the MoE half is the kernel spread over the XCDs
  * (MOERT_K_MOE_XCD) rather than router + gate/up and down. They depend on the shapes, the model kind and its modes
- * (the cache's prefetch branch uses none of them); MOERT_LAYER=0 at create keeps the three launches per layer. No
- * reference counterpart. */
+ * (the cache's prefetch side branch uses none of them; its prefetch inside the attention launch keeps the
+ * attention block); MOERT_LAYER=0 at create keeps the three launches per layer. No reference counterpart. */
 int moert_model_path(const moert_model* m, int* layer, int* attn_block, int* moe_xcd);
 
 /* Test hook for the failure path of the fused kernels (MOERT_K_ATTN_BLOCK, MOERT_K_MOE_XCD); it has no counterpart
@@ -269,7 +269,8 @@ int moert_model_path(const moert_model* m, int* layer, int* attn_block, int* moe
  * for an epoch no launch writes, with every wait of those launches bounded to a few hundred polls, so that the wait
  * gives up and the kernels still end normally; the next synchronising call then reports MOERT_E_DEVICE naming the
  * wait, and the model is poisoned. MOERT_E_CONFIG for an expert-cache or hybrid model, or one that does not use
- * the fused kernels. */
+ * the fused kernels. Bit 16 alone (the wait of the cache prefetch's copy workgroups for the layer's predicted misses)
+ * applies to an expert-cache model whose prefetch runs inside the attention launch, and to no other. */
 int moert_fault_inject(moert_model* m, unsigned bits);
 
 /* Phase timeline of one decode step (measurement build libmoert_tl.so only; MOERT_E_CONFIG otherwise): one graph

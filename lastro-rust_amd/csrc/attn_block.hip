@@ -421,12 +421,16 @@ __global__ __launch_bounds__(G * T * 64) void k_attn_block_pf(DMat m, const floa
   }
   const unsigned sctr = __builtin_amdgcn_readfirstlane(
       __builtin_amdgcn_raw_buffer_load_b32(l2_buffer(step_ctr, 4), 0, 0, 0));
-  const unsigned err0 =
-      __builtin_amdgcn_readfirstlane(__builtin_amdgcn_raw_buffer_load_b32(l2_buffer(err, 8), 0, 0, 0));
+  // err[0]: error bits (a launch that finds one set waits for nothing); err[1]: the host's test mask
+  // (moert_fault_inject): with bit 16 the copy workgroups wait for an epoch the decide does not write, and with any
+  // bit every wait polls at most kInjectSpin times
+  const auto ev = __builtin_amdgcn_raw_buffer_load_b64(l2_buffer(err, 8), 0, 0, 0);
+  const unsigned err0 = __builtin_amdgcn_readfirstlane(ev[0]), inj = __builtin_amdgcn_readfirstlane(ev[1]);
   const unsigned epoch = sctr * 64u + layer + 1u;
   if (extra == 0) {
     pf_decide<DT, K, NT>(pf, h, epoch);
-  } else if (!pf_copy<NT>(pf.c, epoch, extra - 1, err0 != 0) && threadIdx.x == 0 && !err0) {
+  } else if (!pf_copy<NT>(pf.c, (inj & 16u) ? kNoEpoch : epoch, extra - 1, err0 ? 0 : inj ? kInjectSpin : kPfSpin) &&
+             threadIdx.x == 0 && !err0) {
     atomicOr(err, 16u);
   }
 }

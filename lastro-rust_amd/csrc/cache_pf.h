@@ -113,15 +113,14 @@ __device__ __forceinline__ void pf_decide(const PfArgs& a, const float* __restri
   }
 }
 
-// Copy workgroup `part` (NT threads): waits (bounded) for the list, then copies part `part` of each listed record.
-// Returns false when the wait gave up.
+// Copy workgroup `part` (NT threads): waits (at most `spin` polls) for the list entries carrying `epoch`, then copies
+// part `part` of each listed record. Returns false when the wait gave up.
 template <int NT>
-__device__ __forceinline__ bool pf_copy(const CacheDev& c, unsigned epoch, int part, bool dead) {
+__device__ __forceinline__ bool pf_copy(const CacheDev& c, unsigned epoch, int part, int spin) {
   __shared__ int list_s[1 + 2 * 8];
   if (threadIdx.x < 64) {
     const int lane = threadIdx.x;
     // the count first, then the pairs it announces
-    int spin = dead ? 0 : kPfSpin;
     bool ok = false;
     unsigned n = 0;
     for (int it = 0; it < spin; it++) {

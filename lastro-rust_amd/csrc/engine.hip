@@ -1880,10 +1880,17 @@ int moert_model_path(const moert_model* m, int* layer, int* attn_block, int* moe
 
 int moert_fault_inject(moert_model* m, unsigned bits) {
   MODEL_OK(m);
-  CHECK_CFG((bits & ~14u) == 0, "fault_inject: bits %#x outside 2 | 4 | 8", bits);
-  // resident models only: there every index a failed launch leaves behind (token, routed expert) is still in range,
-  // while the expert cache would take slot-table decisions from the garbage values of a failed launch
-  CHECK_CFG(m->use_ab && !m->hybrid && !m->cached, "fault_inject: a resident model with the fused kernels only");
+  CHECK_CFG((bits & ~30u) == 0, "fault_inject: bits %#x outside 2 | 4 | 8 | 16", bits);
+  if (bits & 16u) {
+    // the prefetch's copy wait alone: the decision before it ran normally, so the slot tables stay consistent;
+    // the step that fails reports and poisons the handle before any later step reads the uncopied slots
+    CHECK_CFG(bits == 16u && m->cached && m->prefetch && m->pf_blk,
+              "fault_inject: bit 16 (alone) needs a cached model with the prefetch inside the attention launch");
+  } else {
+    // resident models only: there every index a failed launch leaves behind (token, routed expert) is still in
+    // range, while the expert cache would take slot-table decisions from the garbage values of a failed launch
+    CHECK_CFG(m->use_ab && !m->hybrid && !m->cached, "fault_inject: a resident model with the fused kernels only");
+  }
   CHECK_CFG(bits == 0 || (bits & 8u) == 0 || m->use_mx, "fault_inject: bit 8 needs the MoE kernel spread over the XCDs");
   MTRY(m, model_sync(m));
   MTRY(m, model_copy_in(m, m->ab.err + 1, &bits, 4));

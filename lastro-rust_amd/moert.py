@@ -605,8 +605,9 @@ class GpuModel:
         return "unfused"
 
     def fault_inject(self, bits: int):
-        """Test hook: the fused kernels' waits named by `bits` (2 queries / K/V row, 4 split partials, 8 act vector)
-        give up in the following launches, which still end normally (moert_fault_inject)."""
+        """Test hook: the fused kernels' waits named by `bits` (2 queries / K/V row, 4 split partials, 8 act vector;
+        16 alone: the cache prefetch's copy wait) give up in the following launches, which still end normally
+        (moert_fault_inject)."""
         check(lib().moert_fault_inject(self.h, bits))
 
 

@@ -387,3 +387,48 @@ def test_prefill_then_fused_decode_equals_the_oracle(gpu, granite_1b_wide, path)
     else:
         assert launches(g, moert.K_ATTN_BLOCK) == cfg.layers and launches(g, moert.K_MOE_XCD) == cfg.layers
     g.close()
+
+
+def test_prefetch_copy_wait_failure_is_reported_and_poisons(gpu):
+    """The failure path of the prefetch inside the attention launch, forced from the host (moert_fault_inject bit
+    16: the copy workgroups wait for an epoch the decide does not write, a few hundred polls): the step returns
+    MOERT_E_DEVICE naming the prefetch's wait, every kernel ends, the handle is poisoned afterwards, and a fresh
+    cached model with the prefetch in the same process still decodes bit-identically to the resident model. The bit
+    is refused without the in-launch prefetch and together with other bits."""
+    cfg = moert.Config(**moert.GRANITE_1B)
+    say("1B cached build (prefetch failure path)")
+    m = moert.SynthModel(cfg, seed=81, wdtype=moert.Q8_0, embed_dtype=moert.Q8_0, zipf_s=1.1)
+    res = three_kernel_model(m, MAX_LEN, SPLITS)
+    cac = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS, cache_slots=192)
+    with pytest.raises(moert.MoertError) as e:
+        cac.fault_inject(16)  # prefetch off
+    assert e.value.code == moert.E_CONFIG
+    cac.cache_prefetch_mode(True)
+    with pytest.raises(moert.MoertError) as e:
+        cac.fault_inject(16 | 2)
+    assert e.value.code == moert.E_CONFIG
+    toks = np.random.default_rng(52).integers(0, cfg.vocab, 12)
+    for tok in toks[:4]:
+        lr, _, _, _ = res.step(int(tok))
+        lc, _, _, _ = cac.step(int(tok))
+        assert bits_equal(lr, lc)
+    cac.fault_inject(16)
+    with pytest.raises(moert.MoertError) as e:
+        cac.step(int(toks[4]))
+    assert e.value.code == moert.E_DEVICE and "prefetch" in str(e.value), str(e.value)
+    with pytest.raises(moert.MoertError) as e:
+        cac.step(int(toks[5]))
+    assert e.value.code == moert.E_POISONED
+    cac.close()
+    res.close()
+    say("fresh cached model after the failure")
+    res = three_kernel_model(m, MAX_LEN, SPLITS)
+    fresh = moert.GpuModel(m, MAX_LEN, attn_splits=SPLITS, cache_slots=192)
+    fresh.cache_prefetch_mode(True)
+    assert fresh.kernel_path() == "block"
+    for tok in toks:
+        lr, ir, wr, _ = res.step(int(tok))
+        lc, ic, wc, _ = fresh.step(int(tok))
+        assert bits_equal(lr, lc) and np.array_equal(ir, ic) and bits_equal(wr, wc)
+    fresh.close()
+    res.close()
