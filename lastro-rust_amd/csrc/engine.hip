@@ -1006,7 +1006,17 @@ struct moert_block {
       CHECK_HIP(launch_grouped_block(s, L, m, dims.top_k, dims.inter, gx, g, gy, ev));
       return MOERT_OK;
     }
-    if (++fb_epoch == 0) fb_epoch = 1;
+    if (++fb_epoch == 0) {
+      // the epochs wrapped: every exchange entry back to epoch 0, which no launch writes, so that an entry left by a
+      // launch 2^32 steps ago can never pass for a current one
+      const size_t H = dims.hidden, P = kFbPos;
+      CHECK_HIP(hipMemsetAsync(fb.lg, 0, 8 * P * 64 * 8, s));
+      CHECK_HIP(hipMemsetAsync(fb.xflag, 0, 8 * P * 8, s));
+      CHECK_HIP(hipMemsetAsync(fb.act, 0, (size_t)kFbExperts * (kFbInter / 32) * kFbActW * P * 8, s));
+      CHECK_HIP(hipMemsetAsync(fb.o, 0, P * 8 * H * 8, s));
+      CHECK_HIP(hipMemsetAsync(fb.rk, 0, 8 * P * 16 * 8, s));
+      fb_epoch = 1;
+    }
     if (ev) arm_launch_events(ev[0], ev[1]);
     CHECK_HIP(launch_grp_fused(s, L, m, dims.top_k, dims.inter, gx, g, fb, fb_epoch, gy, cus));
     return MOERT_OK;
