@@ -516,17 +516,20 @@ __device__ __forceinline__ void code_block(const float (&v)[4], uint32_t& hw, ui
 }
 
 // Wave-level poll of one record of W entries per lane (entry i at src + S i, device-wide) until every used record
-// of the wave carries `epoch`; val gets the values. Returns false when the poll gave up (at once for spin 0).
+// of the wave carries `epoch`; val gets the values (left unset in a lane that does not use its record). Returns
+// false when the poll gave up (at once for spin 0).
 template <int W, int S>
 __device__ __forceinline__ bool poll_rec(const uint2* src, bool use, unsigned epoch, int spin, unsigned (&val)[W]) {
   for (int it = 0; it < spin; it++) {
     poll_fence();
     bool stale = false;
+    if (use) {  // one branch around the whole record: its loads still go out together, unused lanes load nothing
 #pragma unroll
-    for (int i = 0; i < W; i++) {
-      const uint2 e = get_dev(src + S * i);
-      val[i] = e.x;
-      stale |= use && e.y != epoch;
+      for (int i = 0; i < W; i++) {
+        const uint2 e = get_dev(src + S * i);
+        val[i] = e.x;
+        stale |= e.y != epoch;
+      }
     }
     if (__ballot(stale) == 0) return true;
     __builtin_amdgcn_s_sleep(1);
